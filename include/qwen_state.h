@@ -1,0 +1,151 @@
+/*
+ * qwen_state.h — C ABI of the MI355X (gfx950) decode-time state path of the hybrid Gated-DeltaNet /
+ * full-attention Qwen3.6-27B engine (libqwen_state.so).
+ *
+ * Conventions shared by every entry point:
+ *   - all data pointers are DEVICE memory owned by the caller; bf16 tensors are passed as uint16_t bit
+ *     patterns, fp32 as float, indices as int32;
+ *   - every call takes the HIP stream (hipStream_t, passed as void*) it enqueues on, returns 0 on success,
+ *     QS_EINVAL for an argument the library rejects (the message is in qs_last_error()), QS_EHIP for a HIP
+ *     launch error; no call allocates device memory, synchronises the host or records a memset, so every
+ *     call can be captured into a HIP graph;
+ *   - state tensors are updated in place where the reference updates them in place
+ *     (kernels/gdn_head_writer.cpp:109-114, kernels/attn_worker_writer.cpp:128-139);
+ *   - workspaces are caller-owned device buffers of the size the matching *_workspace_bytes() returns,
+ *     ZEROED ONCE before first use; the kernels leave them zeroed again (self-resetting counters), so one
+ *     workspace serves every later call on the same stream. Calls that run concurrently must not share a
+ *     workspace.
+ *
+ * Reference interfaces replaced are cited as path:line into sott0n/tt-qwen-resident.
+ *
+ * Layouts:
+ *   conv state   [B, C, K-1] bf16, oldest input first; taps [C, K] bf16 (tap 0 multiplies the oldest)
+ *   GDN state    [B, NV, DK, DV] fp32, S[k][v] row-major; value head h uses key head h / (NV / NK)
+ *   q|k|v        conv channels q (NK*DK) | k (NK*DK) | v (NV*DV)
+ *   KV pool      [num_blocks, NKV, block, HD] bf16; position p of user b lives in page
+ *                block_table[b * max_blocks + p / block], row p % block
+ */
+#ifndef QWEN_STATE_H
+#define QWEN_STATE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QS_OK 0
+#define QS_EINVAL (-1)
+#define QS_EHIP (-2)
+
+/* ABI version (bumped when a signature changes) and the last error message of the calling thread. */
+int qs_abi_version(void);
+const char *qs_last_error(void);
+
+/* ---------------------------------------------------------------------------------------- a1: conv1d
+ * Causal depthwise conv1d update + SiLU for one token per user, state shifted in place.
+ * Replaces the conv pass of the streamer (kernels/streamer_compute.cpp:275-370, ring order
+ * kernels/streamer_common.hpp:158-166) whose torch statement is model.py:255-259.
+ *   x [B, C] bf16, conv_state [B, C, K-1] bf16 (in/out), taps [C, K] bf16 -> y [B, C] bf16.  K == 4. */
+int qs_conv1d_update(const uint16_t *x, uint16_t *conv_state, const uint16_t *taps, uint16_t *y, int B, int C,
+                     int K, void *stream);
+
+/* ---------------------------------------------------------------------------------------- a3: gates
+ * g = neg_a * softplus(a + dt_bias) (threshold 20), beta = sigmoid(b) per (user, value head).
+ * Replaces the gate stage of kernels/gdn_head_compute.cpp:198-243 (torch model.py:268-269).
+ *   a, b [B, NV] bf16; dt_bias, neg_a [NV] fp32 -> g, beta [B, NV] fp32. */
+int qs_gdn_gates(const uint16_t *a, const uint16_t *b, const float *dt_bias, const float *neg_a, float *g,
+                 float *beta, int B, int NV, void *stream);
+
+/* ---------------------------------------------------------------------------------------- a2+a4: delta rule
+ * One gated delta rule decode step from post-conv q, k, v: L2-norm of q (times scale) and k, then
+ * delta = beta (v - (e^g k)^T S), S <- e^g S + k delta^T (in place), o = q^T S.
+ * Replaces the GDN head cores (kernels/gdn_head_compute.cpp:180-350, reader :105-212, writer :39-122;
+ * torch model.py:262-273).
+ *   q, k [B, NK, DK] bf16; v [B, NV, DV] bf16; g, beta [B, NV] fp32; state [B, NV, DK, DV] fp32 (in/out)
+ *   -> o [B, NV, DV] bf16.  DK == DV == 128, NV % NK == 0. */
+int qs_gdn_decode_step(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *g, const float *beta,
+                       float *state, uint16_t *o, int B, int NK, int NV, int DK, int DV, float scale, float eps,
+                       void *stream);
+
+/* Workspace of qs_gdn_decode_fused: one self-resetting counter per (user, key head). */
+size_t qs_gdn_workspace_bytes(int B, int NK);
+
+/* Conv1d update + L2-norm + delta rule of one decode step in one launch (a1+a2+a4): the GDN mixer state
+ * path of torch_step model.py:255-273 behind the projection. x [B, C] is the projection's q|k|v slice
+ * (C = 2 NK DK + NV DV); conv_state is shifted in place; y_out (nullable) receives the conv output. */
+int qs_gdn_decode_fused(const uint16_t *x, uint16_t *conv_state, const uint16_t *taps, const float *g,
+                        const float *beta, float *state, uint16_t *o, uint16_t *y_out, void *workspace, int B,
+                        int NK, int NV, int DK, int DV, int K, float scale, float eps, void *stream);
+
+/* ---------------------------------------------------------------------------------------- a7: verify
+ * T tokens per user (1 <= T <= 8) through conv + delta rule in sequence, keeping every intermediate:
+ *   x [B, T, C] bf16; conv_state_in [B, C, K-1]; g, beta [B, T, NV]; state_in [B, NV, DK, DV]
+ *   -> conv_states_out [T, B, C, K-1], states_out [T, B, NV, DK, DV], o [B, T, NV, DV], y_out (nullable)
+ *   [B, T, C]. Inputs are not modified.
+ * Replaces the verify rows of the GDN head cores (kernels/gdn_head_reader.cpp:149-187,
+ * gdn_head_writer.cpp:60-66, :109) and the conv pair-slot ring (kernels/streamer_common.hpp:38-44). */
+int qs_gdn_verify_step(const uint16_t *x, const uint16_t *conv_state_in, uint16_t *conv_states_out,
+                       const uint16_t *taps, const float *g, const float *beta, const float *state_in,
+                       float *states_out, uint16_t *o, uint16_t *y_out, int B, int T, int NK, int NV, int DK,
+                       int DV, int K, float scale, float eps, void *stream);
+
+/* Rollback after verify: state[b] <- states_out[accept_len[b]-1, b], conv_state[b] <- conv_states_out[...]
+ * (bit-exact copies), and, when seq_lens is non-null, seq_lens[b] <- base_lens[b] + accept_len[b] (the KV
+ * truncation; no KV bytes move). accept_len is device memory, 1 <= accept_len[b] <= T.
+ * Replaces the slot/ring advance of the hub (kernels/mlp_hub.cpp:48-58; model.py:1314-1318). */
+int qs_gdn_rollback(const float *states_out, float *state, const uint16_t *conv_states_out, uint16_t *conv_state,
+                    const int *accept_len, int *seq_lens, const int *base_lens, int B, int T, int NV, int DK,
+                    int DV, int C, int K, void *stream);
+
+/* ---------------------------------------------------------------------------------------- a5: paged append
+ * Write T new K and V rows per user at positions positions[b] + t into the paged pools (bit-exact).
+ *   k, v [B, T, NKV, HD] bf16; pools [num_blocks, NKV, block, HD]; block_table [B, max_blocks]; positions [B].
+ * Replaces the tail-core append (kernels/attn_compute_common.hpp:281-341, kernels/attn_worker_writer.cpp
+ * :128-143; torch model.py:245-246) with the vLLM block-table contract (block 64, tt-model.yaml:41). */
+int qs_paged_kv_append(const uint16_t *k, const uint16_t *v, uint16_t *k_cache, uint16_t *v_cache,
+                       const int *block_table, const int *positions, int B, int T, int NKV, int HD, int block,
+                       int max_blocks, int num_blocks, void *stream);
+
+/* ---------------------------------------------------------------------------------------- a9: paged fill
+ * paged_fill_cache for one sequence: token i of k, v [NKV, T, HD] goes to page page_table[(start+i)/block],
+ * row (start+i) % block. Either of k/k_cache or v/v_cache may be null.
+ * Replaces ttnn.experimental.paged_fill_cache (prefill/pp_prefill.py:826-827). */
+int qs_paged_kv_fill(const uint16_t *k, const uint16_t *v, uint16_t *k_cache, uint16_t *v_cache,
+                     const int *page_table, int T, int start, int NKV, int HD, int block, int table_len,
+                     int num_blocks, void *stream);
+
+/* ---------------------------------------------------------------------------------------- a6: attention
+ * Paged GQA decode attention with split-K over block-table pages and an in-kernel ordered merge.
+ *   q [B, T, NQ, HD] bf16; seq_lens [B] = positions valid after this step's T tokens; query t of user b
+ *   attends positions 0 .. seq_lens[b] - T + t (causal among the T new rows); o [B, T, NQ, HD] bf16.
+ *   When k_new/v_new [B, T, NKV, HD] are non-null the T new rows are also appended (a5 fused): they are
+ *   written into their pages and attended from the inputs, so no call sees a half-written row.
+ *   pages_per_split: pages one workgroup walks (the split-K grain); the workspace holds the partials.
+ * Replaces the attention leader / chunk workers / tail core (kernels/attn_worker_compute.cpp:77-270,
+ * kernels/attn_leader_compute.cpp:42-105, kernels/attn_leader_writer.cpp:86-106, split schedule
+ * kernels/attn_common.hpp:139-154; torch model.py:239-246). HD == 256, block == 64, NQ / NKV <= 8. */
+size_t qs_paged_attention_workspace_bytes(int B, int T, int NQ, int NKV, int HD, int max_blocks,
+                                          int pages_per_split);
+int qs_paged_gqa_decode(const uint16_t *q, const uint16_t *k_new, const uint16_t *v_new, uint16_t *k_cache,
+                        uint16_t *v_cache, const int *block_table, const int *seq_lens, uint16_t *o,
+                        void *workspace, int B, int T, int NQ, int NKV, int HD, int block, int max_blocks,
+                        int num_blocks, int pages_per_split, float scale, void *stream);
+
+/* ---------------------------------------------------------------------------------------- a8: prefill
+ * Chunked gated delta rule over one sequence (WY/UT form, bf16 MFMA, fp32 state carry), L2-norm of q
+ * (times scale) and k inside:
+ *   q, k [T, NK, DK] bf16; v [T, NV, DV] bf16; g, beta [T, NV] fp32; initial_state [NV, DK, DV] fp32
+ *   -> o [T, NV, DV] bf16 (token-major), final_state [NV, DK, DV] fp32 (may alias initial_state).
+ * Replaces ttnn.transformer.chunk_gated_delta_rule as called at prefill/pp_prefill.py:791-807. */
+size_t qs_gdn_chunk_prefill_workspace_bytes(int T, int NK, int NV, int DK, int DV, int chunk);
+int qs_gdn_chunk_prefill(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *g,
+                         const float *beta, const float *initial_state, uint16_t *o, float *final_state,
+                         void *workspace, int T, int NK, int NV, int DK, int DV, int chunk, float scale,
+                         float eps, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QWEN_STATE_H */

@@ -1,0 +1,78 @@
+"""Paged GQA decode attention on the GPU against the oracle (gather + fp32 softmax over the pages):
+bf16 output rtol 2e-2; the fused append leaves the pools bit-identical to the oracle's append."""
+import pytest
+import torch
+from conftest import assert_bf16_output
+
+from oracle import state_path as O
+from qwen36_state import ops, workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+def run_case(dev, d, pps, fused=True):
+    """Attention (+ append) on the GPU and the same step through the oracle; returns (o_gpu, o_ref,
+    pools equal)."""
+    g = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in d.items()}
+    B, T = d["q"].shape[:2]
+    pos = d["seq_lens"] - T
+    if fused:
+        o = ops.paged_gqa_decode(g["q"], g["k_cache"], g["v_cache"], g["block_table"], g["seq_lens"], d["scale"],
+                                 k_new=g["k_new"], v_new=g["v_new"], pages_per_split=pps)  # fmt: skip
+    else:
+        ops.paged_kv_append(g["k_new"], g["v_new"], g["k_cache"], g["v_cache"], g["block_table"], pos.to(dev))
+        o = ops.paged_gqa_decode(g["q"], g["k_cache"], g["v_cache"], g["block_table"], g["seq_lens"], d["scale"],
+                                 pages_per_split=pps)  # fmt: skip
+    kc, vc = d["k_cache"].clone(), d["v_cache"].clone()
+    O.paged_append(kc, vc, d["k_new"], d["v_new"], d["block_table"], pos)
+    o_ref = O.gqa_decode(d["q"], kc, vc, d["block_table"], d["seq_lens"], d["scale"])
+    same = torch.equal(g["k_cache"].cpu(), kc) and torch.equal(g["v_cache"].cpu(), vc)
+    return o, O.bf16(o_ref), same
+
+
+@pytest.mark.parametrize(
+    "B,ctx,T,pps",
+    [
+        (1, 32768, 1, 8),  # one layer at 32k context: 512 pages, 64 splits, 2-level merge tree
+        (8, 4096, 1, 8),  # batch 8 at 4k: 64 pages per user
+        (1, 8192, 4, 8),  # verify: 4 new rows, causal among them
+        (1, 32768, 1, 1),  # 512 splits: 3-level merge tree
+        (2, 4096, 1, 64),  # one split: no merge
+    ],
+)
+def test_attention(dev, B, ctx, T, pps):
+    d = W.attn_layer(B, ctx, "cpu", seed=B + ctx + T + pps, T=T)
+    o, o_ref, same = run_case(dev, d, pps)
+    assert same
+    assert_bf16_output(o, o_ref)
+
+
+def test_attention_ragged_users(dev):
+    """Users at different lengths (1 position, exactly one page, one past a page, mid-page) in one launch."""
+    d = W.attn_layer(4, 11 * 64, "cpu", seed=77, T=1, num_blocks=64)
+    d["seq_lens"] = torch.tensor([1, 64, 65, 700], dtype=torch.int32)
+    o, o_ref, same = run_case(dev, d, pps=2)
+    assert same
+    assert_bf16_output(o, o_ref)
+    # a user with a single position attends only to its new row: o = v_new exactly (up to bf16 rounding)
+    torch.testing.assert_close(o[0, 0].cpu().float(), d["v_new"][0, 0].float().repeat_interleave(6, 0), rtol=0, atol=0)
+
+
+def test_attention_unfused_equals_fused(dev):
+    d = W.attn_layer(2, 1000, "cpu", seed=5, T=2, num_blocks=64)
+    o1, ref, _ = run_case(dev, d, pps=4, fused=True)
+    o2, _, same = run_case(dev, d, pps=4, fused=False)
+    assert same
+    assert torch.equal(o1.cpu(), o2.cpu())
+    assert_bf16_output(o1, ref)
+
+
+def test_attention_repeatable(dev):
+    d = W.attn_layer(1, 32768, "cpu", seed=9)
+    g = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in d.items()}
+    outs = [
+        ops.paged_gqa_decode(g["q"], g["k_cache"], g["v_cache"], g["block_table"], g["seq_lens"], d["scale"],
+                             k_new=g["k_new"], v_new=g["v_new"], pages_per_split=8).cpu()  # fmt: skip
+        for _ in range(3)
+    ]
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])

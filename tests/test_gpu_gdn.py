@@ -1,0 +1,137 @@
+"""GDN decode path on the GPU against the CPU oracle (conv1d update, gates, delta rule decode, fused
+conv + delta rule, T-token verify, rollback). Tolerances: conv state, snapshots and rollback bit-exact;
+conv outputs within one bf16 ulp (SiLU's exp differs in the last fp32 bit between libraries); fp32 state
+rtol 1e-4; bf16 o rtol 2e-2. The delta-rule checks feed the oracle the kernel's own conv output so a
+rare 1-ulp conv difference cannot masquerade as a state error."""
+import pytest
+import torch
+from conftest import assert_bf16_output, assert_state, bf16_ulp_mismatch
+
+from oracle import state_path as O
+from qwen36_state import ops, workloads as W
+
+pytestmark = pytest.mark.gpu
+NK, NV, DK, DV = 16, 48, 128, 128
+
+
+def inputs(B, seed=0, T=None):
+    return W.gdn_layer(B, "cpu", seed=seed, T=T)
+
+
+def to(d, dev):
+    return {k: v.to(dev) for k, v in d.items()}
+
+
+def check_conv(y_gpu, y_ref):
+    ulps, frac = bf16_ulp_mismatch(y_gpu, y_ref)
+    assert ulps <= 1 and frac < 1e-3, (ulps, frac)
+
+
+@pytest.mark.parametrize("B", [1, 8])
+def test_conv1d_update(dev, B):
+    d = inputs(B, seed=B)
+    g = to(d, dev)
+    y = ops.causal_conv1d_update(g["x"], g["conv_state"], g["taps"])
+    y_ref, cs_ref = O.conv1d_update(d["x"], d["conv_state"], d["taps"])
+    assert torch.equal(g["conv_state"].cpu().float(), cs_ref)
+    check_conv(y, y_ref)
+
+
+def test_gates(dev):
+    gen = torch.Generator().manual_seed(3)
+    a, b = torch.randn(8, NV, generator=gen).bfloat16(), torch.randn(8, NV, generator=gen).bfloat16()
+    dt, neg_a = 0.5 * torch.randn(NV, generator=gen), -torch.exp(torch.rand(NV, generator=gen) * 2 - 1)
+    a[0, :4] = torch.tensor([25.0, 19.5, -30.0, 0.0]).bfloat16()  # around the softplus threshold
+    g, beta = ops.gdn_gates(a.to(dev), b.to(dev), dt.to(dev), neg_a.to(dev))
+    g_ref, b_ref = O.gdn_gates(a.float(), b.float(), dt, neg_a)
+    torch.testing.assert_close(g.cpu(), g_ref, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(beta.cpu(), b_ref, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("B", [1, 8])
+def test_gdn_decode_step(dev, B):
+    """The unfused step (post-conv q, k, v) at the single-layer shapes: 16 key / 48 value heads, 128 x 128."""
+    d = inputs(B, seed=10 + B)
+    g = to(d, dev)
+    o = ops.gdn_decode_step(g["q"], g["k"], g["v"], g["g"], g["beta"], g["state"])
+    o_ref, S_ref = O.gdn_step(d["q"].float(), d["k"].float(), d["v"].float(), d["g"], d["beta"], d["state"])
+    assert_state(g["state"], S_ref)
+    assert_bf16_output(o, O.bf16(o_ref))
+
+
+@pytest.mark.parametrize("B", [1, 8])
+def test_gdn_decode_fused(dev, B):
+    """Conv + L2-norm + delta rule in one launch, called twice in a row (the second call proves the
+    per-key-head counters re-armed themselves)."""
+    d = inputs(B, seed=20 + B)
+    g = to(d, dev)
+    S, cs = d["state"], d["conv_state"].float()
+    for call in range(2):
+        x = W._randn((B, W.C_QKV), torch.Generator().manual_seed(100 + call), "cpu", torch.bfloat16)
+        y = torch.empty(B, W.C_QKV, dtype=torch.bfloat16, device=dev)
+        o = ops.gdn_decode_fused(x.to(dev), g["conv_state"], g["taps"], g["g"], g["beta"], g["state"], y_out=y)
+        y_ref, cs = O.conv1d_update(x, cs, d["taps"])
+        check_conv(y, y_ref)
+        assert torch.equal(g["conv_state"].cpu().float(), cs)
+        q, k, v = O.split_qkv(y.cpu().float(), NK, NV, DK, DV)
+        o_ref, S = O.gdn_step(q, k, v, d["g"], d["beta"], S)
+        assert_state(g["state"], S)
+        assert_bf16_output(o, O.bf16(o_ref))
+        S = g["state"].cpu()  # continue from the kernel's state (no drift between the two references)
+
+
+def test_gdn_masked_rows_leave_state(dev):
+    """g = 0, beta = 0 is the identity on the state, bit-exact (the prefill's masking rule)."""
+    d = inputs(2, seed=5)
+    g = to(d, dev)
+    before = g["state"].clone()
+    ops.gdn_decode_step(g["q"], g["k"], g["v"], torch.zeros_like(g["g"]), torch.zeros_like(g["beta"]), g["state"])
+    assert torch.equal(g["state"], before)
+
+
+def test_gdn_repeatable(dev):
+    d = inputs(8, seed=6)
+    outs = []
+    for _ in range(2):
+        g = to(d, dev)
+        o = ops.gdn_decode_fused(g["x"], g["conv_state"], g["taps"], g["g"], g["beta"], g["state"])
+        outs.append((o.cpu(), g["state"].cpu(), g["conv_state"].cpu()))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("B,T", [(1, 4), (3, 2)])
+def test_gdn_verify_and_rollback(dev, B, T):
+    d = inputs(B, seed=30 + T, T=T)
+    g = to(d, dev)
+    o, states, convs, y = ops.gdn_verify_step(g["x"], g["conv_state"], g["taps"], g["g"], g["beta"], g["state"],
+                                              return_y=True)  # fmt: skip
+    # inputs untouched
+    assert torch.equal(g["state"].cpu(), d["state"]) and torch.equal(g["conv_state"].cpu(), d["conv_state"])
+    S, cs = d["state"], d["conv_state"].float()
+    for t in range(T):
+        y_ref, cs = O.conv1d_update(d["x"][:, t], cs, d["taps"])
+        check_conv(y[:, t], y_ref)
+        assert torch.equal(convs[t].cpu().float(), cs)
+        q, k, v = O.split_qkv(y[:, t].cpu().float(), NK, NV, DK, DV)
+        o_ref, S = O.gdn_step(q, k, v, d["g"][:, t], d["beta"][:, t], S)
+        assert_state(states[t], S)
+        assert_bf16_output(o[:, t], O.bf16(o_ref))
+        S = states[t].cpu()
+    # rollback to a seeded accepted length per user, with the KV truncation
+    acc = torch.randint(1, T + 1, (B,), generator=torch.Generator().manual_seed(T), dtype=torch.int32)
+    base = torch.full((B,), 8188, dtype=torch.int32)
+    seq = torch.zeros(B, dtype=torch.int32, device=dev)
+    ops.gdn_rollback(states, convs, acc.to(dev), g["state"], g["conv_state"], seq, base.to(dev))
+    ref_s, ref_c = O.gdn_rollback(states.cpu(), convs.cpu(), acc)
+    assert torch.equal(g["state"].cpu(), ref_s) and torch.equal(g["conv_state"].cpu(), ref_c)
+    assert torch.equal(seq.cpu(), base + acc)
+
+
+def test_verify_one_token_equals_decode(dev):
+    d = inputs(2, seed=40)
+    g1, g2 = to(d, dev), to(d, dev)
+    o1 = ops.gdn_decode_fused(g1["x"], g1["conv_state"], g1["taps"], g1["g"], g1["beta"], g1["state"])
+    o2, st, cv = ops.gdn_verify_step(g2["x"][:, None], g2["conv_state"], g2["taps"], g2["g"][:, None],
+                                     g2["beta"][:, None], g2["state"])  # fmt: skip
+    assert torch.equal(o1, o2[:, 0]) and torch.equal(g1["state"], st[0]) and torch.equal(g1["conv_state"], cv[0])

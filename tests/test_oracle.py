@@ -1,0 +1,297 @@
+"""Pins the CPU oracle: golden fixtures (scalar fp64 loops), closed forms, invariants and special cases
+chosen so a plausible mistake (a swapped tap order, a wrong key-head index, a dropped decay, a transposed
+state, an off-by-one page index, a missing causal mask) fails at least one check. No GPU needed."""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import state_path as O
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "state_path_small.npz")
+
+
+@pytest.fixture(scope="module")
+def gold():
+    with np.load(GOLD, allow_pickle=False) as z:
+        return {k: torch.from_numpy(z[k]) for k in z.files}
+
+
+def bfr(*shape, gen, std=1.0):
+    return O.bf16(std * torch.randn(*shape, generator=gen))
+
+
+# ------------------------------------------------------------------------------------------- golden vectors
+
+
+def test_golden_conv(gold):
+    y, ns = O.conv1d_update(gold["conv_x"], gold["conv_state"], gold["conv_taps"])
+    assert torch.equal(ns, gold["conv_new_state"])
+    # bf16 outputs: at most one bf16 ulp from the fp64-silu fixture
+    assert torch.allclose(y, gold["conv_y"], rtol=2**-8, atol=0)
+
+
+def test_golden_gdn_step(gold):
+    o, S2 = O.gdn_step(gold["gdn_q"], gold["gdn_k"], gold["gdn_v"], gold["gdn_g"], gold["gdn_beta"], gold["gdn_S"])
+    torch.testing.assert_close(o, gold["gdn_o"], rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(S2, gold["gdn_S2"], rtol=1e-12, atol=1e-12)
+
+
+def test_golden_attention(gold):
+    o = O.gqa_decode(gold["att_q"], gold["att_k"], gold["att_v"], gold["att_table"], gold["att_seq"],
+                     scale=1 / math.sqrt(8), dtype=torch.float64)  # fmt: skip
+    torch.testing.assert_close(o, gold["att_o"], rtol=1e-12, atol=1e-12)
+
+
+def test_golden_prefill(gold):
+    args = [gold[f"pre_{n}"] for n in ("q", "k", "v", "g", "beta", "S0")]
+    o, S = O.gdn_chunk_prefill(*args)
+    torch.testing.assert_close(o, gold["pre_o"], rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(S, gold["pre_ST"], rtol=1e-12, atol=1e-12)
+    o2, S2 = O.gdn_chunk_prefill_wy(*args, chunk=4)  # 9 tokens: chunks of 4, 4, 1
+    torch.testing.assert_close(o2, gold["pre_o"], rtol=1e-10, atol=1e-12)
+    torch.testing.assert_close(S2, gold["pre_ST"], rtol=1e-10, atol=1e-12)
+
+
+# ------------------------------------------------------------------------------------------- a1 conv
+
+
+def test_conv_matches_loops():
+    g = torch.Generator().manual_seed(0)
+    x, cs, taps = bfr(3, 17, gen=g), bfr(3, 17, 3, gen=g), bfr(17, 4, gen=g, std=0.5)
+    y, ns = O.conv1d_update(x, cs, taps)
+    y2, ns2 = O.conv1d_update_loops(x, cs, taps)
+    assert torch.equal(ns, ns2)
+    assert torch.allclose(y, y2, rtol=2**-8, atol=0)
+
+
+def test_conv_tap_order_and_impulse():
+    """Tap 0 multiplies the oldest input (weights.py:58): state [a, 0, 0], x = 0 gives silu(w0 a); an
+    impulse in x with a zero state gives silu(w3)."""
+    taps = torch.tensor([[0.5, -0.25, 2.0, 1.5]])
+    a = torch.tensor([[[3.0, 0.0, 0.0]]])
+    y, ns = O.conv1d_update(torch.zeros(1, 1), a, taps)
+    assert float(y) == float(O.bf16(torch.nn.functional.silu(torch.tensor(1.5))))
+    assert ns.tolist() == [[[0.0, 0.0, 0.0]]]
+    y, _ = O.conv1d_update(torch.ones(1, 1), torch.zeros(1, 1, 3), taps)
+    assert float(y) == float(O.bf16(torch.nn.functional.silu(torch.tensor(1.5))))
+    y, _ = O.conv1d_update(torch.zeros(1, 1), torch.tensor([[[0.0, 0.0, 1.0]]]), taps)
+    assert float(y) == float(O.bf16(torch.nn.functional.silu(torch.tensor(2.0))))
+
+
+def test_conv_shift_invariant():
+    """After K-1 new inputs the state is exactly those inputs (oldest first)."""
+    g = torch.Generator().manual_seed(1)
+    cs, taps = bfr(2, 5, 3, gen=g), bfr(5, 4, gen=g)
+    xs = [bfr(2, 5, gen=g) for _ in range(3)]
+    for x in xs:
+        _, cs = O.conv1d_update(x, cs, taps)
+    assert torch.equal(cs, torch.stack(xs, -1))
+
+
+# ------------------------------------------------------------------------------------------- a2 / a3
+
+
+def test_l2norm_unit_and_scale_invariant():
+    g = torch.Generator().manual_seed(2)
+    k = torch.randn(4, 128, generator=g, dtype=torch.float64)
+    n = O.l2norm(k, eps=0.0)
+    torch.testing.assert_close(n.norm(dim=-1), torch.ones(4, dtype=torch.float64))
+    torch.testing.assert_close(O.l2norm(7.5 * k, eps=0.0), n)
+    # eps enters under the square root: |k̂|^2 = s / (s + eps)
+    s = k.pow(2).sum(-1)
+    torch.testing.assert_close(O.l2norm(k, eps=1e-2).pow(2).sum(-1), s / (s + 1e-2))
+
+
+def test_gates_scalar():
+    a = torch.tensor([-3.0, 0.2, 19.0, 25.0])
+    dt = torch.tensor([0.5, -0.1, 0.5, 0.0])
+    neg_a = torch.tensor([-0.7, -1.3, -0.2, -0.9])
+    b = torch.tensor([-2.0, 0.0, 1.0, 30.0])
+    g, beta = O.gdn_gates(a, b, dt, neg_a)
+    for i in range(4):
+        z = float(a[i] + dt[i])
+        sp = z if z > 20 else math.log1p(math.exp(z))
+        assert abs(float(g[i]) - float(neg_a[i]) * sp) < 1e-5 * max(1.0, abs(sp))
+        assert abs(float(beta[i]) - 1 / (1 + math.exp(-float(b[i])))) < 1e-6
+    assert float(g[3]) == float(neg_a[3] * 25.0)  # above the threshold softplus is the identity
+
+
+# ------------------------------------------------------------------------------------------- a4 delta rule
+
+
+def _gdn_inputs(B=2, NK=2, NV=6, DK=8, DV=8, seed=3, dtype=torch.float64):
+    g = torch.Generator().manual_seed(seed)
+    q, k = torch.randn(B, NK, DK, generator=g), torch.randn(B, NK, DK, generator=g)
+    v = torch.randn(B, NV, DV, generator=g)
+    gg = -torch.nn.functional.softplus(torch.randn(B, NV, generator=g))
+    beta = torch.sigmoid(torch.randn(B, NV, generator=g))
+    S = 0.1 * torch.randn(B, NV, DK, DV, generator=g)
+    return [t.to(dtype) for t in (q, k, v, gg, beta, S)]
+
+
+def test_gdn_step_matches_loops():
+    q, k, v, g, beta, S = _gdn_inputs()
+    o, S2 = O.gdn_step(q, k, v, g, beta, S)
+    o2, S3 = O.gdn_step_loops(q, k, v, g, beta, S)
+    torch.testing.assert_close(o, o2, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(S2, S3, rtol=1e-12, atol=1e-12)
+
+
+def test_gdn_identity_when_masked():
+    """g = 0, beta = 0 (the prefill's masked rows, prefill/pp_prefill.py:14-17) leaves the state bit-exact."""
+    q, k, v, g, beta, S = _gdn_inputs(dtype=torch.float32)
+    _, S2 = O.gdn_step(q, k, v, torch.zeros_like(g), torch.zeros_like(beta), S)
+    assert torch.equal(S2, S)
+
+
+def test_gdn_rank1_from_zero_state():
+    q, k, v, g, beta, S = _gdn_inputs()
+    o, S2 = O.gdn_step(q, k, v, g, beta, torch.zeros_like(S))
+    kn = O.l2norm(k.repeat_interleave(3, 1))
+    qn = O.l2norm(q.repeat_interleave(3, 1)) * 8**-0.5
+    ref = beta[..., None, None] * kn[..., :, None] * v[..., None, :]
+    torch.testing.assert_close(S2, ref)
+    torch.testing.assert_close(o, (qn * kn).sum(-1, keepdim=True) * beta[..., None] * v)
+
+
+def test_gdn_writes_value_at_key():
+    """decay = 1, beta = 1: k̂^T S' = v up to the L2-norm eps (the delta rule's defining property)."""
+    q, k, v, g, beta, S = _gdn_inputs()
+    _, S2 = O.gdn_step(q, k, v, torch.zeros_like(g), torch.ones_like(beta), S, eps=0.0)
+    kn = O.l2norm(k.repeat_interleave(3, 1), eps=0.0)
+    torch.testing.assert_close((kn[..., None, :] @ S2).squeeze(-2), v, rtol=1e-10, atol=1e-10)
+
+
+def test_gdn_key_head_grouping_and_columns():
+    """Value head h reads key head h // (NV / NK); value columns are independent."""
+    q, k, v, g, beta, S = _gdn_inputs()
+    o, S2 = O.gdn_step(q, k, v, g, beta, S)
+    for h in range(6):
+        kh = h // 3
+        oh, Sh = O.gdn_step(q[:, kh : kh + 1], k[:, kh : kh + 1], v[:, h : h + 1], g[:, h : h + 1],
+                            beta[:, h : h + 1], S[:, h : h + 1])  # fmt: skip
+        torch.testing.assert_close(oh[:, 0], o[:, h], rtol=0, atol=0)
+        torch.testing.assert_close(Sh[:, 0], S2[:, h], rtol=0, atol=0)
+    oc, Sc = O.gdn_step(q, k, v[..., 2:5], g, beta, S[..., 2:5].contiguous())
+    torch.testing.assert_close(oc, o[..., 2:5], rtol=1e-14, atol=1e-14)
+    torch.testing.assert_close(Sc, S2[..., 2:5], rtol=1e-14, atol=1e-14)
+
+
+# ------------------------------------------------------------------------------------------- a7 verify
+
+
+def test_verify_equals_sequential_and_rollback():
+    g = torch.Generator().manual_seed(4)
+    NK, NV, DK, DV, B, T = 1, 3, 4, 4, 2, 3
+    C = 2 * NK * DK + NV * DV
+    x, cs, taps = bfr(B, T, C, gen=g), bfr(B, C, 3, gen=g), bfr(C, 4, gen=g, std=0.5)
+    gg = -torch.rand(B, T, NV, generator=g)
+    beta = torch.rand(B, T, NV, generator=g)
+    S = 0.1 * torch.randn(B, NV, DK, DV, generator=g)
+    o, states, convs, ys = O.gdn_verify(x, cs, taps, gg, beta, S, NK, NV, DK, DV)
+    St, cst = S, cs
+    for t in range(T):
+        ot, St, cst, yt = O.gdn_decode(x[:, t], cst, taps, gg[:, t], beta[:, t], St, NK, NV, DK, DV)
+        assert torch.equal(ot, o[:, t]) and torch.equal(St, states[t]) and torch.equal(cst, convs[t])
+    o1, s1, c1, _ = O.gdn_verify(x[:, :1], cs, taps, gg[:, :1], beta[:, :1], S, NK, NV, DK, DV)
+    od, Sd, cd, _ = O.gdn_decode(x[:, 0], cs, taps, gg[:, 0], beta[:, 0], S, NK, NV, DK, DV)
+    assert torch.equal(o1[:, 0], od) and torch.equal(s1[0], Sd) and torch.equal(c1[0], cd)
+    st, cv = O.gdn_rollback(states, convs, [2, 3])
+    assert torch.equal(st[0], states[1, 0]) and torch.equal(st[1], states[2, 1])
+    assert torch.equal(cv[0], convs[1, 0]) and torch.equal(cv[1], convs[2, 1])
+
+
+# ------------------------------------------------------------------------------------------- a5 / a9 paged
+
+
+def test_paged_append_matches_loops_and_gather():
+    g = torch.Generator().manual_seed(5)
+    nb, nkv, block, hd, B, T = 9, 2, 4, 8, 3, 3
+    k1 = bfr(nb, nkv, block, hd, gen=g)
+    v1 = bfr(nb, nkv, block, hd, gen=g)
+    k2, v2 = k1.clone(), v1.clone()
+    table = torch.randperm(nb, generator=g)[:9].view(3, 3).int()
+    pos = torch.tensor([0, 3, 7], dtype=torch.int32)  # crosses page boundaries
+    kn, vn = bfr(B, T, nkv, hd, gen=g), bfr(B, T, nkv, hd, gen=g)
+    O.paged_append(k1, v1, kn, vn, table, pos)
+    O.paged_append_loops(k2, v2, kn, vn, table, pos)
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
+    for b in range(B):
+        gk = O.paged_gather(k1, table[b], int(pos[b]) + T)
+        assert torch.equal(gk[:, int(pos[b]) :].permute(1, 0, 2), kn[b])
+
+
+def test_paged_fill_roundtrip():
+    g = torch.Generator().manual_seed(6)
+    cache = torch.zeros(12, 2, 4, 8)
+    x = bfr(2, 10, 8, gen=g)
+    pt = torch.tensor([7, 2, 11], dtype=torch.int32)
+    O.paged_fill(cache, x, pt)
+    assert torch.equal(O.paged_gather(cache, pt, 10), x)
+    assert torch.equal(cache[2, :, 1], x[:, 5])  # token 5 -> page pt[1] = 2, row 1
+    untouched = [i for i in range(12) if i not in (7, 2, 11)]
+    assert cache[untouched].abs().sum() == 0
+
+
+# ------------------------------------------------------------------------------------------- a6 attention
+
+
+def test_attention_one_position_and_shift_invariance():
+    g = torch.Generator().manual_seed(7)
+    kc, vc = torch.randn(4, 2, 4, 8, generator=g), torch.randn(4, 2, 4, 8, generator=g)
+    table = torch.tensor([[3, 1]], dtype=torch.int32)
+    q = torch.randn(1, 1, 4, 8, generator=g)
+    o = O.gqa_decode(q, kc, vc, table, torch.tensor([1]), scale=0.3)
+    for h in range(4):
+        torch.testing.assert_close(o[0, 0, h], vc[3, h // 2, 0])
+    # adding a constant score offset (q along a direction all keys share) leaves o unchanged
+    kc2 = kc + 0.0
+    kc2[..., 0] = 1.0
+    q2 = q.clone()
+    base = O.gqa_decode(q2, kc2, vc, table, torch.tensor([6]), scale=0.3)
+    q2[..., 0] += 5.0
+    torch.testing.assert_close(O.gqa_decode(q2, kc2, vc, table, torch.tensor([6]), scale=0.3), base)
+
+
+def test_attention_split_merge_equals_one_pass():
+    g = torch.Generator().manual_seed(8)
+    K, V, q = torch.randn(200, 16, generator=g), torch.randn(200, 16, generator=g), torch.randn(16, generator=g)
+    full = torch.softmax((K @ q) * 0.25, -1) @ V
+    parts = O.attention_partials(q, K, V, 0.25, [(0, 64), (64, 128), (128, 192), (192, 200)])
+    torch.testing.assert_close(O.merge_partials(parts), full)
+
+
+def test_attention_causal_among_new_tokens():
+    """Query t of a T-token step equals a 1-token step over the sequence truncated after t."""
+    g = torch.Generator().manual_seed(9)
+    kc, vc = torch.randn(6, 2, 4, 8, generator=g), torch.randn(6, 2, 4, 8, generator=g)
+    table = torch.tensor([[5, 0, 3]], dtype=torch.int32)
+    q = torch.randn(1, 4, 4, 8, generator=g)
+    o = O.gqa_decode(q, kc, vc, table, torch.tensor([11]), scale=0.35)
+    for t in range(4):
+        ot = O.gqa_decode(q[:, t : t + 1], kc, vc, table, torch.tensor([8 + t]), scale=0.35)
+        torch.testing.assert_close(o[:, t], ot[:, 0])
+
+
+# ------------------------------------------------------------------------------------------- a8 prefill
+
+
+def test_prefill_chunked_equals_recurrence():
+    g = torch.Generator().manual_seed(10)
+    T, NK, NV, DK = 150, 2, 6, 16
+    q, k = torch.randn(T, NK, DK, generator=g).double(), torch.randn(T, NK, DK, generator=g).double()
+    v = torch.randn(T, NV, DK, generator=g).double()
+    gg = (-torch.nn.functional.softplus(torch.randn(T, NV, generator=g)) * torch.exp(-3 * torch.rand(T, NV, generator=g))).double()
+    beta = torch.sigmoid(torch.randn(T, NV, generator=g)).double()
+    S0 = 0.02 * torch.randn(NV, DK, DK, generator=g).double()
+    o, S = O.gdn_chunk_prefill(q, k, v, gg, beta, S0)
+    for chunk in (16, 64):
+        o2, S2 = O.gdn_chunk_prefill_wy(q, k, v, gg, beta, S0, chunk=chunk)
+        torch.testing.assert_close(o2, o, rtol=1e-10, atol=1e-12)
+        torch.testing.assert_close(S2, S, rtol=1e-10, atol=1e-12)
+    # masked rows (g = 0, beta = 0) leave the state unchanged
+    _, Sm = O.gdn_chunk_prefill(q[:5], k[:5], v[:5], torch.zeros(5, NV).double(), torch.zeros(5, NV).double(), S0)
+    assert torch.equal(Sm, S0)

@@ -1,0 +1,90 @@
+// Paged KV-cache movement on gfx950: decode append (T rows per user through the block table) and prefill
+// fill (paged_fill_cache). Pure byte copies in 16-byte units; page indices read from device memory are
+// range-checked in the kernel (a row whose page is out of range is skipped, never written out of bounds).
+#include "qs_common.h"
+
+namespace {
+
+// thread i copies 16-byte chunk (i % cpr) of row (i / cpr); rows are ordered (b, t, kv head)
+__global__ __launch_bounds__(256) void append_kernel(const uint16_t *k, const uint16_t *v, uint16_t *kc,
+                                                     uint16_t *vc, const int *block_table, const int *positions,
+                                                     int B, int T, int NKV, int HD, int block, int max_blocks,
+                                                     int num_blocks) {
+    const int cpr = HD / 8;
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    const long total = (long)B * T * NKV * cpr;
+    if (i >= total) return;
+    const int ch = (int)(i % cpr);
+    const long r = i / cpr;
+    const int hk = (int)(r % NKV);
+    const long bt = r / NKV;
+    const int t = (int)(bt % T);
+    const int b = (int)(bt / T);
+    const int p = positions[b] + t;
+    if (p < 0) return;
+    const int bi = p / block;
+    if (bi >= max_blocks) return;
+    const int page = block_table[(long)b * max_blocks + bi];
+    if (page < 0 || page >= num_blocks) return;
+    const size_t dst = (((size_t)page * NKV + hk) * block + p % block) * HD + ch * 8;
+    const size_t src = (size_t)r * HD + ch * 8;
+    if (k) *reinterpret_cast<uint4 *>(kc + dst) = *reinterpret_cast<const uint4 *>(k + src);
+    if (v) *reinterpret_cast<uint4 *>(vc + dst) = *reinterpret_cast<const uint4 *>(v + src);
+}
+
+// x [NKV, T, HD]: thread i copies chunk (i % cpr) of token ((i / cpr) % T), kv head (i / cpr / T)
+__global__ __launch_bounds__(256) void fill_kernel(const uint16_t *k, const uint16_t *v, uint16_t *kc, uint16_t *vc,
+                                                   const int *page_table, int T, int start, int NKV, int HD,
+                                                   int block, int table_len, int num_blocks) {
+    const int cpr = HD / 8;
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    const long total = (long)NKV * T * cpr;
+    if (i >= total) return;
+    const int ch = (int)(i % cpr);
+    const long r = i / cpr;
+    const int tok = (int)(r % T);
+    const int hk = (int)(r / T);
+    const int p = start + tok;
+    const int bi = p / block;
+    if (bi >= table_len) return;
+    const int page = page_table[bi];
+    if (page < 0 || page >= num_blocks) return;
+    const size_t dst = (((size_t)page * NKV + hk) * block + p % block) * HD + ch * 8;
+    const size_t src = (size_t)r * HD + ch * 8;
+    if (k) *reinterpret_cast<uint4 *>(kc + dst) = *reinterpret_cast<const uint4 *>(k + src);
+    if (v) *reinterpret_cast<uint4 *>(vc + dst) = *reinterpret_cast<const uint4 *>(v + src);
+}
+
+}  // namespace
+
+extern "C" int qs_paged_kv_append(const uint16_t *k, const uint16_t *v, uint16_t *k_cache, uint16_t *v_cache,
+                                  const int *block_table, const int *positions, int B, int T, int NKV, int HD,
+                                  int block, int max_blocks, int num_blocks, void *stream) {
+    QS_REQUIRE(k && v && k_cache && v_cache && block_table && positions, "qs_paged_kv_append: null pointer");
+    QS_REQUIRE(B > 0 && T > 0 && NKV > 0 && block > 0 && max_blocks > 0 && num_blocks > 0,
+               "qs_paged_kv_append: sizes must be positive");
+    QS_REQUIRE(HD > 0 && HD % 8 == 0, "qs_paged_kv_append: HD must be a multiple of 8 (got %d)", HD);
+    const long total = (long)B * T * NKV * (HD / 8);
+    if (total == 0) return QS_OK;
+    append_kernel<<<(unsigned)((total + 255) / 256), 256, 0, QS_STREAM(stream)>>>(
+        k, v, k_cache, v_cache, block_table, positions, B, T, NKV, HD, block, max_blocks, num_blocks);
+    return qs::launch_status("qs_paged_kv_append");
+}
+
+extern "C" int qs_paged_kv_fill(const uint16_t *k, const uint16_t *v, uint16_t *k_cache, uint16_t *v_cache,
+                                const int *page_table, int T, int start, int NKV, int HD, int block, int table_len,
+                                int num_blocks, void *stream) {
+    QS_REQUIRE(page_table, "qs_paged_kv_fill: null page table");
+    QS_REQUIRE((k == nullptr) == (k_cache == nullptr) && (v == nullptr) == (v_cache == nullptr) && (k || v),
+               "qs_paged_kv_fill: give k with k_cache and/or v with v_cache");
+    QS_REQUIRE(T >= 0 && start >= 0 && NKV > 0 && block > 0 && table_len > 0 && num_blocks > 0,
+               "qs_paged_kv_fill: bad sizes");
+    QS_REQUIRE(HD > 0 && HD % 8 == 0, "qs_paged_kv_fill: HD must be a multiple of 8 (got %d)", HD);
+    QS_REQUIRE((long)(start + T + block - 1) / block <= table_len,
+               "qs_paged_kv_fill: %d tokens from %d need more than the %d table entries", T, start, table_len);
+    const long total = (long)NKV * T * (HD / 8);
+    if (total == 0) return QS_OK;
+    fill_kernel<<<(unsigned)((total + 255) / 256), 256, 0, QS_STREAM(stream)>>>(
+        k, v, k_cache, v_cache, page_table, T, start, NKV, HD, block, table_len, num_blocks);
+    return qs::launch_status("qs_paged_kv_fill");
+}

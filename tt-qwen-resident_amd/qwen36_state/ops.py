@@ -1,0 +1,331 @@
+"""Operator-level Python API of the MI355X state path, over the C ABI of libqwen_state.so.
+
+Each op keeps the signature and argument meaning of the reference call it replaces (cited per op), checks
+shapes, dtypes, devices and contiguity (ValueError on a mismatch, like the reference's asserts), and
+enqueues HIP kernels on the current torch stream. Tensors are caller-owned; state arguments are updated in
+place as in the reference. Nothing here computes on the CPU.
+"""
+import ctypes
+
+import torch
+
+from ._lib import call, lib
+
+NK, NV, DK, DV, CONV_K = 16, 48, 128, 128, 4  # model.py:48
+NQ, NKV, HD = 24, 4, 256  # model.py:50
+BLOCK = 64  # vLLM block size, tt-model.yaml:41
+EPS = 1e-6  # model.py:264-267
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _stream(dev):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _chk(t, name, dtype, shape=None, dev=None):
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name} must be a tensor")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be on a GPU (got {t.device})")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype} (got {t.dtype})")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)} (got {tuple(t.shape)})")
+    if dev is not None and t.device != dev:
+        raise ValueError(f"{name} is on {t.device}, expected {dev}")
+    return t
+
+
+# ------------------------------------------------------------------------------------------- workspaces
+
+_WS = {}
+
+
+def workspace(kind, nbytes, device):
+    """A zeroed device workspace of at least ``nbytes`` for ``kind`` on ``device`` and the current stream.
+
+    The kernels leave their counters zeroed again, so the buffer is reused by every later call on the
+    same stream. It must exist before a HIP graph capture starts (warm the op up once first)."""
+    device = torch.device(device)
+    key = (kind, device, torch.cuda.current_stream(device).cuda_stream)
+    ws = _WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise ValueError(f"{kind} workspace must be allocated before graph capture: run the op once first")
+        ws = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+        _WS[key] = ws
+    return ws
+
+
+# ------------------------------------------------------------------------------------------- a1, a3
+
+
+def causal_conv1d_update(x, conv_state, taps):
+    """y = silu(causal conv1d over [state, x]) with the state shifted in place (model.py:255-259).
+
+    x [B, C] bf16, conv_state [B, C, K-1] bf16, taps [C, K] bf16 -> y [B, C] bf16."""
+    dev = x.device
+    B, C = x.shape
+    _chk(x, "x", torch.bfloat16)
+    _chk(taps, "taps", torch.bfloat16, (C, CONV_K), dev)
+    _chk(conv_state, "conv_state", torch.bfloat16, (B, C, CONV_K - 1), dev)
+    y = torch.empty_like(x)
+    call("qs_conv1d_update", _p(x), _p(conv_state), _p(taps), _p(y), B, C, CONV_K, _stream(dev))
+    return y
+
+
+def gdn_gates(a, b, dt_bias, neg_a):
+    """g = neg_a * softplus(a + dt_bias), beta = sigmoid(b) (model.py:268-269). a, b [B, NV] bf16."""
+    dev = a.device
+    B, nv = a.shape
+    _chk(a, "a", torch.bfloat16)
+    _chk(b, "b", torch.bfloat16, (B, nv), dev)
+    _chk(dt_bias, "dt_bias", torch.float32, (nv,), dev)
+    _chk(neg_a, "neg_a", torch.float32, (nv,), dev)
+    g = torch.empty(B, nv, dtype=torch.float32, device=dev)
+    beta = torch.empty_like(g)
+    call("qs_gdn_gates", _p(a), _p(b), _p(dt_bias), _p(neg_a), _p(g), _p(beta), B, nv, _stream(dev))
+    return g, beta
+
+
+# ------------------------------------------------------------------------------------------- a2 + a4
+
+
+def gdn_decode_step(q, k, v, g, beta, state, scale=None, eps=EPS, out=None):
+    """One gated delta rule decode step (model.py:262-273), state [B, NV, DK, DV] fp32 updated in place.
+
+    q, k [B, NK, DK] bf16 (before the L2-norm); v [B, NV, DV] bf16; g (log decay), beta [B, NV] fp32.
+    Returns o = qn^T S' [B, NV, DV] bf16."""
+    dev = state.device
+    _chk(state, "state", torch.float32)
+    B, nv, dk, dv = state.shape
+    nk = q.shape[1]
+    _chk(q, "q", torch.bfloat16, (B, nk, dk), dev)
+    _chk(k, "k", torch.bfloat16, (B, nk, dk), dev)
+    _chk(v, "v", torch.bfloat16, (B, nv, dv), dev)
+    _chk(g, "g", torch.float32, (B, nv), dev)
+    _chk(beta, "beta", torch.float32, (B, nv), dev)
+    scale = dk**-0.5 if scale is None else scale
+    o = out if out is not None else torch.empty(B, nv, dv, dtype=torch.bfloat16, device=dev)
+    _chk(o, "out", torch.bfloat16, (B, nv, dv), dev)
+    call("qs_gdn_decode_step", _p(q), _p(k), _p(v), _p(g), _p(beta), _p(state), _p(o),
+         B, nk, nv, dk, dv, float(scale), float(eps), _stream(dev))  # fmt: skip
+    return o
+
+
+def gdn_decode_fused(x, conv_state, taps, g, beta, state, nk=NK, scale=None, eps=EPS, out=None, y_out=None,
+                     ws=None):  # fmt: skip
+    """Conv1d update + L2-norm + delta rule of one decode step in one launch (model.py:255-273).
+
+    x [B, C] bf16 is the projection's q|k|v slice (C = 2 nk DK + NV DV); conv_state [B, C, 3] and state
+    [B, NV, DK, DV] are updated in place. Returns o [B, NV, DV] bf16 (y_out, if given, receives the conv
+    output [B, C])."""
+    dev = state.device
+    _chk(state, "state", torch.float32)
+    B, nv, dk, dv = state.shape
+    C = 2 * nk * dk + nv * dv
+    _chk(x, "x", torch.bfloat16, (B, C), dev)
+    _chk(conv_state, "conv_state", torch.bfloat16, (B, C, CONV_K - 1), dev)
+    _chk(taps, "taps", torch.bfloat16, (C, CONV_K), dev)
+    _chk(g, "g", torch.float32, (B, nv), dev)
+    _chk(beta, "beta", torch.float32, (B, nv), dev)
+    if y_out is not None:
+        _chk(y_out, "y_out", torch.bfloat16, (B, C), dev)
+    scale = dk**-0.5 if scale is None else scale
+    o = out if out is not None else torch.empty(B, nv, dv, dtype=torch.bfloat16, device=dev)
+    _chk(o, "out", torch.bfloat16, (B, nv, dv), dev)
+    if ws is None:
+        ws = workspace("gdn", lib().qs_gdn_workspace_bytes(B, nk), dev)
+    call("qs_gdn_decode_fused", _p(x), _p(conv_state), _p(taps), _p(g), _p(beta), _p(state), _p(o), _p(y_out),
+         _p(ws), B, nk, nv, dk, dv, CONV_K, float(scale), float(eps), _stream(dev))  # fmt: skip
+    return o
+
+
+# ------------------------------------------------------------------------------------------- a7
+
+
+def gdn_verify_step(x, conv_state, taps, g, beta, state, nk=NK, scale=None, eps=EPS, return_y=False):
+    """T tokens per user through conv + delta rule, keeping every intermediate (the verify rows of the
+    reference GDN head cores, kernels/gdn_head_reader.cpp:149-187, gdn_head_writer.cpp:60-66).
+
+    x [B, T, C]; g, beta [B, T, NV]; conv_state [B, C, 3] and state [B, NV, DK, DV] are read only.
+    Returns o [B, T, NV, DV] bf16, states [T, B, NV, DK, DV] fp32, conv_states [T, B, C, 3] bf16
+    (and the conv outputs y [B, T, C] with return_y)."""
+    dev = state.device
+    _chk(state, "state", torch.float32)
+    B, nv, dk, dv = state.shape
+    T = x.shape[1]
+    C = 2 * nk * dk + nv * dv
+    _chk(x, "x", torch.bfloat16, (B, T, C), dev)
+    _chk(conv_state, "conv_state", torch.bfloat16, (B, C, CONV_K - 1), dev)
+    _chk(taps, "taps", torch.bfloat16, (C, CONV_K), dev)
+    _chk(g, "g", torch.float32, (B, T, nv), dev)
+    _chk(beta, "beta", torch.float32, (B, T, nv), dev)
+    scale = dk**-0.5 if scale is None else scale
+    o = torch.empty(B, T, nv, dv, dtype=torch.bfloat16, device=dev)
+    states = torch.empty(T, B, nv, dk, dv, dtype=torch.float32, device=dev)
+    convs = torch.empty(T, B, C, CONV_K - 1, dtype=torch.bfloat16, device=dev)
+    y = torch.empty(B, T, C, dtype=torch.bfloat16, device=dev) if return_y else None
+    call("qs_gdn_verify_step", _p(x), _p(conv_state), _p(convs), _p(taps), _p(g), _p(beta), _p(state),
+         _p(states), _p(o), _p(y), B, T, nk, nv, dk, dv, CONV_K, float(scale), float(eps), _stream(dev))  # fmt: skip
+    return (o, states, convs, y) if return_y else (o, states, convs)
+
+
+def gdn_rollback(states, conv_states, accept_len, state, conv_state, seq_lens=None, base_lens=None):
+    """Restore state <- states[accept_len - 1], conv_state <- conv_states[accept_len - 1] per user (bit-exact),
+    and seq_lens <- base_lens + accept_len when given (the KV truncation). accept_len [B] int32 on device,
+    each in [1, T] (the reference's slot/ring advance, kernels/mlp_hub.cpp:48-58)."""
+    dev = state.device
+    T, B, nv, dk, dv = states.shape
+    C = conv_states.shape[2]
+    _chk(states, "states", torch.float32, None, dev)
+    _chk(conv_states, "conv_states", torch.bfloat16, (T, B, C, CONV_K - 1), dev)
+    _chk(state, "state", torch.float32, (B, nv, dk, dv), dev)
+    _chk(conv_state, "conv_state", torch.bfloat16, (B, C, CONV_K - 1), dev)
+    _chk(accept_len, "accept_len", torch.int32, (B,), dev)
+    if seq_lens is not None:
+        _chk(seq_lens, "seq_lens", torch.int32, (B,), dev)
+        _chk(base_lens, "base_lens", torch.int32, (B,), dev)
+    call("qs_gdn_rollback", _p(states), _p(state), _p(conv_states), _p(conv_state), _p(accept_len), _p(seq_lens),
+         _p(base_lens), B, T, nv, dk, dv, C, CONV_K, _stream(dev))  # fmt: skip
+
+
+# ------------------------------------------------------------------------------------------- a5, a9
+
+
+def _pool_dims(k_cache, v_cache, dev):
+    _chk(k_cache, "k_cache", torch.bfloat16, None, dev)
+    _chk(v_cache, "v_cache", torch.bfloat16, tuple(k_cache.shape), dev)
+    if k_cache.dim() != 4:
+        raise ValueError("KV pools must be [num_blocks, NKV, block, HD]")
+    return k_cache.shape
+
+
+def paged_kv_append(k, v, k_cache, v_cache, block_table, positions):
+    """Write T new rows per user at positions[b] + t through the block table (bit-exact copies).
+
+    k, v [B, T, NKV, HD] bf16; pools [num_blocks, NKV, block, HD]; block_table [B, max_blocks] int32;
+    positions [B] int32 (first new position)."""
+    dev = k_cache.device
+    nb, nkv, block, hd = _pool_dims(k_cache, v_cache, dev)
+    B, T = k.shape[:2]
+    _chk(k, "k", torch.bfloat16, (B, T, nkv, hd), dev)
+    _chk(v, "v", torch.bfloat16, (B, T, nkv, hd), dev)
+    _chk(block_table, "block_table", torch.int32, None, dev)
+    if block_table.dim() != 2 or block_table.shape[0] != B:
+        raise ValueError(f"block_table must be [B={B}, max_blocks]")
+    _chk(positions, "positions", torch.int32, (B,), dev)
+    call("qs_paged_kv_append", _p(k), _p(v), _p(k_cache), _p(v_cache), _p(block_table), _p(positions),
+         B, T, nkv, hd, block, block_table.shape[1], nb, _stream(dev))  # fmt: skip
+
+
+def paged_kv_fill(k, v, k_cache, v_cache, page_table, start=0):
+    """Fill one sequence's K and V [NKV, T, HD] into the pools through its page table [n] (int32)."""
+    dev = k_cache.device
+    nb, nkv, block, hd = _pool_dims(k_cache, v_cache, dev)
+    T = k.shape[1]
+    _chk(k, "k", torch.bfloat16, (nkv, T, hd), dev)
+    _chk(v, "v", torch.bfloat16, (nkv, T, hd), dev)
+    _chk(page_table, "page_table", torch.int32, None, dev)
+    if page_table.dim() != 1:
+        raise ValueError("page_table must be one sequence's [n] table")
+    call("qs_paged_kv_fill", _p(k), _p(v), _p(k_cache), _p(v_cache), _p(page_table), T, int(start), nkv, hd,
+         block, page_table.shape[0], nb, _stream(dev))  # fmt: skip
+
+
+def paged_fill_cache(cache, x, page_table, batch_idx=0):
+    """``ttnn.experimental.paged_fill_cache(cache, x, page_table, batch_idx)`` (prefill/pp_prefill.py:826-827).
+
+    cache [num_blocks, NKV, block, HD] bf16; x [1, NKV, T, HD] bf16; page_table [B, n] int32: token i goes
+    to page page_table[batch_idx, i // block], row i % block."""
+    dev = cache.device
+    _chk(cache, "cache", torch.bfloat16, None, dev)
+    nb, nkv, block, hd = cache.shape
+    if x.dim() != 4 or x.shape[0] != 1:
+        raise ValueError("x must be [1, NKV, T, HD]")
+    T = x.shape[2]
+    _chk(x, "x", torch.bfloat16, (1, nkv, T, hd), dev)
+    _chk(page_table, "page_table", torch.int32, None, dev)
+    row = page_table[batch_idx]
+    call("qs_paged_kv_fill", _p(x), None, _p(cache), None, ctypes.c_void_p(row.data_ptr()), T, 0, nkv, hd, block,
+         row.shape[0], nb, _stream(dev))  # fmt: skip
+
+
+# ------------------------------------------------------------------------------------------- a6
+
+
+def attention_workspace(B, T, nq, nkv, max_blocks, pages_per_split, device):
+    nbytes = lib().qs_paged_attention_workspace_bytes(B, T, nq, nkv, HD, max_blocks, pages_per_split)
+    return workspace(("attn", pages_per_split), nbytes, device)
+
+
+def paged_gqa_decode(q, k_cache, v_cache, block_table, seq_lens, scale, k_new=None, v_new=None,
+                     pages_per_split=8, out=None, ws=None):  # fmt: skip
+    """Paged GQA decode attention ``softmax(q K^T scale) V`` over each user's pages (model.py:239-244).
+
+    q [B, T, NQ, HD] bf16; seq_lens [B] int32 = valid positions after this step; query t of user b sees
+    positions 0 .. seq_lens[b] - T + t. With k_new, v_new [B, T, NKV, HD] the new rows are appended in the
+    same launch. Returns o [B, T, NQ, HD] bf16."""
+    dev = k_cache.device
+    nb, nkv, block, hd = _pool_dims(k_cache, v_cache, dev)
+    B, T, nq = q.shape[:3]
+    _chk(q, "q", torch.bfloat16, (B, T, nq, hd), dev)
+    if (k_new is None) != (v_new is None):
+        raise ValueError("give both k_new and v_new or neither")
+    if k_new is not None:
+        _chk(k_new, "k_new", torch.bfloat16, (B, T, nkv, hd), dev)
+        _chk(v_new, "v_new", torch.bfloat16, (B, T, nkv, hd), dev)
+    _chk(block_table, "block_table", torch.int32, None, dev)
+    if block_table.dim() != 2 or block_table.shape[0] != B:
+        raise ValueError(f"block_table must be [B={B}, max_blocks]")
+    _chk(seq_lens, "seq_lens", torch.int32, (B,), dev)
+    mb = block_table.shape[1]
+    o = out if out is not None else torch.empty(B, T, nq, hd, dtype=torch.bfloat16, device=dev)
+    _chk(o, "out", torch.bfloat16, (B, T, nq, hd), dev)
+    if ws is None and (mb + pages_per_split - 1) // pages_per_split > 1:
+        ws = attention_workspace(B, T, nq, nkv, mb, pages_per_split, dev)
+    call("qs_paged_gqa_decode", _p(q), _p(k_new), _p(v_new), _p(k_cache), _p(v_cache), _p(block_table),
+         _p(seq_lens), _p(o), _p(ws), B, T, nq, nkv, hd, block, mb, nb, int(pages_per_split), float(scale),
+         _stream(dev))  # fmt: skip
+    return o
+
+
+# ------------------------------------------------------------------------------------------- a8
+
+
+def chunk_gated_delta_rule(q, k, v, g, beta, *, scale=None, initial_state=None, output_final_state=True,
+                           chunk_size=64, output_head_major=False, eps=EPS, ws=None):  # fmt: skip
+    """``chunk_gated_delta_rule(q, k, v, g, beta, scale, initial_state, output_final_state, chunk_size,
+    output_head_major)`` as the reference prefill calls it (prefill/pp_prefill.py:791-807): q, k [T, NK*DK]
+    or [T, NK, DK] bf16 token-major (L2-normalised inside, q times scale), v [T, NV*DV] or [T, NV, DV] bf16,
+    g, beta [T, NV] fp32, initial_state [NV, DK, DV] fp32. Returns (o, final_state): o [T, NV, DV] bf16
+    ([NV, T, DV] with output_head_major), final_state [NV, DK, DV] fp32 (None unless output_final_state)."""
+    dev = q.device
+    T = q.shape[0]
+    nv = g.shape[1]
+    q3 = q.reshape(T, -1, DK)
+    nk = q3.shape[1]
+    _chk(q3, "q", torch.bfloat16, (T, nk, DK), dev)
+    _chk(k.reshape(T, -1, DK), "k", torch.bfloat16, (T, nk, DK), dev)
+    _chk(v.reshape(T, -1, DV), "v", torch.bfloat16, (T, nv, DV), dev)
+    _chk(g, "g", torch.float32, (T, nv), dev)
+    _chk(beta, "beta", torch.float32, (T, nv), dev)
+    if initial_state is None:
+        initial_state = torch.zeros(nv, DK, DV, dtype=torch.float32, device=dev)
+    _chk(initial_state, "initial_state", torch.float32, (nv, DK, DV), dev)
+    scale = DK**-0.5 if scale is None else scale
+    o = torch.empty(T, nv, DV, dtype=torch.bfloat16, device=dev)
+    S = torch.empty(nv, DK, DV, dtype=torch.float32, device=dev)
+    if ws is None:
+        nbytes = lib().qs_gdn_chunk_prefill_workspace_bytes(T, nk, nv, DK, DV, chunk_size)
+        ws = workspace(("prefill", chunk_size), nbytes, dev)
+    call("qs_gdn_chunk_prefill", _p(q), _p(k), _p(v), _p(g), _p(beta), _p(initial_state), _p(o), _p(S), _p(ws),
+         T, nk, nv, DK, DV, int(chunk_size), float(scale), float(eps), _stream(dev))  # fmt: skip
+    if output_head_major:
+        o = o.transpose(0, 1).contiguous()
+    return o, (S if output_final_state else None)
