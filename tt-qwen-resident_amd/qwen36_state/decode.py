@@ -1,0 +1,130 @@
+"""The batched decode-step state path of the 64-layer hybrid engine, replayed as one HIP graph.
+
+Per step and layer l (attention iff (l + 1) % interval == 0, model.py:93-94): a GDN layer runs the fused
+conv1d update + L2-norm + delta rule with its fp32 state and conv history updated in place; an attention
+layer appends the step's K/V rows into its paged pools and runs paged GQA decode attention. All layers
+run in order on one stream (in the engine each layer's inputs come from the previous layer's projections,
+which are outside this path), so the step is 64 dependent launches; ``capture()`` records them into one
+HIP graph so the step costs one host submission (the resident engine's trace replay, model.py:1485-1508).
+
+The caller owns every buffer (all allocated here once, up front); a step allocates nothing. Every layer
+has its own independently seeded inputs, so each layer can be checked against its own oracle call.
+"""
+import torch
+
+from . import ops
+from . import workloads as W
+from .ops import BLOCK, CONV_K, DK, DV, HD, NK, NKV, NQ, NV
+
+
+def is_attn(l, interval):
+    """model.py:93-94"""
+    return interval > 0 and (l + 1) % interval == 0
+
+
+def layer_bytes(B, ctx, T=1, attn=False, snapshots=False):
+    """Algorithmic HBM bytes of one layer of the step (each tensor the path must read or write, once).
+
+    GDN: state read + write (T snapshot writes in verify), conv state read + write (T snapshots), taps,
+    the projection slice x, g and beta, the output o. Attention: K and V of all ctx positions per KV head,
+    the T new rows (read from the inputs + written to the pages), q, o, the user's block-table row."""
+    if not attn:
+        st = B * NV * DK * DV * 4
+        conv = B * W.C_QKV * (CONV_K - 1) * 2
+        writes = T if snapshots else 1
+        return (st + writes * st) + (conv + writes * conv) + W.C_QKV * CONV_K * 2 + B * T * (
+            W.C_QKV * 2 + NV * 8 + NV * DV * 2
+        )
+    row = NKV * HD * 2
+    pages = (ctx + BLOCK - 1) // BLOCK
+    return B * (2 * ctx * row + 2 * 2 * T * row + T * NQ * HD * 2 * 2 + pages * 4)
+
+
+def step_bytes(B, ctx, layers=64, interval=4, T=1):
+    n_attn = sum(is_attn(l, interval) for l in range(layers))
+    return (layers - n_attn) * layer_bytes(B, ctx, T, False, T > 1) + n_attn * layer_bytes(B, ctx, T, True)
+
+
+class StatePathStep:
+    """``layers`` layers of state path for B users at ``ctx`` positions (after this step's append)."""
+
+    def __init__(self, B, ctx, layers=64, interval=4, device="cuda", seed=0, num_blocks=2048, pages_per_split=8):
+        self.B, self.ctx, self.layers, self.interval = B, ctx, layers, interval
+        self.device = torch.device(device)
+        self.pps = pages_per_split
+        pages = (ctx + BLOCK - 1) // BLOCK
+        if B * pages > num_blocks:
+            raise ValueError(f"{B} users x {pages} pages do not fit a {num_blocks}-page pool")
+        # one block table per user shared by every attention layer (vLLM's contract); each layer owns pools
+        self.block_table = W.block_tables(B, pages, num_blocks, self.device, seed)
+        self.seq_lens = torch.full((B,), ctx, dtype=torch.int32, device=self.device)
+        self.layer = []
+        for l in range(layers):
+            if is_attn(l, interval):
+                d = W.attn_layer(B, ctx, self.device, seed=seed + 1000 + l, T=1, num_blocks=num_blocks)
+                d["block_table"], d["seq_lens"] = self.block_table, self.seq_lens
+                d["o"] = torch.empty(B, 1, NQ, HD, dtype=torch.bfloat16, device=self.device)
+                d["attn"] = True
+            else:
+                d = W.gdn_layer(B, self.device, seed=seed + l)
+                for k in ("q", "k", "v"):
+                    del d[k]
+                d["o"] = torch.empty(B, NV, DV, dtype=torch.bfloat16, device=self.device)
+                d["attn"] = False
+            self.layer.append(d)
+        self.gdn_ws = ops.workspace("gdn-step", ops.lib().qs_gdn_workspace_bytes(B, NK), self.device)
+        mb = self.block_table.shape[1]
+        self.attn_ws = ops.attention_workspace(B, 1, NQ, NKV, mb, pages_per_split, self.device)
+        self.graph = None
+
+    def run_layer(self, l):
+        d = self.layer[l]
+        if d["attn"]:
+            ops.paged_gqa_decode(d["q"], d["k_cache"], d["v_cache"], d["block_table"], d["seq_lens"], d["scale"],
+                                 k_new=d["k_new"], v_new=d["v_new"], pages_per_split=self.pps, out=d["o"],
+                                 ws=self.attn_ws)  # fmt: skip
+        else:
+            ops.gdn_decode_fused(d["x"], d["conv_state"], d["taps"], d["g"], d["beta"], d["state"], out=d["o"],
+                                 ws=self.gdn_ws)  # fmt: skip
+
+    def step(self):
+        """One eager step: every layer in order on the current stream."""
+        for l in range(self.layers):
+            self.run_layer(l)
+
+    def capture(self):
+        """Record one step into a HIP graph (buffers and workspaces already exist, so nothing allocates)."""
+        s = torch.cuda.Stream(self.device)
+        s.wait_stream(torch.cuda.current_stream(self.device))
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            # the workspaces are per stream: make the capture stream's own before capturing
+            self.gdn_ws = ops.workspace("gdn-step", self.gdn_ws.numel(), self.device)
+            self.attn_ws = ops.workspace(("attn", self.pps), self.attn_ws.numel(), self.device)
+            torch.cuda.synchronize(self.device)
+            with torch.cuda.graph(g, stream=s):
+                self.step()
+        torch.cuda.current_stream(self.device).wait_stream(s)
+        self.graph = g
+        return g
+
+    def replay(self):
+        self.graph.replay()
+
+    def bytes_per_step(self):
+        return step_bytes(self.B, self.ctx, self.layers, self.interval)
+
+    def gdn_layers(self):
+        return [l for l in range(self.layers) if not self.layer[l]["attn"]]
+
+    def attn_layers(self):
+        return [l for l in range(self.layers) if self.layer[l]["attn"]]
+
+    def snapshot(self):
+        """Host-free copy of the recurrent state (GDN states and conv histories) for restore()."""
+        return [(d["state"].clone(), d["conv_state"].clone()) for d in self.layer if not d["attn"]]
+
+    def restore(self, snap):
+        for d, (s, c) in zip((d for d in self.layer if not d["attn"]), snap):
+            d["state"].copy_(s)
+            d["conv_state"].copy_(c)
