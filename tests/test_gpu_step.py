@@ -43,7 +43,7 @@ def test_step_layers_match_oracle(step, dev):
     # attention layer 3: append + attention over the shared block table
     kc, vc = att3["k_cache"], att3["v_cache"]
     O.paged_append(kc, vc, att3["k_new"], att3["v_new"], att3["block_table"], att3["seq_lens"] - 1)
-    o_ref = O.gqa_decode(att3["q"], kc, vc, att3["block_table"], att3["seq_lens"], att3["scale"])
+    o_ref = O.gqa_decode(att3["q"], kc, vc, att3["block_table"], att3["seq_lens"], step.layer[3]["scale"])
     assert_bf16_output(step.layer[3]["o"], O.bf16(o_ref))
     rows = O.paged_gather(step.layer[3]["k_cache"].cpu(), att3["block_table"][5], 4096)[:, -1]
     assert torch.equal(rows, att3["k_new"][5, 0])
