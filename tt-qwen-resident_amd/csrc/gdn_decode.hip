@@ -20,6 +20,7 @@ constexpr int SLAB = 32;
 constexpr int NSLAB = DV / SLAB;
 constexpr int THREADS = 256;
 constexpr int TMAX = 8;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 struct GdnArgs {
     const uint16_t *q, *k, *v;  // q|k|v mode: [B, T, NK, DK], [B, T, NK, DK], [B, T, NV, DV]
@@ -37,26 +38,47 @@ struct GdnArgs {
     float scale, eps;
 };
 
+// Inputs of one channel's causal conv: the K-1 history values, the K taps and the channel's x for every
+// token. Loaded before the state slab so the prologue does not queue behind it.
+template <int TM>
+struct ConvIn {
+    float h[3], w[4];
+    uint32_t x[TM];
+};
+
+template <int TM>
+__device__ __forceinline__ ConvIn<TM> conv_load(const GdnArgs &a, int b, int c, int T) {
+    ConvIn<TM> in;
+    const uint16_t *cs = a.conv_in + ((size_t)b * a.C + c) * (KC - 1);
+    in.h[0] = qs::bf2f(cs[0]);
+    in.h[1] = qs::bf2f(cs[1]);
+    in.h[2] = qs::bf2f(cs[2]);
+    const uint2 tw = *reinterpret_cast<const uint2 *>(a.taps + (size_t)c * KC);
+    in.w[0] = qs::bf_lo(tw.x), in.w[1] = qs::bf_hi(tw.x), in.w[2] = qs::bf_lo(tw.y), in.w[3] = qs::bf_hi(tw.y);
+#pragma unroll
+    for (int t = 0; t < TM; ++t)
+        if (t < T) in.x[t] = a.x[((size_t)b * T + t) * a.C + c];
+    return in;
+}
+
 // Conv1d + SiLU of one channel over T tokens (window oldest first, tap 0 on the oldest input). The tap
 // products of two bf16 values are exact in fp32, so fused or unfused multiply-adds round identically.
 // Writes the bf16-rounded outputs (as fp32) to y[t * ystride], optionally the per-token conv-state
-// snapshots (verify) and returns the final window in h[0..2].
-template <bool SNAP>
-__device__ __forceinline__ void conv_channel(const GdnArgs &a, int b, int c, int T, float *y, int ystride,
-                                             bool write_out, float h[3]) {
-    const uint16_t *cs = a.conv_in + ((size_t)b * a.C + c) * (KC - 1);
-    h[0] = qs::bf2f(cs[0]);
-    h[1] = qs::bf2f(cs[1]);
-    h[2] = qs::bf2f(cs[2]);
-    const uint2 tw = *reinterpret_cast<const uint2 *>(a.taps + (size_t)c * KC);
-    const float w0 = qs::bf_lo(tw.x), w1 = qs::bf_hi(tw.x), w2 = qs::bf_lo(tw.y), w3 = qs::bf_hi(tw.y);
-    for (int t = 0; t < T; ++t) {
-        const uint32_t xr = a.x[((size_t)b * T + t) * a.C + c];
+// snapshots (verify); leaves the final window in in.h[0..2].
+template <bool SNAP, int TM>
+__device__ __forceinline__ void conv_run(const GdnArgs &a, ConvIn<TM> &in, int b, int c, int T, float *y,
+                                         int ystride, bool write_out) {
+    float *h = in.h;
+    const float *w = in.w;
+#pragma unroll
+    for (int t = 0; t < TM; ++t) {
+        if (t >= T) break;
+        const uint32_t xr = in.x[t];
         const float xt = qs::bf2f(xr);
-        float acc = h[0] * w0;
-        acc = acc + h[1] * w1;
-        acc = acc + h[2] * w2;
-        acc = acc + xt * w3;
+        float acc = h[0] * w[0];
+        acc = acc + h[1] * w[1];
+        acc = acc + h[2] * w[2];
+        acc = acc + xt * w[3];
         const uint32_t yb = qs::f2bf(qs::silu(acc));
         y[t * ystride] = qs::bf2f(yb);
         if (write_out && a.y_out) a.y_out[((size_t)b * T + t) * a.C + c] = (uint16_t)yb;
@@ -85,7 +107,7 @@ __device__ __forceinline__ void reduce_cols(float p[4], float (*red)[SLAB], floa
                                             int cg) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        p[j] += __shfl_xor(p[j], 8, 64);
+        p[j] += qs::dpp<0x128>(p[j]);  // xor 8 (row_ror:8)
         p[j] += __shfl_xor(p[j], 16, 64);
         p[j] += __shfl_xor(p[j], 32, 64);
     }
@@ -121,26 +143,30 @@ __global__ __launch_bounds__(THREADS) void gdn_kernel(GdnArgs a) {
     __shared__ float s_red[2][4][SLAB];
     __shared__ int s_last;
 
-    // 1. State slab loads first: their latency overlaps the prologue.
+    // 1. The small conv inputs first, then the state slab: the slab's latency overlaps the prologue.
+    constexpr int TM = VERIFY ? TMAX : 1;
+    const int qd = a.NK * DK;
+    const bool isq = tid < DK;
+    const int c = isq ? kh * DK + tid : qd + kh * DK + (tid - DK);
+    const int cv = 2 * qd + h * DV + s * SLAB + tid;
+    ConvIn<TM> cq, cvin;
+    if (CONV) {
+        cq = conv_load<TM>(a, b, c, T);
+        if (tid < SLAB) cvin = conv_load<TM>(a, b, cv, T);
+    }
     const size_t head = (size_t)(b * a.NV + h) * DK * DV;
     const float *sp = a.s_in + head + s * SLAB + cg * 4;
-    float4 S[4];
+    f32x4 S[4];  // streamed once per step: nontemporal loads and stores keep it from thrashing L2 / MALL
 #pragma unroll
-    for (int i = 0; i < 4; ++i) S[i] = *reinterpret_cast<const float4 *>(sp + (size_t)(rg + 32 * i) * DV);
+    for (int i = 0; i < 4; ++i) S[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(sp + (size_t)(rg + 32 * i) * DV));
 
     // 2. Prologue: q, k of key head kh and the v slab, for every token.
-    const int qd = a.NK * DK;
     if (CONV) {
-        const bool isq = tid < DK;
-        const int c = isq ? kh * DK + tid : qd + kh * DK + (tid - DK);
-        float hq[3];
-        conv_channel<VERIFY>(a, b, c, T, isq ? &s_qn[0][tid] : &s_kn[0][tid - DK], DK, kq_owner, hq);
-        float hv[3];
-        const int cv = 2 * qd + h * DV + s * SLAB + tid;
-        if (tid < SLAB) conv_channel<VERIFY>(a, b, cv, T, &s_v[0][tid], SLAB, true, hv);
+        conv_run<VERIFY>(a, cq, b, c, T, isq ? &s_qn[0][tid] : &s_kn[0][tid - DK], DK, kq_owner);
+        if (tid < SLAB) conv_run<VERIFY>(a, cvin, b, cv, T, &s_v[0][tid], SLAB, true);
         if (!VERIFY) {
             // v channels of this slab are read by this workgroup only: shift them in place now.
-            if (tid < SLAB) store_conv_state(a, b, cv, hv);
+            if (tid < SLAB) store_conv_state(a, b, cv, cvin.h);
             // q/k channels are read by the rep * NSLAB workgroups of key head kh: the last one to arrive
             // (every other has consumed its reads) writes the shifted state and re-arms the counter.
             __syncthreads();
@@ -152,7 +178,7 @@ __global__ __launch_bounds__(THREADS) void gdn_kernel(GdnArgs a) {
                 s_last = last;
             }
             __syncthreads();
-            if (s_last) store_conv_state(a, b, c, hq);
+            if (s_last) store_conv_state(a, b, c, cq.h);
         }
     } else {
         for (int t = 0; t < T; ++t) {
@@ -170,7 +196,7 @@ __global__ __launch_bounds__(THREADS) void gdn_kernel(GdnArgs a) {
     for (int j = w; j < 2 * T; j += 4) {
         float *vec = (j & 1) ? s_kn[j >> 1] : s_qn[j >> 1];
         const float x0 = vec[lane], x1 = vec[lane + 64];
-        const float r = rsqrtf(qs::wave_sum(x0 * x0 + x1 * x1) + a.eps);
+        const float r = rsqrtf(qs::wave_sum_dpp(x0 * x0 + x1 * x1) + a.eps);
         const float f = (j & 1) ? 1.0f : a.scale;
         vec[lane] = x0 * r * f;
         vec[lane + 64] = x1 * r * f;
@@ -217,7 +243,7 @@ __global__ __launch_bounds__(THREADS) void gdn_kernel(GdnArgs a) {
         float* dst = VERIFY ? a.s_out + (size_t)t * a.B * a.NV * DK * DV + head + s * SLAB + cg * 4
                             : a.s_out + head + s * SLAB + cg * 4;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) *reinterpret_cast<float4 *>(dst + (size_t)(rg + 32 * i) * DV) = S[i];
+        for (int i = 0; i < 4; ++i) __builtin_nontemporal_store(S[i], reinterpret_cast<f32x4 *>(dst + (size_t)(rg + 32 * i) * DV));
         float ov[4];
         reduce_cols(po, s_red[1], ov, lane, w, cg);
         if (tid < 8) {

@@ -1,25 +1,26 @@
 // Paged GQA decode attention on gfx950 (HD 256, block 64): split-K over block-table pages, online softmax
 // per wavefront, ordered in-kernel merge, optional fused append of the step's new K/V rows.
 //
-// Grid: one workgroup per (user, KV head, split); a split is `pps` consecutive block-table entries. The 4
-// waves of a workgroup stream pages p0 + w, p0 + w + 4, ... independently (no workgroup barrier inside the
-// page loop), each keeping its own running max m, sum l and o for the G query heads of the KV head (GQA
-// reuse: every K/V byte is loaded once for all G heads):
-//   scores  8 lanes per position, 32 dims per lane (16-byte loads at 128-byte row offsets, so one load
-//           instruction reads eight whole 128-byte lines), packed bf16 dot products (v_dot2_f32_bf16),
-//           3-step lane butterfly; scores and probabilities staged in the wave's LDS slice
-//   softmax one position per lane: wave max / sum, rescale of the running state
-//   P V     4 head dims per lane (one 512-byte V row per load instruction), fp32 FMA
-// The waves are merged in LDS; splits are merged through a fan-in-8 tree of self-resetting counters: the
-// last workgroup to finish a group of 8 merges it in a fixed order (the reference's fan-in-8 reduction
-// tree, kernels/attn_compute_common.hpp:123-151), so results are identical run to run.
+// Grid: one workgroup per (user, KV head, split); a split is `pps` consecutive block-table entries, walked
+// one page at a time by all 4 waves (see attn_kernel). Every K/V byte is loaded once for all G query
+// heads of the KV head (GQA reuse) and, in a verify step, for all query tokens of the step:
+//   scores  4 lanes per row, 64 dims per lane (interleaved in 16-byte pieces so each load instruction
+//           reads 64 contiguous bytes per row), packed bf16 dot products
+//           (v_dot2_f32_bf16) against q broadcast from LDS, 2-step lane butterfly
+//   softmax online per wave over its 16 rows (wave max / sum), probabilities rounded to bf16
+//   P V     4 head dims per lane (one 512-byte V row per load instruction), two rows per v_dot2
+// The waves are merged in LDS; the splits' partials (m, l, unnormalised o per query head) go to the
+// workspace and a second small kernel merges them in split order (the leader side of the reference:
+// global max, rescale, sum, normalise, kernels/attn_leader_writer.cpp:86-106 and
+// kernels/attn_leader_compute.cpp:42-79), so results are identical run to run. The merge is a separate
+// launch because an in-kernel last-arriver merge needs agent-scope release fences, and on this multi-XCD
+// part each such fence writes back the whole L2 (it cost 35-50 us per launch at 256 workgroups).
 #include "qs_common.h"
 
 namespace {
 
 constexpr int HD = 256;
 constexpr int BLK = 64;
-constexpr int FANIN = 8;
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
@@ -35,28 +36,31 @@ struct AttnArgs {
     const int *block_table;             // [B, max_blocks]
     const int *seq_lens;                // [B]
     uint16_t *o;                        // [B, T, NQ, HD]
-    float *part_o;                      // [B, T, NKV, slots, G, HD]
-    float *part_ml;                     // [B, T, NKV, slots, G, 2]
-    int *counters;                      // [B, NKV, slots]
-    int B, T, NQ, NKV, max_blocks, num_blocks, pps, nsplit, slots;
+    float *part_o;                      // [B, T, NKV, nsplit, G, HD]
+    float *part_ml;                     // [B, T, NKV, nsplit, G, 2]
+    int B, T, NQ, NKV, max_blocks, num_blocks, pps, nsplit;
     float scale;
 };
 
-// Workspace layout (bytes): counters | part_ml | part_o, each 256-byte aligned.
+// Workspace layout (bytes): part_ml | part_o, each 256-byte aligned.
 struct WsLayout {
-    size_t cnt, ml, po, total;
+    size_t ml, po, total;
 };
-__host__ __device__ inline WsLayout ws_layout(int B, int T, int NKV, int G, int slots) {
+__host__ __device__ inline WsLayout ws_layout(int B, int T, int NKV, int G, int nsplit) {
     auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
     WsLayout l;
-    l.cnt = 0;
-    l.ml = up((size_t)B * NKV * slots * 4);
-    l.po = l.ml + up((size_t)B * T * NKV * slots * G * 2 * 4);
-    l.total = l.po + up((size_t)B * T * NKV * slots * G * HD * 4);
+    l.ml = 0;
+    l.po = up((size_t)B * T * NKV * nsplit * G * 2 * 4);
+    l.total = l.po + up((size_t)B * T * NKV * nsplit * G * HD * 4);
     return l;
 }
 
-template <int G>
+// One workgroup per (user, KV head, split); the 4 waves work on the same page at a time, wave w owning
+// rows 16 w .. 16 w + 15, so a page's K and V (16 KB per wave) are requested in one round trip:
+//   K   lane = (row 16 w + lane / 4, piece c = lane % 4): dims 32 i + 8 c .. + 7 for i < 8, 8 x 16-byte loads
+//   V   lane = head dims 4 lane .. 4 lane + 3, the wave's 16 rows (one 512-byte row per load instruction)
+// and the loaded page is reused for every query token of the group (TT tokens: the verify rows).
+template <int G, int TT>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     constexpr int GP = (G + 3) & ~3;
     const int nwg = a.B * a.NKV * a.nsplit;
@@ -67,12 +71,11 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int T = a.T;
 
-    __shared__ __align__(16) uint16_t s_q[G][HD];
-    __shared__ __align__(16) float s_p[4][BLK][GP];
+    __shared__ __align__(16) uint16_t s_q[TT][G][HD];
+    __shared__ __align__(16) uint32_t s_pp[4][8][GP];
     __shared__ __align__(16) float s_acc[4][G][HD];
     __shared__ float s_m[4][G], s_l[4][G];
-    __shared__ float s_w[FANIN][G], s_L[G], s_M[G];
-    __shared__ int s_last;
+    __shared__ float s_w[4][G], s_L[G], s_M[G];
 
     int n = a.seq_lens[b];
     n = n < T ? T : (n > a.max_blocks * BLK ? a.max_blocks * BLK : n);
@@ -103,242 +106,237 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         }
     }
 
-    const int c = lane & 7, r = lane >> 3;
-    for (int t = 0; t < T; ++t) {
-        const int valid = base + t + 1;  // positions 0 .. valid-1
-        const int pe = min(p1, (valid + BLK - 1) / BLK);
+    const int kq = lane & 3;               // K: this lane's 16-byte piece of each 64-byte run of the row
+    const int krw = 16 * w + (lane >> 2);  // K: row of the page this lane scores
+    const size_t pstride = (size_t)a.NKV * BLK * HD;  // elements per page
+    const size_t koff = ((size_t)g * BLK + krw) * HD + kq * 8;
+    const size_t voff = ((size_t)g * BLK + 16 * w) * HD + lane * 4;
+    const float sl2 = a.scale * 1.4426950408889634f;  // scores in the log2 domain: p = 2^(s scale log2e - m)
+    for (int tg = 0; tg < T; tg += TT) {
+        const int nt = min(TT, T - tg);
+        const int vend = base + tg + nt;  // rows at or past vend are invalid for every token of the group
+        const int pe = min(p1, (vend + BLK - 1) / BLK);
         __syncthreads();
-        for (int idx = tid; idx < G * 32; idx += 256) {
-            const int hh = idx >> 5, ch = idx & 31;
-            *reinterpret_cast<uint4 *>(&s_q[hh][ch * 8]) = *reinterpret_cast<const uint4 *>(
-                a.q + (((size_t)b * T + t) * a.NQ + g * G + hh) * HD + ch * 8);
+        for (int idx = tid; idx < TT * G * 32; idx += 256) {
+            const int tt = idx / (G * 32), hh = (idx / 32) % G, ch = idx & 31;
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (tt < nt)
+                v = *reinterpret_cast<const uint4 *>(a.q + (((size_t)b * T + tg + tt) * a.NQ + g * G + hh) * HD + ch * 8);
+            *reinterpret_cast<uint4 *>(&s_q[tt][hh][ch * 8]) = v;
         }
         __syncthreads();
 
-        float m[G], l[G], acc[G][4];
+        // m: running max (log2 domain, wave-uniform); lp: this lane's share of the running sum (one lane per
+        // row counts), reduced over the wave once per split
+        float m[TT][G], lp[TT][G], acc[TT][G][4];
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
-            m[h] = -INFINITY;
-            l[h] = 0.f;
-            acc[h][0] = acc[h][1] = acc[h][2] = acc[h][3] = 0.f;
-        }
-
-        for (int pi = p0 + w; pi < pe; pi += 4) {
-            const int pg = page_of(pi);
-            if (pg < 0) continue;
-            const uint16_t *kp = a.k_cache + ((size_t)pg * a.NKV + g) * BLK * HD;
-            const uint16_t *vp = a.v_cache + ((size_t)pg * a.NKV + g) * BLK * HD;
-            const int pbase = pi * BLK;
-            auto krow = [&](int pp) -> const uint16_t * {
-                const int P = pbase + pp;
-                if (a.k_new && P >= base) return a.k_new + (((size_t)b * T + (P - base)) * a.NKV + g) * HD;
-                return kp + (size_t)pp * HD;
-            };
-            auto vrow = [&](int pp) -> const uint16_t * {
-                const int P = pbase + pp;
-                if (a.v_new && P >= base) return a.v_new + (((size_t)b * T + (P - base)) * a.NKV + g) * HD;
-                return vp + (size_t)pp * HD;
-            };
-
-            // ---- scores: 8 passes of 8 positions, 4 passes' loads in flight at a time
-#pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                uint4 kv[4][4];
-#pragma unroll
-                for (int ps = 0; ps < 4; ++ps) {
-                    const int pp = (half * 4 + ps) * 8 + r;
-                    const uint16_t *src = krow(pp) + c * 8;
-                    const bool ok = pbase + pp < valid;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        kv[ps][i] = ok ? *reinterpret_cast<const uint4 *>(src + 64 * i) : make_uint4(0, 0, 0, 0);
-                }
-#pragma unroll
-                for (int ps = 0; ps < 4; ++ps) {
-                    const int pp = (half * 4 + ps) * 8 + r;
-                    float d[G];
-#pragma unroll
-                    for (int h = 0; h < G; ++h) d[h] = 0.f;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-                        for (int h = 0; h < G; ++h) {
-                            const uint4 qv = *reinterpret_cast<const uint4 *>(&s_q[h][c * 8 + 64 * i]);
-                            d[h] = dot2(kv[ps][i].x, qv.x, d[h]);
-                            d[h] = dot2(kv[ps][i].y, qv.y, d[h]);
-                            d[h] = dot2(kv[ps][i].z, qv.z, d[h]);
-                            d[h] = dot2(kv[ps][i].w, qv.w, d[h]);
-                        }
-                    }
-#pragma unroll
-                    for (int h = 0; h < G; ++h) {
-                        d[h] += __shfl_xor(d[h], 1, 64);
-                        d[h] += __shfl_xor(d[h], 2, 64);
-                        d[h] += __shfl_xor(d[h], 4, 64);
-                    }
-                    if (c == 0) {
-                        const bool ok = pbase + pp < valid;
-#pragma unroll
-                        for (int h = 0; h < G; ++h) s_p[w][pp][h] = ok ? d[h] * a.scale : -INFINITY;
-                    }
-                }
-            }
-            __builtin_amdgcn_wave_barrier();
-
-            // ---- online softmax: lane = position
+        for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-                const float x = s_p[w][lane][h];
-                const float mn = fmaxf(m[h], qs::wave_max(x));
-                const float e = x == -INFINITY ? 0.f : expf(x - mn);
-                const float alpha = m[h] == -INFINITY ? 0.f : expf(m[h] - mn);
-                l[h] = l[h] * alpha + qs::wave_sum(e);
-                m[h] = mn;
-                s_p[w][lane][h] = e;
-                acc[h][0] *= alpha;
-                acc[h][1] *= alpha;
-                acc[h][2] *= alpha;
-                acc[h][3] *= alpha;
+                m[tt][h] = -INFINITY;
+                lp[tt][h] = 0.f;
+                acc[tt][h][0] = acc[tt][h][1] = acc[tt][h][2] = acc[tt][h][3] = 0.f;
             }
-            __builtin_amdgcn_wave_barrier();
 
-            // ---- P V: 16 rows' loads in flight at a time
-            const int np = min(BLK, valid - pbase);
-            for (int j0 = 0; j0 < np; j0 += 16) {
-                uint2 vv[16];
+        for (int pi = p0; pi < pe; ++pi) {
+            const int pg = page_of(pi);
+            if (pg < 0) continue;
+            const int rbase = pi * BLK + 16 * w;  // position of the wave's first row
+            const int P = rbase + (lane >> 2);    // position of this lane's K row
+            // rows of the step's new tokens come from the inputs (only the last page can hold any); every
+            // other row, valid or not, from the page, which is always in bounds (invalid rows masked after)
+            const bool fresh = a.k_new && rbase + 15 >= base;
+            const uint16_t *kp = a.k_cache + (size_t)pg * pstride + koff;
+            if (fresh && P >= base && P < n) kp = a.k_new + (((size_t)b * T + (P - base)) * a.NKV + g) * HD + kq * 8;
+            // load i: the row's 4 lanes read 64 contiguous bytes (dims 32 i + 8 kq .. + 7), so each load
+            // instruction touches 16 half-lines and two consecutive loads complete them
+            uint4 kv[8];
 #pragma unroll
-                for (int j = 0; j < 16; ++j)
-                    vv[j] = (j0 + j < np) ? *reinterpret_cast<const uint2 *>(vrow(j0 + j) + lane * 4)
-                                          : make_uint2(0, 0);
+            for (int i = 0; i < 8; ++i) kv[i] = reinterpret_cast<const uint4 *>(kp)[i * 4];
+            const uint16_t *vp = a.v_cache + (size_t)pg * pstride + voff;
+            uint2 vv[16];
+            if (!fresh) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) vv[j] = *reinterpret_cast<const uint2 *>(vp + j * HD);
+            } else {
 #pragma unroll
                 for (int j = 0; j < 16; ++j) {
-                    const float v0 = qs::bf_lo(vv[j].x), v1 = qs::bf_hi(vv[j].x);
-                    const float v2 = qs::bf_lo(vv[j].y), v3 = qs::bf_hi(vv[j].y);
-                    float pr[GP];
+                    const int Pj = rbase + j;
+                    const uint16_t *src = (Pj >= base && Pj < n)
+                                              ? a.v_new + (((size_t)b * T + (Pj - base)) * a.NKV + g) * HD + lane * 4
+                                              : vp + j * HD;
+                    vv[j] = *reinterpret_cast<const uint2 *>(src);
+                }
+            }
+            if (rbase + 15 >= vend) {  // zero rows past every token's window (a stale row times 0 could be NaN)
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    if (rbase + j >= vend) vv[j] = make_uint2(0, 0);
+            }
+
+#pragma unroll
+            for (int tt = 0; tt < TT; ++tt) {
+                if (tt >= nt) break;
+                const int valid = base + tg + tt + 1;  // token tg + tt sees positions 0 .. valid - 1
+                const bool okr = P < valid;
+                // ---- scores of this lane's row over its 64 dims, then across the row's 4 lanes (the q
+                // reads of the 4 lanes are 64 contiguous bytes: conflict-free)
+                float sc[G];
+#pragma unroll
+                for (int h = 0; h < G; ++h) sc[h] = 0.f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+#pragma unroll
+                    for (int h = 0; h < G; ++h) {
+                        const uint4 qv = *reinterpret_cast<const uint4 *>(&s_q[tt][h][i * 32 + kq * 8]);
+                        float d = sc[h];
+                        d = dot2(kv[i].x, qv.x, d);
+                        d = dot2(kv[i].y, qv.y, d);
+                        d = dot2(kv[i].z, qv.z, d);
+                        d = dot2(kv[i].w, qv.w, d);
+                        sc[h] = d;
+                    }
+                }
+#pragma unroll
+                for (int h = 0; h < G; ++h) {
+                    sc[h] += qs::dpp<0xB1>(sc[h]);
+                    sc[h] += qs::dpp<0x4E>(sc[h]);
+                }
+                // ---- online softmax over the wave's 16 rows (log2 domain); probabilities rounded to bf16
+                // (the running sum adds the rounded values, so the normalisation matches what P V uses) and
+                // packed two rows per dword for P V
+#pragma unroll
+                for (int h = 0; h < G; ++h) {
+                    const float x = okr ? sc[h] * sl2 : -INFINITY;
+                    const float mn = fmaxf(m[tt][h], qs::wave_max_bcast(x));
+                    const float e = okr ? __builtin_amdgcn_exp2f(x - mn) : 0.f;
+                    const float alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m[tt][h] - mn);
+                    const uint32_t pk = qs::cvt_pk_bf16(e, qs::dpp<0x104>(e));  // this row | the next row
+                    lp[tt][h] = lp[tt][h] * alpha + (kq == 0 ? __uint_as_float(pk << 16) : 0.f);
+                    m[tt][h] = mn;
+                    acc[tt][h][0] *= alpha;
+                    acc[tt][h][1] *= alpha;
+                    acc[tt][h][2] *= alpha;
+                    acc[tt][h][3] *= alpha;
+                    if ((lane & 7) == 0) s_pp[w][lane >> 3][h] = pk;
+                }
+                __builtin_amdgcn_wave_barrier();
+                // ---- P V over the wave's 16 rows: two rows per v_dot2 (interleaved with v_perm)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint32_t x0 = __builtin_amdgcn_perm(vv[2 * j + 1].x, vv[2 * j].x, 0x05040100u);
+                    const uint32_t x1 = __builtin_amdgcn_perm(vv[2 * j + 1].x, vv[2 * j].x, 0x07060302u);
+                    const uint32_t x2 = __builtin_amdgcn_perm(vv[2 * j + 1].y, vv[2 * j].y, 0x05040100u);
+                    const uint32_t x3 = __builtin_amdgcn_perm(vv[2 * j + 1].y, vv[2 * j].y, 0x07060302u);
+                    uint32_t pr[GP];
 #pragma unroll
                     for (int h4 = 0; h4 < GP; h4 += 4) {
-                        const float4 p4 = *reinterpret_cast<const float4 *>(&s_p[w][j0 + j][h4]);
+                        const uint4 p4 = *reinterpret_cast<const uint4 *>(&s_pp[w][j][h4]);
                         pr[h4] = p4.x, pr[h4 + 1] = p4.y, pr[h4 + 2] = p4.z, pr[h4 + 3] = p4.w;
                     }
 #pragma unroll
                     for (int h = 0; h < G; ++h) {
-                        acc[h][0] += pr[h] * v0;
-                        acc[h][1] += pr[h] * v1;
-                        acc[h][2] += pr[h] * v2;
-                        acc[h][3] += pr[h] * v3;
+                        acc[tt][h][0] = dot2(pr[h], x0, acc[tt][h][0]);
+                        acc[tt][h][1] = dot2(pr[h], x1, acc[tt][h][1]);
+                        acc[tt][h][2] = dot2(pr[h], x2, acc[tt][h][2]);
+                        acc[tt][h][3] = dot2(pr[h], x3, acc[tt][h][3]);
                     }
                 }
+                __builtin_amdgcn_wave_barrier();
             }
-            __builtin_amdgcn_wave_barrier();
         }
 
-        // ---- merge the 4 waves of this workgroup
+        // ---- merge the 4 waves, token by token; one partial (or the output) per token and split
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
-            *reinterpret_cast<float4 *>(&s_acc[w][h][lane * 4]) = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-            if (lane == 0) {
-                s_m[w][h] = m[h];
-                s_l[w][h] = l[h];
-            }
-        }
-        __syncthreads();
-        if (tid < G) {
-            float M = -INFINITY;
-            for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, s_m[ww][tid]);
-            float L = 0.f;
-            for (int ww = 0; ww < 4; ++ww) {
-                const float e = M == -INFINITY ? 0.f : expf(s_m[ww][tid] - M);
-                s_w[ww][tid] = e;
-                L += e * s_l[ww][tid];
-            }
-            s_M[tid] = M;
-            s_L[tid] = L;
-        }
-        __syncthreads();
-        const size_t row = ((size_t)b * T + t) * a.NKV + g;
+        for (int tt = 0; tt < TT; ++tt) {
+            if (tt >= nt) break;
+            const int t = tg + tt;
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
-            const float O = s_w[0][h] * s_acc[0][h][tid] + s_w[1][h] * s_acc[1][h][tid] +
-                            s_w[2][h] * s_acc[2][h][tid] + s_w[3][h] * s_acc[3][h][tid];
-            if (a.nsplit == 1) {
-                a.o[(((size_t)b * T + t) * a.NQ + g * G + h) * HD + tid] = (uint16_t)qs::f2bf(O / s_L[h]);
-            } else {
-                a.part_o[((row * a.slots + split) * G + h) * HD + tid] = O;
+            for (int h = 0; h < G; ++h) {
+                const float lw = qs::wave_sum_dpp(lp[tt][h]);
+                *reinterpret_cast<float4 *>(&s_acc[w][h][lane * 4]) =
+                    make_float4(acc[tt][h][0], acc[tt][h][1], acc[tt][h][2], acc[tt][h][3]);
+                if (lane == 0) {
+                    s_m[w][h] = m[tt][h];
+                    s_l[w][h] = lw;
+                }
             }
-        }
-        if (a.nsplit > 1 && tid < G) {
-            float *ml = a.part_ml + ((row * a.slots + split) * G + tid) * 2;
-            ml[0] = s_M[tid];
-            ml[1] = s_L[tid];
-        }
-    }
-    if (a.nsplit == 1) return;
-
-    // ---- fan-in-8 merge tree over the splits of (b, g)
-    int idx = split, off = 0, cnt_n = a.nsplit;
-    while (cnt_n > 1) {
-        const int grp = idx / FANIN, nxt = off + cnt_n, nn = (cnt_n + FANIN - 1) / FANIN;
-        const int members = min(FANIN, cnt_n - grp * FANIN);
-        __threadfence();
-        __syncthreads();
-        if (tid == 0) {
-            int *cnt = a.counters + ((size_t)b * a.NKV + g) * a.slots + nxt + grp;
-            const int old = atomicAdd(cnt, 1);
-            const int last = old == members - 1;
-            if (last) atomicExch(cnt, 0);
-            s_last = last;
-        }
-        __syncthreads();
-        if (!s_last) return;
-        __threadfence();
-        for (int t = 0; t < T; ++t) {
-            const size_t row = ((size_t)b * T + t) * a.NKV + g;
-            const size_t src0 = row * a.slots + off + grp * FANIN;
+            __syncthreads();
             if (tid < G) {
                 float M = -INFINITY;
-                for (int i = 0; i < members; ++i) M = fmaxf(M, a.part_ml[((src0 + i) * G + tid) * 2]);
+                for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, s_m[ww][tid]);
                 float L = 0.f;
-                for (int i = 0; i < members; ++i) {
-                    const float *ml = a.part_ml + ((src0 + i) * G + tid) * 2;
-                    const float e = M == -INFINITY ? 0.f : expf(ml[0] - M);
-                    s_w[i][tid] = e;
-                    L += e * ml[1];
+                for (int ww = 0; ww < 4; ++ww) {
+                    const float e = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s_m[ww][tid] - M);
+                    s_w[ww][tid] = e;
+                    L += e * s_l[ww][tid];
                 }
                 s_M[tid] = M;
                 s_L[tid] = L;
             }
             __syncthreads();
+            const size_t row = ((size_t)b * T + t) * a.NKV + g;
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-                float O = 0.f;
-                for (int i = 0; i < members; ++i) O += s_w[i][h] * a.part_o[((src0 + i) * G + h) * HD + tid];
-                if (nn == 1)
+                const float O = s_w[0][h] * s_acc[0][h][tid] + s_w[1][h] * s_acc[1][h][tid] +
+                                s_w[2][h] * s_acc[2][h][tid] + s_w[3][h] * s_acc[3][h][tid];
+                if (a.nsplit == 1)
                     a.o[(((size_t)b * T + t) * a.NQ + g * G + h) * HD + tid] = (uint16_t)qs::f2bf(O / s_L[h]);
                 else
-                    a.part_o[((row * a.slots + nxt + grp) * G + h) * HD + tid] = O;
+                    a.part_o[((row * a.nsplit + split) * G + h) * HD + tid] = O;
             }
-            if (nn > 1 && tid < G) {
-                float *ml = a.part_ml + ((row * a.slots + nxt + grp) * G + tid) * 2;
+            if (a.nsplit > 1 && tid < G) {
+                float *ml = a.part_ml + ((row * a.nsplit + split) * G + tid) * 2;
                 ml[0] = s_M[tid];
                 ml[1] = s_L[tid];
             }
             __syncthreads();
         }
-        idx = grp;
-        off = nxt;
-        cnt_n = nn;
     }
 }
 
-int nsplit_of(int max_blocks, int pps) { return (max_blocks + pps - 1) / pps; }
-int slots_of(int nsplit) {
-    int s = 0, n = nsplit;
-    while (n > 1) {
-        s += n;
-        n = (n + FANIN - 1) / FANIN;
+// Merge of the splits of one output row (user, token, query head): thread d owns head dim d. Wave 0 finds
+// the global max M (log2 domain, as the partials store it) and sum L over the splits (lanes over splits, fixed-order butterflies) and leaves the
+// per-split weights e^(m_s - M) / L in LDS; every thread then sums its dim over the splits in split order.
+constexpr int MAX_SPLITS = 1024;
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, int G) {
+    __shared__ float s_wt[MAX_SPLITS];
+    const int rowh = blockIdx.x;  // ((b * T + t) * NKV + g) * G + h
+    const int h = rowh % G, row = rowh / G;
+    const int tid = threadIdx.x;
+    const float *ml = a.part_ml + ((size_t)row * a.nsplit * G + h) * 2;
+    if (tid < 64) {
+        float M = -INFINITY;
+        for (int sp = tid; sp < a.nsplit; sp += 64) M = fmaxf(M, ml[(size_t)sp * G * 2]);
+        M = qs::wave_max(M);
+        float L = 0.f;
+        for (int sp = tid; sp < a.nsplit; sp += 64) {
+            const float m = ml[(size_t)sp * G * 2];
+            const float e = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
+            s_wt[sp] = e;
+            L += e * ml[(size_t)sp * G * 2 + 1];
+        }
+        L = qs::wave_sum(L);
+        for (int sp = tid; sp < a.nsplit; sp += 64) s_wt[sp] /= L;
     }
-    return s + 1;
+    __syncthreads();
+    const float *po = a.part_o + ((size_t)row * a.nsplit * G + h) * HD + tid;
+    float O = 0.f;
+    int sp = 0;
+    for (; sp + 4 <= a.nsplit; sp += 4) {
+        const float x0 = po[(size_t)sp * G * HD], x1 = po[(size_t)(sp + 1) * G * HD];
+        const float x2 = po[(size_t)(sp + 2) * G * HD], x3 = po[(size_t)(sp + 3) * G * HD];
+        O += s_wt[sp] * x0;
+        O += s_wt[sp + 1] * x1;
+        O += s_wt[sp + 2] * x2;
+        O += s_wt[sp + 3] * x3;
+    }
+    for (; sp < a.nsplit; ++sp) O += s_wt[sp] * po[(size_t)sp * G * HD];
+    const int g = row % a.NKV, bt = row / a.NKV;
+    a.o[((size_t)bt * a.NQ + g * G + h) * HD + tid] = (uint16_t)qs::f2bf(O);
 }
+
+int nsplit_of(int max_blocks, int pps) { return (max_blocks + pps - 1) / pps; }
 
 }  // namespace
 
@@ -346,7 +344,7 @@ extern "C" size_t qs_paged_attention_workspace_bytes(int B, int T, int NQ, int N
                                                      int pages_per_split) {
     if (B <= 0 || T <= 0 || NKV <= 0 || NQ % NKV || HDa != HD || max_blocks <= 0 || pages_per_split <= 0) return 0;
     const int ns = nsplit_of(max_blocks, pages_per_split);
-    return ws_layout(B, T, NKV, NQ / NKV, slots_of(ns)).total;
+    return ws_layout(B, T, NKV, NQ / NKV, ns).total;
 }
 
 extern "C" int qs_paged_gqa_decode(const uint16_t *q, const uint16_t *k_new, const uint16_t *v_new,
@@ -364,28 +362,39 @@ extern "C" int qs_paged_gqa_decode(const uint16_t *q, const uint16_t *k_new, con
     const int G = NQ / NKV;
     const int ns = nsplit_of(max_blocks, pages_per_split);
     QS_REQUIRE(ns == 1 || workspace, "qs_paged_gqa_decode: %d splits need a workspace", ns);
+    QS_REQUIRE(ns <= MAX_SPLITS, "qs_paged_gqa_decode: %d splits exceed %d (raise pages_per_split)", ns, MAX_SPLITS);
     QS_REQUIRE((long)B * NKV * ns < (1L << 31), "qs_paged_gqa_decode: grid too large");
     AttnArgs a{};
     a.q = q, a.k_new = k_new, a.v_new = v_new, a.k_cache = k_cache, a.v_cache = v_cache;
     a.block_table = block_table, a.seq_lens = seq_lens, a.o = o;
     a.B = B, a.T = T, a.NQ = NQ, a.NKV = NKV, a.max_blocks = max_blocks, a.num_blocks = num_blocks;
-    a.pps = pages_per_split, a.nsplit = ns, a.slots = slots_of(ns), a.scale = scale;
+    a.pps = pages_per_split, a.nsplit = ns, a.scale = scale;
     if (workspace) {
-        const WsLayout L = ws_layout(B, T, NKV, G, a.slots);
+        const WsLayout L = ws_layout(B, T, NKV, G, ns);
         char *ws = static_cast<char *>(workspace);
-        a.counters = reinterpret_cast<int *>(ws + L.cnt);
         a.part_ml = reinterpret_cast<float *>(ws + L.ml);
         a.part_o = reinterpret_cast<float *>(ws + L.po);
     }
     const dim3 grid(B * NKV * ns);
     hipStream_t st = QS_STREAM(stream);
+    const int TT = T >= 3 ? 4 : T;  // query tokens per pass over the pages
+#define QS_ATTN_LAUNCH(GG)                                                      \
+    if (TT == 1) attn_kernel<GG, 1><<<grid, 256, 0, st>>>(a);                   \
+    else if (TT == 2) attn_kernel<GG, 2><<<grid, 256, 0, st>>>(a);              \
+    else attn_kernel<GG, 4><<<grid, 256, 0, st>>>(a);
     switch (G) {
-        case 1: attn_kernel<1><<<grid, 256, 0, st>>>(a); break;
-        case 2: attn_kernel<2><<<grid, 256, 0, st>>>(a); break;
-        case 4: attn_kernel<4><<<grid, 256, 0, st>>>(a); break;
-        case 6: attn_kernel<6><<<grid, 256, 0, st>>>(a); break;
-        case 8: attn_kernel<8><<<grid, 256, 0, st>>>(a); break;
+        case 1: QS_ATTN_LAUNCH(1) break;
+        case 2: QS_ATTN_LAUNCH(2) break;
+        case 4: QS_ATTN_LAUNCH(4) break;
+        case 6: QS_ATTN_LAUNCH(6) break;
+        case 8: QS_ATTN_LAUNCH(8) break;
         default: QS_REQUIRE(false, "qs_paged_gqa_decode: group size NQ/NKV = %d not in {1, 2, 4, 6, 8}", G);
     }
-    return qs::launch_status("qs_paged_gqa_decode");
+#undef QS_ATTN_LAUNCH
+    if (int e = qs::launch_status("qs_paged_gqa_decode")) return e;
+    if (ns > 1) {
+        attn_merge_kernel<<<B * T * NKV * G, 256, 0, st>>>(a, G);
+        return qs::launch_status("qs_paged_gqa_decode (merge)");
+    }
+    return QS_OK;
 }

@@ -39,6 +39,62 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Cross-lane moves inside 16-lane rows with DPP (no LDS round trip). CTRL: 0xB1 quad_perm [1,0,3,2]
+// (xor 1), 0x4E quad_perm [2,3,0,1] (xor 2), 0x104 row_shl:4 (lane i reads lane i + 4), 0x124 / 0x128
+// row_ror:4 / row_ror:8 (0x128 is xor 8).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float lane_val(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+// Wave-wide max / sum with DPP inside each 16-lane row and readlane across the 4 rows. Every lane of a row
+// holds bit-identical partials (the pairwise combines are commutative), so the result is wave-uniform and
+// deterministic.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, dpp<0xB1>(v));
+    v = fmaxf(v, dpp<0x4E>(v));
+    v = fmaxf(v, dpp<0x124>(v));
+    v = fmaxf(v, dpp<0x128>(v));
+    return fmaxf(fmaxf(lane_val(v, 0), lane_val(v, 16)), fmaxf(lane_val(v, 32), lane_val(v, 48)));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp<0xB1>(v);
+    v += dpp<0x4E>(v);
+    v += dpp<0x124>(v);
+    v += dpp<0x128>(v);
+    return (lane_val(v, 0) + lane_val(v, 16)) + (lane_val(v, 32) + lane_val(v, 48));
+}
+
+// Wave-wide max, wave-uniform result: DPP inside each 16-lane row, then row_bcast:15 (into rows 1, 3) and
+// row_bcast:31 (into rows 2, 3) fold the rows so lane 63 holds the maximum; one readlane broadcasts it.
+__device__ __forceinline__ float wave_max_bcast(float v) {
+    v = fmaxf(v, dpp<0xB1>(v));
+    v = fmaxf(v, dpp<0x4E>(v));
+    v = fmaxf(v, dpp<0x124>(v));
+    v = fmaxf(v, dpp<0x128>(v));
+    const int vi = __builtin_bit_cast(int, v);
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(vi, vi, 0x142, 0xA, 0xF, false)));
+    const int vj = __builtin_bit_cast(int, v);
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(vj, vj, 0x143, 0xC, 0xF, false)));
+    return lane_val(v, 63);
+}
+
+// Two fp32 to packed bf16 (lo = a, hi = b), round-to-nearest-even (gfx950 v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
+    typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+    bf16x2_v v;
+    v[0] = (__bf16)a;
+    v[1] = (__bf16)b;
+    return __builtin_bit_cast(uint32_t, v);
+}
+
 // Workgroup i is dispatched to XCD i % 8. Map hardware ids so that consecutive logical ids land on one XCD
 // (and share its L2): logical = (hw % 8) * (n / 8) + hw / 8. Identity when n is not a multiple of 8.
 __device__ __forceinline__ int xcd_logical(int hw, int n) {
