@@ -1,17 +1,442 @@
-// Chunked-prefill gated delta rule (WY/UT form) on gfx950.
+// Chunked-prefill gated delta rule (WY / UT-transform form) on gfx950, chunk 64, MFMA bf16 with fp32 state.
+//
+// Per chunk of C = 64 tokens, value head h (key head h / (NV / NK)), start state S0 [DK, DV], raw bf16
+// rows q, k (L2 norms r_q (times scale), r_k applied as fp32 row scalings), cumulative log decay G and
+// gamma = e^G:
+//   A_ij = beta_i r_k,i r_k,j (k_i . k_j) e^(G_i - G_j)   (i > j),   Tm = (I + A)^-1
+//   P_ij = r_q,i r_k,j (q_i . k_j) e^(G_i - G_j)           (i >= j)
+//   X  = beta V - diag(beta gamma r_k) (K S0)
+//   d  = Tm X
+//   O  = diag(gamma r_q) (Q S0) + P d
+//   S  = gamma_C S0 + K^T diag(r_k gamma_C / gamma) d
+// (the chunked gated delta rule of Yang et al., "Gated Delta Networks", as FLA's chunk_gated_delta_rule
+// computes it). Two kernels:
+//   chunk_prep  one workgroup per (chunk, key head), fully parallel: K K^T and Q K^T on MFMA from the raw
+//               bf16 rows (exact products, fp32 sums), then for each of the key head's value heads A, P,
+//               the triangular inverse Tm by column-parallel forward substitution in LDS, and the per-token
+//               scalars, into the workspace;
+//   chunk_walk  one workgroup per (value head, 32-column slab of S): the 128 x 32 fp32 state slab stays
+//               in LDS while the workgroup walks the chunks in order. Every product that touches S or d
+//               splits the fp32 operand into bf16 hi + lo halves (two MFMAs, three for Tm x X), so the
+//               state keeps fp32-level accuracy (P is kept as bf16 hi + lo planes for the same reason).
+// MFMA: v_mfma_f32_16x16x32_bf16; lane l holds A[l % 16][8 (l / 16) + j], B[8 (l / 16) + j][l % 16] (j < 8)
+// and C[4 (l / 16) + i][l % 16] (i < 4).
 #include "qs_common.h"
 
-extern "C" size_t qs_gdn_chunk_prefill_workspace_bytes(int T, int NK, int NV, int DK, int DV, int chunk) {
-    (void)T, (void)NK, (void)NV, (void)DK, (void)DV, (void)chunk;
-    return 256;
+namespace {
+
+constexpr int CH = 64;   // chunk
+constexpr int DK = 128;
+constexpr int DV = 128;
+constexpr int SLAB = 32;
+constexpr int NSLAB = DV / SLAB;
+constexpr int KP = DK + 8;  // bf16 row stride of the K / Q chunk tiles in LDS (272 bytes)
+constexpr int FP = CH + 1;  // fp32 row stride of the 64 x 64 matrices in LDS
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ bf16x8 as_frag(uint4 u) { return __builtin_bit_cast(bf16x8, u32x4{u.x, u.y, u.z, u.w}); }
+
+// fp32 x[8] -> bf16 hi = rne(x), lo = rne(x - hi): hi + lo carries 16 mantissa bits
+__device__ __forceinline__ void split8(const float x[8], bf16x8 &hi, bf16x8 &lo) {
+    u32x4 h, l;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const uint32_t hp = qs::cvt_pk_bf16(x[2 * p], x[2 * p + 1]);
+        h[p] = hp;
+        l[p] = qs::cvt_pk_bf16(x[2 * p] - __uint_as_float(hp << 16), x[2 * p + 1] - __uint_as_float(hp & 0xffff0000u));
+    }
+    hi = __builtin_bit_cast(bf16x8, h);
+    lo = __builtin_bit_cast(bf16x8, l);
+}
+
+struct PrefillArgs {
+    const uint16_t *q, *k, *v;  // [T, NK, DK], [T, NK, DK], [T, NV, DV]
+    const float *g, *beta;      // [T, NV]
+    const float *S0;            // [NV, DK, DV]
+    float *ST;                  // [NV, DK, DV]
+    uint16_t *o;                // [T, NV, DV]
+    float *Tm;                  // workspace [nch, NV, 64, 64]
+    uint16_t *P;                // workspace [nch, NV, 2, 64, 64] bf16: hi and lo planes of P
+    float *sc;                  // workspace [nch, NV, 5, 64]: beta | beta gamma r_k | gamma r_q | r_k gamma_C/gamma | gamma_C
+    int T, NK, NV, nch;
+    float scale, eps;
+};
+
+// ------------------------------------------------------------------------------------------------ prep
+
+__global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
+    const int c = blockIdx.x / a.NK, kh = blockIdx.x % a.NK;
+    const int rep = a.NV / a.NK;
+    const int t0 = c * CH;
+    const int nval = min(CH, a.T - t0);
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+
+    __shared__ __align__(16) uint16_t sK[CH][KP];
+    __shared__ __align__(16) uint16_t sQ[CH][KP];
+    __shared__ float sKK[CH][FP], sQK[CH][FP], sA[CH][FP], sT[CH][FP];
+    __shared__ float s_rk[CH], s_rq[CH], s_G[CH], s_b[CH];
+
+    // 1. the chunk's raw q, k rows of key head kh (zeros past the sequence)
+    for (int idx = tid; idx < CH * (DK / 8); idx += 256) {
+        const int r = idx / (DK / 8), ch = idx % (DK / 8);
+        uint4 kv = make_uint4(0, 0, 0, 0), qv = make_uint4(0, 0, 0, 0);
+        if (r < nval) {
+            const size_t off = ((size_t)(t0 + r) * a.NK + kh) * DK + ch * 8;
+            kv = *reinterpret_cast<const uint4 *>(a.k + off);
+            qv = *reinterpret_cast<const uint4 *>(a.q + off);
+        }
+        *reinterpret_cast<uint4 *>(&sK[r][ch * 8]) = kv;
+        *reinterpret_cast<uint4 *>(&sQ[r][ch * 8]) = qv;
+    }
+    __syncthreads();
+
+    // 2. K K^T and Q K^T (exact bf16 products, fp32 sums): wave w owns row tile w
+    const int fr = lane & 15, fk = (lane >> 4) * 8;
+#pragma unroll
+    for (int tc = 0; tc < 4; ++tc) {
+        f32x4 ckk = {0.f, 0.f, 0.f, 0.f}, cqk = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < DK / 32; ++ks) {
+            const bf16x8 ak = as_frag(*reinterpret_cast<const uint4 *>(&sK[16 * w + fr][ks * 32 + fk]));
+            const bf16x8 aq = as_frag(*reinterpret_cast<const uint4 *>(&sQ[16 * w + fr][ks * 32 + fk]));
+            const bf16x8 bk = as_frag(*reinterpret_cast<const uint4 *>(&sK[16 * tc + fr][ks * 32 + fk]));
+            ckk = mfma(ak, bk, ckk);
+            cqk = mfma(aq, bk, cqk);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = 16 * w + (lane >> 4) * 4 + i, col = 16 * tc + fr;
+            sKK[row][col] = ckk[i];
+            sQK[row][col] = cqk[i];
+        }
+    }
+    // 3. q norms: 4 lanes per row, 32 dims each
+    {
+        const int r = tid >> 2, part = tid & 3;
+        float ss = 0.f;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint4 qv = *reinterpret_cast<const uint4 *>(&sQ[r][part * 32 + u * 8]);
+            const uint32_t wd[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float lo = qs::bf_lo(wd[e]), hi = qs::bf_hi(wd[e]);
+                ss = fmaf(lo, lo, ss);
+                ss = fmaf(hi, hi, ss);
+            }
+        }
+        ss += qs::dpp<0xB1>(ss);
+        ss += qs::dpp<0x4E>(ss);
+        if (part == 0) s_rq[r] = rsqrtf(ss + a.eps) * a.scale;
+    }
+    __syncthreads();
+    if (tid < CH) s_rk[tid] = rsqrtf(sKK[tid][tid] + a.eps);  // k . k from the exact K K^T diagonal
+
+    for (int j = 0; j < rep; ++j) {
+        const int hv = kh * rep + j;
+        // 4. gates of value head hv: cumulative log decay (inclusive scan over the 64 tokens)
+        if (w == 0) {
+            const bool ok = lane < nval;
+            float gi = ok ? a.g[(size_t)(t0 + lane) * a.NV + hv] : 0.f;
+            const float bi = ok ? a.beta[(size_t)(t0 + lane) * a.NV + hv] : 0.f;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const float up = __shfl_up(gi, d, 64);
+                if (lane >= d) gi += up;
+            }
+            s_G[lane] = gi;
+            s_b[lane] = bi;
+        }
+        __syncthreads();
+        // 5. A (strictly lower) into LDS, P (lower incl. diagonal) to the workspace as bf16
+        const size_t mat = ((size_t)c * a.NV + hv) * CH * CH;
+        for (int e = tid; e < CH * CH; e += 256) {
+            const int i = e >> 6, jj = e & 63;
+            float av = 0.f, pv = 0.f;
+            if (i >= jj) {
+                const float f = expf(s_G[i] - s_G[jj]);
+                const float rkj = s_rk[jj] * f;
+                if (i > jj) av = s_b[i] * s_rk[i] * rkj * sKK[i][jj];
+                pv = s_rq[i] * rkj * sQK[i][jj];
+            }
+            sA[i][jj] = av;
+            const uint32_t ph = qs::f2bf(pv);
+            a.P[2 * mat + e] = (uint16_t)ph;
+            a.P[2 * mat + CH * CH + e] = (uint16_t)qs::f2bf(pv - qs::bf2f(ph));
+        }
+        __syncthreads();
+        // 6. Tm = (I + A)^-1 by forward substitution, columns in parallel: 4 lanes per column (the k-sum
+        // split 4 ways), column j = 4 * (lane / 4 of the wave) + w so the waves share the work evenly.
+        // A column depends only on earlier rows of itself, so each wave runs its 16 columns alone.
+        {
+            const int part = lane & 3, col = ((lane >> 2) << 2) + w;
+            for (int i = 0; i < CH; ++i) {
+                float s = 0.f;
+                if (i > col)
+                    for (int kk = col + part; kk < i; kk += 4) s = fmaf(sA[i][kk], sT[kk][col], s);
+                s += qs::dpp<0xB1>(s);
+                s += qs::dpp<0x4E>(s);
+                if (part == 0) sT[i][col] = i == col ? 1.f : (i > col ? -s : 0.f);
+                __builtin_amdgcn_wave_barrier();
+            }
+        }
+        __syncthreads();
+        // 7. Tm and the per-token scalars to the workspace
+        for (int e = tid; e < CH * CH; e += 256) a.Tm[mat + e] = sT[e >> 6][e & 63];
+        if (tid < CH) {
+            const int i = tid;
+            const float gam = expf(s_G[i]);
+            float *scp = a.sc + ((size_t)c * a.NV + hv) * 5 * CH;
+            scp[0 * CH + i] = s_b[i];
+            scp[1 * CH + i] = s_b[i] * gam * s_rk[i];
+            scp[2 * CH + i] = s_rq[i] * gam;
+            scp[3 * CH + i] = s_rk[i] * expf(s_G[CH - 1] - s_G[i]);
+            scp[4 * CH + i] = expf(s_G[CH - 1]);
+        }
+        __syncthreads();
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ walk
+
+__global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
+    const int nwg = a.NV * NSLAB;
+    const int lid = qs::xcd_logical(blockIdx.x, nwg);
+    const int slab = lid % NSLAB, h = lid / NSLAB;
+    const int kh = h / (a.NV / a.NK);
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int fr = lane & 15, fk = (lane >> 4) * 8, fq = (lane >> 4) * 4;
+
+    __shared__ float sS[DK][SLAB + 4];
+    __shared__ __align__(16) uint16_t sK[CH][KP];
+    __shared__ __align__(16) uint16_t sQ[CH][KP];
+    __shared__ __align__(16) uint16_t sV[CH][SLAB + 8];
+    __shared__ __align__(16) float sTm[CH][CH + 4];
+    __shared__ __align__(16) uint16_t sP[2][CH][CH + 8];
+    __shared__ float sX[CH][SLAB + 4];
+    __shared__ float sD[CH][SLAB + 4];
+    __shared__ float s_c[5][CH];
+
+    // the state slab S0[h][:, 32 slab .. 32 slab + 31]
+    for (int idx = tid; idx < DK * SLAB / 4; idx += 256) {
+        const int d = idx / (SLAB / 4), v4 = idx % (SLAB / 4);
+        const float4 x = *reinterpret_cast<const float4 *>(a.S0 + ((size_t)h * DK + d) * DV + slab * SLAB + v4 * 4);
+        sS[d][v4 * 4 + 0] = x.x, sS[d][v4 * 4 + 1] = x.y, sS[d][v4 * 4 + 2] = x.z, sS[d][v4 * 4 + 3] = x.w;
+    }
+
+    for (int c = 0; c < a.nch; ++c) {
+        const int t0 = c * CH;
+        const int nval = min(CH, a.T - t0);
+        const size_t mat = ((size_t)c * a.NV + h) * CH * CH;
+        // ---- the chunk's operands into LDS
+        for (int idx = tid; idx < CH * (DK / 8); idx += 256) {
+            const int r = idx / (DK / 8), ch = idx % (DK / 8);
+            uint4 kv = make_uint4(0, 0, 0, 0), qv = make_uint4(0, 0, 0, 0);
+            if (r < nval) {
+                const size_t off = ((size_t)(t0 + r) * a.NK + kh) * DK + ch * 8;
+                kv = *reinterpret_cast<const uint4 *>(a.k + off);
+                qv = *reinterpret_cast<const uint4 *>(a.q + off);
+            }
+            *reinterpret_cast<uint4 *>(&sK[r][ch * 8]) = kv;
+            *reinterpret_cast<uint4 *>(&sQ[r][ch * 8]) = qv;
+        }
+        {
+            const int r = tid >> 2, ch = tid & 3;  // 64 rows x 4 x 8 values of the V slab
+            uint4 vv = make_uint4(0, 0, 0, 0);
+            if (r < nval) vv = *reinterpret_cast<const uint4 *>(a.v + ((size_t)(t0 + r) * a.NV + h) * DV + slab * SLAB + ch * 8);
+            *reinterpret_cast<uint4 *>(&sV[r][ch * 8]) = vv;
+        }
+        for (int idx = tid; idx < CH * CH / 4; idx += 256) {
+            const int r = idx / (CH / 4), c4 = idx % (CH / 4);
+            *reinterpret_cast<float4 *>(&sTm[r][c4 * 4]) = *reinterpret_cast<const float4 *>(a.Tm + mat + r * CH + c4 * 4);
+        }
+        for (int idx = tid; idx < 2 * CH * CH / 8; idx += 256) {
+            const int pl = idx / (CH * CH / 8), r = (idx / (CH / 8)) % CH, c8 = idx % (CH / 8);
+            *reinterpret_cast<uint4 *>(&sP[pl][r][c8 * 8]) =
+                *reinterpret_cast<const uint4 *>(a.P + 2 * mat + pl * CH * CH + r * CH + c8 * 8);
+        }
+        for (int idx = tid; idx < 5 * CH; idx += 256) s_c[idx / CH][idx % CH] = a.sc[((size_t)c * a.NV + h) * 5 * CH + idx];
+        __syncthreads();
+
+        // ---- K S0 and Q S0 for row tile w (S0 split hi + lo)
+        f32x4 kacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        f32x4 qacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int ks = 0; ks < DK / 32; ++ks) {
+            const bf16x8 ak = as_frag(*reinterpret_cast<const uint4 *>(&sK[16 * w + fr][ks * 32 + fk]));
+            const bf16x8 aq = as_frag(*reinterpret_cast<const uint4 *>(&sQ[16 * w + fr][ks * 32 + fk]));
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                float s8[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) s8[e] = sS[ks * 32 + fk + e][nt * 16 + fr];
+                bf16x8 bh, bl;
+                split8(s8, bh, bl);
+                kacc[nt] = mfma(ak, bh, kacc[nt]);
+                kacc[nt] = mfma(ak, bl, kacc[nt]);
+                qacc[nt] = mfma(aq, bh, qacc[nt]);
+                qacc[nt] = mfma(aq, bl, qacc[nt]);
+            }
+        }
+        // ---- X = beta V - (beta gamma r_k) (K S0)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = 16 * w + fq + i, col = nt * 16 + fr;
+                sX[r][col] = s_c[0][r] * qs::bf2f(sV[r][col]) - s_c[1][r] * kacc[nt][i];
+            }
+        __syncthreads();
+
+        // ---- d = Tm X (both fp32: hi*hi + hi*lo + lo*hi)
+        f32x4 dacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int ks = 0; ks < CH / 32; ++ks) {
+            float t8[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) t8[e] = sTm[16 * w + fr][ks * 32 + fk + e];
+            bf16x8 th, tl;
+            split8(t8, th, tl);
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                float x8[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x8[e] = sX[ks * 32 + fk + e][nt * 16 + fr];
+                bf16x8 xh, xl;
+                split8(x8, xh, xl);
+                dacc[nt] = mfma(th, xh, dacc[nt]);
+                dacc[nt] = mfma(th, xl, dacc[nt]);
+                dacc[nt] = mfma(tl, xh, dacc[nt]);
+            }
+        }
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sD[16 * w + fq + i][nt * 16 + fr] = dacc[nt][i];
+        __syncthreads();
+
+        // ---- O = (gamma r_q) (Q S0) + P d  (P and d split hi + lo: hi*hi + hi*lo + lo*hi)
+        f32x4 oacc[2];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) oacc[nt][i] = s_c[2][16 * w + fq + i] * qacc[nt][i];
+#pragma unroll
+        for (int ks = 0; ks < CH / 32; ++ks) {
+            const bf16x8 ap = as_frag(*reinterpret_cast<const uint4 *>(&sP[0][16 * w + fr][ks * 32 + fk]));
+            const bf16x8 apl = as_frag(*reinterpret_cast<const uint4 *>(&sP[1][16 * w + fr][ks * 32 + fk]));
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                float d8[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) d8[e] = sD[ks * 32 + fk + e][nt * 16 + fr];
+                bf16x8 dh, dl;
+                split8(d8, dh, dl);
+                oacc[nt] = mfma(ap, dh, oacc[nt]);
+                oacc[nt] = mfma(ap, dl, oacc[nt]);
+                oacc[nt] = mfma(apl, dh, oacc[nt]);
+            }
+        }
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = 16 * w + fq + i;
+                if (r < nval)
+                    a.o[((size_t)(t0 + r) * a.NV + h) * DV + slab * SLAB + nt * 16 + fr] = (uint16_t)qs::f2bf(oacc[nt][i]);
+            }
+
+        // ---- S = gamma_C S0 + K^T (r_k gamma_C / gamma) d : wave w owns state rows 32 w .. 32 w + 31
+        const float gC = s_c[4][0];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            const int d0 = 32 * w + 16 * mt;
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < CH / 32; ++ks) {
+                    u32x4 kt;  // K^T fragment: 8 consecutive tokens of one state row (exact bf16)
+#pragma unroll
+                    for (int p = 0; p < 4; ++p)
+                        kt[p] = (uint32_t)sK[ks * 32 + fk + 2 * p][d0 + fr] | ((uint32_t)sK[ks * 32 + fk + 2 * p + 1][d0 + fr] << 16);
+                    float d8[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int i = ks * 32 + fk + e;
+                        d8[e] = s_c[3][i] * sD[i][nt * 16 + fr];
+                    }
+                    bf16x8 dh, dl;
+                    split8(d8, dh, dl);
+                    const bf16x8 ka = __builtin_bit_cast(bf16x8, kt);
+                    sacc = mfma(ka, dh, sacc);
+                    sacc = mfma(ka, dl, sacc);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int d = d0 + fq + i, col = nt * 16 + fr;
+                    sS[d][col] = fmaf(gC, sS[d][col], sacc[i]);
+                }
+            }
+        }
+        __syncthreads();
+    }
+
+    for (int idx = tid; idx < DK * SLAB / 4; idx += 256) {
+        const int d = idx / (SLAB / 4), v4 = idx % (SLAB / 4);
+        const float4 x = make_float4(sS[d][v4 * 4 + 0], sS[d][v4 * 4 + 1], sS[d][v4 * 4 + 2], sS[d][v4 * 4 + 3]);
+        *reinterpret_cast<float4 *>(a.ST + ((size_t)h * DK + d) * DV + slab * SLAB + v4 * 4) = x;
+    }
+}
+
+struct PrefillWs {
+    size_t tm, p, sc, total;
+};
+PrefillWs prefill_ws(int T, int NV) {
+    auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const size_t nch = (size_t)(T + CH - 1) / CH;
+    PrefillWs l;
+    l.tm = 0;
+    l.p = up(nch * NV * CH * CH * 4);
+    l.sc = l.p + up(nch * NV * 2 * CH * CH * 2);
+    l.total = l.sc + up(nch * NV * 5 * CH * 4);
+    return l;
+}
+
+}  // namespace
+
+extern "C" size_t qs_gdn_chunk_prefill_workspace_bytes(int T, int NK, int NV, int DKa, int DVa, int chunk) {
+    if (T <= 0 || NK <= 0 || NV <= 0 || NV % NK || DKa != DK || DVa != DV || chunk != CH) return 0;
+    return prefill_ws(T, NV).total;
 }
 
 extern "C" int qs_gdn_chunk_prefill(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *g,
                                     const float *beta, const float *initial_state, uint16_t *o, float *final_state,
-                                    void *workspace, int T, int NK, int NV, int DK, int DV, int chunk, float scale,
+                                    void *workspace, int T, int NK, int NV, int DKa, int DVa, int chunk, float scale,
                                     float eps, void *stream) {
-    (void)q, (void)k, (void)v, (void)g, (void)beta, (void)initial_state, (void)o, (void)final_state;
-    (void)workspace, (void)T, (void)NK, (void)NV, (void)DK, (void)DV, (void)chunk, (void)scale, (void)eps;
-    (void)stream;
-    QS_REQUIRE(false, "qs_gdn_chunk_prefill: not built yet");
+    QS_REQUIRE(q && k && v && g && beta && initial_state && o && final_state && workspace,
+               "qs_gdn_chunk_prefill: null pointer");
+    QS_REQUIRE(T > 0, "qs_gdn_chunk_prefill: T must be positive (got %d)", T);
+    QS_REQUIRE(DKa == DK && DVa == DV, "qs_gdn_chunk_prefill: DK and DV must be 128 (got %d, %d)", DKa, DVa);
+    QS_REQUIRE(NK > 0 && NV > 0 && NV % NK == 0, "qs_gdn_chunk_prefill: NV (%d) must be a multiple of NK (%d)", NV, NK);
+    QS_REQUIRE(chunk == CH, "qs_gdn_chunk_prefill: only chunk %d is built (got %d)", CH, chunk);
+    const PrefillWs L = prefill_ws(T, NV);
+    char *ws = static_cast<char *>(workspace);
+    PrefillArgs a{};
+    a.q = q, a.k = k, a.v = v, a.g = g, a.beta = beta, a.S0 = initial_state, a.ST = final_state, a.o = o;
+    a.Tm = reinterpret_cast<float *>(ws + L.tm);
+    a.P = reinterpret_cast<uint16_t *>(ws + L.p);
+    a.sc = reinterpret_cast<float *>(ws + L.sc);
+    a.T = T, a.NK = NK, a.NV = NV, a.nch = (T + CH - 1) / CH, a.scale = scale, a.eps = eps;
+    hipStream_t st = QS_STREAM(stream);
+    chunk_prep_kernel<<<a.nch * NK, 256, 0, st>>>(a);
+    if (int e = qs::launch_status("qs_gdn_chunk_prefill (prep)")) return e;
+    chunk_walk_kernel<<<NV * NSLAB, 256, 0, st>>>(a);
+    return qs::launch_status("qs_gdn_chunk_prefill (walk)");
 }
