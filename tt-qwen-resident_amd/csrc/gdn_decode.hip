@@ -292,8 +292,9 @@ __global__ __launch_bounds__(256) void gates_kernel(const uint16_t *a, const uin
 
 // -------------------------------------------------------------------------------------------- rollback
 
-// grid (chunks, B): chunk j of user b copies float4 j * 256 + tid of the state and, in chunk 0, the conv
-// state and the new sequence length. accept_len outside [1, T] leaves the user untouched.
+// grid (chunks, B): the chunks of user b copy its state snapshot and its conv-state snapshot in 16-byte
+// units (2-byte units when the conv state is not a multiple of 16 bytes); chunk 0 also sets the new
+// sequence length. accept_len outside [1, T] leaves the user untouched.
 __global__ __launch_bounds__(256) void rollback_kernel(const float *states_out, float *state,
                                                        const uint16_t *conv_states_out, uint16_t *conv_state,
                                                        const int *accept, int *seq_lens, const int *base_lens,
@@ -302,16 +303,20 @@ __global__ __launch_bounds__(256) void rollback_kernel(const float *states_out, 
     const int acc = accept[b];
     if (acc < 1 || acc > T) return;
     const size_t slot = (size_t)(acc - 1) * B + b;
+    const size_t stride = (size_t)gridDim.x * 256, i0 = (size_t)blockIdx.x * 256 + threadIdx.x;
     const float4 *src = reinterpret_cast<const float4 *>(states_out) + slot * state_f4;
     float4 *dst = reinterpret_cast<float4 *>(state) + (size_t)b * state_f4;
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < state_f4; i += (size_t)gridDim.x * 256)
-        dst[i] = src[i];
-    if (blockIdx.x == 0) {
-        const uint16_t *cs = conv_states_out + slot * conv_elems;
-        uint16_t *cd = conv_state + (size_t)b * conv_elems;
-        for (size_t i = threadIdx.x; i < conv_elems; i += 256) cd[i] = cs[i];
-        if (threadIdx.x == 0 && seq_lens) seq_lens[b] = base_lens[b] + acc;
+    for (size_t i = i0; i < state_f4; i += stride) dst[i] = src[i];
+    const uint16_t *cs = conv_states_out + slot * conv_elems;
+    uint16_t *cd = conv_state + (size_t)b * conv_elems;
+    if (conv_elems % 8 == 0) {
+        const uint4 *cs4 = reinterpret_cast<const uint4 *>(cs);
+        uint4 *cd4 = reinterpret_cast<uint4 *>(cd);
+        for (size_t i = i0; i < conv_elems / 8; i += stride) cd4[i] = cs4[i];
+    } else {
+        for (size_t i = i0; i < conv_elems; i += stride) cd[i] = cs[i];
     }
+    if (blockIdx.x == 0 && threadIdx.x == 0 && seq_lens) seq_lens[b] = base_lens[b] + acc;
 }
 
 int check_gdn_shapes(int B, int NK, int NV, int DKa, int DVa) {

@@ -13,8 +13,8 @@
 // computes it). Two kernels:
 //   chunk_prep  one workgroup per (chunk, key head), fully parallel: K K^T and Q K^T on MFMA from the raw
 //               bf16 rows (exact products, fp32 sums), then for each of the key head's value heads A, P,
-//               the triangular inverse Tm by column-parallel forward substitution in LDS, and the per-token
-//               scalars, into the workspace;
+//               the triangular inverse Tm (blocked: 16 x 16 diagonal blocks by forward substitution, then
+//               the off-diagonal blocks by distance) and the per-token scalars, into the workspace;
 //   chunk_walk  one workgroup per (value head, 32-column slab of S): the 128 x 32 fp32 state slab stays
 //               in LDS while the workgroup walks the chunks in order. Every product that touches S or d
 //               splits the fp32 operand into bf16 hi + lo halves (two MFMAs, three for Tm x X), so the
@@ -77,10 +77,17 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
     const int nval = min(CH, a.T - t0);
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
 
-    __shared__ __align__(16) uint16_t sK[CH][KP];
-    __shared__ __align__(16) uint16_t sQ[CH][KP];
-    __shared__ float sKK[CH][FP], sQK[CH][FP], sA[CH][FP], sT[CH][FP];
+    // the K / Q tiles are dead once K K^T, Q K^T and the q norms exist: A and Tm reuse their space, which
+    // keeps the workgroup at 70 KB of LDS (two per CU)
+    __shared__ __align__(16) char s_kq[CH * KP * 2 * 2];
+    __shared__ float sKK[CH][FP], sQK[CH][FP];
     __shared__ float s_rk[CH], s_rq[CH], s_G[CH], s_b[CH];
+    __shared__ float sM[3][16][16];
+    uint16_t(*sK)[KP] = reinterpret_cast<uint16_t(*)[KP]>(s_kq);
+    uint16_t(*sQ)[KP] = reinterpret_cast<uint16_t(*)[KP]>(s_kq + CH * KP * 2);
+    float(*sA)[FP] = reinterpret_cast<float(*)[FP]>(s_kq);
+    float(*sT)[FP] = reinterpret_cast<float(*)[FP]>(s_kq + CH * FP * 4);
+    static_assert(2 * CH * FP * 4 <= CH * KP * 2 * 2, "A and Tm must fit in the K / Q tiles");
 
     // 1. the chunk's raw q, k rows of key head kh (zeros past the sequence)
     for (int idx = tid; idx < CH * (DK / 8); idx += 256) {
@@ -137,6 +144,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
     }
     __syncthreads();
     if (tid < CH) s_rk[tid] = rsqrtf(sKK[tid][tid] + a.eps);  // k . k from the exact K K^T diagonal
+    // (the barrier after the gates below also orders every sK / sQ read before the first write of sA)
 
     for (int j = 0; j < rep; ++j) {
         const int hv = kh * rep + j;
@@ -171,12 +179,13 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
             a.P[2 * mat + CH * CH + e] = (uint16_t)qs::f2bf(pv - qs::bf2f(ph));
         }
         __syncthreads();
-        // 6. Tm = (I + A)^-1 by forward substitution, columns in parallel: 4 lanes per column (the k-sum
-        // split 4 ways), column j = 4 * (lane / 4 of the wave) + w so the waves share the work evenly.
-        // A column depends only on earlier rows of itself, so each wave runs its 16 columns alone.
+        // 6. Tm = (I + A)^-1, blocked: (a) the four 16 x 16 diagonal blocks by forward substitution, one
+        // column per 4 lanes (the k-sum split 4 ways; wave w owns block w, and a column depends only on its
+        // own earlier rows, so no workgroup barrier inside); (b) the off-diagonal blocks by distance
+        // d = 1, 2, 3: T_IJ = -T_II (sum_{K=J}^{I-1} A_IK T_KJ).
         {
-            const int part = lane & 3, col = ((lane >> 2) << 2) + w;
-            for (int i = 0; i < CH; ++i) {
+            const int col = tid >> 2, part = tid & 3, b0 = 16 * w;
+            for (int i = b0; i < b0 + 16; ++i) {
                 float s = 0.f;
                 if (i > col)
                     for (int kk = col + part; kk < i; kk += 4) s = fmaf(sA[i][kk], sT[kk][col], s);
@@ -187,8 +196,25 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
             }
         }
         __syncthreads();
+        for (int dist = 1; dist < 4; ++dist) {
+            const int nb = 4 - dist;
+            for (int e = tid; e < nb * 256; e += 256) {  // M_IJ = sum_K A_IK T_KJ
+                const int J = e >> 8, I = J + dist, r = (e >> 4) & 15, cc = e & 15;
+                float m = 0.f;
+                for (int kk = 16 * J; kk < 16 * I; ++kk) m = fmaf(sA[16 * I + r][kk], sT[kk][16 * J + cc], m);
+                sM[J][r][cc] = m;
+            }
+            __syncthreads();
+            for (int e = tid; e < nb * 256; e += 256) {  // T_IJ = -T_II M_IJ
+                const int J = e >> 8, I = J + dist, r = (e >> 4) & 15, cc = e & 15;
+                float t = 0.f;
+                for (int kk = 0; kk < 16; ++kk) t = fmaf(sT[16 * I + r][16 * I + kk], sM[J][kk][cc], t);
+                sT[16 * I + r][16 * J + cc] = -t;
+            }
+            __syncthreads();
+        }
         // 7. Tm and the per-token scalars to the workspace
-        for (int e = tid; e < CH * CH; e += 256) a.Tm[mat + e] = sT[e >> 6][e & 63];
+        for (int e = tid; e < CH * CH; e += 256) a.Tm[mat + e] = (e >> 6) >= (e & 63) ? sT[e >> 6][e & 63] : 0.f;
         if (tid < CH) {
             const int i = tid;
             const float gam = expf(s_G[i]);
@@ -205,7 +231,20 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
 
 // ------------------------------------------------------------------------------------------------ walk
 
+// 8 consecutive fp32 from LDS (two 16-byte reads)
+__device__ __forceinline__ void lds8(const float *p, float x[8]) {
+    const float4 a = *reinterpret_cast<const float4 *>(p), b = *reinterpret_cast<const float4 *>(p + 4);
+    x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w, x[4] = b.x, x[5] = b.y, x[6] = b.z, x[7] = b.w;
+}
+
+// Operands are kept in LDS in the orientation the MFMA fragments read, so every fragment is two 16-byte
+// reads and every accumulator tile is stored with one: S^T [v][d], X^T and d^T [v][token], K^T [d][token]
+// beside K and Q [token][d]. The next chunk's K, Q and V are loaded into registers while the current
+// chunk computes; Tm, P and the scalars are requested at the start of a chunk and consumed after K S0.
 __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
+    constexpr int SP = DK + 4;   // fp32 row stride of S^T
+    constexpr int XP = CH + 4;   // fp32 row stride of X^T and d^T
+    constexpr int KTP = CH + 8;  // bf16 row stride of K^T
     const int nwg = a.NV * NSLAB;
     const int lid = qs::xcd_logical(blockIdx.x, nwg);
     const int slab = lid % NSLAB, h = lid / NSLAB;
@@ -213,56 +252,77 @@ __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int fr = lane & 15, fk = (lane >> 4) * 8, fq = (lane >> 4) * 4;
 
-    __shared__ float sS[DK][SLAB + 4];
+    __shared__ __align__(16) float sSt[SLAB][SP];
     __shared__ __align__(16) uint16_t sK[CH][KP];
     __shared__ __align__(16) uint16_t sQ[CH][KP];
+    __shared__ __align__(16) uint16_t sKt[DK][KTP];
     __shared__ __align__(16) uint16_t sV[CH][SLAB + 8];
     __shared__ __align__(16) float sTm[CH][CH + 4];
     __shared__ __align__(16) uint16_t sP[2][CH][CH + 8];
-    __shared__ float sX[CH][SLAB + 4];
-    __shared__ float sD[CH][SLAB + 4];
-    __shared__ float s_c[5][CH];
+    __shared__ __align__(16) float sXt[SLAB][XP];
+    __shared__ __align__(16) float sDt[SLAB][XP];
+    __shared__ __align__(16) float s_c[5][CH];
 
-    // the state slab S0[h][:, 32 slab .. 32 slab + 31]
+    // the state slab S0[h][:, 32 slab .. 32 slab + 31], transposed
     for (int idx = tid; idx < DK * SLAB / 4; idx += 256) {
         const int d = idx / (SLAB / 4), v4 = idx % (SLAB / 4);
         const float4 x = *reinterpret_cast<const float4 *>(a.S0 + ((size_t)h * DK + d) * DV + slab * SLAB + v4 * 4);
-        sS[d][v4 * 4 + 0] = x.x, sS[d][v4 * 4 + 1] = x.y, sS[d][v4 * 4 + 2] = x.z, sS[d][v4 * 4 + 3] = x.w;
+        sSt[v4 * 4 + 0][d] = x.x, sSt[v4 * 4 + 1][d] = x.y, sSt[v4 * 4 + 2][d] = x.z, sSt[v4 * 4 + 3][d] = x.w;
     }
+
+    // this thread's share of a chunk's K / Q rows (4 x 16 bytes each) and V slab (16 bytes)
+    uint4 pk[4], pq[4], pv;
+    auto fetch_kqv = [&](int c) {
+        const int t0 = c * CH, nval = min(CH, a.T - t0);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int idx = tid + 256 * m, r = idx >> 4, ch = idx & 15;
+            pk[m] = pq[m] = make_uint4(0, 0, 0, 0);
+            if (r < nval) {
+                const size_t off = ((size_t)(t0 + r) * a.NK + kh) * DK + ch * 8;
+                pk[m] = *reinterpret_cast<const uint4 *>(a.k + off);
+                pq[m] = *reinterpret_cast<const uint4 *>(a.q + off);
+            }
+        }
+        const int r = tid >> 2, ch = tid & 3;
+        pv = make_uint4(0, 0, 0, 0);
+        if (r < nval) pv = *reinterpret_cast<const uint4 *>(a.v + ((size_t)(t0 + r) * a.NV + h) * DV + slab * SLAB + ch * 8);
+    };
+    fetch_kqv(0);
 
     for (int c = 0; c < a.nch; ++c) {
         const int t0 = c * CH;
         const int nval = min(CH, a.T - t0);
         const size_t mat = ((size_t)c * a.NV + h) * CH * CH;
-        // ---- the chunk's operands into LDS
-        for (int idx = tid; idx < CH * (DK / 8); idx += 256) {
-            const int r = idx / (DK / 8), ch = idx % (DK / 8);
-            uint4 kv = make_uint4(0, 0, 0, 0), qv = make_uint4(0, 0, 0, 0);
-            if (r < nval) {
-                const size_t off = ((size_t)(t0 + r) * a.NK + kh) * DK + ch * 8;
-                kv = *reinterpret_cast<const uint4 *>(a.k + off);
-                qv = *reinterpret_cast<const uint4 *>(a.q + off);
+        // ---- K, Q, K^T, V of this chunk from registers into LDS
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int idx = tid + 256 * m, r = idx >> 4, ch = idx & 15;
+            *reinterpret_cast<uint4 *>(&sK[r][ch * 8]) = pk[m];
+            *reinterpret_cast<uint4 *>(&sQ[r][ch * 8]) = pq[m];
+            const uint32_t wd[4] = {pk[m].x, pk[m].y, pk[m].z, pk[m].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                sKt[ch * 8 + 2 * e][r] = (uint16_t)(wd[e] & 0xffffu);
+                sKt[ch * 8 + 2 * e + 1][r] = (uint16_t)(wd[e] >> 16);
             }
-            *reinterpret_cast<uint4 *>(&sK[r][ch * 8]) = kv;
-            *reinterpret_cast<uint4 *>(&sQ[r][ch * 8]) = qv;
         }
-        {
-            const int r = tid >> 2, ch = tid & 3;  // 64 rows x 4 x 8 values of the V slab
-            uint4 vv = make_uint4(0, 0, 0, 0);
-            if (r < nval) vv = *reinterpret_cast<const uint4 *>(a.v + ((size_t)(t0 + r) * a.NV + h) * DV + slab * SLAB + ch * 8);
-            *reinterpret_cast<uint4 *>(&sV[r][ch * 8]) = vv;
+        *reinterpret_cast<uint4 *>(&sV[tid >> 2][(tid & 3) * 8]) = pv;
+        // ---- Tm, P and scalars of this chunk: requested now, stored to LDS after K S0
+        float4 tmr[4];
+        uint4 ppr[4];
+        float scr[2];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int idx = tid + 256 * m;
+            tmr[m] = *reinterpret_cast<const float4 *>(a.Tm + mat + (idx >> 4) * CH + (idx & 15) * 4);
+            ppr[m] = *reinterpret_cast<const uint4 *>(a.P + 2 * mat + (idx >> 9) * CH * CH + ((idx >> 3) & 63) * CH + (idx & 7) * 8);
         }
-        for (int idx = tid; idx < CH * CH / 4; idx += 256) {
-            const int r = idx / (CH / 4), c4 = idx % (CH / 4);
-            *reinterpret_cast<float4 *>(&sTm[r][c4 * 4]) = *reinterpret_cast<const float4 *>(a.Tm + mat + r * CH + c4 * 4);
-        }
-        for (int idx = tid; idx < 2 * CH * CH / 8; idx += 256) {
-            const int pl = idx / (CH * CH / 8), r = (idx / (CH / 8)) % CH, c8 = idx % (CH / 8);
-            *reinterpret_cast<uint4 *>(&sP[pl][r][c8 * 8]) =
-                *reinterpret_cast<const uint4 *>(a.P + 2 * mat + pl * CH * CH + r * CH + c8 * 8);
-        }
-        for (int idx = tid; idx < 5 * CH; idx += 256) s_c[idx / CH][idx % CH] = a.sc[((size_t)c * a.NV + h) * 5 * CH + idx];
+        const float *scg = a.sc + ((size_t)c * a.NV + h) * 5 * CH;
+        scr[0] = scg[tid];
+        scr[1] = tid < 5 * CH - 256 ? scg[256 + tid] : 0.f;
         __syncthreads();
+        if (c + 1 < a.nch) fetch_kqv(c + 1);  // in flight during this chunk
 
         // ---- K S0 and Q S0 for row tile w (S0 split hi + lo)
         f32x4 kacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
@@ -274,8 +334,7 @@ __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
                 float s8[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) s8[e] = sS[ks * 32 + fk + e][nt * 16 + fr];
+                lds8(&sSt[nt * 16 + fr][ks * 32 + fk], s8);
                 bf16x8 bh, bl;
                 split8(s8, bh, bl);
                 kacc[nt] = mfma(ak, bh, kacc[nt]);
@@ -284,30 +343,43 @@ __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
                 qacc[nt] = mfma(aq, bl, qacc[nt]);
             }
         }
-        // ---- X = beta V - (beta gamma r_k) (K S0)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = 16 * w + fq + i, col = nt * 16 + fr;
-                sX[r][col] = s_c[0][r] * qs::bf2f(sV[r][col]) - s_c[1][r] * kacc[nt][i];
-            }
+        for (int m = 0; m < 4; ++m) {
+            const int idx = tid + 256 * m;
+            *reinterpret_cast<float4 *>(&sTm[idx >> 4][(idx & 15) * 4]) = tmr[m];
+            *reinterpret_cast<uint4 *>(&sP[idx >> 9][(idx >> 3) & 63][(idx & 7) * 8]) = ppr[m];
+        }
+        s_c[tid / CH][tid % CH] = scr[0];
+        if (tid < 5 * CH - 256) s_c[(256 + tid) / CH][(256 + tid) % CH] = scr[1];
         __syncthreads();
 
-        // ---- d = Tm X (both fp32: hi*hi + hi*lo + lo*hi)
+        // ---- X = beta V - (beta gamma r_k) (K S0), stored transposed
+        const float4 c0 = *reinterpret_cast<const float4 *>(&s_c[0][16 * w + fq]);
+        const float4 c1 = *reinterpret_cast<const float4 *>(&s_c[1][16 * w + fq]);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const int col = nt * 16 + fr, r0 = 16 * w + fq;
+            float4 x;
+            x.x = c0.x * qs::bf2f(sV[r0 + 0][col]) - c1.x * kacc[nt][0];
+            x.y = c0.y * qs::bf2f(sV[r0 + 1][col]) - c1.y * kacc[nt][1];
+            x.z = c0.z * qs::bf2f(sV[r0 + 2][col]) - c1.z * kacc[nt][2];
+            x.w = c0.w * qs::bf2f(sV[r0 + 3][col]) - c1.w * kacc[nt][3];
+            *reinterpret_cast<float4 *>(&sXt[col][r0]) = x;
+        }
+        __syncthreads();
+
+        // ---- d = Tm X (both fp32: hi*hi + hi*lo + lo*hi), stored transposed
         f32x4 dacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
         for (int ks = 0; ks < CH / 32; ++ks) {
             float t8[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) t8[e] = sTm[16 * w + fr][ks * 32 + fk + e];
+            lds8(&sTm[16 * w + fr][ks * 32 + fk], t8);
             bf16x8 th, tl;
             split8(t8, th, tl);
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
                 float x8[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) x8[e] = sX[ks * 32 + fk + e][nt * 16 + fr];
+                lds8(&sXt[nt * 16 + fr][ks * 32 + fk], x8);
                 bf16x8 xh, xl;
                 split8(x8, xh, xl);
                 dacc[nt] = mfma(th, xh, dacc[nt]);
@@ -317,16 +389,20 @@ __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
         }
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) sD[16 * w + fq + i][nt * 16 + fr] = dacc[nt][i];
+            *reinterpret_cast<float4 *>(&sDt[nt * 16 + fr][16 * w + fq]) =
+                make_float4(dacc[nt][0], dacc[nt][1], dacc[nt][2], dacc[nt][3]);
         __syncthreads();
 
         // ---- O = (gamma r_q) (Q S0) + P d  (P and d split hi + lo: hi*hi + hi*lo + lo*hi)
+        const float4 c2 = *reinterpret_cast<const float4 *>(&s_c[2][16 * w + fq]);
         f32x4 oacc[2];
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) oacc[nt][i] = s_c[2][16 * w + fq + i] * qacc[nt][i];
+        for (int nt = 0; nt < 2; ++nt) {
+            oacc[nt][0] = c2.x * qacc[nt][0];
+            oacc[nt][1] = c2.y * qacc[nt][1];
+            oacc[nt][2] = c2.z * qacc[nt][2];
+            oacc[nt][3] = c2.w * qacc[nt][3];
+        }
 #pragma unroll
         for (int ks = 0; ks < CH / 32; ++ks) {
             const bf16x8 ap = as_frag(*reinterpret_cast<const uint4 *>(&sP[0][16 * w + fr][ks * 32 + fk]));
@@ -334,8 +410,7 @@ __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
                 float d8[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) d8[e] = sD[ks * 32 + fk + e][nt * 16 + fr];
+                lds8(&sDt[nt * 16 + fr][ks * 32 + fk], d8);
                 bf16x8 dh, dl;
                 split8(d8, dh, dl);
                 oacc[nt] = mfma(ap, dh, oacc[nt]);
@@ -362,27 +437,21 @@ __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
                 f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int ks = 0; ks < CH / 32; ++ks) {
-                    u32x4 kt;  // K^T fragment: 8 consecutive tokens of one state row (exact bf16)
+                    const bf16x8 ka = as_frag(*reinterpret_cast<const uint4 *>(&sKt[d0 + fr][ks * 32 + fk]));
+                    float d8[8], c8[8];
+                    lds8(&sDt[nt * 16 + fr][ks * 32 + fk], d8);
+                    lds8(&s_c[3][ks * 32 + fk], c8);
 #pragma unroll
-                    for (int p = 0; p < 4; ++p)
-                        kt[p] = (uint32_t)sK[ks * 32 + fk + 2 * p][d0 + fr] | ((uint32_t)sK[ks * 32 + fk + 2 * p + 1][d0 + fr] << 16);
-                    float d8[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const int i = ks * 32 + fk + e;
-                        d8[e] = s_c[3][i] * sD[i][nt * 16 + fr];
-                    }
+                    for (int e = 0; e < 8; ++e) d8[e] *= c8[e];
                     bf16x8 dh, dl;
                     split8(d8, dh, dl);
-                    const bf16x8 ka = __builtin_bit_cast(bf16x8, kt);
                     sacc = mfma(ka, dh, sacc);
                     sacc = mfma(ka, dl, sacc);
                 }
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int d = d0 + fq + i, col = nt * 16 + fr;
-                    sS[d][col] = fmaf(gC, sS[d][col], sacc[i]);
-                }
+                float4 *sp = reinterpret_cast<float4 *>(&sSt[nt * 16 + fr][d0 + fq]);
+                const float4 old = *sp;
+                *sp = make_float4(fmaf(gC, old.x, sacc[0]), fmaf(gC, old.y, sacc[1]), fmaf(gC, old.z, sacc[2]),
+                                  fmaf(gC, old.w, sacc[3]));
             }
         }
         __syncthreads();
@@ -390,7 +459,7 @@ __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
 
     for (int idx = tid; idx < DK * SLAB / 4; idx += 256) {
         const int d = idx / (SLAB / 4), v4 = idx % (SLAB / 4);
-        const float4 x = make_float4(sS[d][v4 * 4 + 0], sS[d][v4 * 4 + 1], sS[d][v4 * 4 + 2], sS[d][v4 * 4 + 3]);
+        const float4 x = make_float4(sSt[v4 * 4 + 0][d], sSt[v4 * 4 + 1][d], sSt[v4 * 4 + 2][d], sSt[v4 * 4 + 3][d]);
         *reinterpret_cast<float4 *>(a.ST + ((size_t)h * DK + d) * DV + slab * SLAB + v4 * 4) = x;
     }
 }

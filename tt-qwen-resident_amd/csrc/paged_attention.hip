@@ -377,11 +377,10 @@ extern "C" int qs_paged_gqa_decode(const uint16_t *q, const uint16_t *k_new, con
     }
     const dim3 grid(B * NKV * ns);
     hipStream_t st = QS_STREAM(stream);
-    const int TT = T >= 3 ? 4 : T;  // query tokens per pass over the pages
+    const int TT = T >= 2 ? 2 : 1;  // query tokens per pass over the pages (4 would spill registers)
 #define QS_ATTN_LAUNCH(GG)                                                      \
     if (TT == 1) attn_kernel<GG, 1><<<grid, 256, 0, st>>>(a);                   \
-    else if (TT == 2) attn_kernel<GG, 2><<<grid, 256, 0, st>>>(a);              \
-    else attn_kernel<GG, 4><<<grid, 256, 0, st>>>(a);
+    else attn_kernel<GG, 2><<<grid, 256, 0, st>>>(a);
     switch (G) {
         case 1: QS_ATTN_LAUNCH(1) break;
         case 2: QS_ATTN_LAUNCH(2) break;

@@ -128,3 +128,79 @@ class StatePathStep:
         for d, (s, c) in zip((d for d in self.layer if not d["attn"]), snap):
             d["state"].copy_(s)
             d["conv_state"].copy_(c)
+
+
+class VerifyStep:
+    """The MTP verify step of the 64-layer state path: T tokens per user (1 accepted + T - 1 drafts) through
+    every layer — GDN layers keep all T intermediate states and conv histories, attention layers append T
+    rows and attend causally among them — then the rollback to a seeded accepted length per user: state and
+    conv history restored from snapshot a - 1 (bit-exact copies) and the KV length truncated to base + a.
+
+    The reference verify step is the 2-row form of the same protocol (model.py:426-456, README.md:413-421;
+    acceptance kernels/mlp_hub.cpp:48-58)."""
+
+    def __init__(self, B, ctx, T=4, layers=64, interval=4, device="cuda", seed=0, num_blocks=2048,
+                 pages_per_split=2):  # fmt: skip
+        self.B, self.ctx, self.T, self.layers, self.interval = B, ctx, T, layers, interval
+        self.device = torch.device(device)
+        self.pps = pages_per_split
+        pages = (ctx + BLOCK - 1) // BLOCK
+        self.block_table = W.block_tables(B, pages, num_blocks, self.device, seed)
+        self.seq_lens = torch.full((B,), ctx, dtype=torch.int32, device=self.device)
+        self.base_lens = self.seq_lens - T
+        gen = torch.Generator().manual_seed(seed + 7)
+        self.accept = torch.randint(1, T + 1, (B,), generator=gen, dtype=torch.int32).to(self.device)
+        self.layer = []
+        for l in range(layers):
+            if is_attn(l, interval):
+                d = W.attn_layer(B, ctx, self.device, seed=seed + 1000 + l, T=T, num_blocks=num_blocks)
+                d["block_table"], d["seq_lens"] = self.block_table, self.seq_lens
+                d["o"] = torch.empty(B, T, NQ, HD, dtype=torch.bfloat16, device=self.device)
+                d["attn"] = True
+            else:
+                d = W.gdn_layer(B, self.device, seed=seed + l, T=T)
+                d["o"] = torch.empty(B, T, NV, DV, dtype=torch.bfloat16, device=self.device)
+                d["states"] = torch.empty(T, B, NV, DK, DV, dtype=torch.float32, device=self.device)
+                d["convs"] = torch.empty(T, B, W.C_QKV, CONV_K - 1, dtype=torch.bfloat16, device=self.device)
+                d["attn"] = False
+            self.layer.append(d)
+        mb = self.block_table.shape[1]
+        self.attn_ws = ops.attention_workspace(B, T, NQ, NKV, mb, pages_per_split, self.device)
+        self.graph = None
+
+    def verify(self):
+        """All layers of the verify step (no rollback): what the target model's forward does."""
+        for d in self.layer:
+            if d["attn"]:
+                ops.paged_gqa_decode(d["q"], d["k_cache"], d["v_cache"], d["block_table"], d["seq_lens"],
+                                     d["scale"], k_new=d["k_new"], v_new=d["v_new"], pages_per_split=self.pps,
+                                     out=d["o"], ws=self.attn_ws)  # fmt: skip
+            else:
+                ops.gdn_verify_step(d["x"], d["conv_state"], d["taps"], d["g"], d["beta"], d["state"],
+                                    out=(d["o"], d["states"], d["convs"]))  # fmt: skip
+
+    def rollback(self):
+        """Restore every GDN layer to its accepted snapshot and truncate the KV length (once)."""
+        first = True
+        for d in self.layer:
+            if not d["attn"]:
+                ops.gdn_rollback(d["states"], d["convs"], self.accept, d["state"], d["conv_state"],
+                                 self.seq_lens if first else None, self.base_lens if first else None)  # fmt: skip
+                first = False
+
+    def step(self):
+        self.verify()
+        self.rollback()
+
+    def reset_lengths(self):
+        """Undo the KV truncation so the same step can be replayed (benchmarking)."""
+        self.seq_lens.copy_(self.base_lens + self.T)
+
+    def bytes_per_step(self):
+        """Algorithmic bytes of the verify step (rollback by slot selection costs none; the copy this
+        build performs is rollback_bytes())."""
+        return step_bytes(self.B, self.ctx, self.layers, self.interval, self.T)
+
+    def rollback_bytes(self):
+        n_gdn = sum(not d["attn"] for d in self.layer)
+        return n_gdn * self.B * (2 * NV * DK * DV * 4 + 2 * W.C_QKV * (CONV_K - 1) * 2)

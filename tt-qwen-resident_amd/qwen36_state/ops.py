@@ -149,13 +149,13 @@ def gdn_decode_fused(x, conv_state, taps, g, beta, state, nk=NK, scale=None, eps
 # ------------------------------------------------------------------------------------------- a7
 
 
-def gdn_verify_step(x, conv_state, taps, g, beta, state, nk=NK, scale=None, eps=EPS, return_y=False):
+def gdn_verify_step(x, conv_state, taps, g, beta, state, nk=NK, scale=None, eps=EPS, return_y=False, out=None):
     """T tokens per user through conv + delta rule, keeping every intermediate (the verify rows of the
     reference GDN head cores, kernels/gdn_head_reader.cpp:149-187, gdn_head_writer.cpp:60-66).
 
     x [B, T, C]; g, beta [B, T, NV]; conv_state [B, C, 3] and state [B, NV, DK, DV] are read only.
     Returns o [B, T, NV, DV] bf16, states [T, B, NV, DK, DV] fp32, conv_states [T, B, C, 3] bf16
-    (and the conv outputs y [B, T, C] with return_y)."""
+    (and the conv outputs y [B, T, C] with return_y). ``out`` = (o, states, conv_states) preallocated."""
     dev = state.device
     _chk(state, "state", torch.float32)
     B, nv, dk, dv = state.shape
@@ -167,9 +167,15 @@ def gdn_verify_step(x, conv_state, taps, g, beta, state, nk=NK, scale=None, eps=
     _chk(g, "g", torch.float32, (B, T, nv), dev)
     _chk(beta, "beta", torch.float32, (B, T, nv), dev)
     scale = dk**-0.5 if scale is None else scale
-    o = torch.empty(B, T, nv, dv, dtype=torch.bfloat16, device=dev)
-    states = torch.empty(T, B, nv, dk, dv, dtype=torch.float32, device=dev)
-    convs = torch.empty(T, B, C, CONV_K - 1, dtype=torch.bfloat16, device=dev)
+    if out is None:
+        o = torch.empty(B, T, nv, dv, dtype=torch.bfloat16, device=dev)
+        states = torch.empty(T, B, nv, dk, dv, dtype=torch.float32, device=dev)
+        convs = torch.empty(T, B, C, CONV_K - 1, dtype=torch.bfloat16, device=dev)
+    else:
+        o, states, convs = out
+        _chk(o, "out o", torch.bfloat16, (B, T, nv, dv), dev)
+        _chk(states, "out states", torch.float32, (T, B, nv, dk, dv), dev)
+        _chk(convs, "out conv_states", torch.bfloat16, (T, B, C, CONV_K - 1), dev)
     y = torch.empty(B, T, C, dtype=torch.bfloat16, device=dev) if return_y else None
     call("qs_gdn_verify_step", _p(x), _p(conv_state), _p(convs), _p(taps), _p(g), _p(beta), _p(state),
          _p(states), _p(o), _p(y), B, T, nk, nv, dk, dv, CONV_K, float(scale), float(eps), _stream(dev))  # fmt: skip
