@@ -117,7 +117,7 @@ int qs_paged_kv_fill(const uint16_t *k, const uint16_t *v, uint16_t *k_cache, ui
                      int num_blocks, void *stream);
 
 /* ---------------------------------------------------------------------------------------- a6: attention
- * Paged GQA decode attention with split-K over block-table pages and an in-kernel ordered merge.
+ * Paged GQA decode attention with split-K over block-table pages and an ordered merge launch.
  *   q [B, T, NQ, HD] bf16; seq_lens [B] = positions valid after this step's T tokens; query t of user b
  *   attends positions 0 .. seq_lens[b] - T + t (causal among the T new rows); o [B, T, NQ, HD] bf16.
  *   When k_new/v_new [B, T, NKV, HD] are non-null the T new rows are also appended (a5 fused): they are
