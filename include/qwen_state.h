@@ -122,7 +122,7 @@ int qs_paged_kv_fill(const uint16_t *k, const uint16_t *v, uint16_t *k_cache, ui
  *   attends positions 0 .. seq_lens[b] - T + t (causal among the T new rows); o [B, T, NQ, HD] bf16.
  *   When k_new/v_new [B, T, NKV, HD] are non-null the T new rows are also appended (a5 fused): they are
  *   written into their pages and attended from the inputs, so no call sees a half-written row.
- *   pages_per_split: pages one workgroup walks (the split-K grain); the workspace holds the partials.
+ *   pages_per_split (1..64): pages one workgroup walks (the split-K grain); the workspace holds the partials.
  * Replaces the attention leader / chunk workers / tail core (kernels/attn_worker_compute.cpp:77-270,
  * kernels/attn_leader_compute.cpp:42-105, kernels/attn_leader_writer.cpp:86-106, split schedule
  * kernels/attn_common.hpp:139-154; torch model.py:239-246). HD == 256, block == 64, NQ / NKV <= 8. */

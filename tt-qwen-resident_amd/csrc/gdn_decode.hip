@@ -159,27 +159,23 @@ __global__ __launch_bounds__(THREADS) void gdn_kernel(GdnArgs a) {
     f32x4 S[4];  // streamed once per step: nontemporal loads and stores keep it from thrashing L2 / MALL
 #pragma unroll
     for (int i = 0; i < 4; ++i) S[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(sp + (size_t)(rg + 32 * i) * DV));
+    // the gates of every token, requested with the rest so no load waits later in the chain
+    float gdec[TM], gbeta[TM];
+#pragma unroll
+    for (int t = 0; t < TM; ++t) {
+        if (t < T) {
+            const int gi = ((b * T) + t) * a.NV + h;
+            gdec[t] = a.g[gi];
+            gbeta[t] = a.beta[gi];
+        }
+    }
 
     // 2. Prologue: q, k of key head kh and the v slab, for every token.
     if (CONV) {
         conv_run<VERIFY>(a, cq, b, c, T, isq ? &s_qn[0][tid] : &s_kn[0][tid - DK], DK, kq_owner);
         if (tid < SLAB) conv_run<VERIFY>(a, cvin, b, cv, T, &s_v[0][tid], SLAB, true);
-        if (!VERIFY) {
-            // v channels of this slab are read by this workgroup only: shift them in place now.
-            if (tid < SLAB) store_conv_state(a, b, cv, cvin.h);
-            // q/k channels are read by the rep * NSLAB workgroups of key head kh: the last one to arrive
-            // (every other has consumed its reads) writes the shifted state and re-arms the counter.
-            __syncthreads();
-            if (tid == 0) {
-                int *cnt = a.counters + b * a.NK + kh;
-                const int old = atomicAdd(cnt, 1);
-                const int last = old == rep * NSLAB - 1;
-                if (last) atomicExch(cnt, 0);
-                s_last = last;
-            }
-            __syncthreads();
-            if (s_last) store_conv_state(a, b, c, cq.h);
-        }
+        // v channels of this slab are read by this workgroup only: shift them in place now.
+        if (!VERIFY && tid < SLAB) store_conv_state(a, b, cv, cvin.h);
     } else {
         for (int t = 0; t < T; ++t) {
             const size_t qk = (((size_t)b * T + t) * a.NK + kh) * DK;
@@ -191,6 +187,11 @@ __global__ __launch_bounds__(THREADS) void gdn_kernel(GdnArgs a) {
         }
     }
     __syncthreads();
+    // q/k conv channels are read by the rep * NSLAB workgroups of key head kh. Each counts itself in after
+    // the barrier above (its reads are consumed); the last to arrive writes the shifted state at the end
+    // and re-arms the counter. The count's return is only waited for at the end.
+    int arrived = 0;
+    if (CONV && !VERIFY && tid == 0) arrived = atomicAdd(a.counters + b * a.NK + kh, 1);
 
     // 3. L2 norms (q times scale): wave w normalises vectors w, w + 4, ... of (q_0, k_0, q_1, k_1, ...).
     for (int j = w; j < 2 * T; j += 4) {
@@ -206,8 +207,8 @@ __global__ __launch_bounds__(THREADS) void gdn_kernel(GdnArgs a) {
     // 4. Delta rule, token by token, on the slab held in registers.
     for (int t = 0; t < T; ++t) {
         const int gi = ((b * T) + t) * a.NV + h;
-        const float decay = expf(a.g[gi]);
-        const float bt = a.beta[gi];
+        const float decay = expf(gdec[t]);
+        const float bt = gbeta[t];
         float kn[4], qn[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -252,6 +253,15 @@ __global__ __launch_bounds__(THREADS) void gdn_kernel(GdnArgs a) {
             pk.y = qs::pack_bf2(ov[2], ov[3]);
             *reinterpret_cast<uint2 *>(a.o + (size_t)gi * DV + s * SLAB + cg * 4) = pk;
         }
+    }
+    if (CONV && !VERIFY) {
+        if (tid == 0) {
+            const int last = arrived == rep * NSLAB - 1;
+            if (last) atomicExch(a.counters + b * a.NK + kh, 0);
+            s_last = last;
+        }
+        __syncthreads();
+        if (s_last) store_conv_state(a, b, c, cq.h);
     }
 }
 

@@ -1,14 +1,17 @@
 // Paged GQA decode attention on gfx950 (HD 256, block 64): split-K over block-table pages, online softmax
-// per wavefront, ordered in-kernel merge, optional fused append of the step's new K/V rows.
+// per wavefront, an ordered merge launch, optional fused append of the step's new K/V rows.
 //
-// Grid: one workgroup per (user, KV head, split); a split is `pps` consecutive block-table entries, walked
-// one page at a time by all 4 waves (see attn_kernel). Every K/V byte is loaded once for all G query
-// heads of the KV head (GQA reuse) and, in a verify step, for all query tokens of the step:
+// Grid: one workgroup per (user, KV head, split); a split is `pps` (<= 64) consecutive block-table entries,
+// walked one page at a time by all 4 waves (see attn_kernel). Every K/V byte is loaded once for all G
+// query heads of the KV head (GQA reuse) and, in a verify step, for all query tokens of the step:
 //   scores  4 lanes per row, 64 dims per lane (interleaved in 16-byte pieces so each load instruction
 //           reads 64 contiguous bytes per row), packed bf16 dot products
 //           (v_dot2_f32_bf16) against q broadcast from LDS, 2-step lane butterfly
 //   softmax online per wave over its 16 rows (wave max / sum), probabilities rounded to bf16
 //   P V     4 head dims per lane (one 512-byte V row per load instruction), two rows per v_dot2
+// Pages before the one holding the step's first new row load through a buffer descriptor based at the
+// page's head tile (scalar address work only); for one query token three page buffers rotate so the next
+// page's K and V are in flight while a page is computed.
 // The waves are merged in LDS; the splits' partials (m, l, unnormalised o per query head) go to the
 // workspace and a second small kernel merges them in split order (the leader side of the reference:
 // global max, rescale, sum, normalise, kernels/attn_leader_writer.cpp:86-106 and
@@ -23,6 +26,8 @@ constexpr int HD = 256;
 constexpr int BLK = 64;
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
@@ -88,6 +93,14 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         const int pg = bt[pi];
         return (pg >= 0 && pg < a.num_blocks) ? pg : -1;
     };
+    // The split's block-table entries (at most 64), one per lane, read once up front: the page walk takes
+    // each page index with a readlane and never waits on a table read (a wait for one load would also
+    // wait for the K/V loads in flight).
+    const int bt_pre = p0 + lane < p1 ? bt[p0 + lane] : -1;
+    auto page_at = [&](int pi) {
+        const int pg = __builtin_amdgcn_readlane(bt_pre, pi - p0);
+        return (pg >= 0 && pg < a.num_blocks) ? pg : -1;
+    };
 
     // Fused append: the new rows that fall in this split's pages go into the pools. Attention below reads
     // those rows from k_new / v_new, never from the pool, so there is no write-read hazard.
@@ -111,7 +124,9 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     const size_t pstride = (size_t)a.NKV * BLK * HD;  // elements per page
     const size_t koff = ((size_t)g * BLK + krw) * HD + kq * 8;
     const size_t voff = ((size_t)g * BLK + 16 * w) * HD + lane * 4;
-    const float sl2 = a.scale * 1.4426950408889634f;  // scores in the log2 domain: p = 2^(s scale log2e - m)
+    const float sl2 = a.scale * 1.4426950408889634f;
+    const int kvo = krw * HD * 2 + kq * 16;
+    const int vvo = 16 * w * HD * 2 + lane * 8;  // scores in the log2 domain: p = 2^(s scale log2e - m)
     for (int tg = 0; tg < T; tg += TT) {
         const int nt = min(TT, T - tg);
         const int vend = base + tg + nt;  // rows at or past vend are invalid for every token of the group
@@ -138,8 +153,142 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                 acc[tt][h][0] = acc[tt][h][1] = acc[tt][h][2] = acc[tt][h][3] = 0.f;
             }
 
-        for (int pi = p0; pi < pe; ++pi) {
-            const int pg = page_of(pi);
+        // zero the V rows past every token's window (a stale row times a zero probability could be NaN)
+        auto mask_v = [&](int pi, uint4 (&vb)[8]) {
+            const int rbase = pi * BLK + 16 * w;
+            if (rbase + 15 >= vend) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    if (rbase + 2 * j >= vend) vb[j].x = vb[j].y = 0;
+                    if (rbase + 2 * j + 1 >= vend) vb[j].z = vb[j].w = 0;
+                }
+            }
+        };
+        // scores of page pi for token tg + tt, online softmax update, probabilities to s_pp
+        auto scores_tt = [&](int pi, int tt, const uint4 (&kv)[8]) {
+            const int P = pi * BLK + 16 * w + (lane >> 2);
+            const int valid = base + tg + tt + 1;  // token tg + tt sees positions 0 .. valid - 1
+            const bool okr = P < valid;
+            // ---- scores of this lane's row over its 64 dims, then across the row's 4 lanes (the q
+            // reads of the 4 lanes are 64 contiguous bytes: conflict-free)
+            float sc[G];
+#pragma unroll
+            for (int h = 0; h < G; ++h) sc[h] = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+#pragma unroll
+                for (int h = 0; h < G; ++h) {
+                    const uint4 qv = *reinterpret_cast<const uint4 *>(&s_q[tt][h][i * 32 + kq * 8]);
+                    float d = sc[h];
+                    d = dot2(kv[i].x, qv.x, d);
+                    d = dot2(kv[i].y, qv.y, d);
+                    d = dot2(kv[i].z, qv.z, d);
+                    d = dot2(kv[i].w, qv.w, d);
+                    sc[h] = d;
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                sc[h] += qs::dpp<0xB1>(sc[h]);
+                sc[h] += qs::dpp<0x4E>(sc[h]);
+            }
+            // ---- online softmax over the wave's 16 rows (log2 domain); probabilities rounded to bf16
+            // (the running sum adds the rounded values, so the normalisation matches what P V uses) and
+            // packed two rows per dword for P V
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                const float mn = fmaxf(m[tt][h], qs::wave_max_bcast(okr ? sc[h] : -INFINITY) * sl2);
+                const float e = okr ? __builtin_amdgcn_exp2f(fmaf(sc[h], sl2, -mn)) : 0.f;
+                const uint32_t pk = qs::cvt_pk_bf16(e, qs::dpp<0x104>(e));  // this row | the next row
+                if (mn != m[tt][h]) {
+                    const float alpha = m[tt][h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[tt][h] - mn);
+                    lp[tt][h] *= alpha;
+                    acc[tt][h][0] *= alpha;
+                    acc[tt][h][1] *= alpha;
+                    acc[tt][h][2] *= alpha;
+                    acc[tt][h][3] *= alpha;
+                    m[tt][h] = mn;
+                }
+                lp[tt][h] += __uint_as_float(pk << 16);
+                if ((lane & 7) == 0) s_pp[w][lane >> 3][h] = pk;
+            }
+            __builtin_amdgcn_wave_barrier();
+        };
+        // P V of the page for token tg + tt
+        auto pv_tt = [&](int tt, const uint4 (&vb)[8]) {
+            // ---- P V over the wave's 16 rows: two rows per v_dot2 (interleaved with v_perm)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t x0 = __builtin_amdgcn_perm(vb[j].z, vb[j].x, 0x05040100u);
+                const uint32_t x1 = __builtin_amdgcn_perm(vb[j].z, vb[j].x, 0x07060302u);
+                const uint32_t x2 = __builtin_amdgcn_perm(vb[j].w, vb[j].y, 0x05040100u);
+                const uint32_t x3 = __builtin_amdgcn_perm(vb[j].w, vb[j].y, 0x07060302u);
+                uint32_t pr[GP];
+#pragma unroll
+                for (int h4 = 0; h4 < GP; h4 += 4) {
+                    const uint4 p4 = *reinterpret_cast<const uint4 *>(&s_pp[w][j][h4]);
+                    pr[h4] = p4.x, pr[h4 + 1] = p4.y, pr[h4 + 2] = p4.z, pr[h4 + 3] = p4.w;
+                }
+#pragma unroll
+                for (int h = 0; h < G; ++h) {
+                    acc[tt][h][0] = dot2(pr[h], x0, acc[tt][h][0]);
+                    acc[tt][h][1] = dot2(pr[h], x1, acc[tt][h][1]);
+                    acc[tt][h][2] = dot2(pr[h], x2, acc[tt][h][2]);
+                    acc[tt][h][3] = dot2(pr[h], x3, acc[tt][h][3]);
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+        };
+        auto load_k_plain = [&](int pg, uint4 (&kb)[8]) {
+            const auto rk = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint16_t *>(a.k_cache + (size_t)pg * pstride + (size_t)g * BLK * HD), (short)0, BLK * HD * 2, 0x00020000);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, kvo, i * 64, 0);
+                kb[i] = make_uint4(x[0], x[1], x[2], x[3]);
+            }
+        };
+        auto load_v_plain = [&](int pg, uint4 (&vb)[8]) {
+            const auto rv = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint16_t *>(a.v_cache + (size_t)pg * pstride + (size_t)g * BLK * HD), (short)0, BLK * HD * 2, 0x00020000);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const u32x2 x0 = __builtin_amdgcn_raw_buffer_load_b64(rv, vvo, (2 * j) * HD * 2, 0);
+                const u32x2 x1 = __builtin_amdgcn_raw_buffer_load_b64(rv, vvo, (2 * j + 1) * HD * 2, 0);
+                vb[j] = make_uint4(x0[0], x0[1], x1[0], x1[1]);
+            }
+        };
+        int pstart = p0;
+        if constexpr (TT == 1) {
+            // pages before the one holding the step's first new row: two in flight (page pi + 1 loads while
+            // page pi is computed)
+            const int pp = max(p0, min(pe, base / BLK));
+            // Three page buffers rotate through the roles K(pi), V(pi) and K(pi + 1) in flight: after the
+            // scores of page pi its K buffer takes V(pi + 1), after its P V its V buffer takes K(pi + 2)
+            uint4 X[8], Y[8], Z[8];
+            auto step = [&](int pi, uint4 (&kb)[8], uint4 (&vb)[8]) {
+                const bool ok = page_at(pi) >= 0;
+                if (ok) scores_tt(pi, 0, kb);
+                if (pi + 1 < pp && page_at(pi + 1) >= 0) load_v_plain(page_at(pi + 1), kb);
+                if (ok) pv_tt(0, vb);
+                if (pi + 2 < pp && page_at(pi + 2) >= 0) load_k_plain(page_at(pi + 2), vb);
+            };
+            if (p0 < pp && page_at(p0) >= 0) {
+                load_k_plain(page_at(p0), X);
+                load_v_plain(page_at(p0), Y);
+            }
+            if (p0 + 1 < pp && page_at(p0 + 1) >= 0) load_k_plain(page_at(p0 + 1), Z);
+            for (int pi = p0; pi < pp; pi += 3) {
+                step(pi, X, Y);
+                if (pi + 1 >= pp) break;
+                step(pi + 1, Z, X);
+                if (pi + 2 >= pp) break;
+                step(pi + 2, Y, Z);
+            }
+            pstart = pp;
+        }
+        for (int pi = pstart; pi < pe; ++pi) {
+            const int pg = page_at(pi);
             if (pg < 0) continue;
             const int rbase = pi * BLK + 16 * w;  // position of the wave's first row
             const int P = rbase + (lane >> 2);    // position of this lane's K row
@@ -151,14 +300,26 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             // load i: the row's 4 lanes read 64 contiguous bytes (dims 32 i + 8 kq .. + 7), so each load
             // instruction touches 16 half-lines and two consecutive loads complete them
             uint4 kv[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) kv[i] = reinterpret_cast<const uint4 *>(kp)[i * 4];
-            const uint16_t *vp = a.v_cache + (size_t)pg * pstride + voff;
             uint2 vv[16];
+            const uint16_t *vp = a.v_cache + (size_t)pg * pstride + voff;
             if (!fresh) {
+                const auto rk = __builtin_amdgcn_make_buffer_rsrc(
+                    const_cast<uint16_t *>(a.k_cache + (size_t)pg * pstride + (size_t)g * BLK * HD), (short)0, BLK * HD * 2, 0x00020000);
+                const auto rv = __builtin_amdgcn_make_buffer_rsrc(
+                    const_cast<uint16_t *>(a.v_cache + (size_t)pg * pstride + (size_t)g * BLK * HD), (short)0, BLK * HD * 2, 0x00020000);
 #pragma unroll
-                for (int j = 0; j < 16; ++j) vv[j] = *reinterpret_cast<const uint2 *>(vp + j * HD);
+                for (int i = 0; i < 8; ++i) {
+                    const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, kvo, i * 64, 0);
+                    kv[i] = make_uint4(x[0], x[1], x[2], x[3]);
+                }
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rv, vvo, j * HD * 2, 0);
+                    vv[j] = make_uint2(x[0], x[1]);
+                }
             } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) kv[i] = reinterpret_cast<const uint4 *>(kp)[i * 4];
 #pragma unroll
                 for (int j = 0; j < 16; ++j) {
                     const int Pj = rbase + j;
@@ -168,81 +329,15 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                     vv[j] = *reinterpret_cast<const uint2 *>(src);
                 }
             }
-            if (rbase + 15 >= vend) {  // zero rows past every token's window (a stale row times 0 could be NaN)
+            uint4 vb[8];
 #pragma unroll
-                for (int j = 0; j < 16; ++j)
-                    if (rbase + j >= vend) vv[j] = make_uint2(0, 0);
-            }
-
+            for (int j = 0; j < 8; ++j) vb[j] = make_uint4(vv[2 * j].x, vv[2 * j].y, vv[2 * j + 1].x, vv[2 * j + 1].y);
+            mask_v(pi, vb);
 #pragma unroll
             for (int tt = 0; tt < TT; ++tt) {
                 if (tt >= nt) break;
-                const int valid = base + tg + tt + 1;  // token tg + tt sees positions 0 .. valid - 1
-                const bool okr = P < valid;
-                // ---- scores of this lane's row over its 64 dims, then across the row's 4 lanes (the q
-                // reads of the 4 lanes are 64 contiguous bytes: conflict-free)
-                float sc[G];
-#pragma unroll
-                for (int h = 0; h < G; ++h) sc[h] = 0.f;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-#pragma unroll
-                    for (int h = 0; h < G; ++h) {
-                        const uint4 qv = *reinterpret_cast<const uint4 *>(&s_q[tt][h][i * 32 + kq * 8]);
-                        float d = sc[h];
-                        d = dot2(kv[i].x, qv.x, d);
-                        d = dot2(kv[i].y, qv.y, d);
-                        d = dot2(kv[i].z, qv.z, d);
-                        d = dot2(kv[i].w, qv.w, d);
-                        sc[h] = d;
-                    }
-                }
-#pragma unroll
-                for (int h = 0; h < G; ++h) {
-                    sc[h] += qs::dpp<0xB1>(sc[h]);
-                    sc[h] += qs::dpp<0x4E>(sc[h]);
-                }
-                // ---- online softmax over the wave's 16 rows (log2 domain); probabilities rounded to bf16
-                // (the running sum adds the rounded values, so the normalisation matches what P V uses) and
-                // packed two rows per dword for P V
-#pragma unroll
-                for (int h = 0; h < G; ++h) {
-                    const float x = okr ? sc[h] * sl2 : -INFINITY;
-                    const float mn = fmaxf(m[tt][h], qs::wave_max_bcast(x));
-                    const float e = okr ? __builtin_amdgcn_exp2f(x - mn) : 0.f;
-                    const float alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m[tt][h] - mn);
-                    const uint32_t pk = qs::cvt_pk_bf16(e, qs::dpp<0x104>(e));  // this row | the next row
-                    lp[tt][h] = lp[tt][h] * alpha + (kq == 0 ? __uint_as_float(pk << 16) : 0.f);
-                    m[tt][h] = mn;
-                    acc[tt][h][0] *= alpha;
-                    acc[tt][h][1] *= alpha;
-                    acc[tt][h][2] *= alpha;
-                    acc[tt][h][3] *= alpha;
-                    if ((lane & 7) == 0) s_pp[w][lane >> 3][h] = pk;
-                }
-                __builtin_amdgcn_wave_barrier();
-                // ---- P V over the wave's 16 rows: two rows per v_dot2 (interleaved with v_perm)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const uint32_t x0 = __builtin_amdgcn_perm(vv[2 * j + 1].x, vv[2 * j].x, 0x05040100u);
-                    const uint32_t x1 = __builtin_amdgcn_perm(vv[2 * j + 1].x, vv[2 * j].x, 0x07060302u);
-                    const uint32_t x2 = __builtin_amdgcn_perm(vv[2 * j + 1].y, vv[2 * j].y, 0x05040100u);
-                    const uint32_t x3 = __builtin_amdgcn_perm(vv[2 * j + 1].y, vv[2 * j].y, 0x07060302u);
-                    uint32_t pr[GP];
-#pragma unroll
-                    for (int h4 = 0; h4 < GP; h4 += 4) {
-                        const uint4 p4 = *reinterpret_cast<const uint4 *>(&s_pp[w][j][h4]);
-                        pr[h4] = p4.x, pr[h4 + 1] = p4.y, pr[h4 + 2] = p4.z, pr[h4 + 3] = p4.w;
-                    }
-#pragma unroll
-                    for (int h = 0; h < G; ++h) {
-                        acc[tt][h][0] = dot2(pr[h], x0, acc[tt][h][0]);
-                        acc[tt][h][1] = dot2(pr[h], x1, acc[tt][h][1]);
-                        acc[tt][h][2] = dot2(pr[h], x2, acc[tt][h][2]);
-                        acc[tt][h][3] = dot2(pr[h], x3, acc[tt][h][3]);
-                    }
-                }
-                __builtin_amdgcn_wave_barrier();
+                scores_tt(pi, tt, kv);
+                pv_tt(tt, vb);
             }
         }
 
@@ -253,7 +348,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             const int t = tg + tt;
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-                const float lw = qs::wave_sum_dpp(lp[tt][h]);
+                const float lw = 0.25f * qs::wave_sum_dpp(lp[tt][h]);
                 *reinterpret_cast<float4 *>(&s_acc[w][h][lane * 4]) =
                     make_float4(acc[tt][h][0], acc[tt][h][1], acc[tt][h][2], acc[tt][h][3]);
                 if (lane == 0) {
@@ -295,43 +390,45 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     }
 }
 
-// Merge of the splits of one output row (user, token, query head): thread d owns head dim d. Wave 0 finds
-// the global max M (log2 domain, as the partials store it) and sum L over the splits (lanes over splits, fixed-order butterflies) and leaves the
-// per-split weights e^(m_s - M) / L in LDS; every thread then sums its dim over the splits in split order.
+// Merge of the splits of one output row (user, token, query head): thread d owns head dim d. The first 16
+// splits' partials are requested before the weights are known, so a merge of up to 16 splits costs one
+// memory round trip. Wave 0 finds the global max M (log2 domain, as the partials store it) and sum L over
+// the splits (fixed-order butterflies) and leaves the weights e^(m_s - M) / L in LDS; every thread then
+// sums its dim over the splits in split order.
 constexpr int MAX_SPLITS = 1024;
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, int G) {
+    constexpr int CH = 16;
     __shared__ float s_wt[MAX_SPLITS];
     const int rowh = blockIdx.x;  // ((b * T + t) * NKV + g) * G + h
     const int h = rowh % G, row = rowh / G;
     const int tid = threadIdx.x;
-    const float *ml = a.part_ml + ((size_t)row * a.nsplit * G + h) * 2;
+    const int ns = a.nsplit;
+    const size_t sstride = (size_t)G * HD;  // floats between consecutive splits of one row
+    const float *ml = a.part_ml + ((size_t)row * ns * G + h) * 2;
+    const float *po = a.part_o + ((size_t)row * ns * G + h) * HD + tid;
+    float x[CH];
+#pragma unroll
+    for (int k = 0; k < CH; ++k) x[k] = k < ns ? po[k * sstride] : 0.f;
     if (tid < 64) {
         float M = -INFINITY;
-        for (int sp = tid; sp < a.nsplit; sp += 64) M = fmaxf(M, ml[(size_t)sp * G * 2]);
+        for (int sp = tid; sp < ns; sp += 64) M = fmaxf(M, ml[(size_t)sp * G * 2]);
         M = qs::wave_max(M);
         float L = 0.f;
-        for (int sp = tid; sp < a.nsplit; sp += 64) {
+        for (int sp = tid; sp < ns; sp += 64) {
             const float m = ml[(size_t)sp * G * 2];
             const float e = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
             s_wt[sp] = e;
             L += e * ml[(size_t)sp * G * 2 + 1];
         }
         L = qs::wave_sum(L);
-        for (int sp = tid; sp < a.nsplit; sp += 64) s_wt[sp] /= L;
+        for (int sp = tid; sp < ns; sp += 64) s_wt[sp] /= L;
     }
     __syncthreads();
-    const float *po = a.part_o + ((size_t)row * a.nsplit * G + h) * HD + tid;
     float O = 0.f;
-    int sp = 0;
-    for (; sp + 4 <= a.nsplit; sp += 4) {
-        const float x0 = po[(size_t)sp * G * HD], x1 = po[(size_t)(sp + 1) * G * HD];
-        const float x2 = po[(size_t)(sp + 2) * G * HD], x3 = po[(size_t)(sp + 3) * G * HD];
-        O += s_wt[sp] * x0;
-        O += s_wt[sp + 1] * x1;
-        O += s_wt[sp + 2] * x2;
-        O += s_wt[sp + 3] * x3;
-    }
-    for (; sp < a.nsplit; ++sp) O += s_wt[sp] * po[(size_t)sp * G * HD];
+#pragma unroll
+    for (int k = 0; k < CH; ++k)
+        if (k < ns) O += s_wt[k] * x[k];
+    for (int sp = CH; sp < ns; ++sp) O += s_wt[sp] * po[(size_t)sp * sstride];
     const int g = row % a.NKV, bt = row / a.NKV;
     a.o[((size_t)bt * a.NQ + g * G + h) * HD + tid] = (uint16_t)qs::f2bf(O);
 }
@@ -358,7 +455,9 @@ extern "C" int qs_paged_gqa_decode(const uint16_t *q, const uint16_t *k_new, con
     QS_REQUIRE(B > 0 && T >= 1 && T <= 16, "qs_paged_gqa_decode: need B > 0 and 1 <= T <= 16");
     QS_REQUIRE(NKV > 0 && NQ > 0 && NQ % NKV == 0, "qs_paged_gqa_decode: NQ (%d) must be a multiple of NKV (%d)",
                NQ, NKV);
-    QS_REQUIRE(max_blocks > 0 && num_blocks > 0 && pages_per_split > 0, "qs_paged_gqa_decode: bad page counts");
+    QS_REQUIRE(max_blocks > 0 && num_blocks > 0, "qs_paged_gqa_decode: bad page counts");
+    QS_REQUIRE(pages_per_split > 0 && pages_per_split <= 64,
+               "qs_paged_gqa_decode: pages_per_split must be in [1, 64] (got %d)", pages_per_split);
     const int G = NQ / NKV;
     const int ns = nsplit_of(max_blocks, pages_per_split);
     QS_REQUIRE(ns == 1 || workspace, "qs_paged_gqa_decode: %d splits need a workspace", ns);

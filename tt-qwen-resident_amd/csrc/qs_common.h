@@ -40,15 +40,16 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 // Cross-lane moves inside 16-lane rows with DPP (no LDS round trip). CTRL: 0xB1 quad_perm [1,0,3,2]
-// (xor 1), 0x4E quad_perm [2,3,0,1] (xor 2), 0x104 row_shl:4 (lane i reads lane i + 4), 0x124 / 0x128
-// row_ror:4 / row_ror:8 (0x128 is xor 8).
+// (xor 1), 0x4E quad_perm [2,3,0,1] (xor 2), 0x104 row_shl:4 (lane i reads lane i + 4; lanes 12..15 of
+// a row read 0), 0x124 / 0x128 row_ror:4 / row_ror:8 (0x128 is xor 8). bound_ctrl set and no old value,
+// so the compiler folds the move into the consuming add / max as its DPP source.
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, true);
 }
 __device__ __forceinline__ float lane_val(float v, int l) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));

@@ -38,6 +38,9 @@ FLAGS = [
     f"-I{INCLUDE}",
     f"-I{CSRC}",
 ]
+# Per-source additions. Attention: its wave max reductions never see a NaN (masked scores are -inf), and
+# without NaN semantics each max folds its DPP operand instead of quieting both inputs first.
+FILE_FLAGS = {"paged_attention.hip": ["-fno-honor-nans"]}
 
 
 def sources():
@@ -46,7 +49,7 @@ def sources():
 
 def _compile(src):
     obj = os.path.join(BUILD, os.path.basename(src)[:-4] + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     p = subprocess.run(cmd, capture_output=True, text=True)
     err = "\n".join(l for l in p.stderr.splitlines() if "packed-fp32-ops" not in l)
     if p.returncode != 0:
