@@ -1,14 +1,14 @@
 // Gated DeltaNet decode-time state path on gfx950: conv1d update, gates, L2-norm + gated delta rule
 // (decode and T-token verify) and the verify rollback.
 //
-// Workgroup decomposition of the delta rule. For value column v the step is column-separable:
+// Decomposition of the delta rule. For value column v the step is column-separable:
 //     delta_v = beta (v_v - e^g sum_k k_k S_kv),  S'_kv = e^g S_kv + k_k delta_v,  o_v = sum_k q_k S'_kv
-// so one workgroup owns a 128 x 32 slab S[:, 32 s .. 32 s + 31] of one (user, value head): 4 slabs per head,
-// B * NV * 4 workgroups of 256 threads. Thread (rg = tid / 8, cg = tid % 8) holds rows rg + 32 i (i < 4),
-// columns 4 cg .. 4 cg + 3 of the slab in 16 VGPRs; one wave-wide dwordx4 load covers 8 full 128-byte rows
-// of the slab. The two k-reductions (S^T k and S'^T q) run as a 3-step lane butterfly inside the wave plus
-// one LDS stage across the 4 waves, in a fixed order (bit-reproducible run to run). The state is read once
-// and written once per token.
+// so one wavefront owns a 128 x 32 slab S[:, 32 s .. 32 s + 31] of one (user, value head): 4 slabs per head,
+// B * NV * 4 single-wave workgroups. Lane (rg = lane / 8, cg = lane % 8) holds rows rg + 8 i (i < 16),
+// columns 4 cg .. 4 cg + 3 of the slab in 64 VGPRs; each dwordx4 load or store instruction covers 8 full
+// 128-byte rows. The k-reductions (S^T k and S'^T q) sum a lane's 16 rows in registers, then the 8 row
+// groups (lane bits 3..5) with one DPP step and two lane swaps in a fixed order (bit-reproducible run to
+// run), so no step needs a workgroup barrier. The state is read once and written once per token.
 #include "qs_common.h"
 
 namespace {
@@ -18,9 +18,9 @@ constexpr int DV = 128;
 constexpr int KC = 4;  // conv taps
 constexpr int SLAB = 32;
 constexpr int NSLAB = DV / SLAB;
-constexpr int THREADS = 256;
 constexpr int TMAX = 8;
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
 
 struct GdnArgs {
     const uint16_t *q, *k, *v;  // q|k|v mode: [B, T, NK, DK], [B, T, NK, DK], [B, T, NV, DV]
@@ -38,93 +38,102 @@ struct GdnArgs {
     float scale, eps;
 };
 
-// Inputs of one channel's causal conv: the K-1 history values, the K taps and the channel's x for every
-// token. Loaded before the state slab so the prologue does not queue behind it.
+// Inputs of the causal conv of two adjacent channels (c, c + 1), as loaded (bf16 bits): their K-1 history
+// values (12 contiguous bytes: c's three, then c + 1's), their taps (16 bytes) and x of both for every token
+// (4 bytes per token). Three wide loads per pair instead of ten narrow ones; nothing reads them until
+// conv_run, so no wait sits between them and the state loads issued after.
 template <int TM>
-struct ConvIn {
-    float h[3], w[4];
+struct ConvPair {
+    u32x3 h;
+    uint4 tw;
     uint32_t x[TM];
 };
 
 template <int TM>
-__device__ __forceinline__ ConvIn<TM> conv_load(const GdnArgs &a, int b, int c, int T) {
-    ConvIn<TM> in;
-    const uint16_t *cs = a.conv_in + ((size_t)b * a.C + c) * (KC - 1);
-    in.h[0] = qs::bf2f(cs[0]);
-    in.h[1] = qs::bf2f(cs[1]);
-    in.h[2] = qs::bf2f(cs[2]);
-    const uint2 tw = *reinterpret_cast<const uint2 *>(a.taps + (size_t)c * KC);
-    in.w[0] = qs::bf_lo(tw.x), in.w[1] = qs::bf_hi(tw.x), in.w[2] = qs::bf_lo(tw.y), in.w[3] = qs::bf_hi(tw.y);
+__device__ __forceinline__ ConvPair<TM> conv_load(const GdnArgs &a, int b, int c, int T) {
+    ConvPair<TM> in;
+    in.h = *reinterpret_cast<const u32x3 *>(a.conv_in + ((size_t)b * a.C + c) * (KC - 1));
+    in.tw = *reinterpret_cast<const uint4 *>(a.taps + (size_t)c * KC);
 #pragma unroll
     for (int t = 0; t < TM; ++t)
-        if (t < T) in.x[t] = a.x[((size_t)b * T + t) * a.C + c];
+        if (t < T) in.x[t] = *reinterpret_cast<const uint32_t *>(a.x + ((size_t)b * T + t) * a.C + c);
     return in;
 }
 
-// Conv1d + SiLU of one channel over T tokens (window oldest first, tap 0 on the oldest input). The tap
+// The 3 + T inputs of channel e (0: c, 1: c + 1) in time order: history, then x_0 .. x_{T-1}.
+template <int TM>
+__device__ __forceinline__ uint32_t conv_seq(const ConvPair<TM> &in, int e, int i) {
+    if (i < 3) {
+        const int k = 3 * e + i;  // half-word index into the 12 history bytes
+        const uint32_t w = k < 2 ? in.h.x : (k < 4 ? in.h.y : in.h.z);
+        return (k & 1) ? w >> 16 : w & 0xffffu;
+    }
+    return e ? in.x[i - 3] >> 16 : in.x[i - 3] & 0xffffu;
+}
+
+// Conv1d + SiLU of the pair over T tokens (window oldest first, tap 0 on the oldest input). The tap
 // products of two bf16 values are exact in fp32, so fused or unfused multiply-adds round identically.
-// Writes the bf16-rounded outputs (as fp32) to y[t * ystride], optionally the per-token conv-state
-// snapshots (verify); leaves the final window in in.h[0..2].
-template <bool SNAP, int TM>
-__device__ __forceinline__ void conv_run(const GdnArgs &a, ConvIn<TM> &in, int b, int c, int T, float *y,
-                                         int ystride, bool write_out) {
-    float *h = in.h;
-    const float *w = in.w;
+// y[e][t] receives the bf16-rounded outputs as fp32, yb[t] their bits packed (c | c + 1 << 16).
+template <int TM>
+__device__ __forceinline__ void conv_run(const ConvPair<TM> &in, int T, float y[2][TM], uint32_t yb[TM]) {
 #pragma unroll
-    for (int t = 0; t < TM; ++t) {
-        if (t >= T) break;
-        const uint32_t xr = in.x[t];
-        const float xt = qs::bf2f(xr);
-        float acc = h[0] * w[0];
-        acc = acc + h[1] * w[1];
-        acc = acc + h[2] * w[2];
-        acc = acc + xt * w[3];
-        const uint32_t yb = qs::f2bf(qs::silu(acc));
-        y[t * ystride] = qs::bf2f(yb);
-        if (write_out && a.y_out) a.y_out[((size_t)b * T + t) * a.C + c] = (uint16_t)yb;
-        h[0] = h[1];
-        h[1] = h[2];
-        h[2] = xt;
-        if (SNAP && write_out) {
-            uint16_t *d = a.conv_out + (((size_t)t * a.B + b) * a.C + c) * (KC - 1);
-            d[0] = (uint16_t)qs::f2bf(h[0]);
-            d[1] = (uint16_t)qs::f2bf(h[1]);
-            d[2] = (uint16_t)xr;
+    for (int t = 0; t < TM; ++t) yb[t] = 0;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const uint32_t tw0 = e ? in.tw.z : in.tw.x, tw1 = e ? in.tw.w : in.tw.y;
+        const float w0 = qs::bf_lo(tw0), w1 = qs::bf_hi(tw0), w2 = qs::bf_lo(tw1), w3 = qs::bf_hi(tw1);
+        float h0 = qs::bf2f(conv_seq(in, e, 0)), h1 = qs::bf2f(conv_seq(in, e, 1)), h2 = qs::bf2f(conv_seq(in, e, 2));
+#pragma unroll
+        for (int t = 0; t < TM; ++t) {
+            if (t >= T) break;
+            const float xt = qs::bf2f(conv_seq(in, e, 3 + t));
+            float acc = h0 * w0;
+            acc = acc + h1 * w1;
+            acc = acc + h2 * w2;
+            acc = acc + xt * w3;
+            const uint32_t r = qs::f2bf(qs::silu(acc));
+            y[e][t] = qs::bf2f(r);
+            yb[t] |= r << (16 * e);
+            h0 = h1;
+            h1 = h2;
+            h2 = xt;
         }
     }
 }
 
-__device__ __forceinline__ void store_conv_state(const GdnArgs &a, int b, int c, const float h[3]) {
-    uint16_t *d = a.conv_out + ((size_t)b * a.C + c) * (KC - 1);
-    d[0] = (uint16_t)qs::f2bf(h[0]);
-    d[1] = (uint16_t)qs::f2bf(h[1]);
-    d[2] = (uint16_t)qs::f2bf(h[2]);
+// The pair's global outputs, issued once the state loads have been consumed: the conv outputs (y_out,
+// when given and write_y) and, with write_state, every token's window (SNAP: verify snapshots, slot t of
+// conv_out) or the final window in place (decode). Windows are runs of the input sequence, all bf16
+// already, so they are copied as bits: window after token t = inputs t + 1 .. t + 3 of each channel.
+template <bool SNAP, int TM>
+__device__ __forceinline__ void conv_commit(const GdnArgs &a, const ConvPair<TM> &in, const uint32_t yb[TM], int b,
+                                            int c, int T, bool write_y, bool write_state) {
+    auto window = [&](int t) {
+        u32x3 w;
+        w.x = conv_seq(in, 0, t + 1) | (conv_seq(in, 0, t + 2) << 16);
+        w.y = conv_seq(in, 0, t + 3) | (conv_seq(in, 1, t + 1) << 16);
+        w.z = conv_seq(in, 1, t + 2) | (conv_seq(in, 1, t + 3) << 16);
+        return w;
+    };
+#pragma unroll
+    for (int t = 0; t < TM; ++t) {
+        if (t >= T) break;
+        if (write_y && a.y_out) *reinterpret_cast<uint32_t *>(a.y_out + ((size_t)b * T + t) * a.C + c) = yb[t];
+        if (SNAP && write_state)
+            *reinterpret_cast<u32x3 *>(a.conv_out + (((size_t)t * a.B + b) * a.C + c) * (KC - 1)) = window(t);
+    }
+    if (!SNAP && write_state)  // decode: T == 1, the window after x_0
+        *reinterpret_cast<u32x3 *>(a.conv_out + ((size_t)b * a.C + c) * (KC - 1)) = window(0);
 }
 
-// Sum of p[0..3] (this thread's 4 columns) over the 32 row groups: lane butterfly over the 8 row groups of
-// the wave (lane bits 3..5), then the 4 waves through LDS in a fixed order.
-__device__ __forceinline__ void reduce_cols(float p[4], float (*red)[SLAB], float out[4], int lane, int w,
-                                            int cg) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        p[j] += qs::dpp<0x128>(p[j]);  // xor 8 (row_ror:8)
-        p[j] += __shfl_xor(p[j], 16, 64);
-        p[j] += __shfl_xor(p[j], 32, 64);
-    }
-    if (lane < 8) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) red[w][lane * 4 + j] = p[j];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int col = cg * 4 + j;
-        out[j] = (red[0][col] + red[1][col]) + (red[2][col] + red[3][col]);
-    }
-}
-
+// One wavefront per slab. The conv runs on all 64 lanes: q channels 2 lane, 2 lane + 1 of key head kh,
+// the same k channels, and the slab's v channels 2 (lane % 16), + 1 (lanes 16..63 compute copies).
+// Memory order: every load is issued first (conv inputs, then the state, then the gates as scalar loads);
+// no global store or atomic is issued before the state loads are consumed, because vmcnt counts loads and
+// stores together and a store in flight would turn each wait for a state load into a wait for everything.
 template <bool CONV, bool VERIFY>
-__global__ __launch_bounds__(THREADS) void gdn_kernel(GdnArgs a) {
+__global__ __launch_bounds__(64) void gdn_kernel(GdnArgs a) {
+    constexpr int TM = VERIFY ? TMAX : 1;
     const int nwg = a.B * a.NV * NSLAB;
     const int lid = qs::xcd_logical(blockIdx.x, nwg);
     const int s = lid % NSLAB;
@@ -132,34 +141,33 @@ __global__ __launch_bounds__(THREADS) void gdn_kernel(GdnArgs a) {
     const int b = lid / (NSLAB * a.NV);
     const int rep = a.NV / a.NK;
     const int kh = h / rep;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int cg = tid & 7, rg = tid >> 3;
+    const int lane = threadIdx.x;
+    const int cg = lane & 7, rg = lane >> 3;
     const int T = VERIFY ? a.T : 1;
     const bool kq_owner = (h % rep == 0) && (s == 0);  // writes the shared q/k channel outputs
 
-    __shared__ float s_qn[TMAX][DK];
-    __shared__ float s_kn[TMAX][DK];
-    __shared__ float s_v[TMAX][SLAB];
-    __shared__ float s_red[2][4][SLAB];
-    __shared__ int s_last;
+    // q / k normalised per token, row r stored at (r % 8) * 16 + r / 8: lane rg reads its 16 rows as 4
+    // contiguous 16-byte pieces
+    __shared__ __align__(16) float s_qn[TM][DK];
+    __shared__ __align__(16) float s_kn[TM][DK];
+    __shared__ __align__(16) float s_v[TM][SLAB];
 
-    // 1. The small conv inputs first, then the state slab: the slab's latency overlaps the prologue.
-    constexpr int TM = VERIFY ? TMAX : 1;
+    // 1. Loads. Conv inputs (raw bits, untouched until used), the state slab, the gates.
     const int qd = a.NK * DK;
-    const bool isq = tid < DK;
-    const int c = isq ? kh * DK + tid : qd + kh * DK + (tid - DK);
-    const int cv = 2 * qd + h * DV + s * SLAB + tid;
-    ConvIn<TM> cq, cvin;
+    const int cq = kh * DK + 2 * lane, ck = qd + cq;                           // q, k channel pairs
+    const int cv = 2 * qd + h * DV + s * SLAB + 2 * (lane & (SLAB / 2 - 1));  // v channel pair
+    ConvPair<TM> inq, ink, inv;
     if (CONV) {
-        cq = conv_load<TM>(a, b, c, T);
-        if (tid < SLAB) cvin = conv_load<TM>(a, b, cv, T);
+        inq = conv_load<TM>(a, b, cq, T);
+        ink = conv_load<TM>(a, b, ck, T);
+        inv = conv_load<TM>(a, b, cv, T);
     }
     const size_t head = (size_t)(b * a.NV + h) * DK * DV;
     const float *sp = a.s_in + head + s * SLAB + cg * 4;
-    f32x4 S[4];  // streamed once per step: nontemporal loads and stores keep it from thrashing L2 / MALL
+    f32x4 S[16];  // streamed once per step: nontemporal loads and stores keep it from thrashing L2 / MALL
 #pragma unroll
-    for (int i = 0; i < 4; ++i) S[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(sp + (size_t)(rg + 32 * i) * DV));
-    // the gates of every token, requested with the rest so no load waits later in the chain
+    for (int i = 0; i < 16; ++i)
+        S[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(sp + (size_t)(rg + 8 * i) * DV));
     float gdec[TM], gbeta[TM];
 #pragma unroll
     for (int t = 0; t < TM; ++t) {
@@ -170,68 +178,86 @@ __global__ __launch_bounds__(THREADS) void gdn_kernel(GdnArgs a) {
         }
     }
 
-    // 2. Prologue: q, k of key head kh and the v slab, for every token.
+    // 2. q, k (rows 2 lane, 2 lane + 1) and the v slab for every token, L2 norms (q times scale).
+    float qv[2][TM], kv[2][TM], vv[2][TM];
+    uint32_t yq[TM], yk[TM], yv[TM];
     if (CONV) {
-        conv_run<VERIFY>(a, cq, b, c, T, isq ? &s_qn[0][tid] : &s_kn[0][tid - DK], DK, kq_owner);
-        if (tid < SLAB) conv_run<VERIFY>(a, cvin, b, cv, T, &s_v[0][tid], SLAB, true);
-        // v channels of this slab are read by this workgroup only: shift them in place now.
-        if (!VERIFY && tid < SLAB) store_conv_state(a, b, cv, cvin.h);
+        conv_run<TM>(inq, T, qv, yq);
+        conv_run<TM>(ink, T, kv, yk);
+        conv_run<TM>(inv, T, vv, yv);
     } else {
-        for (int t = 0; t < T; ++t) {
-            const size_t qk = (((size_t)b * T + t) * a.NK + kh) * DK;
-            if (tid < DK)
-                s_qn[t][tid] = qs::bf2f(a.q[qk + tid]);
-            else
-                s_kn[t][tid - DK] = qs::bf2f(a.k[qk + tid - DK]);
-            if (tid < SLAB) s_v[t][tid] = qs::bf2f(a.v[(((size_t)b * T + t) * a.NV + h) * DV + s * SLAB + tid]);
+#pragma unroll
+        for (int t = 0; t < TM; ++t) {
+            if (t >= T) break;
+            const size_t qk0 = (((size_t)b * T + t) * a.NK + kh) * DK + 2 * lane;
+            const uint32_t q2 = *reinterpret_cast<const uint32_t *>(a.q + qk0);
+            const uint32_t k2 = *reinterpret_cast<const uint32_t *>(a.k + qk0);
+            const uint32_t v2 = *reinterpret_cast<const uint32_t *>(
+                a.v + (((size_t)b * T + t) * a.NV + h) * DV + s * SLAB + 2 * (lane & (SLAB / 2 - 1)));
+            qv[0][t] = qs::bf_lo(q2), qv[1][t] = qs::bf_hi(q2);
+            kv[0][t] = qs::bf_lo(k2), kv[1][t] = qs::bf_hi(k2);
+            vv[0][t] = qs::bf_lo(v2), vv[1][t] = qs::bf_hi(v2);
         }
     }
-    __syncthreads();
-    // q/k conv channels are read by the rep * NSLAB workgroups of key head kh. Each counts itself in after
-    // the barrier above (its reads are consumed); the last to arrive writes the shifted state at the end
-    // and re-arms the counter. The count's return is only waited for at the end.
-    int arrived = 0;
-    if (CONV && !VERIFY && tid == 0) arrived = atomicAdd(a.counters + b * a.NK + kh, 1);
-
-    // 3. L2 norms (q times scale): wave w normalises vectors w, w + 4, ... of (q_0, k_0, q_1, k_1, ...).
-    for (int j = w; j < 2 * T; j += 4) {
-        float *vec = (j & 1) ? s_kn[j >> 1] : s_qn[j >> 1];
-        const float x0 = vec[lane], x1 = vec[lane + 64];
-        const float r = rsqrtf(qs::wave_sum_dpp(x0 * x0 + x1 * x1) + a.eps);
-        const float f = (j & 1) ? 1.0f : a.scale;
-        vec[lane] = x0 * r * f;
-        vec[lane + 64] = x1 * r * f;
+    const int p0 = ((2 * lane) & 7) * 16 + ((2 * lane) >> 3);  // stored position of row 2 lane (+ 16: row + 1)
+#pragma unroll
+    for (int t = 0; t < TM; ++t) {
+        if (t >= T) break;
+        const float rq = rsqrtf(qs::wave_sum_dpp(qv[0][t] * qv[0][t] + qv[1][t] * qv[1][t]) + a.eps) * a.scale;
+        const float rk = rsqrtf(qs::wave_sum_dpp(kv[0][t] * kv[0][t] + kv[1][t] * kv[1][t]) + a.eps);
+        s_qn[t][p0] = qv[0][t] * rq;
+        s_qn[t][p0 + 16] = qv[1][t] * rq;
+        s_kn[t][p0] = kv[0][t] * rk;
+        s_kn[t][p0 + 16] = kv[1][t] * rk;
+        if (lane < SLAB / 2) *reinterpret_cast<float2 *>(&s_v[t][2 * lane]) = make_float2(vv[0][t], vv[1][t]);
     }
-    __syncthreads();
+    __builtin_amdgcn_wave_barrier();
 
-    // 4. Delta rule, token by token, on the slab held in registers.
+    // 3. Delta rule, token by token, on the slab held in registers.
+    int arrived = 0;
     for (int t = 0; t < T; ++t) {
         const int gi = ((b * T) + t) * a.NV + h;
         const float decay = expf(gdec[t]);
         const float bt = gbeta[t];
-        float kn[4], qn[4];
+        float kn[16], qn[16];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            kn[i] = s_kn[t][rg + 32 * i];
-            qn[i] = s_qn[t][rg + 32 * i];
+        for (int i4 = 0; i4 < 4; ++i4) {
+            const float4 k4 = *reinterpret_cast<const float4 *>(&s_kn[t][rg * 16 + 4 * i4]);
+            const float4 q4 = *reinterpret_cast<const float4 *>(&s_qn[t][rg * 16 + 4 * i4]);
+            kn[4 * i4] = k4.x, kn[4 * i4 + 1] = k4.y, kn[4 * i4 + 2] = k4.z, kn[4 * i4 + 3] = k4.w;
+            qn[4 * i4] = q4.x, qn[4 * i4 + 1] = q4.y, qn[4 * i4 + 2] = q4.z, qn[4 * i4 + 3] = q4.w;
         }
+        const float4 v4 = *reinterpret_cast<const float4 *>(&s_v[t][cg * 4]);
         float p[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 16; ++i) {
             const float kd = decay * kn[i];
             p[0] = fmaf(kd, S[i].x, p[0]);
             p[1] = fmaf(kd, S[i].y, p[1]);
             p[2] = fmaf(kd, S[i].z, p[2]);
             p[3] = fmaf(kd, S[i].w, p[3]);
         }
-        float ks[4];
-        reduce_cols(p, s_red[0], ks, lane, w, cg);
-        float dl[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) dl[j] = bt * (s_v[t][cg * 4 + j] - ks[j]);
+        for (int j = 0; j < 4; ++j) {
+            p[j] += qs::dpp<0x128>(p[j]);  // xor 8 (row_ror:8)
+            p[j] += __shfl_xor(p[j], 16, 64);
+            p[j] += __shfl_xor(p[j], 32, 64);
+        }
+        if (CONV && t == 0) {
+            // The state loads are consumed: now the conv's global outputs. v channels of this slab belong
+            // to this workgroup alone (shifted in place / snapshotted here); the q/k channels are read by
+            // the rep * NSLAB workgroups of key head kh, so in decode each counts itself in (its reads
+            // were consumed above) and the last to arrive writes the shifted state at the end and re-arms
+            // the counter. The count's return is waited for only there.
+            conv_commit<VERIFY, TM>(a, inv, yv, b, cv, T, lane < SLAB / 2, lane < SLAB / 2);
+            conv_commit<VERIFY, TM>(a, inq, yq, b, cq, T, kq_owner, VERIFY && kq_owner);
+            conv_commit<VERIFY, TM>(a, ink, yk, b, ck, T, kq_owner, VERIFY && kq_owner);
+            if (!VERIFY && lane == 0) arrived = atomicAdd(a.counters + b * a.NK + kh, 1);
+        }
+        const float dl[4] = {bt * (v4.x - p[0]), bt * (v4.y - p[1]), bt * (v4.z - p[2]), bt * (v4.w - p[3])};
         float po[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 16; ++i) {
             S[i].x = fmaf(kn[i], dl[0], decay * S[i].x);
             S[i].y = fmaf(kn[i], dl[1], decay * S[i].y);
             S[i].z = fmaf(kn[i], dl[2], decay * S[i].z);
@@ -241,27 +267,31 @@ __global__ __launch_bounds__(THREADS) void gdn_kernel(GdnArgs a) {
             po[2] = fmaf(qn[i], S[i].z, po[2]);
             po[3] = fmaf(qn[i], S[i].w, po[3]);
         }
-        float* dst = VERIFY ? a.s_out + (size_t)t * a.B * a.NV * DK * DV + head + s * SLAB + cg * 4
+        float *dst = VERIFY ? a.s_out + (size_t)t * a.B * a.NV * DK * DV + head + s * SLAB + cg * 4
                             : a.s_out + head + s * SLAB + cg * 4;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) __builtin_nontemporal_store(S[i], reinterpret_cast<f32x4 *>(dst + (size_t)(rg + 32 * i) * DV));
-        float ov[4];
-        reduce_cols(po, s_red[1], ov, lane, w, cg);
-        if (tid < 8) {
+        for (int i = 0; i < 16; ++i)
+            __builtin_nontemporal_store(S[i], reinterpret_cast<f32x4 *>(dst + (size_t)(rg + 8 * i) * DV));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            po[j] += qs::dpp<0x128>(po[j]);
+            po[j] += __shfl_xor(po[j], 16, 64);
+            po[j] += __shfl_xor(po[j], 32, 64);
+        }
+        if (lane < 8) {
             uint2 pk;
-            pk.x = qs::pack_bf2(ov[0], ov[1]);
-            pk.y = qs::pack_bf2(ov[2], ov[3]);
+            pk.x = qs::pack_bf2(po[0], po[1]);
+            pk.y = qs::pack_bf2(po[2], po[3]);
             *reinterpret_cast<uint2 *>(a.o + (size_t)gi * DV + s * SLAB + cg * 4) = pk;
         }
     }
     if (CONV && !VERIFY) {
-        if (tid == 0) {
-            const int last = arrived == rep * NSLAB - 1;
-            if (last) atomicExch(a.counters + b * a.NK + kh, 0);
-            s_last = last;
+        const int last = __builtin_amdgcn_readfirstlane(arrived) == rep * NSLAB - 1;
+        if (last) {
+            if (lane == 0) atomicExch(a.counters + b * a.NK + kh, 0);
+            conv_commit<false, TM>(a, inq, yq, b, cq, T, false, true);
+            conv_commit<false, TM>(a, ink, yk, b, ck, T, false, true);
         }
-        __syncthreads();
-        if (s_last) store_conv_state(a, b, c, cq.h);
     }
 }
 
@@ -329,6 +359,19 @@ __global__ __launch_bounds__(256) void rollback_kernel(const float *states_out, 
     if (blockIdx.x == 0 && threadIdx.x == 0 && seq_lens) seq_lens[b] = base_lens[b] + acc;
 }
 
+template <bool CONV, bool VERIFY>
+void launch_gdn(const GdnArgs &a, hipStream_t st) {
+    gdn_kernel<CONV, VERIFY><<<a.B * a.NV * NSLAB, 64, 0, st>>>(a);
+}
+
+// The conv reads channel pairs with 4-, 12- and 16-byte loads.
+int check_conv_alignment(const void *x, const void *conv, const void *conv_out, const void *taps, const void *y_out) {
+    auto al = [](const void *p, uintptr_t n) { return ((uintptr_t)p % n) == 0; };
+    QS_REQUIRE(al(x, 4) && al(conv, 4) && al(conv_out, 4) && al(taps, 16) && al(y_out, 4),
+               "x, conv state and y_out must be 4-byte aligned, taps 16-byte aligned");
+    return QS_OK;
+}
+
 int check_gdn_shapes(int B, int NK, int NV, int DKa, int DVa) {
     QS_REQUIRE(B > 0, "B must be positive (got %d)", B);
     QS_REQUIRE(DKa == DK && DVa == DV, "DK and DV must be 128 (got %d, %d)", DKa, DVa);
@@ -361,11 +404,12 @@ extern "C" int qs_gdn_decode_step(const uint16_t *q, const uint16_t *k, const ui
                                   const float *beta, float *state, uint16_t *o, int B, int NK, int NV, int DKa,
                                   int DVa, float scale, float eps, void *stream) {
     QS_REQUIRE(q && k && v && g && beta && state && o, "qs_gdn_decode_step: null pointer");
+    QS_REQUIRE(((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) % 4 == 0, "qs_gdn_decode_step: q, k, v must be 4-byte aligned");
     if (int e = check_gdn_shapes(B, NK, NV, DKa, DVa)) return e;
     GdnArgs a{};
     a.q = q, a.k = k, a.v = v, a.g = g, a.beta = beta, a.s_in = state, a.s_out = state, a.o = o;
     a.B = B, a.T = 1, a.NK = NK, a.NV = NV, a.C = 2 * NK * DK + NV * DV, a.scale = scale, a.eps = eps;
-    gdn_kernel<false, false><<<B * NV * NSLAB, THREADS, 0, QS_STREAM(stream)>>>(a);
+    launch_gdn<false, false>(a, QS_STREAM(stream));
     return qs::launch_status("qs_gdn_decode_step");
 }
 
@@ -379,12 +423,13 @@ extern "C" int qs_gdn_decode_fused(const uint16_t *x, uint16_t *conv_state, cons
                "qs_gdn_decode_fused: null pointer");
     if (int e = check_gdn_shapes(B, NK, NV, DKa, DVa)) return e;
     QS_REQUIRE(K == KC, "qs_gdn_decode_fused: only K = 4 taps are supported (got %d)", K);
+    if (int e = check_conv_alignment(x, conv_state, conv_state, taps, y_out)) return e;
     GdnArgs a{};
     a.x = x, a.conv_in = conv_state, a.conv_out = conv_state, a.taps = taps, a.y_out = y_out;
     a.g = g, a.beta = beta, a.s_in = state, a.s_out = state, a.o = o;
     a.counters = static_cast<int *>(workspace);
     a.B = B, a.T = 1, a.NK = NK, a.NV = NV, a.C = 2 * NK * DK + NV * DV, a.scale = scale, a.eps = eps;
-    gdn_kernel<true, false><<<B * NV * NSLAB, THREADS, 0, QS_STREAM(stream)>>>(a);
+    launch_gdn<true, false>(a, QS_STREAM(stream));
     return qs::launch_status("qs_gdn_decode_fused");
 }
 
@@ -397,12 +442,13 @@ extern "C" int qs_gdn_verify_step(const uint16_t *x, const uint16_t *conv_state_
     if (int e = check_gdn_shapes(B, NK, NV, DKa, DVa)) return e;
     QS_REQUIRE(T >= 1 && T <= TMAX, "qs_gdn_verify_step: T must be in [1, %d] (got %d)", TMAX, T);
     QS_REQUIRE(K == KC, "qs_gdn_verify_step: only K = 4 taps are supported (got %d)", K);
+    if (int e = check_conv_alignment(x, conv_state_in, conv_states_out, taps, y_out)) return e;
     QS_REQUIRE(states_out != state_in, "qs_gdn_verify_step: states_out must not alias state_in");
     GdnArgs a{};
     a.x = x, a.conv_in = conv_state_in, a.conv_out = conv_states_out, a.taps = taps, a.y_out = y_out;
     a.g = g, a.beta = beta, a.s_in = state_in, a.s_out = states_out, a.o = o;
     a.B = B, a.T = T, a.NK = NK, a.NV = NV, a.C = 2 * NK * DK + NV * DV, a.scale = scale, a.eps = eps;
-    gdn_kernel<true, true><<<B * NV * NSLAB, THREADS, 0, QS_STREAM(stream)>>>(a);
+    launch_gdn<true, true>(a, QS_STREAM(stream));
     return qs::launch_status("qs_gdn_verify_step");
 }
 

@@ -40,7 +40,12 @@ FLAGS = [
 ]
 # Per-source additions. Attention: its wave max reductions never see a NaN (masked scores are -inf), and
 # without NaN semantics each max folds its DPP operand instead of quieting both inputs first.
-FILE_FLAGS = {"paged_attention.hip": ["-fno-honor-nans"]}
+# GDN decode: its conv counter is bumped by one lane and the count is read at the very end; without the
+# atomic optimizer the compiler waits for the count only where it is read, not right after the add.
+FILE_FLAGS = {
+    "paged_attention.hip": ["-fno-honor-nans"],
+    "gdn_decode.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
+}
 
 
 def sources():
