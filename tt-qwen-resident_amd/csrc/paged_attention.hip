@@ -9,15 +9,15 @@
 //           (v_dot2_f32_bf16) against q broadcast from LDS, 2-step lane butterfly
 //   softmax online per wave over its 16 rows (wave max / sum), probabilities rounded to bf16
 //   P V     4 head dims per lane (one 512-byte V row per load instruction), two rows per v_dot2
-// Pages before the one holding the step's first new row load through a buffer descriptor based at the
-// page's head tile (scalar address work only); for one query token three page buffers rotate so the next
-// page's K and V are in flight while a page is computed.
+// Pages load through a buffer descriptor based at the page's head tile (scalar address work only); for one
+// query token three page buffers rotate so the next page's K and V are in flight while a page is computed.
+// The new rows are appended first, so every row is read from the pool.
 // The waves are merged in LDS; the splits' partials (m, l, unnormalised o per query head) go to the
 // workspace and a second small kernel merges them in split order (the leader side of the reference:
 // global max, rescale, sum, normalise, kernels/attn_leader_writer.cpp:86-106 and
 // kernels/attn_leader_compute.cpp:42-79), so results are identical run to run. The merge is a separate
-// launch because an in-kernel last-arriver merge needs agent-scope release fences, and on this multi-XCD
-// part each such fence writes back the whole L2 (it cost 35-50 us per launch at 256 workgroups).
+// launch: a merge by the last split to finish runs serially in one workgroup and measured slower, and an
+// in-kernel fan-in through release / acquire fences writes back and invalidates the whole L2 of each XCD.
 #include "qs_common.h"
 
 namespace {
@@ -89,10 +89,6 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     const int p0 = split * a.pps;
     const int p1 = min(npages, p0 + a.pps);
     const int *bt = a.block_table + (size_t)b * a.max_blocks;
-    auto page_of = [&](int pi) {
-        const int pg = bt[pi];
-        return (pg >= 0 && pg < a.num_blocks) ? pg : -1;
-    };
     // The split's block-table entries (at most 64), one per lane, read once up front: the page walk takes
     // each page index with a readlane and never waits on a table read (a wait for one load would also
     // wait for the K/V loads in flight).
@@ -102,31 +98,57 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         return (pg >= 0 && pg < a.num_blocks) ? pg : -1;
     };
 
-    // Fused append: the new rows that fall in this split's pages go into the pools. Attention below reads
-    // those rows from k_new / v_new, never from the pool, so there is no write-read hazard.
-    if (a.k_new) {
+    // Fused append, first: the new rows that fall in this split's pages go into the pools, and the stores
+    // complete before the barrier that precedes the page walk, so the walk reads every row - new ones
+    // included - from the pool. No other workgroup reads these pages.
+    if (a.k_new && p0 <= (n - 1) / BLK && base / BLK < p1) {
         for (int idx = tid; idx < T * 64; idx += 256) {
             const int t = idx >> 6, kv = (idx >> 5) & 1, ch = idx & 31;
             const int pos = base + t, pi = pos / BLK;
             if (pi < p0 || pi >= p1) continue;
-            const int pg = page_of(pi);
-            if (pg < 0) continue;
+            const int pg = bt[pi];  // per thread: the new rows may straddle two pages
+            if (pg < 0 || pg >= a.num_blocks) continue;
             const size_t dst = (((size_t)pg * a.NKV + g) * BLK + (pos % BLK)) * HD + ch * 8;
             const size_t src = (((size_t)b * T + t) * a.NKV + g) * HD + ch * 8;
             const uint16_t *s = kv ? a.v_new : a.k_new;
             uint16_t *d = kv ? a.v_cache : a.k_cache;
             *reinterpret_cast<uint4 *>(d + dst) = *reinterpret_cast<const uint4 *>(s + src);
         }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
 
     const int kq = lane & 3;               // K: this lane's 16-byte piece of each 64-byte run of the row
     const int krw = 16 * w + (lane >> 2);  // K: row of the page this lane scores
     const size_t pstride = (size_t)a.NKV * BLK * HD;  // elements per page
-    const size_t koff = ((size_t)g * BLK + krw) * HD + kq * 8;
-    const size_t voff = ((size_t)g * BLK + 16 * w) * HD + lane * 4;
-    const float sl2 = a.scale * 1.4426950408889634f;
-    const int kvo = krw * HD * 2 + kq * 16;
-    const int vvo = 16 * w * HD * 2 + lane * 8;  // scores in the log2 domain: p = 2^(s scale log2e - m)
+    const float sl2 = a.scale * 1.4426950408889634f;  // scores in the log2 domain: p = 2^(s scale log2e - m)
+    const int kvo = krw * HD * 2 + kq * 16;           // bytes: this lane's K piece in a head tile
+    const int vvo = 16 * w * HD * 2 + lane * 8;       // bytes: this lane's V dims in the wave's first row
+
+    // Page loads through a buffer descriptor based at the page's head tile (the per-page address work is
+    // scalar). A K buffer holds the wave's 16 K rows (4 lanes per row, 8 x 16 bytes per lane); a V buffer
+    // its 16 V rows, 4 dims per lane, rows 2 j and 2 j + 1 in entry j (.xy, .zw). Loads only issue here.
+    auto load_k = [&](int pg, uint4 (&kb)[8]) {
+        const auto rk = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t *>(a.k_cache + (size_t)pg * pstride + (size_t)g * BLK * HD), (short)0, BLK * HD * 2,
+            0x00020000);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, kvo, i * 64, 0);
+            kb[i] = make_uint4(x[0], x[1], x[2], x[3]);
+        }
+    };
+    auto load_v = [&](int pg, uint4 (&vb)[8]) {
+        const auto rv = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t *>(a.v_cache + (size_t)pg * pstride + (size_t)g * BLK * HD), (short)0, BLK * HD * 2,
+            0x00020000);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const u32x2 x0 = __builtin_amdgcn_raw_buffer_load_b64(rv, vvo, (2 * j) * HD * 2, 0);
+            const u32x2 x1 = __builtin_amdgcn_raw_buffer_load_b64(rv, vvo, (2 * j + 1) * HD * 2, 0);
+            vb[j] = make_uint4(x0[0], x0[1], x1[0], x1[1]);
+        }
+    };
+
     for (int tg = 0; tg < T; tg += TT) {
         const int nt = min(TT, T - tg);
         const int vend = base + tg + nt;  // rows at or past vend are invalid for every token of the group
@@ -141,8 +163,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         }
         __syncthreads();
 
-        // m: running max (log2 domain, wave-uniform); lp: this lane's share of the running sum (one lane per
-        // row counts), reduced over the wave once per split
+        // m: running max (log2 domain, wave-uniform); lp: every lane adds its row's rounded probability (so
+        // the wave sum is 4x the row sum), reduced over the wave once per split
         float m[TT][G], lp[TT][G], acc[TT][G][4];
 #pragma unroll
         for (int tt = 0; tt < TT; ++tt)
@@ -166,11 +188,10 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         };
         // scores of page pi for token tg + tt, online softmax update, probabilities to s_pp
         auto scores_tt = [&](int pi, int tt, const uint4 (&kv)[8]) {
-            const int P = pi * BLK + 16 * w + (lane >> 2);
-            const int valid = base + tg + tt + 1;  // token tg + tt sees positions 0 .. valid - 1
-            const bool okr = P < valid;
-            // ---- scores of this lane's row over its 64 dims, then across the row's 4 lanes (the q
-            // reads of the 4 lanes are 64 contiguous bytes: conflict-free)
+            const int P = pi * BLK + krw;
+            const bool okr = P < base + tg + tt + 1;  // token tg + tt sees positions 0 .. base + tg + tt
+            // this lane's row over its 64 dims, then across the row's 4 lanes (the q reads of the 4 lanes
+            // are 64 contiguous bytes; all 16 rows read the same q)
             float sc[G];
 #pragma unroll
             for (int h = 0; h < G; ++h) sc[h] = 0.f;
@@ -192,15 +213,15 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                 sc[h] += qs::dpp<0xB1>(sc[h]);
                 sc[h] += qs::dpp<0x4E>(sc[h]);
             }
-            // ---- online softmax over the wave's 16 rows (log2 domain); probabilities rounded to bf16
-            // (the running sum adds the rounded values, so the normalisation matches what P V uses) and
-            // packed two rows per dword for P V
+            // online softmax over the wave's 16 rows (log2 domain; the max is taken on the raw scores, the
+            // scale being positive); probabilities rounded to bf16 (the running sum adds the rounded values,
+            // so the normalisation matches what P V uses) and packed two rows per dword for P V
 #pragma unroll
             for (int h = 0; h < G; ++h) {
                 const float mn = fmaxf(m[tt][h], qs::wave_max_bcast(okr ? sc[h] : -INFINITY) * sl2);
                 const float e = okr ? __builtin_amdgcn_exp2f(fmaf(sc[h], sl2, -mn)) : 0.f;
                 const uint32_t pk = qs::cvt_pk_bf16(e, qs::dpp<0x104>(e));  // this row | the next row
-                if (mn != m[tt][h]) {
+                if (mn != m[tt][h]) {  // wave-uniform: rescale only when the running max moved
                     const float alpha = m[tt][h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[tt][h] - mn);
                     lp[tt][h] *= alpha;
                     acc[tt][h][0] *= alpha;
@@ -214,9 +235,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             }
             __builtin_amdgcn_wave_barrier();
         };
-        // P V of the page for token tg + tt
+        // P V of the page for token tg + tt: two rows per v_dot2 (interleaved with v_perm)
         auto pv_tt = [&](int tt, const uint4 (&vb)[8]) {
-            // ---- P V over the wave's 16 rows: two rows per v_dot2 (interleaved with v_perm)
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const uint32_t x0 = __builtin_amdgcn_perm(vb[j].z, vb[j].x, 0x05040100u);
@@ -239,105 +259,49 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             }
             __builtin_amdgcn_wave_barrier();
         };
-        auto load_k_plain = [&](int pg, uint4 (&kb)[8]) {
-            const auto rk = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<uint16_t *>(a.k_cache + (size_t)pg * pstride + (size_t)g * BLK * HD), (short)0, BLK * HD * 2, 0x00020000);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, kvo, i * 64, 0);
-                kb[i] = make_uint4(x[0], x[1], x[2], x[3]);
-            }
-        };
-        auto load_v_plain = [&](int pg, uint4 (&vb)[8]) {
-            const auto rv = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<uint16_t *>(a.v_cache + (size_t)pg * pstride + (size_t)g * BLK * HD), (short)0, BLK * HD * 2, 0x00020000);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const u32x2 x0 = __builtin_amdgcn_raw_buffer_load_b64(rv, vvo, (2 * j) * HD * 2, 0);
-                const u32x2 x1 = __builtin_amdgcn_raw_buffer_load_b64(rv, vvo, (2 * j + 1) * HD * 2, 0);
-                vb[j] = make_uint4(x0[0], x0[1], x1[0], x1[1]);
-            }
-        };
-        int pstart = p0;
+
         if constexpr (TT == 1) {
-            // pages before the one holding the step's first new row: two in flight (page pi + 1 loads while
-            // page pi is computed)
-            const int pp = max(p0, min(pe, base / BLK));
             // Three page buffers rotate through the roles K(pi), V(pi) and K(pi + 1) in flight: after the
-            // scores of page pi its K buffer takes V(pi + 1), after its P V its V buffer takes K(pi + 2)
+            // scores of page pi its K buffer takes V(pi + 1), after its P V its V buffer takes K(pi + 2), so
+            // each load has about a page of compute to arrive in.
             uint4 X[8], Y[8], Z[8];
             auto step = [&](int pi, uint4 (&kb)[8], uint4 (&vb)[8]) {
                 const bool ok = page_at(pi) >= 0;
                 if (ok) scores_tt(pi, 0, kb);
-                if (pi + 1 < pp && page_at(pi + 1) >= 0) load_v_plain(page_at(pi + 1), kb);
-                if (ok) pv_tt(0, vb);
-                if (pi + 2 < pp && page_at(pi + 2) >= 0) load_k_plain(page_at(pi + 2), vb);
+                if (pi + 1 < pe && page_at(pi + 1) >= 0) load_v(page_at(pi + 1), kb);
+                if (ok) {
+                    mask_v(pi, vb);
+                    pv_tt(0, vb);
+                }
+                if (pi + 2 < pe && page_at(pi + 2) >= 0) load_k(page_at(pi + 2), vb);
             };
-            if (p0 < pp && page_at(p0) >= 0) {
-                load_k_plain(page_at(p0), X);
-                load_v_plain(page_at(p0), Y);
+            if (p0 < pe && page_at(p0) >= 0) {
+                load_k(page_at(p0), X);
+                load_v(page_at(p0), Y);
             }
-            if (p0 + 1 < pp && page_at(p0 + 1) >= 0) load_k_plain(page_at(p0 + 1), Z);
-            for (int pi = p0; pi < pp; pi += 3) {
-                step(pi, X, Y);
-                if (pi + 1 >= pp) break;
-                step(pi + 1, Z, X);
-                if (pi + 2 >= pp) break;
-                step(pi + 2, Y, Z);
+            if (p0 + 1 < pe && page_at(p0 + 1) >= 0) load_k(page_at(p0 + 1), Z);
+            for (int pi = p0; pi < pe; pi += 3) {
+                step(pi, X, Y);  // loads V(pi + 1) -> X, K(pi + 2) -> Y
+                if (pi + 1 >= pe) break;
+                step(pi + 1, Z, X);  // loads V(pi + 2) -> Z, K(pi + 3) -> X
+                if (pi + 2 >= pe) break;
+                step(pi + 2, Y, Z);  // loads V(pi + 3) -> Y, K(pi + 4) -> Z
             }
-            pstart = pp;
-        }
-        for (int pi = pstart; pi < pe; ++pi) {
-            const int pg = page_at(pi);
-            if (pg < 0) continue;
-            const int rbase = pi * BLK + 16 * w;  // position of the wave's first row
-            const int P = rbase + (lane >> 2);    // position of this lane's K row
-            // rows of the step's new tokens come from the inputs (only the last page can hold any); every
-            // other row, valid or not, from the page, which is always in bounds (invalid rows masked after)
-            const bool fresh = a.k_new && rbase + 15 >= base;
-            const uint16_t *kp = a.k_cache + (size_t)pg * pstride + koff;
-            if (fresh && P >= base && P < n) kp = a.k_new + (((size_t)b * T + (P - base)) * a.NKV + g) * HD + kq * 8;
-            // load i: the row's 4 lanes read 64 contiguous bytes (dims 32 i + 8 kq .. + 7), so each load
-            // instruction touches 16 half-lines and two consecutive loads complete them
-            uint4 kv[8];
-            uint2 vv[16];
-            const uint16_t *vp = a.v_cache + (size_t)pg * pstride + voff;
-            if (!fresh) {
-                const auto rk = __builtin_amdgcn_make_buffer_rsrc(
-                    const_cast<uint16_t *>(a.k_cache + (size_t)pg * pstride + (size_t)g * BLK * HD), (short)0, BLK * HD * 2, 0x00020000);
-                const auto rv = __builtin_amdgcn_make_buffer_rsrc(
-                    const_cast<uint16_t *>(a.v_cache + (size_t)pg * pstride + (size_t)g * BLK * HD), (short)0, BLK * HD * 2, 0x00020000);
+        } else {
+            // verify rows: the accumulators of TT tokens leave no registers for pages in flight
+            for (int pi = p0; pi < pe; ++pi) {
+                const int pg = page_at(pi);
+                if (pg < 0) continue;
+                uint4 X[8], Y[8];
+                load_k(pg, X);
+                load_v(pg, Y);
+                mask_v(pi, Y);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, kvo, i * 64, 0);
-                    kv[i] = make_uint4(x[0], x[1], x[2], x[3]);
+                for (int tt = 0; tt < TT; ++tt) {
+                    if (tt >= nt) break;
+                    scores_tt(pi, tt, X);
+                    pv_tt(tt, Y);
                 }
-#pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rv, vvo, j * HD * 2, 0);
-                    vv[j] = make_uint2(x[0], x[1]);
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) kv[i] = reinterpret_cast<const uint4 *>(kp)[i * 4];
-#pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    const int Pj = rbase + j;
-                    const uint16_t *src = (Pj >= base && Pj < n)
-                                              ? a.v_new + (((size_t)b * T + (Pj - base)) * a.NKV + g) * HD + lane * 4
-                                              : vp + j * HD;
-                    vv[j] = *reinterpret_cast<const uint2 *>(src);
-                }
-            }
-            uint4 vb[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) vb[j] = make_uint4(vv[2 * j].x, vv[2 * j].y, vv[2 * j + 1].x, vv[2 * j + 1].y);
-            mask_v(pi, vb);
-#pragma unroll
-            for (int tt = 0; tt < TT; ++tt) {
-                if (tt >= nt) break;
-                scores_tt(pi, tt, kv);
-                pv_tt(tt, vb);
             }
         }
 
