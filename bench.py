@@ -63,21 +63,29 @@ def graph_time(torch, fn, steps, warmup):
     return e0.elapsed_time(e1) / steps, g
 
 
-def kernel_time(torch, calls, reps):
-    """Average ms of one launch: HIP events around reps x len(calls) back-to-back C-ABI launches (pre-built
-    argument tuples, no Python checks in the loop) on the current stream."""
+def kernel_time(torch, make_calls, reps):
+    """Average ms of one launch: reps x len(calls) back-to-back C-ABI launches (pre-built argument tuples)
+    captured into a HIP graph on a side stream, replayed once untimed and once between HIP events, so no
+    host work sits between the launches. make_calls(stream) returns the (entry point, args) list."""
     from qwen36_state._lib import lib
 
     L = lib()
-    fns = [(getattr(L, name), args) for name, args in calls]
-    for f, a in fns:
-        assert f(*a) == 0, L.qs_last_error()
+    s = torch.cuda.Stream()
+    fns = [(getattr(L, name), args) for name, args in make_calls(ctypes.c_void_p(s.cuda_stream))]
+    with torch.cuda.stream(s):
+        for f, a in fns:
+            assert f(*a) == 0, L.qs_last_error()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for _ in range(reps):
+            for f, a in fns:
+                f(*a)
+    g.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(reps):
-        for f, a in fns:
-            f(*a)
+    g.replay()
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / (reps * len(fns))
@@ -140,11 +148,10 @@ def bench_step(args, torch):
     ms, _ = graph_time(torch, step.step, args.steps, args.warmup)
     nbytes = step.bytes_per_step()
     log(f"step: {ms * 1e3:.1f} µs, {nbytes / ms / 1e6:.0f} GB/s")
-    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    t_gdn = kernel_time(torch, [gdn_call(step.layer[l], step.B, step.gdn_ws, st, step.layer[l]["o"]) for l in gl],
-                        args.kernel_reps)  # fmt: skip
-    t_att = kernel_time(torch, [attn_call(step.layer[l], step.B, 1, step.pps, step.attn_ws, st, step.layer[l]["o"])
-                                for l in al], args.kernel_reps)  # fmt: skip
+    t_gdn = kernel_time(torch, lambda st: [gdn_call(step.layer[l], step.B, step.gdn_ws, st, step.layer[l]["o"])
+                                           for l in gl], args.kernel_reps)  # fmt: skip
+    t_att = kernel_time(torch, lambda st: [attn_call(step.layer[l], step.B, 1, step.pps, step.attn_ws, st,
+                                                     step.layer[l]["o"]) for l in al], args.kernel_reps)  # fmt: skip
     b_gdn, b_att = layer_bytes(args.batch, args.ctx), layer_bytes(args.batch, args.ctx, attn=True)
     kern = {"gdn_decode_fused": (t_gdn, b_gdn, len(gl)), "paged_gqa_decode": (t_att, b_att, len(al))}
     for k, (t, b, n) in kern.items():
@@ -171,8 +178,7 @@ def bench_gdn_layer(args, torch):
     layers = [W.gdn_layer(1, "cuda:0", seed=i) for i in range(48)]
     outs = [torch.empty(1, 48, 128, dtype=torch.bfloat16, device="cuda:0") for _ in layers]
     ws = ops.workspace("bench-gdn", ops.lib().qs_gdn_workspace_bytes(1, 16), "cuda:0")
-    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    ms = kernel_time(torch, [gdn_call(d, 1, ws, st, o) for d, o in zip(layers, outs)], args.kernel_reps)
+    ms = kernel_time(torch, lambda st: [gdn_call(d, 1, ws, st, o) for d, o in zip(layers, outs)], args.kernel_reps)
     nbytes = layer_bytes(1, 0)
     return line(args, "one GDN layer decode, batch 1: conv1d update (10240 channels) + L2-norm + gated delta "
                 "rule on fp32 [1, 48, 128, 128]", nbytes, ms, roofline("gdn_decode_fused", nbytes, ms))
@@ -188,9 +194,8 @@ def bench_attn_layer(args, torch):
     layers = [W.attn_layer(1, 32768, "cuda:0", seed=i) for i in range(4)]
     outs = [torch.empty(1, 1, 24, 256, dtype=torch.bfloat16, device="cuda:0") for _ in layers]
     ws = ops.attention_workspace(1, 1, 24, 4, 512, pps, "cuda:0")
-    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    calls = [attn_call(d, 1, 1, pps, ws, st, o) for d, o in zip(layers, outs)]
-    ms = kernel_time(torch, calls, args.kernel_reps)
+    ms = kernel_time(torch, lambda st: [attn_call(d, 1, 1, pps, ws, st, o) for d, o in zip(layers, outs)],
+                     args.kernel_reps)  # fmt: skip
     nbytes = layer_bytes(1, 32768, attn=True)
     return line(args, f"one attention layer decode, batch 1, 32768 positions: append + paged GQA (24/4 heads x "
                 f"256, block 64, 512 random pages of 2048), split {pps} pages + merge", nbytes, ms,
