@@ -4,11 +4,11 @@
 // Decomposition of the delta rule. For value column v the step is column-separable:
 //     delta_v = beta (v_v - e^g sum_k k_k S_kv),  S'_kv = e^g S_kv + k_k delta_v,  o_v = sum_k q_k S'_kv
 // so one wavefront owns a 128 x 32 slab S[:, 32 s .. 32 s + 31] of one (user, value head): 4 slabs per head,
-// B * NV * 4 single-wave workgroups. Lane (rg = lane / 8, cg = lane % 8) holds rows rg + 8 i (i < 16),
-// columns 4 cg .. 4 cg + 3 of the slab in 64 VGPRs; each dwordx4 load or store instruction covers 8 full
-// 128-byte rows. The k-reductions (S^T k and S'^T q) sum a lane's 16 rows in registers, then the 8 row
-// groups (lane bits 3..5) with one DPP step and two lane swaps in a fixed order (bit-reproducible run to
-// run), so no step needs a workgroup barrier. The state is read once and written once per token.
+// B * NV * 4 single-wave workgroups. Lane (rg = lane / 8, cg = lane % 8) holds rows rg + 8 i (i < 16), columns 4 cg .. 4 cg + 3 of the
+// slab in 64 VGPRs; each dwordx4 load or store instruction covers 8 full 128-byte rows. The k-reductions
+// (S^T k and S'^T q) sum a lane's rows in registers, then the row groups (lane bits 3..5) with one DPP step
+// and two lane swaps in a fixed order (bit-reproducible run to run), so no step needs a workgroup barrier.
+// The state is read once and written once per token.
 #include "qs_common.h"
 
 namespace {
@@ -16,8 +16,6 @@ namespace {
 constexpr int DK = 128;
 constexpr int DV = 128;
 constexpr int KC = 4;  // conv taps
-constexpr int SLAB = 32;
-constexpr int NSLAB = DV / SLAB;
 constexpr int TMAX = 8;
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
@@ -131,9 +129,24 @@ __device__ __forceinline__ void conv_commit(const GdnArgs &a, const ConvPair<TM>
 // Memory order: every load is issued first (conv inputs, then the state, then the gates as scalar loads);
 // no global store or atomic is issued before the state loads are consumed, because vmcnt counts loads and
 // stores together and a store in flight would turn each wait for a state load into a wait for everything.
-template <bool CONV, bool VERIFY>
+// Sum over the row groups of a slab wave (lane bits log2(CG) .. 5) as a butterfly in a fixed order: every
+// lane ends with bit-identical sums of its column group.
+template <int CG>
+__device__ __forceinline__ float sum_row_groups(float x) {
+    if (CG == 4) x += __shfl_xor(x, 4, 64);
+    x += qs::dpp<0x128>(x);  // xor 8 (row_ror:8)
+    x += __shfl_xor(x, 16, 64);
+    x += __shfl_xor(x, 32, 64);
+    return x;
+}
+
+template <bool CONV, bool VERIFY, int SLAB>
 __global__ __launch_bounds__(64) void gdn_kernel(GdnArgs a) {
     constexpr int TM = VERIFY ? TMAX : 1;
+    constexpr int NSLAB = DV / SLAB;
+    constexpr int CG = SLAB / 4;   // column groups of 4 (lane % CG)
+    constexpr int RG = 64 / CG;    // row groups (lane / CG): lane holds rows rg + RG i
+    constexpr int RPL = DK / RG;   // rows per lane
     const int nwg = a.B * a.NV * NSLAB;
     const int lid = qs::xcd_logical(blockIdx.x, nwg);
     const int s = lid % NSLAB;
@@ -142,11 +155,11 @@ __global__ __launch_bounds__(64) void gdn_kernel(GdnArgs a) {
     const int rep = a.NV / a.NK;
     const int kh = h / rep;
     const int lane = threadIdx.x;
-    const int cg = lane & 7, rg = lane >> 3;
+    const int cg = lane % CG, rg = lane / CG;
     const int T = VERIFY ? a.T : 1;
     const bool kq_owner = (h % rep == 0) && (s == 0);  // writes the shared q/k channel outputs
 
-    // q / k normalised per token, row r stored at (r % 8) * 16 + r / 8: lane rg reads its 16 rows as 4
+    // q / k normalised per token, row r stored at (r % RG) * RPL + r / RG: lane rg reads its RPL rows as
     // contiguous 16-byte pieces
     __shared__ __align__(16) float s_qn[TM][DK];
     __shared__ __align__(16) float s_kn[TM][DK];
@@ -164,10 +177,10 @@ __global__ __launch_bounds__(64) void gdn_kernel(GdnArgs a) {
     }
     const size_t head = (size_t)(b * a.NV + h) * DK * DV;
     const float *sp = a.s_in + head + s * SLAB + cg * 4;
-    f32x4 S[16];  // streamed once per step: nontemporal loads and stores keep it from thrashing L2 / MALL
+    f32x4 S[RPL];  // streamed once per step: nontemporal loads and stores keep it from thrashing L2 / MALL
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
-        S[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(sp + (size_t)(rg + 8 * i) * DV));
+    for (int i = 0; i < RPL; ++i)
+        S[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(sp + (size_t)(rg + RG * i) * DV));
     float gdec[TM], gbeta[TM];
 #pragma unroll
     for (int t = 0; t < TM; ++t) {
@@ -199,16 +212,16 @@ __global__ __launch_bounds__(64) void gdn_kernel(GdnArgs a) {
             vv[0][t] = qs::bf_lo(v2), vv[1][t] = qs::bf_hi(v2);
         }
     }
-    const int p0 = ((2 * lane) & 7) * 16 + ((2 * lane) >> 3);  // stored position of row 2 lane (+ 16: row + 1)
+    const int p0 = ((2 * lane) % RG) * RPL + (2 * lane) / RG;  // stored position of row 2 lane (+ RPL: row + 1)
 #pragma unroll
     for (int t = 0; t < TM; ++t) {
         if (t >= T) break;
         const float rq = rsqrtf(qs::wave_sum_dpp(qv[0][t] * qv[0][t] + qv[1][t] * qv[1][t]) + a.eps) * a.scale;
         const float rk = rsqrtf(qs::wave_sum_dpp(kv[0][t] * kv[0][t] + kv[1][t] * kv[1][t]) + a.eps);
         s_qn[t][p0] = qv[0][t] * rq;
-        s_qn[t][p0 + 16] = qv[1][t] * rq;
+        s_qn[t][p0 + RPL] = qv[1][t] * rq;
         s_kn[t][p0] = kv[0][t] * rk;
-        s_kn[t][p0 + 16] = kv[1][t] * rk;
+        s_kn[t][p0 + RPL] = kv[1][t] * rk;
         if (lane < SLAB / 2) *reinterpret_cast<float2 *>(&s_v[t][2 * lane]) = make_float2(vv[0][t], vv[1][t]);
     }
     __builtin_amdgcn_wave_barrier();
@@ -219,18 +232,18 @@ __global__ __launch_bounds__(64) void gdn_kernel(GdnArgs a) {
         const int gi = ((b * T) + t) * a.NV + h;
         const float decay = expf(gdec[t]);
         const float bt = gbeta[t];
-        float kn[16], qn[16];
+        float kn[RPL], qn[RPL];
 #pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) {
-            const float4 k4 = *reinterpret_cast<const float4 *>(&s_kn[t][rg * 16 + 4 * i4]);
-            const float4 q4 = *reinterpret_cast<const float4 *>(&s_qn[t][rg * 16 + 4 * i4]);
+        for (int i4 = 0; i4 < RPL / 4; ++i4) {
+            const float4 k4 = *reinterpret_cast<const float4 *>(&s_kn[t][rg * RPL + 4 * i4]);
+            const float4 q4 = *reinterpret_cast<const float4 *>(&s_qn[t][rg * RPL + 4 * i4]);
             kn[4 * i4] = k4.x, kn[4 * i4 + 1] = k4.y, kn[4 * i4 + 2] = k4.z, kn[4 * i4 + 3] = k4.w;
             qn[4 * i4] = q4.x, qn[4 * i4 + 1] = q4.y, qn[4 * i4 + 2] = q4.z, qn[4 * i4 + 3] = q4.w;
         }
         const float4 v4 = *reinterpret_cast<const float4 *>(&s_v[t][cg * 4]);
         float p[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
+        for (int i = 0; i < RPL; ++i) {
             const float kd = decay * kn[i];
             p[0] = fmaf(kd, S[i].x, p[0]);
             p[1] = fmaf(kd, S[i].y, p[1]);
@@ -238,11 +251,7 @@ __global__ __launch_bounds__(64) void gdn_kernel(GdnArgs a) {
             p[3] = fmaf(kd, S[i].w, p[3]);
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            p[j] += qs::dpp<0x128>(p[j]);  // xor 8 (row_ror:8)
-            p[j] += __shfl_xor(p[j], 16, 64);
-            p[j] += __shfl_xor(p[j], 32, 64);
-        }
+        for (int j = 0; j < 4; ++j) p[j] = sum_row_groups<CG>(p[j]);
         if (CONV && t == 0) {
             // The state loads are consumed: now the conv's global outputs. v channels of this slab belong
             // to this workgroup alone (shifted in place / snapshotted here); the q/k channels are read by
@@ -257,7 +266,7 @@ __global__ __launch_bounds__(64) void gdn_kernel(GdnArgs a) {
         const float dl[4] = {bt * (v4.x - p[0]), bt * (v4.y - p[1]), bt * (v4.z - p[2]), bt * (v4.w - p[3])};
         float po[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
+        for (int i = 0; i < RPL; ++i) {
             S[i].x = fmaf(kn[i], dl[0], decay * S[i].x);
             S[i].y = fmaf(kn[i], dl[1], decay * S[i].y);
             S[i].z = fmaf(kn[i], dl[2], decay * S[i].z);
@@ -270,15 +279,11 @@ __global__ __launch_bounds__(64) void gdn_kernel(GdnArgs a) {
         float *dst = VERIFY ? a.s_out + (size_t)t * a.B * a.NV * DK * DV + head + s * SLAB + cg * 4
                             : a.s_out + head + s * SLAB + cg * 4;
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-            __builtin_nontemporal_store(S[i], reinterpret_cast<f32x4 *>(dst + (size_t)(rg + 8 * i) * DV));
+        for (int i = 0; i < RPL; ++i)
+            __builtin_nontemporal_store(S[i], reinterpret_cast<f32x4 *>(dst + (size_t)(rg + RG * i) * DV));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            po[j] += qs::dpp<0x128>(po[j]);
-            po[j] += __shfl_xor(po[j], 16, 64);
-            po[j] += __shfl_xor(po[j], 32, 64);
-        }
-        if (lane < 8) {
+        for (int j = 0; j < 4; ++j) po[j] = sum_row_groups<CG>(po[j]);
+        if (lane < CG) {
             uint2 pk;
             pk.x = qs::pack_bf2(po[0], po[1]);
             pk.y = qs::pack_bf2(po[2], po[3]);
@@ -332,36 +337,58 @@ __global__ __launch_bounds__(256) void gates_kernel(const uint16_t *a, const uin
 
 // -------------------------------------------------------------------------------------------- rollback
 
-// grid (chunks, B): the chunks of user b copy its state snapshot and its conv-state snapshot in 16-byte
-// units (2-byte units when the conv state is not a multiple of 16 bytes); chunk 0 also sets the new
-// sequence length. accept_len outside [1, T] leaves the user untouched.
+// grid (chunks, B): chunk c of user b copies 4 16-byte units per thread of its state snapshot (all loads
+// issued before the stores), the chunks after the state's copy the conv-state snapshot the same way (2-byte
+// units when the conv state is not a multiple of 16 bytes); chunk 0 also sets the new sequence length.
+// accept_len outside [1, T] leaves the user untouched.
+constexpr int RB_UNITS = 4;  // 16-byte units per thread
+
+// Units i0, i0 + 256, i0 + 512, i0 + 768 of src to dst (those below n): every load first (clamped into
+// range, so nothing is indexed dynamically), then the stores.
+template <typename V>
+__device__ __forceinline__ void copy4(const V *__restrict__ src, V *__restrict__ dst, size_t i0, size_t n) {
+    const V a0 = src[min(i0, n - 1)], a1 = src[min(i0 + 256, n - 1)];
+    const V a2 = src[min(i0 + 512, n - 1)], a3 = src[min(i0 + 768, n - 1)];
+    if (i0 < n) dst[i0] = a0;
+    if (i0 + 256 < n) dst[i0 + 256] = a1;
+    if (i0 + 512 < n) dst[i0 + 512] = a2;
+    if (i0 + 768 < n) dst[i0 + 768] = a3;
+}
 __global__ __launch_bounds__(256) void rollback_kernel(const float *states_out, float *state,
                                                        const uint16_t *conv_states_out, uint16_t *conv_state,
                                                        const int *accept, int *seq_lens, const int *base_lens,
-                                                       int B, int T, size_t state_f4, size_t conv_elems) {
+                                                       int B, int T, size_t state_f4, size_t conv_elems,
+                                                       int state_chunks) {
     const int b = blockIdx.y;
     const int acc = accept[b];
     if (acc < 1 || acc > T) return;
     const size_t slot = (size_t)(acc - 1) * B + b;
-    const size_t stride = (size_t)gridDim.x * 256, i0 = (size_t)blockIdx.x * 256 + threadIdx.x;
-    const float4 *src = reinterpret_cast<const float4 *>(states_out) + slot * state_f4;
-    float4 *dst = reinterpret_cast<float4 *>(state) + (size_t)b * state_f4;
-    for (size_t i = i0; i < state_f4; i += stride) dst[i] = src[i];
-    const uint16_t *cs = conv_states_out + slot * conv_elems;
-    uint16_t *cd = conv_state + (size_t)b * conv_elems;
-    if (conv_elems % 8 == 0) {
-        const uint4 *cs4 = reinterpret_cast<const uint4 *>(cs);
-        uint4 *cd4 = reinterpret_cast<uint4 *>(cd);
-        for (size_t i = i0; i < conv_elems / 8; i += stride) cd4[i] = cs4[i];
+    if ((int)blockIdx.x < state_chunks) {
+        const float4 *src = reinterpret_cast<const float4 *>(states_out) + slot * state_f4;
+        float4 *dst = reinterpret_cast<float4 *>(state) + (size_t)b * state_f4;
+        const size_t i0 = (size_t)blockIdx.x * 256 * RB_UNITS + threadIdx.x;
+        copy4(src, dst, i0, state_f4);
     } else {
-        for (size_t i = i0; i < conv_elems; i += stride) cd[i] = cs[i];
+        const uint16_t *cs = conv_states_out + slot * conv_elems;
+        uint16_t *cd = conv_state + (size_t)b * conv_elems;
+        const size_t i0 = (size_t)(blockIdx.x - state_chunks) * 256 * RB_UNITS + threadIdx.x;
+        if (conv_elems % 8 == 0) {
+            const uint4 *cs4 = reinterpret_cast<const uint4 *>(cs);
+            uint4 *cd4 = reinterpret_cast<uint4 *>(cd);
+            copy4(cs4, cd4, i0, conv_elems / 8);
+        } else {
+            for (size_t i = i0 * 8; i < conv_elems && i < (i0 + 1) * 8 * RB_UNITS; ++i) cd[i] = cs[i];
+        }
     }
     if (blockIdx.x == 0 && threadIdx.x == 0 && seq_lens) seq_lens[b] = base_lens[b] + acc;
 }
 
+// 32-column slabs (B * NV * 4 waves) for decode and verify alike, so a one-token verify reproduces decode
+// bit for bit (the column sums run in the same order). 16-column slabs (SLAB = 16, twice the waves) make a
+// batch-1 verify about 9% faster but sum in another order.
 template <bool CONV, bool VERIFY>
 void launch_gdn(const GdnArgs &a, hipStream_t st) {
-    gdn_kernel<CONV, VERIFY><<<a.B * a.NV * NSLAB, 64, 0, st>>>(a);
+    gdn_kernel<CONV, VERIFY, 32><<<a.B * a.NV * (DV / 32), 64, 0, st>>>(a);
 }
 
 // The conv reads channel pairs with 4-, 12- and 16-byte loads.
@@ -376,7 +403,7 @@ int check_gdn_shapes(int B, int NK, int NV, int DKa, int DVa) {
     QS_REQUIRE(B > 0, "B must be positive (got %d)", B);
     QS_REQUIRE(DKa == DK && DVa == DV, "DK and DV must be 128 (got %d, %d)", DKa, DVa);
     QS_REQUIRE(NK > 0 && NV > 0 && NV % NK == 0, "NV (%d) must be a positive multiple of NK (%d)", NV, NK);
-    QS_REQUIRE((long)B * NV * NSLAB < (1L << 31), "grid too large");
+    QS_REQUIRE((long)B * NV * (DV / 16) < (1L << 31), "grid too large");
     return QS_OK;
 }
 
@@ -461,9 +488,13 @@ extern "C" int qs_gdn_rollback(const float *states_out, float *state, const uint
     QS_REQUIRE(DKa == DK && DVa == DV, "qs_gdn_rollback: DK and DV must be 128");
     const size_t state_f4 = (size_t)NV * DK * DV / 4;
     const size_t conv_elems = (size_t)C * (K - 1);
-    const int chunks = (int)((state_f4 + 255) / 256 < 256 ? (state_f4 + 255) / 256 : 256);
-    rollback_kernel<<<dim3(chunks, B), 256, 0, QS_STREAM(stream)>>>(states_out, state, conv_states_out, conv_state,
-                                                                    accept_len, seq_lens, base_lens, B, T,
-                                                                    state_f4, conv_elems);
+    const size_t per_chunk = 256 * RB_UNITS;  // 16-byte units per workgroup
+    const size_t conv_units = conv_elems % 8 == 0 ? conv_elems / 8 : (conv_elems + 7) / 8;
+    const int state_chunks = (int)((state_f4 + per_chunk - 1) / per_chunk);
+    const int conv_chunks = (int)((conv_units + per_chunk - 1) / per_chunk);
+    QS_REQUIRE((long)state_chunks + conv_chunks < 65536, "qs_gdn_rollback: state too large");
+    rollback_kernel<<<dim3(state_chunks + conv_chunks, B), 256, 0, QS_STREAM(stream)>>>(
+        states_out, state, conv_states_out, conv_state, accept_len, seq_lens, base_lens, B, T, state_f4, conv_elems,
+        state_chunks);
     return qs::launch_status("qs_gdn_rollback");
 }
