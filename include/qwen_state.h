@@ -99,6 +99,16 @@ int qs_gdn_rollback(const float *states_out, float *state, const uint16_t *conv_
                     const int *accept_len, int *seq_lens, const int *base_lens, int B, int T, int NV, int DK,
                     int DV, int C, int K, void *stream);
 
+/* The same rollback for L GDN layers in one launch (the hub switches every layer's slot at once,
+ * kernels/mlp_hub.cpp:48-58): layer l's tensors start l * <its layer stride> elements past the given
+ * pointers (states_out [L][T, B, NV, DK, DV], state [L][B, NV, DK, DV], conv_states_out [L][T, B, C, K-1],
+ * conv_state [L][B, C, K-1]); seq_lens, when non-null, is set once. */
+int qs_gdn_rollback_layers(const float *states_out, size_t states_out_layer_stride, float *state,
+                           size_t state_layer_stride, const uint16_t *conv_states_out,
+                           size_t conv_states_out_layer_stride, uint16_t *conv_state, size_t conv_state_layer_stride,
+                           const int *accept_len, int *seq_lens, const int *base_lens, int L, int B, int T, int NV,
+                           int DK, int DV, int C, int K, void *stream);
+
 /* ---------------------------------------------------------------------------------------- a5: paged append
  * Write T new K and V rows per user at positions positions[b] + t into the paged pools (bit-exact).
  *   k, v [B, T, NKV, HD] bf16; pools [num_blocks, NKV, block, HD]; block_table [B, max_blocks]; positions [B].

@@ -128,6 +128,28 @@ def test_gdn_verify_and_rollback(dev, B, T):
     assert torch.equal(seq.cpu(), base + acc)
 
 
+def test_rollback_layers_equals_per_layer(dev):
+    """The one-launch rollback of L layers restores exactly what L single-layer rollbacks do."""
+    L, T, B, C = 3, 3, 2, 10240
+    gen = torch.Generator(device="cpu").manual_seed(77)
+    states = torch.randn(L, T, B, NV, DK, DV, generator=gen).to(dev)
+    convs = torch.randn(L, T, B, C, 3, generator=gen).to(torch.bfloat16).to(dev)
+    acc = torch.tensor([2, 3], dtype=torch.int32, device=dev)
+    base = torch.tensor([100, 200], dtype=torch.int32, device=dev)
+    st1 = torch.zeros(L, B, NV, DK, DV, device=dev)
+    cv1 = torch.zeros(L, B, C, 3, dtype=torch.bfloat16, device=dev)
+    st2, cv2 = st1.clone(), cv1.clone()
+    seq1 = torch.zeros(B, dtype=torch.int32, device=dev)
+    seq2 = seq1.clone()
+    ops.gdn_rollback_layers(states, convs, acc, st1, cv1, seq1, base)
+    for l in range(L):
+        ops.gdn_rollback(states[l], convs[l], acc, st2[l], cv2[l], seq2 if l == 0 else None, base if l == 0 else None)
+    assert torch.equal(st1, st2) and torch.equal(cv1, cv2) and torch.equal(seq1, seq2)
+    for l in range(L):
+        for b in range(B):
+            assert torch.equal(st1[l, b], states[l, int(acc[b]) - 1, b])
+
+
 def test_verify_one_token_equals_decode(dev):
     d = inputs(2, seed=40)
     g1, g2 = to(d, dev), to(d, dev)

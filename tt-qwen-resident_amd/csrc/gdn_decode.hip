@@ -337,10 +337,11 @@ __global__ __launch_bounds__(256) void gates_kernel(const uint16_t *a, const uin
 
 // -------------------------------------------------------------------------------------------- rollback
 
-// grid (chunks, B): chunk c of user b copies 4 16-byte units per thread of its state snapshot (all loads
-// issued before the stores), the chunks after the state's copy the conv-state snapshot the same way (2-byte
-// units when the conv state is not a multiple of 16 bytes); chunk 0 also sets the new sequence length.
-// accept_len outside [1, T] leaves the user untouched.
+// grid (chunks, B, layers): chunk c of user b copies 4 16-byte units per thread of its state snapshot (all
+// loads issued before the stores), the chunks after the state's copy the conv-state snapshot the same way
+// (2-byte units when the conv state is not a multiple of 16 bytes); chunk 0 of layer 0 also sets the new
+// sequence length. Layer z's tensors start z * (its stride) elements past the given pointers. accept_len
+// outside [1, T] leaves the user untouched.
 constexpr int RB_UNITS = 4;  // 16-byte units per thread
 
 // Units i0, i0 + 256, i0 + 512, i0 + 768 of src to dst (those below n): every load first (clamped into
@@ -358,8 +359,13 @@ __global__ __launch_bounds__(256) void rollback_kernel(const float *states_out, 
                                                        const uint16_t *conv_states_out, uint16_t *conv_state,
                                                        const int *accept, int *seq_lens, const int *base_lens,
                                                        int B, int T, size_t state_f4, size_t conv_elems,
-                                                       int state_chunks) {
-    const int b = blockIdx.y;
+                                                       int state_chunks, size_t so_stride, size_t s_stride,
+                                                       size_t co_stride, size_t c_stride) {
+    const int b = blockIdx.y, z = blockIdx.z;
+    states_out += z * so_stride;
+    state += z * s_stride;
+    conv_states_out += z * co_stride;
+    conv_state += z * c_stride;
     const int acc = accept[b];
     if (acc < 1 || acc > T) return;
     const size_t slot = (size_t)(acc - 1) * B + b;
@@ -380,7 +386,7 @@ __global__ __launch_bounds__(256) void rollback_kernel(const float *states_out, 
             for (size_t i = i0 * 8; i < conv_elems && i < (i0 + 1) * 8 * RB_UNITS; ++i) cd[i] = cs[i];
         }
     }
-    if (blockIdx.x == 0 && threadIdx.x == 0 && seq_lens) seq_lens[b] = base_lens[b] + acc;
+    if (blockIdx.x == 0 && z == 0 && threadIdx.x == 0 && seq_lens) seq_lens[b] = base_lens[b] + acc;
 }
 
 // 32-column slabs (B * NV * 4 waves) for decode and verify alike, so a one-token verify reproduces decode
@@ -479,22 +485,42 @@ extern "C" int qs_gdn_verify_step(const uint16_t *x, const uint16_t *conv_state_
     return qs::launch_status("qs_gdn_verify_step");
 }
 
-extern "C" int qs_gdn_rollback(const float *states_out, float *state, const uint16_t *conv_states_out,
-                               uint16_t *conv_state, const int *accept_len, int *seq_lens, const int *base_lens,
-                               int B, int T, int NV, int DKa, int DVa, int C, int K, void *stream) {
-    QS_REQUIRE(states_out && state && conv_states_out && conv_state && accept_len, "qs_gdn_rollback: null pointer");
-    QS_REQUIRE(!seq_lens || base_lens, "qs_gdn_rollback: seq_lens needs base_lens");
-    QS_REQUIRE(B > 0 && T >= 1 && T <= TMAX && NV > 0 && C > 0 && K == KC, "qs_gdn_rollback: bad shape");
-    QS_REQUIRE(DKa == DK && DVa == DV, "qs_gdn_rollback: DK and DV must be 128");
+static int rollback_launch(const float *states_out, size_t so_stride, float *state, size_t s_stride,
+                           const uint16_t *conv_states_out, size_t co_stride, uint16_t *conv_state, size_t c_stride,
+                           const int *accept_len, int *seq_lens, const int *base_lens, int L, int B, int T, int NV,
+                           int DKa, int DVa, int C, int K, void *stream, const char *who) {
+    QS_REQUIRE(states_out && state && conv_states_out && conv_state && accept_len, "%s: null pointer", who);
+    QS_REQUIRE(!seq_lens || base_lens, "%s: seq_lens needs base_lens", who);
+    QS_REQUIRE(L >= 1 && L <= 65535 && B > 0 && B <= 65535 && T >= 1 && T <= TMAX && NV > 0 && C > 0 && K == KC,
+               "%s: bad shape", who);
+    QS_REQUIRE(DKa == DK && DVa == DV, "%s: DK and DV must be 128", who);
     const size_t state_f4 = (size_t)NV * DK * DV / 4;
     const size_t conv_elems = (size_t)C * (K - 1);
     const size_t per_chunk = 256 * RB_UNITS;  // 16-byte units per workgroup
     const size_t conv_units = conv_elems % 8 == 0 ? conv_elems / 8 : (conv_elems + 7) / 8;
     const int state_chunks = (int)((state_f4 + per_chunk - 1) / per_chunk);
     const int conv_chunks = (int)((conv_units + per_chunk - 1) / per_chunk);
-    QS_REQUIRE((long)state_chunks + conv_chunks < 65536, "qs_gdn_rollback: state too large");
-    rollback_kernel<<<dim3(state_chunks + conv_chunks, B), 256, 0, QS_STREAM(stream)>>>(
+    QS_REQUIRE((long)state_chunks + conv_chunks < (1L << 31), "%s: state too large", who);
+    rollback_kernel<<<dim3(state_chunks + conv_chunks, B, L), 256, 0, QS_STREAM(stream)>>>(
         states_out, state, conv_states_out, conv_state, accept_len, seq_lens, base_lens, B, T, state_f4, conv_elems,
-        state_chunks);
-    return qs::launch_status("qs_gdn_rollback");
+        state_chunks, so_stride, s_stride, co_stride, c_stride);
+    return qs::launch_status(who);
+}
+
+extern "C" int qs_gdn_rollback(const float *states_out, float *state, const uint16_t *conv_states_out,
+                               uint16_t *conv_state, const int *accept_len, int *seq_lens, const int *base_lens,
+                               int B, int T, int NV, int DKa, int DVa, int C, int K, void *stream) {
+    return rollback_launch(states_out, 0, state, 0, conv_states_out, 0, conv_state, 0, accept_len, seq_lens, base_lens,
+                           1, B, T, NV, DKa, DVa, C, K, stream, "qs_gdn_rollback");
+}
+
+extern "C" int qs_gdn_rollback_layers(const float *states_out, size_t states_out_layer_stride, float *state,
+                                      size_t state_layer_stride, const uint16_t *conv_states_out,
+                                      size_t conv_states_out_layer_stride, uint16_t *conv_state,
+                                      size_t conv_state_layer_stride, const int *accept_len, int *seq_lens,
+                                      const int *base_lens, int L, int B, int T, int NV, int DKa, int DVa, int C,
+                                      int K, void *stream) {
+    return rollback_launch(states_out, states_out_layer_stride, state, state_layer_stride, conv_states_out,
+                           conv_states_out_layer_stride, conv_state, conv_state_layer_stride, accept_len, seq_lens,
+                           base_lens, L, B, T, NV, DKa, DVa, C, K, stream, "qs_gdn_rollback_layers");
 }

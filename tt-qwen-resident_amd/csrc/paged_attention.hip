@@ -356,7 +356,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 
 // Merge of the splits of one output row (user, token, query head): thread d owns head dim d. The first 16
 // splits' partials are requested before the weights are known, so a merge of up to 16 splits costs one
-// memory round trip. Wave 0 finds the global max M (log2 domain, as the partials store it) and sum L over
+// memory round trip (and each further 16 one more). Wave 0 finds the global max M (log2 domain, as the partials store it) and sum L over
 // the splits (fixed-order butterflies) and leaves the weights e^(m_s - M) / L in LDS; every thread then
 // sums its dim over the splits in split order.
 constexpr int MAX_SPLITS = 1024;
@@ -372,7 +372,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, int G) {
     const float *po = a.part_o + ((size_t)row * ns * G + h) * HD + tid;
     float x[CH];
 #pragma unroll
-    for (int k = 0; k < CH; ++k) x[k] = k < ns ? po[k * sstride] : 0.f;
+    for (int k = 0; k < CH; ++k) x[k] = po[(size_t)min(k, ns - 1) * sstride];
     if (tid < 64) {
         float M = -INFINITY;
         for (int sp = tid; sp < ns; sp += 64) M = fmaxf(M, ml[(size_t)sp * G * 2]);
@@ -392,7 +392,14 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, int G) {
 #pragma unroll
     for (int k = 0; k < CH; ++k)
         if (k < ns) O += s_wt[k] * x[k];
-    for (int sp = CH; sp < ns; ++sp) O += s_wt[sp] * po[(size_t)sp * sstride];
+    // further splits in chunks of CH, each chunk's loads all in flight before its first use
+    for (int s0 = CH; s0 < ns; s0 += CH) {
+#pragma unroll
+        for (int k = 0; k < CH; ++k) x[k] = po[(size_t)min(s0 + k, ns - 1) * sstride];
+#pragma unroll
+        for (int k = 0; k < CH; ++k)
+            if (s0 + k < ns) O += s_wt[s0 + k] * x[k];
+    }
     const int g = row % a.NKV, bt = row / a.NKV;
     a.o[((size_t)bt * a.NQ + g * G + h) * HD + tid] = (uint16_t)qs::f2bf(O);
 }

@@ -24,6 +24,8 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _F, _P],
     ),
     "qs_gdn_rollback": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "qs_gdn_rollback_layers": (
+        _I, [_P, _Z, _P, _Z, _P, _Z, _P, _Z, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "qs_paged_kv_append": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "qs_paged_kv_fill": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "qs_paged_attention_workspace_bytes": (_Z, [_I, _I, _I, _I, _I, _I, _I]),

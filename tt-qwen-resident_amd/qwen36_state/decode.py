@@ -150,7 +150,16 @@ class VerifyStep:
         self.base_lens = self.seq_lens - T
         gen = torch.Generator().manual_seed(seed + 7)
         self.accept = torch.randint(1, T + 1, (B,), generator=gen, dtype=torch.int32).to(self.device)
+        # the GDN layers' states, conv histories and their T snapshots live in one tensor each (layer-major),
+        # so the rollback restores every layer in one launch
+        n_gdn = sum(not is_attn(l, interval) for l in range(layers))
+        f32, bf = torch.float32, torch.bfloat16
+        self.g_state = torch.empty(n_gdn, B, NV, DK, DV, dtype=f32, device=self.device)
+        self.g_conv = torch.empty(n_gdn, B, W.C_QKV, CONV_K - 1, dtype=bf, device=self.device)
+        self.g_states = torch.empty(n_gdn, T, B, NV, DK, DV, dtype=f32, device=self.device)
+        self.g_convs = torch.empty(n_gdn, T, B, W.C_QKV, CONV_K - 1, dtype=bf, device=self.device)
         self.layer = []
+        gi = 0
         for l in range(layers):
             if is_attn(l, interval):
                 d = W.attn_layer(B, ctx, self.device, seed=seed + 1000 + l, T=T, num_blocks=num_blocks)
@@ -159,10 +168,13 @@ class VerifyStep:
                 d["attn"] = True
             else:
                 d = W.gdn_layer(B, self.device, seed=seed + l, T=T)
+                self.g_state[gi].copy_(d["state"])
+                self.g_conv[gi].copy_(d["conv_state"])
+                d["state"], d["conv_state"] = self.g_state[gi], self.g_conv[gi]
                 d["o"] = torch.empty(B, T, NV, DV, dtype=torch.bfloat16, device=self.device)
-                d["states"] = torch.empty(T, B, NV, DK, DV, dtype=torch.float32, device=self.device)
-                d["convs"] = torch.empty(T, B, W.C_QKV, CONV_K - 1, dtype=torch.bfloat16, device=self.device)
+                d["states"], d["convs"] = self.g_states[gi], self.g_convs[gi]
                 d["attn"] = False
+                gi += 1
             self.layer.append(d)
         mb = self.block_table.shape[1]
         self.attn_ws = ops.attention_workspace(B, T, NQ, NKV, mb, pages_per_split, self.device)
@@ -180,13 +192,9 @@ class VerifyStep:
                                     out=(d["o"], d["states"], d["convs"]))  # fmt: skip
 
     def rollback(self):
-        """Restore every GDN layer to its accepted snapshot and truncate the KV length (once)."""
-        first = True
-        for d in self.layer:
-            if not d["attn"]:
-                ops.gdn_rollback(d["states"], d["convs"], self.accept, d["state"], d["conv_state"],
-                                 self.seq_lens if first else None, self.base_lens if first else None)  # fmt: skip
-                first = False
+        """Restore every GDN layer to its accepted snapshot and truncate the KV length, in one launch."""
+        ops.gdn_rollback_layers(self.g_states, self.g_convs, self.accept, self.g_state, self.g_conv, self.seq_lens,
+                                self.base_lens)  # fmt: skip
 
     def step(self):
         self.verify()

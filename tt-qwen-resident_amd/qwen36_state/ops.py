@@ -201,6 +201,30 @@ def gdn_rollback(states, conv_states, accept_len, state, conv_state, seq_lens=No
          _p(base_lens), B, T, nv, dk, dv, C, CONV_K, _stream(dev))  # fmt: skip
 
 
+def gdn_rollback_layers(states, conv_states, accept_len, state, conv_state, seq_lens=None, base_lens=None):
+    """gdn_rollback for L layers in one launch: states [L, T, B, NV, DK, DV], conv_states [L, T, B, C, K-1],
+    state [L, B, NV, DK, DV], conv_state [L, B, C, K-1] (each layer's slice contiguous; the layer stride
+    is read from the tensor), seq_lens set once (the hub's all-layer slot switch, kernels/mlp_hub.cpp:48-58)."""
+    dev = state.device
+    L, T, B, nv, dk, dv = states.shape
+    C = conv_states.shape[3]
+    for name, t, dt, shp in (("states", states, torch.float32, (L, T, B, nv, dk, dv)),
+                             ("conv_states", conv_states, torch.bfloat16, (L, T, B, C, CONV_K - 1)),
+                             ("state", state, torch.float32, (L, B, nv, dk, dv)),
+                             ("conv_state", conv_state, torch.bfloat16, (L, B, C, CONV_K - 1))):  # fmt: skip
+        if t.dtype != dt or tuple(t.shape) != shp or t.device != dev:
+            raise ValueError(f"{name}: expected {dt} {shp} on {dev}, got {t.dtype} {tuple(t.shape)} on {t.device}")
+        if not t[0].is_contiguous():
+            raise ValueError(f"{name}: each layer's slice must be contiguous")
+    _chk(accept_len, "accept_len", torch.int32, (B,), dev)
+    if seq_lens is not None:
+        _chk(seq_lens, "seq_lens", torch.int32, (B,), dev)
+        _chk(base_lens, "base_lens", torch.int32, (B,), dev)
+    call("qs_gdn_rollback_layers", _p(states), states.stride(0), _p(state), state.stride(0), _p(conv_states),
+         conv_states.stride(0), _p(conv_state), conv_state.stride(0), _p(accept_len), _p(seq_lens), _p(base_lens),
+         L, B, T, nv, dk, dv, C, CONV_K, _stream(dev))  # fmt: skip
+
+
 # ------------------------------------------------------------------------------------------- a5, a9
 
 
