@@ -42,26 +42,13 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
 }
 __device__ __forceinline__ bf16x8 as_frag(uint4 u) { return __builtin_bit_cast(bf16x8, u32x4{u.x, u.y, u.z, u.w}); }
 
-// fp32 x[8] -> bf16 hi = rne(x), lo = rne(x - hi): hi + lo carries 16 mantissa bits
-__device__ __forceinline__ void split8(const float x[8], bf16x8 &hi, bf16x8 &lo) {
-    u32x4 h, l;
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        const uint32_t hp = qs::cvt_pk_bf16(x[2 * p], x[2 * p + 1]);
-        h[p] = hp;
-        l[p] = qs::cvt_pk_bf16(x[2 * p] - __uint_as_float(hp << 16), x[2 * p + 1] - __uint_as_float(hp & 0xffff0000u));
-    }
-    hi = __builtin_bit_cast(bf16x8, h);
-    lo = __builtin_bit_cast(bf16x8, l);
-}
-
 struct PrefillArgs {
     const uint16_t *q, *k, *v;  // [T, NK, DK], [T, NK, DK], [T, NV, DV]
     const float *g, *beta;      // [T, NV]
     const float *S0;            // [NV, DK, DV]
     float *ST;                  // [NV, DK, DV]
     uint16_t *o;                // [T, NV, DV]
-    float *Tm;                  // workspace [nch, NV, 64, 64]
+    uint16_t *Tm;               // workspace [nch, NV, 2, 64, 64] bf16: hi and lo planes of Tm
     uint16_t *P;                // workspace [nch, NV, 2, 64, 64] bf16: hi and lo planes of P
     float *sc;                  // workspace [nch, NV, 5, 64]: beta | beta gamma r_k | gamma r_q | r_k gamma_C/gamma | gamma_C
     int T, NK, NV, nch;
@@ -214,7 +201,12 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
             __syncthreads();
         }
         // 7. Tm and the per-token scalars to the workspace
-        for (int e = tid; e < CH * CH; e += 256) a.Tm[mat + e] = (e >> 6) >= (e & 63) ? sT[e >> 6][e & 63] : 0.f;
+        for (int e = tid; e < CH * CH; e += 256) {
+            const float tv = (e >> 6) >= (e & 63) ? sT[e >> 6][e & 63] : 0.f;
+            const uint32_t th = qs::f2bf(tv);
+            a.Tm[2 * mat + e] = (uint16_t)th;
+            a.Tm[2 * mat + CH * CH + e] = (uint16_t)qs::f2bf(tv - qs::bf2f(th));
+        }
         if (tid < CH) {
             const int i = tid;
             const float gam = expf(s_G[i]);
@@ -231,20 +223,35 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
 
 // ------------------------------------------------------------------------------------------------ walk
 
-// 8 consecutive fp32 from LDS (two 16-byte reads)
-__device__ __forceinline__ void lds8(const float *p, float x[8]) {
-    const float4 a = *reinterpret_cast<const float4 *>(p), b = *reinterpret_cast<const float4 *>(p + 4);
-    x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w, x[4] = b.x, x[5] = b.y, x[6] = b.z, x[7] = b.w;
+typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
+
+// four fp32 -> bf16 hi = rne(x), lo = rne(x - hi), each as four packed bf16 (8 bytes)
+__device__ __forceinline__ void split4(float x0, float x1, float x2, float x3, uint2 &hi, uint2 &lo) {
+    const uint32_t h0 = qs::cvt_pk_bf16(x0, x1), h1 = qs::cvt_pk_bf16(x2, x3);
+    hi = make_uint2(h0, h1);
+    lo = make_uint2(qs::cvt_pk_bf16(x0 - __uint_as_float(h0 << 16), x1 - __uint_as_float(h0 & 0xffff0000u)),
+                    qs::cvt_pk_bf16(x2 - __uint_as_float(h1 << 16), x3 - __uint_as_float(h1 & 0xffff0000u)));
 }
 
-// Operands are kept in LDS in the orientation the MFMA fragments read, so every fragment is two 16-byte
-// reads and every accumulator tile is stored with one: S^T [v][d], X^T and d^T [v][token], K^T [d][token]
-// beside K and Q [token][d]. The next chunk's K, Q and V are loaded into registers while the current
-// chunk computes; Tm, P and the scalars are requested at the start of a chunk and consumed after K S0.
+__device__ __forceinline__ bf16x8 frag(const uint16_t *p) { return as_frag(*reinterpret_cast<const uint4 *>(p)); }
+
+// K^T [d][token] rows are 64 tokens (128 bytes) with the 16-byte token groups XOR-swizzled by
+// (d ^ d / 8) % 8: the paired-token writes of the transpose and the MFMA fragment reads are both free of
+// bank conflicts without padding.
+__device__ __forceinline__ int kt_index(int d, int t) {
+    return d * CH + ((((t >> 3) ^ (d ^ (d >> 3))) & 7) << 3) + (t & 7);
+}
+
+// One workgroup (4 waves) per (value head, 32-column slab of S). The slab's fp32 state lives in registers
+// (wave w owns state rows 32 w .. 32 w + 31, the layout of its S-update MFMA tiles) and is mirrored in LDS
+// as bf16 hi + lo planes, the operand of K S0 and Q S0. Every other operand sits in LDS in the orientation
+// its MFMA fragments read (S^T, X^T, d^T [v][token], K^T [d][token], K, Q, Tm, P [token][.]) and is split
+// into bf16 hi + lo once, by the wave that produces it. The next chunk's K, Q, V, Tm, P and scalars are
+// loaded into registers while the current chunk computes; reads past the sequence end return zeros through
+// the buffer descriptors' range checks and writes past it are dropped the same way.
 __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
-    constexpr int SP = DK + 4;   // fp32 row stride of S^T
-    constexpr int XP = CH + 4;   // fp32 row stride of X^T and d^T
-    constexpr int KTP = CH + 8;  // bf16 row stride of K^T
+    constexpr int SKP = DK + 8;  // bf16 row stride of the S^T planes
+    constexpr int TP = CH + 8;   // bf16 row stride of the [.][token] planes
     const int nwg = a.NV * NSLAB;
     const int lid = qs::xcd_logical(blockIdx.x, nwg);
     const int slab = lid % NSLAB, h = lid / NSLAB;
@@ -252,182 +259,227 @@ __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int fr = lane & 15, fk = (lane >> 4) * 8, fq = (lane >> 4) * 4;
 
-    __shared__ __align__(16) float sSt[SLAB][SP];
+    __shared__ __align__(16) uint16_t sS[2][SLAB][SKP];
     __shared__ __align__(16) uint16_t sK[CH][KP];
     __shared__ __align__(16) uint16_t sQ[CH][KP];
-    __shared__ __align__(16) uint16_t sKt[DK][KTP];
+    __shared__ __align__(16) uint16_t sKt[DK * CH];
     __shared__ __align__(16) uint16_t sV[CH][SLAB + 8];
-    __shared__ __align__(16) float sTm[CH][CH + 4];
-    __shared__ __align__(16) uint16_t sP[2][CH][CH + 8];
-    __shared__ __align__(16) float sXt[SLAB][XP];
-    __shared__ __align__(16) float sDt[SLAB][XP];
+    __shared__ __align__(16) uint16_t sTm[2][CH][TP];
+    __shared__ __align__(16) uint16_t sP[2][CH][TP];
+    __shared__ __align__(16) uint16_t sX[2][SLAB][TP];
+    __shared__ __align__(16) uint16_t sD[2][SLAB][TP];
+    __shared__ __align__(16) uint16_t sE[2][SLAB][TP];
     __shared__ __align__(16) float s_c[5][CH];
 
-    // the state slab S0[h][:, 32 slab .. 32 slab + 31], transposed
-    for (int idx = tid; idx < DK * SLAB / 4; idx += 256) {
-        const int d = idx / (SLAB / 4), v4 = idx % (SLAB / 4);
-        const float4 x = *reinterpret_cast<const float4 *>(a.S0 + ((size_t)h * DK + d) * DV + slab * SLAB + v4 * 4);
-        sSt[v4 * 4 + 0][d] = x.x, sSt[v4 * 4 + 1][d] = x.y, sSt[v4 * 4 + 2][d] = x.z, sSt[v4 * 4 + 3][d] = x.w;
-    }
+    // state rows 32 w + 16 mt + fq + i, columns 32 slab + 16 nt + fr
+    float S[2][2][4];
+    auto mirror = [&](int mt, int nt) {
+        uint2 hi, lo;
+        split4(S[mt][nt][0], S[mt][nt][1], S[mt][nt][2], S[mt][nt][3], hi, lo);
+        const int v = 16 * nt + fr, d = 32 * w + 16 * mt + fq;
+        *reinterpret_cast<uint2 *>(&sS[0][v][d]) = hi;
+        *reinterpret_cast<uint2 *>(&sS[1][v][d]) = lo;
+    };
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                S[mt][nt][i] = a.S0[((size_t)h * DK + 32 * w + 16 * mt + fq + i) * DV + SLAB * slab + 16 * nt + fr];
+            mirror(mt, nt);
+        }
 
-    // this thread's share of a chunk's K / Q rows (4 x 16 bytes each) and V slab (16 bytes)
-    uint4 pk[4], pq[4], pv;
-    auto fetch_kqv = [&](int c) {
-        const int t0 = c * CH, nval = min(CH, a.T - t0);
+    // per-thread share of a chunk: K and Q rows 2 p + (m & 1), p = pp + 4 w + 16 (m >> 1), 16 bytes at
+    // group kc (each half-wave covers 8 groups x 4 row pairs); V row tid / 4, group tid % 4; Tm and P
+    // 16-byte pieces tid + 256 m of their hi | lo planes; scalars tid and 256 + tid
+    const int kc = (lane & 7) + 8 * (lane >> 5), pp = (lane >> 3) & 3;
+    const size_t krow = (size_t)a.NK * DK * 2, vrow = (size_t)a.NV * DV * 2;  // bytes per token
+    // (vectors, not arrays: they stay in registers whatever the unroll order)
+    u32x16 pk, pq, ptm, ppm;
+    u32x4 pv;
+    float psc0, psc1;
+    auto fetch = [&](int c) {
+        const int t0 = c * CH, nv = min(CH, a.T - t0);
+        const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.k) + (size_t)t0 * a.NK * DK,
+                                                          (short)0, (int)(nv * krow), 0x00020000);
+        const auto rq = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.q) + (size_t)t0 * a.NK * DK,
+                                                          (short)0, (int)(nv * krow), 0x00020000);
+        const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.v) + (size_t)t0 * a.NV * DV,
+                                                          (short)0, (int)(nv * vrow), 0x00020000);
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-            const int idx = tid + 256 * m, r = idx >> 4, ch = idx & 15;
-            pk[m] = pq[m] = make_uint4(0, 0, 0, 0);
-            if (r < nval) {
-                const size_t off = ((size_t)(t0 + r) * a.NK + kh) * DK + ch * 8;
-                pk[m] = *reinterpret_cast<const uint4 *>(a.k + off);
-                pq[m] = *reinterpret_cast<const uint4 *>(a.q + off);
-            }
+            const int r = 2 * (pp + 4 * w + 16 * (m >> 1)) + (m & 1);
+            const int off = (int)(r * krow) + (kh * DK + kc * 8) * 2;
+            const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0);
+            const u32x4 y = __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) pk[4 * m + j] = x[j], pq[4 * m + j] = y[j];
         }
-        const int r = tid >> 2, ch = tid & 3;
-        pv = make_uint4(0, 0, 0, 0);
-        if (r < nval) pv = *reinterpret_cast<const uint4 *>(a.v + ((size_t)(t0 + r) * a.NV + h) * DV + slab * SLAB + ch * 8);
+        pv = __builtin_amdgcn_raw_buffer_load_b128(rv, (int)((tid >> 2) * vrow) + (h * DV + SLAB * slab + (tid & 3) * 8) * 2,
+                                                   0, 0);
+        const size_t mat = ((size_t)c * a.NV + h) * CH * CH;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const uint4 x = *reinterpret_cast<const uint4 *>(a.Tm + 2 * mat + (tid + 256 * m) * 8);
+            const uint4 y = *reinterpret_cast<const uint4 *>(a.P + 2 * mat + (tid + 256 * m) * 8);
+            ptm[4 * m] = x.x, ptm[4 * m + 1] = x.y, ptm[4 * m + 2] = x.z, ptm[4 * m + 3] = x.w;
+            ppm[4 * m] = y.x, ppm[4 * m + 1] = y.y, ppm[4 * m + 2] = y.z, ppm[4 * m + 3] = y.w;
+        }
+        const float *scg = a.sc + ((size_t)c * a.NV + h) * 5 * CH;
+        psc0 = scg[tid];
+        psc1 = scg[256 + (tid & 63)];
     };
-    fetch_kqv(0);
+    fetch(0);
+
+    // a chunk's output rows are stored at the start of the next chunk, after that chunk's operands have
+    // been waited for, so the stores never sit in front of a prefetch in the memory counter
+    f32x4 opend[2];
+    auto store_o = [&](int c) {
+        const int t0 = c * CH, nv = min(CH, a.T - t0), r0 = 16 * w + fq;
+        const auto ro = __builtin_amdgcn_make_buffer_rsrc(a.o + (size_t)t0 * a.NV * DV, (short)0, (int)(nv * vrow),
+                                                          0x00020000);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                __builtin_amdgcn_raw_buffer_store_b16((unsigned short)qs::f2bf(opend[nt][i]), ro,
+                                                      (int)((r0 + i) * vrow) + (h * DV + SLAB * slab + nt * 16 + fr) * 2, 0,
+                                                      0);
+    };
 
     for (int c = 0; c < a.nch; ++c) {
-        const int t0 = c * CH;
-        const int nval = min(CH, a.T - t0);
-        const size_t mat = ((size_t)c * a.NV + h) * CH * CH;
-        // ---- K, Q, K^T, V of this chunk from registers into LDS
+        // ---- this chunk's operands from registers into LDS
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-            const int idx = tid + 256 * m, r = idx >> 4, ch = idx & 15;
-            *reinterpret_cast<uint4 *>(&sK[r][ch * 8]) = pk[m];
-            *reinterpret_cast<uint4 *>(&sQ[r][ch * 8]) = pq[m];
-            const uint32_t wd[4] = {pk[m].x, pk[m].y, pk[m].z, pk[m].w};
+            const int r = 2 * (pp + 4 * w + 16 * (m >> 1)) + (m & 1);
+            *reinterpret_cast<uint4 *>(&sK[r][kc * 8]) = make_uint4(pk[4 * m], pk[4 * m + 1], pk[4 * m + 2], pk[4 * m + 3]);
+            *reinterpret_cast<uint4 *>(&sQ[r][kc * 8]) = make_uint4(pq[4 * m], pq[4 * m + 1], pq[4 * m + 2], pq[4 * m + 3]);
+        }
+#pragma unroll
+        for (int m2 = 0; m2 < 2; ++m2) {  // K^T: token pairs (2 p, 2 p + 1) as one 32-bit word per d
+            const int t = 2 * (pp + 4 * w + 16 * m2);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                sKt[ch * 8 + 2 * e][r] = (uint16_t)(wd[e] & 0xffffu);
-                sKt[ch * 8 + 2 * e + 1][r] = (uint16_t)(wd[e] >> 16);
+                const int d = kc * 8 + 2 * e;
+                const uint32_t ev = pk[8 * m2 + e], od = pk[8 * m2 + 4 + e];
+                *reinterpret_cast<uint32_t *>(&sKt[kt_index(d, t)]) = (ev & 0xffffu) | (od << 16);
+                *reinterpret_cast<uint32_t *>(&sKt[kt_index(d + 1, t)]) = (ev >> 16) | (od & 0xffff0000u);
             }
         }
-        *reinterpret_cast<uint4 *>(&sV[tid >> 2][(tid & 3) * 8]) = pv;
-        // ---- Tm, P and scalars of this chunk: requested now, stored to LDS after K S0
-        float4 tmr[4];
-        uint4 ppr[4];
-        float scr[2];
+        *reinterpret_cast<uint4 *>(&sV[tid >> 2][(tid & 3) * 8]) = make_uint4(pv[0], pv[1], pv[2], pv[3]);
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             const int idx = tid + 256 * m;
-            tmr[m] = *reinterpret_cast<const float4 *>(a.Tm + mat + (idx >> 4) * CH + (idx & 15) * 4);
-            ppr[m] = *reinterpret_cast<const uint4 *>(a.P + 2 * mat + (idx >> 9) * CH * CH + ((idx >> 3) & 63) * CH + (idx & 7) * 8);
+            *reinterpret_cast<uint4 *>(&sTm[idx >> 9][(idx >> 3) & 63][(idx & 7) * 8]) =
+                make_uint4(ptm[4 * m], ptm[4 * m + 1], ptm[4 * m + 2], ptm[4 * m + 3]);
+            *reinterpret_cast<uint4 *>(&sP[idx >> 9][(idx >> 3) & 63][(idx & 7) * 8]) =
+                make_uint4(ppm[4 * m], ppm[4 * m + 1], ppm[4 * m + 2], ppm[4 * m + 3]);
         }
-        const float *scg = a.sc + ((size_t)c * a.NV + h) * 5 * CH;
-        scr[0] = scg[tid];
-        scr[1] = tid < 5 * CH - 256 ? scg[256 + tid] : 0.f;
+        s_c[tid >> 6][tid & 63] = psc0;
+        if (tid < 64) s_c[4][tid] = psc1;
+        if (c > 0) store_o(c - 1);
         __syncthreads();
-        if (c + 1 < a.nch) fetch_kqv(c + 1);  // in flight during this chunk
+        if (c + 1 < a.nch) fetch(c + 1);  // in flight during this chunk
 
-        // ---- K S0 and Q S0 for row tile w (S0 split hi + lo)
+        // ---- K S0 and Q S0 for token tile w (S0 as hi + lo)
         f32x4 kacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
         f32x4 qacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
         for (int ks = 0; ks < DK / 32; ++ks) {
-            const bf16x8 ak = as_frag(*reinterpret_cast<const uint4 *>(&sK[16 * w + fr][ks * 32 + fk]));
-            const bf16x8 aq = as_frag(*reinterpret_cast<const uint4 *>(&sQ[16 * w + fr][ks * 32 + fk]));
+            const bf16x8 ak = frag(&sK[16 * w + fr][ks * 32 + fk]);
+            const bf16x8 aq = frag(&sQ[16 * w + fr][ks * 32 + fk]);
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
-                float s8[8];
-                lds8(&sSt[nt * 16 + fr][ks * 32 + fk], s8);
-                bf16x8 bh, bl;
-                split8(s8, bh, bl);
+                const bf16x8 bh = frag(&sS[0][nt * 16 + fr][ks * 32 + fk]);
+                const bf16x8 bl = frag(&sS[1][nt * 16 + fr][ks * 32 + fk]);
                 kacc[nt] = mfma(ak, bh, kacc[nt]);
                 kacc[nt] = mfma(ak, bl, kacc[nt]);
                 qacc[nt] = mfma(aq, bh, qacc[nt]);
                 qacc[nt] = mfma(aq, bl, qacc[nt]);
             }
         }
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const int idx = tid + 256 * m;
-            *reinterpret_cast<float4 *>(&sTm[idx >> 4][(idx & 15) * 4]) = tmr[m];
-            *reinterpret_cast<uint4 *>(&sP[idx >> 9][(idx >> 3) & 63][(idx & 7) * 8]) = ppr[m];
-        }
-        s_c[tid / CH][tid % CH] = scr[0];
-        if (tid < 5 * CH - 256) s_c[(256 + tid) / CH][(256 + tid) % CH] = scr[1];
-        __syncthreads();
 
-        // ---- X = beta V - (beta gamma r_k) (K S0), stored transposed
-        const float4 c0 = *reinterpret_cast<const float4 *>(&s_c[0][16 * w + fq]);
-        const float4 c1 = *reinterpret_cast<const float4 *>(&s_c[1][16 * w + fq]);
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-            const int col = nt * 16 + fr, r0 = 16 * w + fq;
-            float4 x;
-            x.x = c0.x * qs::bf2f(sV[r0 + 0][col]) - c1.x * kacc[nt][0];
-            x.y = c0.y * qs::bf2f(sV[r0 + 1][col]) - c1.y * kacc[nt][1];
-            x.z = c0.z * qs::bf2f(sV[r0 + 2][col]) - c1.z * kacc[nt][2];
-            x.w = c0.w * qs::bf2f(sV[r0 + 3][col]) - c1.w * kacc[nt][3];
-            *reinterpret_cast<float4 *>(&sXt[col][r0]) = x;
-        }
-        __syncthreads();
-
-        // ---- d = Tm X (both fp32: hi*hi + hi*lo + lo*hi), stored transposed
-        f32x4 dacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-        for (int ks = 0; ks < CH / 32; ++ks) {
-            float t8[8];
-            lds8(&sTm[16 * w + fr][ks * 32 + fk], t8);
-            bf16x8 th, tl;
-            split8(t8, th, tl);
+        // ---- X = beta V - (beta gamma r_k) (K S0), as X^T hi + lo
+        {
+            const int r0 = 16 * w + fq;
+            const float4 c0 = *reinterpret_cast<const float4 *>(&s_c[0][r0]);
+            const float4 c1 = *reinterpret_cast<const float4 *>(&s_c[1][r0]);
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
-                float x8[8];
-                lds8(&sXt[nt * 16 + fr][ks * 32 + fk], x8);
-                bf16x8 xh, xl;
-                split8(x8, xh, xl);
-                dacc[nt] = mfma(th, xh, dacc[nt]);
-                dacc[nt] = mfma(th, xl, dacc[nt]);
-                dacc[nt] = mfma(tl, xh, dacc[nt]);
+                const int col = nt * 16 + fr;
+                uint2 hi, lo;
+                split4(c0.x * qs::bf2f(sV[r0 + 0][col]) - c1.x * kacc[nt][0],
+                       c0.y * qs::bf2f(sV[r0 + 1][col]) - c1.y * kacc[nt][1],
+                       c0.z * qs::bf2f(sV[r0 + 2][col]) - c1.z * kacc[nt][2],
+                       c0.w * qs::bf2f(sV[r0 + 3][col]) - c1.w * kacc[nt][3], hi, lo);
+                *reinterpret_cast<uint2 *>(&sX[0][col][r0]) = hi;
+                *reinterpret_cast<uint2 *>(&sX[1][col][r0]) = lo;
             }
         }
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-            *reinterpret_cast<float4 *>(&sDt[nt * 16 + fr][16 * w + fq]) =
-                make_float4(dacc[nt][0], dacc[nt][1], dacc[nt][2], dacc[nt][3]);
         __syncthreads();
 
-        // ---- O = (gamma r_q) (Q S0) + P d  (P and d split hi + lo: hi*hi + hi*lo + lo*hi)
-        const float4 c2 = *reinterpret_cast<const float4 *>(&s_c[2][16 * w + fq]);
-        f32x4 oacc[2];
+        // ---- d = Tm X (hi*hi + hi*lo + lo*hi), as d^T hi + lo and e^T = (d (r_k gamma_C / gamma))^T hi + lo
+        {
+            f32x4 dacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-            oacc[nt][0] = c2.x * qacc[nt][0];
-            oacc[nt][1] = c2.y * qacc[nt][1];
-            oacc[nt][2] = c2.z * qacc[nt][2];
-            oacc[nt][3] = c2.w * qacc[nt][3];
-        }
+            for (int ks = 0; ks < CH / 32; ++ks) {
+                const bf16x8 th = frag(&sTm[0][16 * w + fr][ks * 32 + fk]);
+                const bf16x8 tl = frag(&sTm[1][16 * w + fr][ks * 32 + fk]);
 #pragma unroll
-        for (int ks = 0; ks < CH / 32; ++ks) {
-            const bf16x8 ap = as_frag(*reinterpret_cast<const uint4 *>(&sP[0][16 * w + fr][ks * 32 + fk]));
-            const bf16x8 apl = as_frag(*reinterpret_cast<const uint4 *>(&sP[1][16 * w + fr][ks * 32 + fk]));
+                for (int nt = 0; nt < 2; ++nt) {
+                    const bf16x8 xh = frag(&sX[0][nt * 16 + fr][ks * 32 + fk]);
+                    const bf16x8 xl = frag(&sX[1][nt * 16 + fr][ks * 32 + fk]);
+                    dacc[nt] = mfma(th, xh, dacc[nt]);
+                    dacc[nt] = mfma(th, xl, dacc[nt]);
+                    dacc[nt] = mfma(tl, xh, dacc[nt]);
+                }
+            }
+            const int r0 = 16 * w + fq;
+            const float4 c3 = *reinterpret_cast<const float4 *>(&s_c[3][r0]);
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
-                float d8[8];
-                lds8(&sDt[nt * 16 + fr][ks * 32 + fk], d8);
-                bf16x8 dh, dl;
-                split8(d8, dh, dl);
-                oacc[nt] = mfma(ap, dh, oacc[nt]);
-                oacc[nt] = mfma(ap, dl, oacc[nt]);
-                oacc[nt] = mfma(apl, dh, oacc[nt]);
+                const int col = nt * 16 + fr;
+                uint2 hi, lo;
+                split4(dacc[nt][0], dacc[nt][1], dacc[nt][2], dacc[nt][3], hi, lo);
+                *reinterpret_cast<uint2 *>(&sD[0][col][r0]) = hi;
+                *reinterpret_cast<uint2 *>(&sD[1][col][r0]) = lo;
+                split4(dacc[nt][0] * c3.x, dacc[nt][1] * c3.y, dacc[nt][2] * c3.z, dacc[nt][3] * c3.w, hi, lo);
+                *reinterpret_cast<uint2 *>(&sE[0][col][r0]) = hi;
+                *reinterpret_cast<uint2 *>(&sE[1][col][r0]) = lo;
             }
         }
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = 16 * w + fq + i;
-                if (r < nval)
-                    a.o[((size_t)(t0 + r) * a.NV + h) * DV + slab * SLAB + nt * 16 + fr] = (uint16_t)qs::f2bf(oacc[nt][i]);
-            }
+        __syncthreads();
 
-        // ---- S = gamma_C S0 + K^T (r_k gamma_C / gamma) d : wave w owns state rows 32 w .. 32 w + 31
+        // ---- O = (gamma r_q) (Q S0) + P d  (hi*hi + hi*lo + lo*hi)
+        {
+            const int r0 = 16 * w + fq;
+            const float4 c2 = *reinterpret_cast<const float4 *>(&s_c[2][r0]);
+            f32x4 oacc[2];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                oacc[nt][0] = c2.x * qacc[nt][0];
+                oacc[nt][1] = c2.y * qacc[nt][1];
+                oacc[nt][2] = c2.z * qacc[nt][2];
+                oacc[nt][3] = c2.w * qacc[nt][3];
+            }
+#pragma unroll
+            for (int ks = 0; ks < CH / 32; ++ks) {
+                const bf16x8 ap = frag(&sP[0][16 * w + fr][ks * 32 + fk]);
+                const bf16x8 apl = frag(&sP[1][16 * w + fr][ks * 32 + fk]);
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
+                    const bf16x8 dh = frag(&sD[0][nt * 16 + fr][ks * 32 + fk]);
+                    const bf16x8 dl = frag(&sD[1][nt * 16 + fr][ks * 32 + fk]);
+                    oacc[nt] = mfma(ap, dh, oacc[nt]);
+                    oacc[nt] = mfma(ap, dl, oacc[nt]);
+                    oacc[nt] = mfma(apl, dh, oacc[nt]);
+                }
+            }
+            opend[0] = oacc[0], opend[1] = oacc[1];
+        }
+
+        // ---- S = gamma_C S0 + K^T e : wave w owns state rows 32 w .. 32 w + 31
         const float gC = s_c[4][0];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
@@ -437,31 +489,28 @@ __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
                 f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int ks = 0; ks < CH / 32; ++ks) {
-                    const bf16x8 ka = as_frag(*reinterpret_cast<const uint4 *>(&sKt[d0 + fr][ks * 32 + fk]));
-                    float d8[8], c8[8];
-                    lds8(&sDt[nt * 16 + fr][ks * 32 + fk], d8);
-                    lds8(&s_c[3][ks * 32 + fk], c8);
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) d8[e] *= c8[e];
-                    bf16x8 dh, dl;
-                    split8(d8, dh, dl);
-                    sacc = mfma(ka, dh, sacc);
-                    sacc = mfma(ka, dl, sacc);
+                    const bf16x8 ka = frag(&sKt[kt_index(d0 + fr, ks * 32 + fk)]);
+                    const bf16x8 eh = frag(&sE[0][nt * 16 + fr][ks * 32 + fk]);
+                    const bf16x8 el = frag(&sE[1][nt * 16 + fr][ks * 32 + fk]);
+                    sacc = mfma(ka, eh, sacc);
+                    sacc = mfma(ka, el, sacc);
                 }
-                float4 *sp = reinterpret_cast<float4 *>(&sSt[nt * 16 + fr][d0 + fq]);
-                const float4 old = *sp;
-                *sp = make_float4(fmaf(gC, old.x, sacc[0]), fmaf(gC, old.y, sacc[1]), fmaf(gC, old.z, sacc[2]),
-                                  fmaf(gC, old.w, sacc[3]));
+#pragma unroll
+                for (int i = 0; i < 4; ++i) S[mt][nt][i] = fmaf(gC, S[mt][nt][i], sacc[i]);
+                mirror(mt, nt);
             }
         }
         __syncthreads();
     }
+    store_o(a.nch - 1);
 
-    for (int idx = tid; idx < DK * SLAB / 4; idx += 256) {
-        const int d = idx / (SLAB / 4), v4 = idx % (SLAB / 4);
-        const float4 x = make_float4(sSt[v4 * 4 + 0][d], sSt[v4 * 4 + 1][d], sSt[v4 * 4 + 2][d], sSt[v4 * 4 + 3][d]);
-        *reinterpret_cast<float4 *>(a.ST + ((size_t)h * DK + d) * DV + slab * SLAB + v4 * 4) = x;
-    }
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                a.ST[((size_t)h * DK + 32 * w + 16 * mt + fq + i) * DV + SLAB * slab + 16 * nt + fr] = S[mt][nt][i];
 }
 
 struct PrefillWs {
@@ -499,7 +548,7 @@ extern "C" int qs_gdn_chunk_prefill(const uint16_t *q, const uint16_t *k, const 
     char *ws = static_cast<char *>(workspace);
     PrefillArgs a{};
     a.q = q, a.k = k, a.v = v, a.g = g, a.beta = beta, a.S0 = initial_state, a.ST = final_state, a.o = o;
-    a.Tm = reinterpret_cast<float *>(ws + L.tm);
+    a.Tm = reinterpret_cast<uint16_t *>(ws + L.tm);
     a.P = reinterpret_cast<uint16_t *>(ws + L.p);
     a.sc = reinterpret_cast<float *>(ws + L.sc);
     a.T = T, a.NK = NK, a.NV = NV, a.nch = (T + CH - 1) / CH, a.scale = scale, a.eps = eps;
