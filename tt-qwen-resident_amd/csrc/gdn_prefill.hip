@@ -13,12 +13,13 @@
 // computes it). Two kernels:
 //   chunk_prep  one workgroup per (chunk, key head), fully parallel: K K^T and Q K^T on MFMA from the raw
 //               bf16 rows (exact products, fp32 sums), then for each of the key head's value heads A, P,
-//               the triangular inverse Tm (blocked: 16 x 16 diagonal blocks by forward substitution, then
-//               the off-diagonal blocks by distance) and the per-token scalars, into the workspace;
+//               the triangular inverse Tm (16 x 16 diagonal blocks by forward substitution, then the 32 x 32
+//               and 64 x 64 levels of the block recursion [T1 0; -T2 A21 T1  T2] on fp32 MFMA) and the
+//               per-token scalars, into the workspace (Tm and P as bf16 hi + lo planes);
 //   chunk_walk  one workgroup per (value head, 32-column slab of S): the 128 x 32 fp32 state slab stays
-//               in LDS while the workgroup walks the chunks in order. Every product that touches S or d
+//               on chip while the workgroup walks the chunks in order. Every product that touches S or d
 //               splits the fp32 operand into bf16 hi + lo halves (two MFMAs, three for Tm x X), so the
-//               state keeps fp32-level accuracy (P is kept as bf16 hi + lo planes for the same reason).
+//               state keeps fp32-level accuracy.
 // MFMA: v_mfma_f32_16x16x32_bf16; lane l holds A[l % 16][8 (l / 16) + j], B[8 (l / 16) + j][l % 16] (j < 8)
 // and C[4 (l / 16) + i][l % 16] (i < 4).
 #include "qs_common.h"
@@ -57,6 +58,20 @@ struct PrefillArgs {
 
 // ------------------------------------------------------------------------------------------------ prep
 
+// C += X Y for 16 x 16 fp32 blocks in LDS (row strides xs, ys) on v_mfma_f32_16x16x4_f32: lane l supplies
+// X[l % 16][4 kc + l / 16] and Y[4 kc + l / 16][l % 16]; C is in the accumulator layout C[4 (l / 16) + i][l % 16].
+__device__ __forceinline__ void mm16(f32x4 &c, const float *X, int xs, const float *Y, int ys, int lane) {
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc)
+        c = __builtin_amdgcn_mfma_f32_16x16x4f32(X[(lane & 15) * xs + 4 * kc + (lane >> 4)],
+                                                 Y[(4 * kc + (lane >> 4)) * ys + (lane & 15)], c, 0, 0, 0);
+}
+// an accumulator-layout 16 x 16 block into LDS
+__device__ __forceinline__ void put16(float *D, int ds, f32x4 c, int lane) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) D[(4 * (lane >> 4) + i) * ds + (lane & 15)] = c[i];
+}
+
 __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
     const int c = blockIdx.x / a.NK, kh = blockIdx.x % a.NK;
     const int rep = a.NV / a.NK;
@@ -69,7 +84,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
     __shared__ __align__(16) char s_kq[CH * KP * 2 * 2];
     __shared__ float sKK[CH][FP], sQK[CH][FP];
     __shared__ float s_rk[CH], s_rq[CH], s_G[CH], s_b[CH];
-    __shared__ float sM[3][16][16];
+    __shared__ float sM[4][16][16];
     uint16_t(*sK)[KP] = reinterpret_cast<uint16_t(*)[KP]>(s_kq);
     uint16_t(*sQ)[KP] = reinterpret_cast<uint16_t(*)[KP]>(s_kq + CH * KP * 2);
     float(*sA)[FP] = reinterpret_cast<float(*)[FP]>(s_kq);
@@ -133,13 +148,22 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
     if (tid < CH) s_rk[tid] = rsqrtf(sKK[tid][tid] + a.eps);  // k . k from the exact K K^T diagonal
     // (the barrier after the gates below also orders every sK / sQ read before the first write of sA)
 
+    // gates of the first value head, requested now (wave 0: lane = token)
+    float gnext = 0.f, bnext = 0.f;
+    auto fetch_gates = [&](int hv) {
+        if (w == 0 && lane < nval) {
+            gnext = a.g[(size_t)(t0 + lane) * a.NV + hv];
+            bnext = a.beta[(size_t)(t0 + lane) * a.NV + hv];
+        }
+    };
+    fetch_gates(kh * rep);
+
     for (int j = 0; j < rep; ++j) {
         const int hv = kh * rep + j;
         // 4. gates of value head hv: cumulative log decay (inclusive scan over the 64 tokens)
         if (w == 0) {
-            const bool ok = lane < nval;
-            float gi = ok ? a.g[(size_t)(t0 + lane) * a.NV + hv] : 0.f;
-            const float bi = ok ? a.beta[(size_t)(t0 + lane) * a.NV + hv] : 0.f;
+            float gi = gnext;
+            const float bi = bnext;
 #pragma unroll
             for (int d = 1; d < 64; d <<= 1) {
                 const float up = __shfl_up(gi, d, 64);
@@ -147,65 +171,107 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
             }
             s_G[lane] = gi;
             s_b[lane] = bi;
+            if (j + 1 < rep) fetch_gates(hv + 1);
         }
         __syncthreads();
-        // 5. A (strictly lower) into LDS, P (lower incl. diagonal) to the workspace as bf16
+        // 5. A (strictly lower) into LDS; P (lower incl. diagonal) to the workspace as bf16 hi and lo planes.
+        //    Thread: row i = tid / 4, columns 16 (tid % 4) .. + 15.
         const size_t mat = ((size_t)c * a.NV + hv) * CH * CH;
-        for (int e = tid; e < CH * CH; e += 256) {
-            const int i = e >> 6, jj = e & 63;
-            float av = 0.f, pv = 0.f;
-            if (i >= jj) {
-                const float f = expf(s_G[i] - s_G[jj]);
-                const float rkj = s_rk[jj] * f;
-                if (i > jj) av = s_b[i] * s_rk[i] * rkj * sKK[i][jj];
-                pv = s_rq[i] * rkj * sQK[i][jj];
-            }
-            sA[i][jj] = av;
-            const uint32_t ph = qs::f2bf(pv);
-            a.P[2 * mat + e] = (uint16_t)ph;
-            a.P[2 * mat + CH * CH + e] = (uint16_t)qs::f2bf(pv - qs::bf2f(ph));
-        }
-        __syncthreads();
-        // 6. Tm = (I + A)^-1, blocked: (a) the four 16 x 16 diagonal blocks by forward substitution, one
-        // column per 4 lanes (the k-sum split 4 ways; wave w owns block w, and a column depends only on its
-        // own earlier rows, so no workgroup barrier inside); (b) the off-diagonal blocks by distance
-        // d = 1, 2, 3: T_IJ = -T_II (sum_{K=J}^{I-1} A_IK T_KJ).
         {
-            const int col = tid >> 2, part = tid & 3, b0 = 16 * w;
-            for (int i = b0; i < b0 + 16; ++i) {
-                float s = 0.f;
-                if (i > col)
-                    for (int kk = col + part; kk < i; kk += 4) s = fmaf(sA[i][kk], sT[kk][col], s);
-                s += qs::dpp<0xB1>(s);
-                s += qs::dpp<0x4E>(s);
-                if (part == 0) sT[i][col] = i == col ? 1.f : (i > col ? -s : 0.f);
-                __builtin_amdgcn_wave_barrier();
+            const int i = tid >> 2, j0 = (tid & 3) * 16;
+            const float Gi = s_G[i], rqi = s_rq[i], bki = s_b[i] * s_rk[i];
+            uint32_t ph[8], pl[8];
+#pragma unroll
+            for (int u = 0; u < 16; u += 2) {
+                float pv[2];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int jj = j0 + u + e;
+                    float av = 0.f, p = 0.f;
+                    if (i >= jj) {
+                        const float rkj = s_rk[jj] * expf(Gi - s_G[jj]);
+                        if (i > jj) av = bki * rkj * sKK[i][jj];
+                        p = rqi * rkj * sQK[i][jj];
+                    }
+                    sA[i][jj] = av;
+                    pv[e] = p;
+                }
+                const uint32_t h0 = qs::f2bf(pv[0]), h1 = qs::f2bf(pv[1]);
+                ph[u / 2] = h0 | (h1 << 16);
+                pl[u / 2] = qs::f2bf(pv[0] - qs::bf2f(h0)) | (qs::f2bf(pv[1] - qs::bf2f(h1)) << 16);
             }
+            uint4 *dh = reinterpret_cast<uint4 *>(a.P + 2 * mat + i * CH + j0);
+            uint4 *dl = reinterpret_cast<uint4 *>(a.P + 2 * mat + CH * CH + i * CH + j0);
+            dh[0] = make_uint4(ph[0], ph[1], ph[2], ph[3]);
+            dh[1] = make_uint4(ph[4], ph[5], ph[6], ph[7]);
+            dl[0] = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+            dl[1] = make_uint4(pl[4], pl[5], pl[6], pl[7]);
         }
         __syncthreads();
-        for (int dist = 1; dist < 4; ++dist) {
-            const int nb = 4 - dist;
-            for (int e = tid; e < nb * 256; e += 256) {  // M_IJ = sum_K A_IK T_KJ
-                const int J = e >> 8, I = J + dist, r = (e >> 4) & 15, cc = e & 15;
-                float m = 0.f;
-                for (int kk = 16 * J; kk < 16 * I; ++kk) m = fmaf(sA[16 * I + r][kk], sT[kk][16 * J + cc], m);
-                sM[J][r][cc] = m;
+        // 6. Tm = (I + A)^-1 by 16 x 16 blocks.
+        //  (a) diagonal blocks by forward substitution, wave 0, one column per lane (16 lanes per block):
+        //      t_i = [i == col] - sum_{k < i} A_ik t_k, the column held in registers;
+        if (w == 0) {
+            const int b0 = 16 * (lane >> 4), col = lane & 15;
+            float t[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                float s = i == col ? 1.f : 0.f;
+#pragma unroll
+                for (int k = 0; k < i; ++k) s = fmaf(-sA[b0 + i][b0 + k], t[k], s);
+                t[i] = s;
             }
-            __syncthreads();
-            for (int e = tid; e < nb * 256; e += 256) {  // T_IJ = -T_II M_IJ
-                const int J = e >> 8, I = J + dist, r = (e >> 4) & 15, cc = e & 15;
-                float t = 0.f;
-                for (int kk = 0; kk < 16; ++kk) t = fmaf(sT[16 * I + r][16 * I + kk], sM[J][kk][cc], t);
-                sT[16 * I + r][16 * J + cc] = -t;
-            }
-            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sT[b0 + i][b0 + col] = t[i];
         }
-        // 7. Tm and the per-token scalars to the workspace
-        for (int e = tid; e < CH * CH; e += 256) {
-            const float tv = (e >> 6) >= (e & 63) ? sT[e >> 6][e & 63] : 0.f;
-            const uint32_t th = qs::f2bf(tv);
-            a.Tm[2 * mat + e] = (uint16_t)th;
-            a.Tm[2 * mat + CH * CH + e] = (uint16_t)qs::f2bf(tv - qs::bf2f(th));
+        __syncthreads();
+        //  (b) 32 x 32 diagonal blocks: T_10 = -T_11 (A_10 T_00) and T_32 = -T_33 (A_32 T_22), waves 0 and 1;
+        if (w < 2) {
+            const int b = 32 * w;
+            f32x4 m = {0.f, 0.f, 0.f, 0.f};
+            mm16(m, &sA[b + 16][b], FP, &sT[b][b], FP, lane);
+            put16(&sM[w][0][0], 16, m, lane);
+        }
+        __syncthreads();
+        if (w < 2) {
+            const int b = 32 * w;
+            f32x4 r = {0.f, 0.f, 0.f, 0.f};
+            mm16(r, &sT[b + 16][b + 16], FP, &sM[w][0][0], 16, lane);
+            put16(&sT[b + 16][b], FP, -r, lane);
+        }
+        __syncthreads();
+        //  (c) the lower-left 32 x 32 quarter: X_IJ = sum_{K=J}^{1} A_IK T_KJ, then T_IJ = -sum_{K=2}^{I} T_IK X_KJ,
+        //      wave w owns block (I, J) = (2 + w / 2, w % 2). MFMA 16x16x4 fp32: exact fp32 products.
+        const int I = 2 + (w >> 1), J = w & 1;
+        {
+            f32x4 x = {0.f, 0.f, 0.f, 0.f};
+            for (int K = J; K < 2; ++K) mm16(x, &sA[16 * I][16 * K], FP, &sT[16 * K][16 * J], FP, lane);
+            put16(&sM[w][0][0], 16, x, lane);
+        }
+        __syncthreads();
+        {
+            f32x4 r = {0.f, 0.f, 0.f, 0.f};
+            for (int K = 2; K <= I; ++K) mm16(r, &sT[16 * I][16 * K], FP, &sM[2 * (K - 2) + J][0][0], 16, lane);
+            put16(&sT[16 * I][16 * J], FP, -r, lane);
+        }
+        __syncthreads();
+        // 7. Tm (bf16 hi and lo planes, zero above the diagonal) and the per-token scalars to the workspace
+        {
+            const int i = tid >> 2, j0 = (tid & 3) * 16;
+            uint32_t th[8], tl[8];
+#pragma unroll
+            for (int u = 0; u < 16; u += 2) {
+                const float v0 = i >= j0 + u ? sT[i][j0 + u] : 0.f, v1 = i >= j0 + u + 1 ? sT[i][j0 + u + 1] : 0.f;
+                const uint32_t h0 = qs::f2bf(v0), h1 = qs::f2bf(v1);
+                th[u / 2] = h0 | (h1 << 16);
+                tl[u / 2] = qs::f2bf(v0 - qs::bf2f(h0)) | (qs::f2bf(v1 - qs::bf2f(h1)) << 16);
+            }
+            uint4 *dh = reinterpret_cast<uint4 *>(a.Tm + 2 * mat + i * CH + j0);
+            uint4 *dl = reinterpret_cast<uint4 *>(a.Tm + 2 * mat + CH * CH + i * CH + j0);
+            dh[0] = make_uint4(th[0], th[1], th[2], th[3]);
+            dh[1] = make_uint4(th[4], th[5], th[6], th[7]);
+            dl[0] = make_uint4(tl[0], tl[1], tl[2], tl[3]);
+            dl[1] = make_uint4(tl[4], tl[5], tl[6], tl[7]);
         }
         if (tid < CH) {
             const int i = tid;
