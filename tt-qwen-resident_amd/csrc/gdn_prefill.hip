@@ -290,6 +290,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
 // ------------------------------------------------------------------------------------------------ walk
 
 typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // four fp32 -> bf16 hi = rne(x), lo = rne(x - hi), each as four packed bf16 (8 bytes)
 __device__ __forceinline__ void split4(float x0, float x1, float x2, float x3, uint2 &hi, uint2 &lo) {
@@ -329,7 +330,7 @@ __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
     __shared__ __align__(16) uint16_t sK[CH][KP];
     __shared__ __align__(16) uint16_t sQ[CH][KP];
     __shared__ __align__(16) uint16_t sKt[DK * CH];
-    __shared__ __align__(16) uint16_t sV[CH][SLAB + 8];
+    __shared__ __align__(16) uint16_t sVt[SLAB][CH + 4];
     __shared__ __align__(16) uint16_t sTm[2][CH][TP];
     __shared__ __align__(16) uint16_t sP[2][CH][TP];
     __shared__ __align__(16) uint16_t sX[2][SLAB][TP];
@@ -357,15 +358,17 @@ __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
         }
 
     // per-thread share of a chunk: K and Q rows 2 p + (m & 1), p = pp + 4 w + 16 (m >> 1), 16 bytes at
-    // group kc (each half-wave covers 8 groups x 4 row pairs); V row tid / 4, group tid % 4; Tm and P
-    // 16-byte pieces tid + 256 m of their hi | lo planes; scalars tid and 256 + tid
+    // group kc (each half-wave covers 8 groups x 4 row pairs); V rows 2 (tid / 8) and 2 (tid / 8) + 1,
+    // columns 4 (tid % 8) .. + 3; Tm and P 16-byte pieces tid + 256 m of their hi | lo planes; scalars tid
+    // and 256 + tid. K, Q, V of the next chunk are requested after the first barrier after K S0, Tm, P and
+    // the scalars after the second: no prefetch register is live while K S0 and Q S0 read their operands.
     const int kc = (lane & 7) + 8 * (lane >> 5), pp = (lane >> 3) & 3;
     const size_t krow = (size_t)a.NK * DK * 2, vrow = (size_t)a.NV * DV * 2;  // bytes per token
     // (vectors, not arrays: they stay in registers whatever the unroll order)
     u32x16 pk, pq, ptm, ppm;
-    u32x4 pv;
+    u32x2 pv0, pv1;
     float psc0, psc1;
-    auto fetch = [&](int c) {
+    auto fetch_kqv = [&](int c) {
         const int t0 = c * CH, nv = min(CH, a.T - t0);
         const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.k) + (size_t)t0 * a.NK * DK,
                                                           (short)0, (int)(nv * krow), 0x00020000);
@@ -382,8 +385,11 @@ __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) pk[4 * m + j] = x[j], pq[4 * m + j] = y[j];
         }
-        pv = __builtin_amdgcn_raw_buffer_load_b128(rv, (int)((tid >> 2) * vrow) + (h * DV + SLAB * slab + (tid & 3) * 8) * 2,
-                                                   0, 0);
+        const int vo = (int)(2 * (tid >> 3) * vrow) + (h * DV + SLAB * slab + (tid & 7) * 4) * 2;
+        pv0 = __builtin_amdgcn_raw_buffer_load_b64(rv, vo, 0, 0);
+        pv1 = __builtin_amdgcn_raw_buffer_load_b64(rv, vo + (int)vrow, 0, 0);
+    };
+    auto fetch_tp = [&](int c) {
         const size_t mat = ((size_t)c * a.NV + h) * CH * CH;
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
@@ -396,7 +402,8 @@ __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
         psc0 = scg[tid];
         psc1 = scg[256 + (tid & 63)];
     };
-    fetch(0);
+    fetch_kqv(0);
+    fetch_tp(0);
 
     // a chunk's output rows are stored at the start of the next chunk, after that chunk's operands have
     // been waited for, so the stores never sit in front of a prefetch in the memory counter
@@ -433,7 +440,12 @@ __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
                 *reinterpret_cast<uint32_t *>(&sKt[kt_index(d + 1, t)]) = (ev >> 16) | (od & 0xffff0000u);
             }
         }
-        *reinterpret_cast<uint4 *>(&sV[tid >> 2][(tid & 3) * 8]) = make_uint4(pv[0], pv[1], pv[2], pv[3]);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {  // V^T: token pairs as one 32-bit word per column
+            const int col = (tid & 7) * 4 + 2 * e, t = 2 * (tid >> 3);
+            *reinterpret_cast<uint32_t *>(&sVt[col][t]) = (pv0[e] & 0xffffu) | (pv1[e] << 16);
+            *reinterpret_cast<uint32_t *>(&sVt[col + 1][t]) = (pv0[e] >> 16) | (pv1[e] & 0xffff0000u);
+        }
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             const int idx = tid + 256 * m;
@@ -446,24 +458,33 @@ __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
         if (tid < 64) s_c[4][tid] = psc1;
         if (c > 0) store_o(c - 1);
         __syncthreads();
-        if (c + 1 < a.nch) fetch(c + 1);  // in flight during this chunk
 
-        // ---- K S0 and Q S0 for token tile w (S0 as hi + lo)
+        // ---- K S0 and Q S0 for token tile w (S0 as hi + lo); every fragment is requested before the first
+        // MFMA (the scheduler barrier keeps the reads together)
         f32x4 kacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
         f32x4 qacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        {
+            bf16x8 ak[4], aq[4], bh[4][2], bl[4][2];
 #pragma unroll
-        for (int ks = 0; ks < DK / 32; ++ks) {
-            const bf16x8 ak = frag(&sK[16 * w + fr][ks * 32 + fk]);
-            const bf16x8 aq = frag(&sQ[16 * w + fr][ks * 32 + fk]);
+            for (int ks = 0; ks < DK / 32; ++ks) {
+                ak[ks] = frag(&sK[16 * w + fr][ks * 32 + fk]);
+                aq[ks] = frag(&sQ[16 * w + fr][ks * 32 + fk]);
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                const bf16x8 bh = frag(&sS[0][nt * 16 + fr][ks * 32 + fk]);
-                const bf16x8 bl = frag(&sS[1][nt * 16 + fr][ks * 32 + fk]);
-                kacc[nt] = mfma(ak, bh, kacc[nt]);
-                kacc[nt] = mfma(ak, bl, kacc[nt]);
-                qacc[nt] = mfma(aq, bh, qacc[nt]);
-                qacc[nt] = mfma(aq, bl, qacc[nt]);
+                for (int nt = 0; nt < 2; ++nt) {
+                    bh[ks][nt] = frag(&sS[0][nt * 16 + fr][ks * 32 + fk]);
+                    bl[ks][nt] = frag(&sS[1][nt * 16 + fr][ks * 32 + fk]);
+                }
             }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int ks = 0; ks < DK / 32; ++ks)
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
+                    kacc[nt] = mfma(ak[ks], bh[ks][nt], kacc[nt]);
+                    kacc[nt] = mfma(ak[ks], bl[ks][nt], kacc[nt]);
+                    qacc[nt] = mfma(aq[ks], bh[ks][nt], qacc[nt]);
+                    qacc[nt] = mfma(aq[ks], bl[ks][nt], qacc[nt]);
+                }
         }
 
         // ---- X = beta V - (beta gamma r_k) (K S0), as X^T hi + lo
@@ -474,33 +495,40 @@ __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
                 const int col = nt * 16 + fr;
+                const uint2 v4 = *reinterpret_cast<const uint2 *>(&sVt[col][r0]);
                 uint2 hi, lo;
-                split4(c0.x * qs::bf2f(sV[r0 + 0][col]) - c1.x * kacc[nt][0],
-                       c0.y * qs::bf2f(sV[r0 + 1][col]) - c1.y * kacc[nt][1],
-                       c0.z * qs::bf2f(sV[r0 + 2][col]) - c1.z * kacc[nt][2],
-                       c0.w * qs::bf2f(sV[r0 + 3][col]) - c1.w * kacc[nt][3], hi, lo);
+                split4(c0.x * qs::bf_lo(v4.x) - c1.x * kacc[nt][0], c0.y * qs::bf_hi(v4.x) - c1.y * kacc[nt][1],
+                       c0.z * qs::bf_lo(v4.y) - c1.z * kacc[nt][2], c0.w * qs::bf_hi(v4.y) - c1.w * kacc[nt][3], hi, lo);
                 *reinterpret_cast<uint2 *>(&sX[0][col][r0]) = hi;
                 *reinterpret_cast<uint2 *>(&sX[1][col][r0]) = lo;
             }
         }
         __syncthreads();
+        if (c + 1 < a.nch) fetch_kqv(c + 1);  // lands during d, O, S and the next fill
 
         // ---- d = Tm X (hi*hi + hi*lo + lo*hi), as d^T hi + lo and e^T = (d (r_k gamma_C / gamma))^T hi + lo
         {
             f32x4 dacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+            bf16x8 th[2], tl[2], xh[2][2], xl[2][2];
 #pragma unroll
             for (int ks = 0; ks < CH / 32; ++ks) {
-                const bf16x8 th = frag(&sTm[0][16 * w + fr][ks * 32 + fk]);
-                const bf16x8 tl = frag(&sTm[1][16 * w + fr][ks * 32 + fk]);
+                th[ks] = frag(&sTm[0][16 * w + fr][ks * 32 + fk]);
+                tl[ks] = frag(&sTm[1][16 * w + fr][ks * 32 + fk]);
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt) {
-                    const bf16x8 xh = frag(&sX[0][nt * 16 + fr][ks * 32 + fk]);
-                    const bf16x8 xl = frag(&sX[1][nt * 16 + fr][ks * 32 + fk]);
-                    dacc[nt] = mfma(th, xh, dacc[nt]);
-                    dacc[nt] = mfma(th, xl, dacc[nt]);
-                    dacc[nt] = mfma(tl, xh, dacc[nt]);
+                    xh[ks][nt] = frag(&sX[0][nt * 16 + fr][ks * 32 + fk]);
+                    xl[ks][nt] = frag(&sX[1][nt * 16 + fr][ks * 32 + fk]);
                 }
             }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int ks = 0; ks < CH / 32; ++ks)
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
+                    dacc[nt] = mfma(th[ks], xh[ks][nt], dacc[nt]);
+                    dacc[nt] = mfma(th[ks], xl[ks][nt], dacc[nt]);
+                    dacc[nt] = mfma(tl[ks], xh[ks][nt], dacc[nt]);
+                }
             const int r0 = 16 * w + fq;
             const float4 c3 = *reinterpret_cast<const float4 *>(&s_c[3][r0]);
 #pragma unroll
@@ -516,11 +544,30 @@ __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
             }
         }
         __syncthreads();
+        if (c + 1 < a.nch) fetch_tp(c + 1);
 
-        // ---- O = (gamma r_q) (Q S0) + P d  (hi*hi + hi*lo + lo*hi)
+        // ---- O = (gamma r_q) (Q S0) + P d  (hi*hi + hi*lo + lo*hi) and S = gamma_C S0 + K^T e, where wave w
+        // owns state rows 32 w .. 32 w + 31; the fragments of both are requested before the first MFMA
         {
+            bf16x8 ap[2], apl[2], dh[2][2], dl[2][2], ka[2][2], eh[2][2], el[2][2];
+#pragma unroll
+            for (int ks = 0; ks < CH / 32; ++ks) {
+                ap[ks] = frag(&sP[0][16 * w + fr][ks * 32 + fk]);
+                apl[ks] = frag(&sP[1][16 * w + fr][ks * 32 + fk]);
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
+                    dh[ks][nt] = frag(&sD[0][nt * 16 + fr][ks * 32 + fk]);
+                    dl[ks][nt] = frag(&sD[1][nt * 16 + fr][ks * 32 + fk]);
+                    eh[ks][nt] = frag(&sE[0][nt * 16 + fr][ks * 32 + fk]);
+                    el[ks][nt] = frag(&sE[1][nt * 16 + fr][ks * 32 + fk]);
+                }
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) ka[ks][mt] = frag(&sKt[kt_index(32 * w + 16 * mt + fr, ks * 32 + fk)]);
+            }
             const int r0 = 16 * w + fq;
             const float4 c2 = *reinterpret_cast<const float4 *>(&s_c[2][r0]);
+            const float gC = s_c[4][0];
+            __builtin_amdgcn_sched_barrier(0);
             f32x4 oacc[2];
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
@@ -530,41 +577,28 @@ __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
                 oacc[nt][3] = c2.w * qacc[nt][3];
             }
 #pragma unroll
-            for (int ks = 0; ks < CH / 32; ++ks) {
-                const bf16x8 ap = frag(&sP[0][16 * w + fr][ks * 32 + fk]);
-                const bf16x8 apl = frag(&sP[1][16 * w + fr][ks * 32 + fk]);
+            for (int ks = 0; ks < CH / 32; ++ks)
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt) {
-                    const bf16x8 dh = frag(&sD[0][nt * 16 + fr][ks * 32 + fk]);
-                    const bf16x8 dl = frag(&sD[1][nt * 16 + fr][ks * 32 + fk]);
-                    oacc[nt] = mfma(ap, dh, oacc[nt]);
-                    oacc[nt] = mfma(ap, dl, oacc[nt]);
-                    oacc[nt] = mfma(apl, dh, oacc[nt]);
+                    oacc[nt] = mfma(ap[ks], dh[ks][nt], oacc[nt]);
+                    oacc[nt] = mfma(ap[ks], dl[ks][nt], oacc[nt]);
+                    oacc[nt] = mfma(apl[ks], dh[ks][nt], oacc[nt]);
                 }
-            }
             opend[0] = oacc[0], opend[1] = oacc[1];
-        }
-
-        // ---- S = gamma_C S0 + K^T e : wave w owns state rows 32 w .. 32 w + 31
-        const float gC = s_c[4][0];
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-            const int d0 = 32 * w + 16 * mt;
+            for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+                for (int nt = 0; nt < 2; ++nt) {
+                    f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int ks = 0; ks < CH / 32; ++ks) {
-                    const bf16x8 ka = frag(&sKt[kt_index(d0 + fr, ks * 32 + fk)]);
-                    const bf16x8 eh = frag(&sE[0][nt * 16 + fr][ks * 32 + fk]);
-                    const bf16x8 el = frag(&sE[1][nt * 16 + fr][ks * 32 + fk]);
-                    sacc = mfma(ka, eh, sacc);
-                    sacc = mfma(ka, el, sacc);
+                    for (int ks = 0; ks < CH / 32; ++ks) {
+                        sacc = mfma(ka[ks][mt], eh[ks][nt], sacc);
+                        sacc = mfma(ka[ks][mt], el[ks][nt], sacc);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) S[mt][nt][i] = fmaf(gC, S[mt][nt][i], sacc[i]);
+                    mirror(mt, nt);
                 }
-#pragma unroll
-                for (int i = 0; i < 4; ++i) S[mt][nt][i] = fmaf(gC, S[mt][nt][i], sacc[i]);
-                mirror(mt, nt);
-            }
         }
         __syncthreads();
     }
