@@ -69,7 +69,7 @@ int qs_gdn_decode_step(const uint16_t *q, const uint16_t *k, const uint16_t *v, 
                        float *state, uint16_t *o, int B, int NK, int NV, int DK, int DV, float scale, float eps,
                        void *stream);
 
-/* Workspace of qs_gdn_decode_fused: one self-resetting counter per (user, key head). */
+/* Workspace of qs_gdn_decode_fused: two self-resetting counters (q and k channels) per (user, key head). */
 size_t qs_gdn_workspace_bytes(int B, int NK);
 
 /* Conv1d update + L2-norm + delta rule of one decode step in one launch (a1+a2+a4): the GDN mixer state

@@ -62,7 +62,7 @@ def test_rejects_bad_arguments():
 
 def test_workspace_sizes():
     L = Q.lib()
-    assert L.qs_gdn_workspace_bytes(8, 16) == 8 * 16 * 4
+    assert L.qs_gdn_workspace_bytes(8, 16) == 8 * 16 * 2 * 4
     one = L.qs_paged_attention_workspace_bytes(1, 1, 24, 4, 256, 512, 8)
     assert one > 64 * 4 * 6 * 256 * 4  # at least the level-0 partials of 64 splits
     assert L.qs_paged_attention_workspace_bytes(1, 1, 24, 4, 128, 512, 8) == 0

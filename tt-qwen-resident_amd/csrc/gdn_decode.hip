@@ -31,7 +31,9 @@ struct GdnArgs {
     const float *s_in;          // [B, NV, DK, DV]
     float *s_out;               // decode: == s_in (in place); verify: [T, B, NV, DK, DV]
     uint16_t *o;                // [B, T, NV, DV]
-    int *counters;              // decode + conv: [B, NK] self-resetting
+    int *counters;              // decode + conv: [B, NK, 2] (q, k) self-resetting
+    const int *in_slot;         // verify, nullable: [B] slot of s_in / conv_in holding user b's input
+    int n_slots;                // slots in s_in / conv_in
     int B, T, NK, NV, C;
     float scale, eps;
 };
@@ -48,13 +50,13 @@ struct ConvPair {
 };
 
 template <int TM>
-__device__ __forceinline__ ConvPair<TM> conv_load(const GdnArgs &a, int b, int c, int T) {
+__device__ __forceinline__ ConvPair<TM> conv_load(const GdnArgs &a, const uint16_t *conv_b, int b, int c, int T) {
     ConvPair<TM> in;
-    in.h = *reinterpret_cast<const u32x3 *>(a.conv_in + ((size_t)b * a.C + c) * (KC - 1));
+    in.h = *reinterpret_cast<const u32x3 *>(conv_b + (size_t)c * (KC - 1));
     in.tw = *reinterpret_cast<const uint4 *>(a.taps + (size_t)c * KC);
 #pragma unroll
-    for (int t = 0; t < TM; ++t)
-        if (t < T) in.x[t] = *reinterpret_cast<const uint32_t *>(a.x + ((size_t)b * T + t) * a.C + c);
+    for (int t = 0; t < TM; ++t)  // tokens past T repeat token 0 (in range; their results are never used)
+        in.x[t] = *reinterpret_cast<const uint32_t *>(a.x + ((size_t)b * T + (t < T ? t : 0)) * a.C + c);
     return in;
 }
 
@@ -74,8 +76,7 @@ __device__ __forceinline__ uint32_t conv_seq(const ConvPair<TM> &in, int e, int 
 // y[e][t] receives the bf16-rounded outputs as fp32, yb[t] their bits packed (c | c + 1 << 16).
 template <int TM>
 __device__ __forceinline__ void conv_run(const ConvPair<TM> &in, int T, float y[2][TM], uint32_t yb[TM]) {
-#pragma unroll
-    for (int t = 0; t < TM; ++t) yb[t] = 0;
+    float sv[2][TM];
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
         const uint32_t tw0 = e ? in.tw.z : in.tw.x, tw1 = e ? in.tw.w : in.tw.y;
@@ -83,19 +84,22 @@ __device__ __forceinline__ void conv_run(const ConvPair<TM> &in, int T, float y[
         float h0 = qs::bf2f(conv_seq(in, e, 0)), h1 = qs::bf2f(conv_seq(in, e, 1)), h2 = qs::bf2f(conv_seq(in, e, 2));
 #pragma unroll
         for (int t = 0; t < TM; ++t) {
-            if (t >= T) break;
             const float xt = qs::bf2f(conv_seq(in, e, 3 + t));
             float acc = h0 * w0;
             acc = acc + h1 * w1;
             acc = acc + h2 * w2;
             acc = acc + xt * w3;
-            const uint32_t r = qs::f2bf(qs::silu(acc));
-            y[e][t] = qs::bf2f(r);
-            yb[t] |= r << (16 * e);
+            sv[e][t] = qs::silu_fast(acc);
             h0 = h1;
             h1 = h2;
             h2 = xt;
         }
+    }
+#pragma unroll
+    for (int t = 0; t < TM; ++t) {
+        yb[t] = qs::cvt_pk_bf16(sv[0][t], sv[1][t]);
+        y[0][t] = qs::bf_lo(yb[t]);
+        y[1][t] = qs::bf_hi(yb[t]);
     }
 }
 
@@ -124,11 +128,6 @@ __device__ __forceinline__ void conv_commit(const GdnArgs &a, const ConvPair<TM>
         *reinterpret_cast<u32x3 *>(a.conv_out + ((size_t)b * a.C + c) * (KC - 1)) = window(0);
 }
 
-// One wavefront per slab. The conv runs on all 64 lanes: q channels 2 lane, 2 lane + 1 of key head kh,
-// the same k channels, and the slab's v channels 2 (lane % 16), + 1 (lanes 16..63 compute copies).
-// Memory order: every load is issued first (conv inputs, then the state, then the gates as scalar loads);
-// no global store or atomic is issued before the state loads are consumed, because vmcnt counts loads and
-// stores together and a store in flight would turn each wait for a state load into a wait for everything.
 // Sum over the row groups of a slab wave (lane bits log2(CG) .. 5) as a butterfly in a fixed order: every
 // lane ends with bit-identical sums of its column group.
 template <int CG>
@@ -140,13 +139,34 @@ __device__ __forceinline__ float sum_row_groups(float x) {
     return x;
 }
 
-template <bool CONV, bool VERIFY, int SLAB>
-__global__ __launch_bounds__(64) void gdn_kernel(GdnArgs a) {
-    constexpr int TM = VERIFY ? TMAX : 1;
+// One workgroup of NW wavefronts per (user, value head, SLAB-column slab); wave w holds rows
+// w * RW .. (w + 1) * RW - 1 (RW = 128 / NW) of the slab, lane (rg = lane / CG, cg = lane % CG) rows
+// w * RW + rg + RG i (i < RPL), columns 4 cg .. 4 cg + 3. NW = 1 at large batch (each wave streams a
+// 16 KB slab); NW = 4 when one wave per slab would leave the chip underfilled (small batch), which also
+// spreads the conv prologue over three waves and cuts the serial work per token by 4, for one LDS
+// exchange per token.
+// Per token both column reductions are taken from the state before the update, in one pass:
+//     p_v = sum_k k_k S_kv,  r_v = sum_k q_k S_kv,  delta_v = beta (v_v - e^g p_v)
+//     S'_kv = e^g S_kv + k_k delta_v,  o_v = q^T S'_v = e^g r_v + (q . k) delta_v
+// so the update and the stores of S' follow the reduction with no second reduction in between.
+// The conv: q channels 2 lane, 2 lane + 1 of key head kh on wave WQ, the same k channels on wave WK, the
+// slab's v channels 2 (lane % (SLAB / 2)), + 1 on wave WV (all wave 0 when NW = 1).
+// Memory order: every load is issued first (conv inputs, then the state, then the gates as scalar loads);
+// no global store or atomic is issued before the state loads are consumed, because vmcnt counts loads and
+// stores together and a store in flight would turn each wait for a state load into a wait for everything.
+// in_slot (verify only, nullable): user b's input state and conv state are slot in_slot[b] of s_in and
+// conv_in ([n_slots, B, ...]); a slot outside [0, n_slots) reads slot 0.
+template <bool CONV, bool VERIFY, int TM, int SLAB, int NW>
+__global__ __launch_bounds__(64 * NW) void gdn_kernel(GdnArgs a) {
     constexpr int NSLAB = DV / SLAB;
     constexpr int CG = SLAB / 4;   // column groups of 4 (lane % CG)
-    constexpr int RG = 64 / CG;    // row groups (lane / CG): lane holds rows rg + RG i
-    constexpr int RPL = DK / RG;   // rows per lane
+    constexpr int RG = 64 / CG;    // row groups (lane / CG)
+    constexpr int RW = DK / NW;    // rows per wave
+    constexpr int RPL = RW / RG;   // rows per lane
+    static_assert(RPL >= 1 && RW % RG == 0 && (VERIFY || TM == 1), "slab shape");
+    constexpr int WQ = 0;
+    constexpr int WK = NW >= 4 ? 1 : 0;
+    constexpr int WV = NW >= 4 ? 2 : NW - 1;
     const int nwg = a.B * a.NV * NSLAB;
     const int lid = qs::xcd_logical(blockIdx.x, nwg);
     const int s = lid % NSLAB;
@@ -154,148 +174,207 @@ __global__ __launch_bounds__(64) void gdn_kernel(GdnArgs a) {
     const int b = lid / (NSLAB * a.NV);
     const int rep = a.NV / a.NK;
     const int kh = h / rep;
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int w = NW > 1 ? (int)(threadIdx.x >> 6) : 0;
     const int cg = lane % CG, rg = lane / CG;
     const int T = VERIFY ? a.T : 1;
     const bool kq_owner = (h % rep == 0) && (s == 0);  // writes the shared q/k channel outputs
+    int slot = 0;
+    if (VERIFY && a.in_slot) {
+        slot = a.in_slot[b];
+        slot = (slot >= 0 && slot < a.n_slots) ? slot : 0;
+    }
+    const size_t user_in = (size_t)slot * a.B + b;  // this user's input in s_in / conv_in
 
-    // q / k normalised per token, row r stored at (r % RG) * RPL + r / RG: lane rg reads its RPL rows as
-    // contiguous 16-byte pieces
+    // q / k normalised per token, row r = w' RW + g + RG i stored at w' RW + g RPL + i: lane rg of wave w
+    // reads its RPL rows as contiguous pieces
     __shared__ __align__(16) float s_qn[TM][DK];
     __shared__ __align__(16) float s_kn[TM][DK];
     __shared__ __align__(16) float s_v[TM][SLAB];
+    __shared__ __align__(16) f32x4 s_red[NW > 1 ? 2 : 1][NW][2][CG];  // per token parity: wave column sums
 
-    // 1. Loads. Conv inputs (raw bits, untouched until used), the state slab, the gates.
+    // 1. Loads. Conv inputs (raw bits, untouched until used), this wave's state rows, the gates.
     const int qd = a.NK * DK;
     const int cq = kh * DK + 2 * lane, ck = qd + cq;                           // q, k channel pairs
     const int cv = 2 * qd + h * DV + s * SLAB + 2 * (lane & (SLAB / 2 - 1));  // v channel pair
+    const uint16_t *conv_b = CONV ? a.conv_in + user_in * a.C * (KC - 1) : nullptr;
     ConvPair<TM> inq, ink, inv;
     if (CONV) {
-        inq = conv_load<TM>(a, b, cq, T);
-        ink = conv_load<TM>(a, b, ck, T);
-        inv = conv_load<TM>(a, b, cv, T);
+        if (w == WQ) inq = conv_load<TM>(a, conv_b, b, cq, T);
+        if (w == WK) ink = conv_load<TM>(a, conv_b, b, ck, T);
+        if (w == WV) inv = conv_load<TM>(a, conv_b, b, cv, T);
     }
     const size_t head = (size_t)(b * a.NV + h) * DK * DV;
-    const float *sp = a.s_in + head + s * SLAB + cg * 4;
+    const float *sp = a.s_in + (user_in * a.NV + h) * DK * DV + s * SLAB + cg * 4 + (size_t)(w * RW + rg) * DV;
     f32x4 S[RPL];  // streamed once per step: nontemporal loads and stores keep it from thrashing L2 / MALL
 #pragma unroll
     for (int i = 0; i < RPL; ++i)
-        S[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(sp + (size_t)(rg + RG * i) * DV));
+        S[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(sp + (size_t)(RG * i) * DV));
     float gdec[TM], gbeta[TM];
 #pragma unroll
     for (int t = 0; t < TM; ++t) {
-        if (t < T) {
-            const int gi = ((b * T) + t) * a.NV + h;
-            gdec[t] = a.g[gi];
-            gbeta[t] = a.beta[gi];
-        }
+        const int gi = ((b * T) + (t < T ? t : 0)) * a.NV + h;
+        gdec[t] = a.g[gi];
+        gbeta[t] = a.beta[gi];
     }
 
-    // 2. q, k (rows 2 lane, 2 lane + 1) and the v slab for every token, L2 norms (q times scale).
+    // 2. q, k (rows 2 lane, 2 lane + 1) and the v slab for every token; L2 norms (q times scale).
     float qv[2][TM], kv[2][TM], vv[2][TM];
     uint32_t yq[TM], yk[TM], yv[TM];
     if (CONV) {
-        conv_run<TM>(inq, T, qv, yq);
-        conv_run<TM>(ink, T, kv, yk);
-        conv_run<TM>(inv, T, vv, yv);
+        if (w == WQ) conv_run<TM>(inq, T, qv, yq);
+        if (w == WK) conv_run<TM>(ink, T, kv, yk);
+        if (w == WV) conv_run<TM>(inv, T, vv, yv);
     } else {
 #pragma unroll
         for (int t = 0; t < TM; ++t) {
             if (t >= T) break;
             const size_t qk0 = (((size_t)b * T + t) * a.NK + kh) * DK + 2 * lane;
-            const uint32_t q2 = *reinterpret_cast<const uint32_t *>(a.q + qk0);
-            const uint32_t k2 = *reinterpret_cast<const uint32_t *>(a.k + qk0);
-            const uint32_t v2 = *reinterpret_cast<const uint32_t *>(
-                a.v + (((size_t)b * T + t) * a.NV + h) * DV + s * SLAB + 2 * (lane & (SLAB / 2 - 1)));
-            qv[0][t] = qs::bf_lo(q2), qv[1][t] = qs::bf_hi(q2);
-            kv[0][t] = qs::bf_lo(k2), kv[1][t] = qs::bf_hi(k2);
-            vv[0][t] = qs::bf_lo(v2), vv[1][t] = qs::bf_hi(v2);
+            if (w == WQ) {
+                const uint32_t q2 = *reinterpret_cast<const uint32_t *>(a.q + qk0);
+                qv[0][t] = qs::bf_lo(q2), qv[1][t] = qs::bf_hi(q2);
+            }
+            if (w == WK) {
+                const uint32_t k2 = *reinterpret_cast<const uint32_t *>(a.k + qk0);
+                kv[0][t] = qs::bf_lo(k2), kv[1][t] = qs::bf_hi(k2);
+            }
+            if (w == WV) {
+                const uint32_t v2 = *reinterpret_cast<const uint32_t *>(
+                    a.v + (((size_t)b * T + t) * a.NV + h) * DV + s * SLAB + 2 * (lane & (SLAB / 2 - 1)));
+                vv[0][t] = qs::bf_lo(v2), vv[1][t] = qs::bf_hi(v2);
+            }
         }
     }
-    const int p0 = ((2 * lane) % RG) * RPL + (2 * lane) / RG;  // stored position of row 2 lane (+ RPL: row + 1)
+    {
+        const int r0 = 2 * lane, rr = r0 % RW;
+        const int p0 = (r0 / RW) * RW + (rr % RG) * RPL + rr / RG;  // stored position of row r0 (+ RPL: r0 + 1)
 #pragma unroll
-    for (int t = 0; t < TM; ++t) {
-        if (t >= T) break;
-        const float rq = rsqrtf(qs::wave_sum_dpp(qv[0][t] * qv[0][t] + qv[1][t] * qv[1][t]) + a.eps) * a.scale;
-        const float rk = rsqrtf(qs::wave_sum_dpp(kv[0][t] * kv[0][t] + kv[1][t] * kv[1][t]) + a.eps);
-        s_qn[t][p0] = qv[0][t] * rq;
-        s_qn[t][p0 + RPL] = qv[1][t] * rq;
-        s_kn[t][p0] = kv[0][t] * rk;
-        s_kn[t][p0 + RPL] = kv[1][t] * rk;
-        if (lane < SLAB / 2) *reinterpret_cast<float2 *>(&s_v[t][2 * lane]) = make_float2(vv[0][t], vv[1][t]);
+        for (int t = 0; t < TM; ++t) {
+            if (t >= T) break;
+            if (w == WQ) {
+                const float rq = rsqrtf(qs::wave_sum_dpp(qv[0][t] * qv[0][t] + qv[1][t] * qv[1][t]) + a.eps) * a.scale;
+                s_qn[t][p0] = qv[0][t] * rq;
+                s_qn[t][p0 + RPL] = qv[1][t] * rq;
+            }
+            if (w == WK) {
+                const float rk = rsqrtf(qs::wave_sum_dpp(kv[0][t] * kv[0][t] + kv[1][t] * kv[1][t]) + a.eps);
+                s_kn[t][p0] = kv[0][t] * rk;
+                s_kn[t][p0 + RPL] = kv[1][t] * rk;
+            }
+            if (w == WV && lane < SLAB / 2)
+                *reinterpret_cast<float2 *>(&s_v[t][2 * lane]) = make_float2(vv[0][t], vv[1][t]);
+        }
     }
-    __builtin_amdgcn_wave_barrier();
+    if (NW > 1)
+        __syncthreads();
+    else
+        __builtin_amdgcn_wave_barrier();
 
-    // 3. Delta rule, token by token, on the slab held in registers.
+    // 3. Delta rule, token by token, on the rows held in registers.
     int arrived = 0;
     for (int t = 0; t < T; ++t) {
         const int gi = ((b * T) + t) * a.NV + h;
         const float decay = expf(gdec[t]);
         const float bt = gbeta[t];
+        float qk = 0.f;  // q . k of the token (wave 0 writes o)
+        if (w == 0) {
+            const float2 q2 = *reinterpret_cast<const float2 *>(&s_qn[t][2 * lane]);
+            const float2 k2 = *reinterpret_cast<const float2 *>(&s_kn[t][2 * lane]);
+            qk = qs::wave_sum_dpp(q2.x * k2.x + q2.y * k2.y);
+        }
         float kn[RPL], qn[RPL];
 #pragma unroll
-        for (int i4 = 0; i4 < RPL / 4; ++i4) {
-            const float4 k4 = *reinterpret_cast<const float4 *>(&s_kn[t][rg * RPL + 4 * i4]);
-            const float4 q4 = *reinterpret_cast<const float4 *>(&s_qn[t][rg * RPL + 4 * i4]);
-            kn[4 * i4] = k4.x, kn[4 * i4 + 1] = k4.y, kn[4 * i4 + 2] = k4.z, kn[4 * i4 + 3] = k4.w;
-            qn[4 * i4] = q4.x, qn[4 * i4 + 1] = q4.y, qn[4 * i4 + 2] = q4.z, qn[4 * i4 + 3] = q4.w;
+        for (int i4 = 0; i4 < (RPL + 3) / 4; ++i4) {
+            const float *kp = &s_kn[t][w * RW + rg * RPL + 4 * i4];
+            const float *qp = &s_qn[t][w * RW + rg * RPL + 4 * i4];
+            if constexpr (RPL >= 4) {
+                const float4 k4 = *reinterpret_cast<const float4 *>(kp);
+                const float4 q4 = *reinterpret_cast<const float4 *>(qp);
+                kn[4 * i4] = k4.x, kn[4 * i4 + 1] = k4.y, kn[4 * i4 + 2] = k4.z, kn[4 * i4 + 3] = k4.w;
+                qn[4 * i4] = q4.x, qn[4 * i4 + 1] = q4.y, qn[4 * i4 + 2] = q4.z, qn[4 * i4 + 3] = q4.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < RPL; ++j) kn[j] = kp[j], qn[j] = qp[j];
+            }
         }
         const float4 v4 = *reinterpret_cast<const float4 *>(&s_v[t][cg * 4]);
-        float p[4] = {0.f, 0.f, 0.f, 0.f};
+        float p[4] = {0.f, 0.f, 0.f, 0.f}, r[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int i = 0; i < RPL; ++i) {
-            const float kd = decay * kn[i];
-            p[0] = fmaf(kd, S[i].x, p[0]);
-            p[1] = fmaf(kd, S[i].y, p[1]);
-            p[2] = fmaf(kd, S[i].z, p[2]);
-            p[3] = fmaf(kd, S[i].w, p[3]);
+            p[0] = fmaf(kn[i], S[i].x, p[0]);
+            p[1] = fmaf(kn[i], S[i].y, p[1]);
+            p[2] = fmaf(kn[i], S[i].z, p[2]);
+            p[3] = fmaf(kn[i], S[i].w, p[3]);
+            r[0] = fmaf(qn[i], S[i].x, r[0]);
+            r[1] = fmaf(qn[i], S[i].y, r[1]);
+            r[2] = fmaf(qn[i], S[i].z, r[2]);
+            r[3] = fmaf(qn[i], S[i].w, r[3]);
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) p[j] = sum_row_groups<CG>(p[j]);
+        for (int j = 0; j < 4; ++j) {
+            p[j] = sum_row_groups<CG>(p[j]);
+            r[j] = sum_row_groups<CG>(r[j]);
+        }
+        if constexpr (NW > 1) {
+            // the waves' column sums, added in wave order by every wave (bit-identical everywhere); two
+            // buffers by token parity, so one barrier per token suffices
+            auto &red = s_red[t & 1];
+            if (rg == 0) {
+                red[w][0][cg] = f32x4{p[0], p[1], p[2], p[3]};
+                red[w][1][cg] = f32x4{r[0], r[1], r[2], r[3]};
+            }
+            __syncthreads();
+            f32x4 P = red[0][0][cg], R = red[0][1][cg];
+#pragma unroll
+            for (int ww = 1; ww < NW; ++ww) {
+                P += red[ww][0][cg];
+                R += red[ww][1][cg];
+            }
+            p[0] = P.x, p[1] = P.y, p[2] = P.z, p[3] = P.w;
+            r[0] = R.x, r[1] = R.y, r[2] = R.z, r[3] = R.w;
+        }
         if (CONV && t == 0) {
             // The state loads are consumed: now the conv's global outputs. v channels of this slab belong
             // to this workgroup alone (shifted in place / snapshotted here); the q/k channels are read by
-            // the rep * NSLAB workgroups of key head kh, so in decode each counts itself in (its reads
-            // were consumed above) and the last to arrive writes the shifted state at the end and re-arms
-            // the counter. The count's return is waited for only there.
-            conv_commit<VERIFY, TM>(a, inv, yv, b, cv, T, lane < SLAB / 2, lane < SLAB / 2);
-            conv_commit<VERIFY, TM>(a, inq, yq, b, cq, T, kq_owner, VERIFY && kq_owner);
-            conv_commit<VERIFY, TM>(a, ink, yk, b, ck, T, kq_owner, VERIFY && kq_owner);
-            if (!VERIFY && lane == 0) arrived = atomicAdd(a.counters + b * a.NK + kh, 1);
+            // the rep * NSLAB workgroups of key head kh, so in decode the wave holding them counts itself
+            // in (its reads were consumed above; q and k count separately when different waves hold them)
+            // and the last to arrive writes the shifted state at the end and re-arms the counter. The
+            // count's return is waited for only there.
+            if (w == WV) conv_commit<VERIFY, TM>(a, inv, yv, b, cv, T, lane < SLAB / 2, lane < SLAB / 2);
+            if (w == WQ) conv_commit<VERIFY, TM>(a, inq, yq, b, cq, T, kq_owner, VERIFY && kq_owner);
+            if (w == WK) conv_commit<VERIFY, TM>(a, ink, yk, b, ck, T, kq_owner, VERIFY && kq_owner);
+            if (!VERIFY && (w == WQ || w == WK) && lane == 0)
+                arrived = atomicAdd(a.counters + (b * a.NK + kh) * 2 + (w == WQ ? 0 : 1), 1);
         }
-        const float dl[4] = {bt * (v4.x - p[0]), bt * (v4.y - p[1]), bt * (v4.z - p[2]), bt * (v4.w - p[3])};
-        float po[4] = {0.f, 0.f, 0.f, 0.f};
+        float dl[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dl[j] = bt * ((&v4.x)[j] - decay * p[j]);
+        float *dst = (VERIFY ? a.s_out + (size_t)t * a.B * a.NV * DK * DV : a.s_out) + head + s * SLAB + cg * 4 +
+                     (size_t)(w * RW + rg) * DV;
 #pragma unroll
         for (int i = 0; i < RPL; ++i) {
             S[i].x = fmaf(kn[i], dl[0], decay * S[i].x);
             S[i].y = fmaf(kn[i], dl[1], decay * S[i].y);
             S[i].z = fmaf(kn[i], dl[2], decay * S[i].z);
             S[i].w = fmaf(kn[i], dl[3], decay * S[i].w);
-            po[0] = fmaf(qn[i], S[i].x, po[0]);
-            po[1] = fmaf(qn[i], S[i].y, po[1]);
-            po[2] = fmaf(qn[i], S[i].z, po[2]);
-            po[3] = fmaf(qn[i], S[i].w, po[3]);
+            __builtin_nontemporal_store(S[i], reinterpret_cast<f32x4 *>(dst + (size_t)(RG * i) * DV));
         }
-        float *dst = VERIFY ? a.s_out + (size_t)t * a.B * a.NV * DK * DV + head + s * SLAB + cg * 4
-                            : a.s_out + head + s * SLAB + cg * 4;
+        if (w == 0 && lane < CG) {
+            float po[4];
 #pragma unroll
-        for (int i = 0; i < RPL; ++i)
-            __builtin_nontemporal_store(S[i], reinterpret_cast<f32x4 *>(dst + (size_t)(rg + RG * i) * DV));
-#pragma unroll
-        for (int j = 0; j < 4; ++j) po[j] = sum_row_groups<CG>(po[j]);
-        if (lane < CG) {
+            for (int j = 0; j < 4; ++j) po[j] = fmaf(qk, dl[j], decay * r[j]);
             uint2 pk;
             pk.x = qs::pack_bf2(po[0], po[1]);
             pk.y = qs::pack_bf2(po[2], po[3]);
             *reinterpret_cast<uint2 *>(a.o + (size_t)gi * DV + s * SLAB + cg * 4) = pk;
         }
     }
-    if (CONV && !VERIFY) {
+    if (CONV && !VERIFY && (w == WQ || w == WK)) {
         const int last = __builtin_amdgcn_readfirstlane(arrived) == rep * NSLAB - 1;
         if (last) {
-            if (lane == 0) atomicExch(a.counters + b * a.NK + kh, 0);
-            conv_commit<false, TM>(a, inq, yq, b, cq, T, false, true);
-            conv_commit<false, TM>(a, ink, yk, b, ck, T, false, true);
+            if (lane == 0) atomicExch(a.counters + (b * a.NK + kh) * 2 + (w == WQ ? 0 : 1), 0);
+            if (w == WQ) conv_commit<false, TM>(a, inq, yq, b, cq, T, false, true);
+            if (w == WK) conv_commit<false, TM>(a, ink, yk, b, ck, T, false, true);
         }
     }
 }
@@ -316,7 +395,7 @@ __global__ __launch_bounds__(256) void conv1d_update_kernel(const uint16_t *x, u
     acc = acc + h1 * qs::bf_hi(tw.x);
     acc = acc + h2 * qs::bf_lo(tw.y);
     acc = acc + xt * qs::bf_hi(tw.y);
-    y[i] = (uint16_t)qs::f2bf(qs::silu(acc));
+    y[i] = (uint16_t)(qs::cvt_pk_bf16(qs::silu_fast(acc), 0.f) & 0xffffu);
     st[0] = st[1];
     st[1] = st[2];
     st[2] = (uint16_t)xr;
@@ -389,12 +468,26 @@ __global__ __launch_bounds__(256) void rollback_kernel(const float *states_out, 
     if (blockIdx.x == 0 && z == 0 && threadIdx.x == 0 && seq_lens) seq_lens[b] = base_lens[b] + acc;
 }
 
-// 32-column slabs (B * NV * 4 waves) for decode and verify alike, so a one-token verify reproduces decode
-// bit for bit (the column sums run in the same order). 16-column slabs (SLAB = 16, twice the waves) make a
-// batch-1 verify about 9% faster but sum in another order.
+// 32-column slabs. One wave per slab when that gives at least 1024 waves (batch >= 6 at 48 value heads);
+// below that each slab's rows are split over 4 waves so the grid fills the chip. The choice depends on the
+// batch only, so a one-token verify reproduces decode bit for bit at every batch. Verify kernels are
+// compiled for up to 4 and up to 8 tokens.
+template <bool CONV, bool VERIFY, int TM>
+void launch_gdn_tm(const GdnArgs &a, hipStream_t st) {
+    const int grid = a.B * a.NV * (DV / 32);
+    if (grid >= 1024)
+        gdn_kernel<CONV, VERIFY, TM, 32, 1><<<grid, 64, 0, st>>>(a);
+    else
+        gdn_kernel<CONV, VERIFY, TM, 32, 4><<<grid, 256, 0, st>>>(a);
+}
 template <bool CONV, bool VERIFY>
 void launch_gdn(const GdnArgs &a, hipStream_t st) {
-    gdn_kernel<CONV, VERIFY, 32><<<a.B * a.NV * (DV / 32), 64, 0, st>>>(a);
+    if constexpr (!VERIFY)
+        launch_gdn_tm<CONV, VERIFY, 1>(a, st);
+    else if (a.T <= 4)
+        launch_gdn_tm<CONV, VERIFY, 4>(a, st);
+    else
+        launch_gdn_tm<CONV, VERIFY, TMAX>(a, st);
 }
 
 // The conv reads channel pairs with 4-, 12- and 16-byte loads.
@@ -446,7 +539,7 @@ extern "C" int qs_gdn_decode_step(const uint16_t *q, const uint16_t *k, const ui
     return qs::launch_status("qs_gdn_decode_step");
 }
 
-extern "C" size_t qs_gdn_workspace_bytes(int B, int NK) { return (size_t)(B > 0 ? B : 0) * (NK > 0 ? NK : 0) * 4; }
+extern "C" size_t qs_gdn_workspace_bytes(int B, int NK) { return (size_t)(B > 0 ? B : 0) * (NK > 0 ? NK : 0) * 8; }
 
 extern "C" int qs_gdn_decode_fused(const uint16_t *x, uint16_t *conv_state, const uint16_t *taps, const float *g,
                                    const float *beta, float *state, uint16_t *o, uint16_t *y_out, void *workspace,

@@ -26,6 +26,13 @@ __device__ __forceinline__ uint32_t f2bf(float f) {
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
 
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+// SiLU from the hardware exponential and reciprocal (v_exp_f32, v_rcp_f32; each within 1 ulp):
+// x / (1 + 2^(-x log2 e)). Within a few fp32 ulps of x / (1 + e^-x), so its bf16 rounding agrees with the
+// correctly rounded value except on rare ties; -inf exponent arguments give -0.
+__device__ __forceinline__ float silu_fast(float x) {
+    const float e = __builtin_amdgcn_exp2f(-x * 1.4426950408889634f);
+    return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
 
 // sum / max over the 64 lanes of a wavefront (butterfly: every lane ends with the result)
 __device__ __forceinline__ float wave_sum(float v) {
