@@ -203,21 +203,25 @@ def bench_attn_layer(args, torch):
 
 
 def bench_verify(args, torch):
+    """The MTP verify step with acceptance by slot selection: the graph holds two consecutive steps (the
+    two snapshot sets alternate), each with its KV lengths restored for the replay; time per step = half."""
     from qwen36_state.decode import VerifyStep
 
-    vs = VerifyStep(1, 8192, T=4, device="cuda:0")
+    vs = VerifyStep(1, 8192, T=4, device="cuda:0", pages_per_split=args.pps_verify)
 
     def fn():
-        vs.verify()
-        vs.rollback()
-        vs.reset_lengths()
+        for _ in range(2):
+            vs.verify()
+            vs.rollback()
+            vs.reset_lengths()
 
-    ms, _ = graph_time(torch, fn, args.steps, args.warmup)
+    ms2, _ = graph_time(torch, fn, args.steps, args.warmup)
+    ms = ms2 / 2
     nbytes = vs.bytes_per_step()
     return line(args, "MTP verify step, batch 1, 8192 positions, 1 + 3 draft tokens through 48 GDN + 16 attention "
-                "layers, then rollback to a seeded accepted length (state copies)", nbytes, ms,
+                "layers, then acceptance of a seeded length by snapshot-slot selection", nbytes, ms,
                 roofline("verify_step", nbytes, ms),
-                dict(rollback_copy_bytes=vs.rollback_bytes(), accept=vs.accept.tolist()))  # fmt: skip
+                dict(rollback_copy_bytes=vs.rollback_bytes(), accept=vs.accept.tolist(), pages_per_split=vs.pps))  # fmt: skip
 
 
 def bench_prefill(args, torch):
@@ -303,7 +307,8 @@ def main():
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--layers", type=int, default=64)
     ap.add_argument("--pps", type=int, default=4, help="pages per split-K workgroup (step workload)")
-    ap.add_argument("--pps-attn1", type=int, default=4, help="pages per split (attn-layer workload)")
+    ap.add_argument("--pps-attn1", type=int, default=8, help="pages per split (attn-layer workload)")
+    ap.add_argument("--pps-verify", type=int, default=2, help="pages per split (verify-step workload)")
     ap.add_argument("--kernel-reps", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     args = ap.parse_args()

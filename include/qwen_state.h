@@ -91,6 +91,25 @@ int qs_gdn_verify_step(const uint16_t *x, const uint16_t *conv_state_in, uint16_
                        float *states_out, uint16_t *o, uint16_t *y_out, int B, int T, int NK, int NV, int DK,
                        int DV, int K, float scale, float eps, void *stream);
 
+/* The verify step reading each user's input from a slot of the previous verify step's snapshots, so a
+ * rollback costs no copy (the reference's slot select: kernels/gdn_head_reader.cpp:17-20, :149-187, the
+ * conv pair slots kernels/streamer_common.hpp:38-44): user b's state and conv history are slot in_slot[b]
+ * of states_in [n_slots, B, NV, DK, DV] and conv_states_in [n_slots, B, C, K-1]; in_slot [B] int32 is
+ * device memory (a slot outside [0, n_slots) reads slot 0). Outputs as qs_gdn_verify_step; they must not
+ * alias the inputs (callers alternate two snapshot sets). */
+int qs_gdn_verify_step_slots(const uint16_t *x, const uint16_t *conv_states_in, uint16_t *conv_states_out,
+                             const uint16_t *taps, const float *g, const float *beta, const float *states_in,
+                             float *states_out, const int *in_slot, int n_slots, uint16_t *o, uint16_t *y_out,
+                             int B, int T, int NK, int NV, int DK, int DV, int K, float scale, float eps,
+                             void *stream);
+
+/* Acceptance without copies: slot[b] <- accept_len[b] - 1 (the snapshot the next verify step reads) and,
+ * when seq_lens is non-null, seq_lens[b] <- base_lens[b] + accept_len[b] (the KV truncation), for
+ * accept_len[b] in [1, T]. Replaces the hub's slot/ring advance (kernels/mlp_hub.cpp:48-58;
+ * model.py:1314-1318). */
+int qs_verify_accept(const int *accept_len, int *slot, int *seq_lens, const int *base_lens, int B, int T,
+                     void *stream);
+
 /* Rollback after verify: state[b] <- states_out[accept_len[b]-1, b], conv_state[b] <- conv_states_out[...]
  * (bit-exact copies), and, when seq_lens is non-null, seq_lens[b] <- base_lens[b] + accept_len[b] (the KV
  * truncation; no KV bytes move). accept_len is device memory, 1 <= accept_len[b] <= T.

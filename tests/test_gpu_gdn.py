@@ -157,3 +157,34 @@ def test_verify_one_token_equals_decode(dev):
     o2, st, cv = ops.gdn_verify_step(g2["x"][:, None], g2["conv_state"], g2["taps"], g2["g"][:, None],
                                      g2["beta"][:, None], g2["state"])  # fmt: skip
     assert torch.equal(o1, o2[:, 0]) and torch.equal(g1["state"], st[0]) and torch.equal(g1["conv_state"], cv[0])
+
+
+def test_verify_slots_equals_copy_rollback(dev):
+    """Slot selection (the next verify reads snapshot a - 1 of the previous step in place) reproduces the
+    copy rollback bit for bit: same outputs, snapshots and conv histories for the next verify step."""
+    B, T = 3, 3
+    d = inputs(B, seed=51, T=T)
+    g = to(d, dev)
+    o1, states, convs = ops.gdn_verify_step(g["x"], g["conv_state"], g["taps"], g["g"], g["beta"], g["state"])
+    acc = torch.tensor([2, 3, 1], dtype=torch.int32, device=dev)
+    base = torch.tensor([10, 20, 30], dtype=torch.int32, device=dev)
+    # copy path: restore, then verify from the restored state
+    st, cv = g["state"].clone(), g["conv_state"].clone()
+    seq_c = torch.zeros(B, dtype=torch.int32, device=dev)
+    ops.gdn_rollback(states, convs, acc, st, cv, seq_c, base)
+    d2 = inputs(B, seed=52, T=T)
+    g2 = to(d2, dev)
+    ref = ops.gdn_verify_step(g2["x"], cv, g2["taps"], g2["g"], g2["beta"], st)
+    # slot path: accept, then verify reading the snapshots in place
+    slot = torch.full((B,), 7, dtype=torch.int32, device=dev)
+    seq_s = torch.zeros(B, dtype=torch.int32, device=dev)
+    ops.verify_accept(acc, T, slot, seq_s, base)
+    assert torch.equal(slot.cpu(), acc.cpu() - 1) and torch.equal(seq_s, seq_c)
+    out = (torch.empty_like(ref[0]), torch.empty_like(ref[1]), torch.empty_like(ref[2]))
+    ops.gdn_verify_step_slots(g2["x"], convs, g2["taps"], g2["g"], g2["beta"], states, slot, out=out)
+    for a, b in zip(out, ref):
+        assert torch.equal(a, b)
+    # an out-of-range accept length leaves the slot and the length untouched
+    bad = torch.tensor([0, 5, 2], dtype=torch.int32, device=dev)
+    ops.verify_accept(bad, T, slot, seq_s, base)
+    assert slot.cpu().tolist() == [1, 2, 1] and seq_s.cpu().tolist() == [12, 23, 32]

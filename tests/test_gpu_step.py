@@ -65,3 +65,25 @@ def test_graph_replay_equals_eager(step, dev):
             if not d["attn"]:
                 assert torch.equal(d["state"], ref[l][1]), (rep, l)
         _ = torch.randn(1024, device=dev).sum().item()  # eager work between replays
+
+
+def test_verify_step_slots_equals_copy(dev):
+    """Two consecutive MTP verify steps (8 layers, batch 2, T = 3): acceptance by slot selection gives the
+    same outputs and accepted states as acceptance by copies."""
+    from qwen36_state.decode import VerifyStep
+
+    steps = {m: VerifyStep(2, 1024, T=3, layers=8, device=dev, rollback=m) for m in ("slots", "copy")}
+    for k in range(2):
+        for vs in steps.values():
+            vs.verify()
+            vs.rollback()
+            vs.reset_lengths()
+        torch.cuda.synchronize()
+        a, c = steps["slots"], steps["copy"]
+        for la, lc in zip(a.layer, c.layer):
+            assert torch.equal(la["o"], lc["o"]), (k, "o")
+        for gi in range(6):
+            for b in range(2):
+                sa, ca = a.state_of(gi, b)
+                sc, cc = c.state_of(gi, b)
+                assert torch.equal(sa, sc) and torch.equal(ca, cc), (k, gi, b)

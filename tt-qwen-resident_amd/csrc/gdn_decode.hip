@@ -578,6 +578,49 @@ extern "C" int qs_gdn_verify_step(const uint16_t *x, const uint16_t *conv_state_
     return qs::launch_status("qs_gdn_verify_step");
 }
 
+extern "C" int qs_gdn_verify_step_slots(const uint16_t *x, const uint16_t *conv_states_in, uint16_t *conv_states_out,
+                                        const uint16_t *taps, const float *g, const float *beta,
+                                        const float *states_in, float *states_out, const int *in_slot, int n_slots,
+                                        uint16_t *o, uint16_t *y_out, int B, int T, int NK, int NV, int DKa,
+                                        int DVa, int K, float scale, float eps, void *stream) {
+    QS_REQUIRE(x && conv_states_in && conv_states_out && taps && g && beta && states_in && states_out && in_slot && o,
+               "qs_gdn_verify_step_slots: null pointer");
+    if (int e = check_gdn_shapes(B, NK, NV, DKa, DVa)) return e;
+    QS_REQUIRE(T >= 1 && T <= TMAX, "qs_gdn_verify_step_slots: T must be in [1, %d] (got %d)", TMAX, T);
+    QS_REQUIRE(n_slots >= 1, "qs_gdn_verify_step_slots: n_slots must be positive (got %d)", n_slots);
+    QS_REQUIRE(K == KC, "qs_gdn_verify_step_slots: only K = 4 taps are supported (got %d)", K);
+    if (int e = check_conv_alignment(x, conv_states_in, conv_states_out, taps, y_out)) return e;
+    QS_REQUIRE(states_out != states_in && conv_states_out != conv_states_in,
+               "qs_gdn_verify_step_slots: outputs must not alias the input slots");
+    GdnArgs a{};
+    a.x = x, a.conv_in = conv_states_in, a.conv_out = conv_states_out, a.taps = taps, a.y_out = y_out;
+    a.g = g, a.beta = beta, a.s_in = states_in, a.s_out = states_out, a.o = o;
+    a.in_slot = in_slot, a.n_slots = n_slots;
+    a.B = B, a.T = T, a.NK = NK, a.NV = NV, a.C = 2 * NK * DK + NV * DV, a.scale = scale, a.eps = eps;
+    launch_gdn<true, true>(a, QS_STREAM(stream));
+    return qs::launch_status("qs_gdn_verify_step_slots");
+}
+
+// Acceptance by slot selection: slot[b] <- accept[b] - 1 and seq_lens[b] <- base_lens[b] + accept[b] for
+// accept[b] in [1, T]; other users are left untouched.
+__global__ void verify_accept_kernel(const int *accept, int *slot, int *seq_lens, const int *base_lens, int B, int T) {
+    const int b = blockIdx.x * 64 + threadIdx.x;
+    if (b >= B) return;
+    const int acc = accept[b];
+    if (acc < 1 || acc > T) return;
+    slot[b] = acc - 1;
+    if (seq_lens) seq_lens[b] = base_lens[b] + acc;
+}
+
+extern "C" int qs_verify_accept(const int *accept_len, int *slot, int *seq_lens, const int *base_lens, int B, int T,
+                                void *stream) {
+    QS_REQUIRE(accept_len && slot, "qs_verify_accept: null pointer");
+    QS_REQUIRE(!seq_lens || base_lens, "qs_verify_accept: seq_lens needs base_lens");
+    QS_REQUIRE(B > 0 && T >= 1 && T <= TMAX, "qs_verify_accept: bad shape (B %d, T %d)", B, T);
+    verify_accept_kernel<<<(B + 63) / 64, 64, 0, QS_STREAM(stream)>>>(accept_len, slot, seq_lens, base_lens, B, T);
+    return qs::launch_status("qs_verify_accept");
+}
+
 static int rollback_launch(const float *states_out, size_t so_stride, float *state, size_t s_stride,
                            const uint16_t *conv_states_out, size_t co_stride, uint16_t *conv_state, size_t c_stride,
                            const int *accept_len, int *seq_lens, const int *base_lens, int L, int B, int T, int NV,

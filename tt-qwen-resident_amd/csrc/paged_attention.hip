@@ -18,6 +18,8 @@
 // kernels/attn_leader_compute.cpp:42-79), so results are identical run to run. The merge is a separate
 // launch: a merge by the last split to finish runs serially in one workgroup and measured slower, and an
 // in-kernel fan-in through release / acquire fences writes back and invalidates the whole L2 of each XCD.
+#include <stdlib.h>
+
 #include "qs_common.h"
 
 namespace {
@@ -354,54 +356,362 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     }
 }
 
-// Merge of the splits of one output row (user, token, query head): thread d owns head dim d. The first 16
-// splits' partials are requested before the weights are known, so a merge of up to 16 splits costs one
-// memory round trip (and each further 16 one more). Wave 0 finds the global max M (log2 domain, as the partials store it) and sum L over
-// the splits (fixed-order butterflies) and leaves the weights e^(m_s - M) / L in LDS; every thread then
-// sums its dim over the splits in split order.
+// ------------------------------------------------------------------------------ MFMA kernel (verify rows)
+// For T query tokens the T * G query rows of a KV head form a dense [T G x 256] x [256 x rows] product, so
+// the multi-token (verify) step runs it on MFMA. One workgroup per (user, KV head, split of pps pages); the
+// split's 4 pps 16-row page slices are divided into 4 contiguous runs, one per wave, each wave keeping its
+// own online softmax; the 4 waves are merged in LDS at the end (fixed tree order), so a split still leaves
+// one partial. Per slice (16 rows) and 16-query-row tile:
+//   S^T [16 rows x 16 q] = K [16 x 256] Q^T      8 x v_mfma_f32_16x16x32_bf16; lane l holds K row l % 16,
+//                                                 dims 32 j + 8 (l / 16) .. + 7 (one 16-byte load per j)
+//   softmax over the slice's rows, in the accumulator layout (lane: q row l % 16, rows 4 (l / 16) + i)
+//   O^T [256 x 16 q] += V^T [256 x 16 rows] P^T  16 x v_mfma_f32_16x16x16_bf16; P^T is the score
+//                                                 accumulator itself (bf16), V^T comes from the slice staged
+//                                                 in LDS through the transposing read ds_read_b64_tr_b16
+// Every lane's O^T values belong to one query row, so a rescale by the running max is per lane.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+constexpr int QPAD = HD + 8;   // s_q row pitch (bf16): 16-byte skew between rows
+constexpr int VPAD = HD + 16;  // s_v row pitch (bf16): 32-byte skew between rows
+
+template <int QT>
+struct MfmaLds {
+    static constexpr int VBYTES = 4 * 16 * VPAD * 2;         // per-wave V slices
+    static constexpr int XBYTES = 2 * QT * 16 * 64 * 16;     // merge: two waves' O^T (float4 per lane)
+    static constexpr int UBYTES = VBYTES > XBYTES ? VBYTES : XBYTES;
+};
+
+template <int G, int QT>
+__global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
+    constexpr int NQR = 16 * QT;
+    const int nwg = a.B * a.NKV * a.nsplit;
+    const int lid = qs::xcd_logical(blockIdx.x, nwg);
+    const int split = lid % a.nsplit;
+    const int g = (lid / a.nsplit) % a.NKV;
+    const int b = lid / (a.nsplit * a.NKV);
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int T = a.T;
+
+    __shared__ __align__(16) uint16_t s_q[NQR][QPAD];
+    __shared__ __align__(16) unsigned char s_u[MfmaLds<QT>::UBYTES];  // V slices, then the merge buffers
+    __shared__ float s_mx[2][QT][64], s_lx[2][QT][64];
+    uint16_t(*s_v)[VPAD] = reinterpret_cast<uint16_t(*)[VPAD]>(s_u) + 16 * w;  // this wave's 16 rows
+    f32x4_t *s_x = reinterpret_cast<f32x4_t *>(s_u);
+
+    int n = a.seq_lens[b];
+    n = n < T ? T : (n > a.max_blocks * BLK ? a.max_blocks * BLK : n);
+    const int base = n - T;  // first new position
+    const int nsl = (n + 15) / 16;  // valid slices of this user
+    const int p0 = split * a.pps;
+    const int s0 = 4 * p0 + w * a.pps, s1 = min(nsl, s0 + a.pps);  // this wave's slices [s0, s1)
+    const int *bt = a.block_table + (size_t)b * a.max_blocks;
+    // the wave's block-table entries (at most 64 pages), one per lane
+    const int pw0 = s0 / 4;
+    const int bt_pre = pw0 + lane < a.max_blocks ? bt[pw0 + lane] : -1;  // a wave spans <= 17 pages
+    auto page_of = [&](int sl) {
+        const int pg = __builtin_amdgcn_readlane(bt_pre, sl / 4 - pw0);
+        return (pg >= 0 && pg < a.num_blocks) ? pg : -1;
+    };
+    const size_t pstride = (size_t)a.NKV * BLK * HD;  // elements per page
+
+    // Fused append, first: the new rows that fall in this wave's slices go into the pools and are waited
+    // for, so the slice loads read them back from the pool. No other wave reads these slices.
+    if (a.k_new && s0 < s1 && base / 16 < s1 && (n - 1) / 16 >= s0) {
+        for (int idx = lane; idx < T * 64; idx += 64) {
+            const int t = idx >> 6, kv = (idx >> 5) & 1, ch = idx & 31;
+            const int pos = base + t, sl = pos / 16;
+            if (sl < s0 || sl >= s1) continue;
+            const int pg = bt[pos / BLK];  // per lane: the new rows may straddle slices and pages
+            if (pg < 0 || pg >= a.num_blocks) continue;
+            const size_t dst = (((size_t)pg * a.NKV + g) * BLK + (pos % BLK)) * HD + ch * 8;
+            const size_t src = (((size_t)b * T + t) * a.NKV + g) * HD + ch * 8;
+            const uint16_t *sv = kv ? a.v_new : a.k_new;
+            uint16_t *d = kv ? a.v_cache : a.k_cache;
+            *reinterpret_cast<uint4 *>(d + dst) = *reinterpret_cast<const uint4 *>(sv + src);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+
+    // query rows qr = t G + hh (zero past T G)
+    for (int idx = tid; idx < NQR * 32; idx += 256) {
+        const int qr = idx >> 5, ch = idx & 31;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (qr < T * G) {
+            const int t = qr / G, hh = qr % G;
+            v = *reinterpret_cast<const uint4 *>(a.q + (((size_t)b * T + t) * a.NQ + g * G + hh) * HD + ch * 8);
+        }
+        *reinterpret_cast<uint4 *>(&s_q[qr][ch * 8]) = v;
+    }
+    __syncthreads();
+
+    const float sl2 = a.scale * 1.4426950408889634f;  // log2 domain
+    f32x4_t oacc[QT][16];
+    float m[QT], lp[QT];
+#pragma unroll
+    for (int nt = 0; nt < QT; ++nt) {
+        m[nt] = -INFINITY;
+        lp[nt] = 0.f;
+#pragma unroll
+        for (int dt = 0; dt < 16; ++dt) oacc[nt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    // each lane's causal limit per query-row tile: token (l16 + 16 nt) / G sees positions <= base + token
+    int lim[QT];
+#pragma unroll
+    for (int nt = 0; nt < QT; ++nt) {
+        const int qr = l16 + 16 * nt;
+        lim[nt] = qr < T * G ? base + qr / G : -1;
+    }
+
+    auto load_k = [&](int pg, int sl, uint4 (&kb)[8]) {
+        const auto rk = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t *>(a.k_cache + (size_t)pg * pstride + (size_t)g * BLK * HD), (short)0, BLK * HD * 2,
+            0x00020000);
+        const int off = ((sl & 3) * 16 + l16) * HD * 2 + lg * 16;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, off, j * 64, 0);
+            kb[j] = make_uint4(x[0], x[1], x[2], x[3]);
+        }
+    };
+    auto load_v = [&](int pg, int sl, uint4 (&vb)[8]) {
+        const auto rv = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t *>(a.v_cache + (size_t)pg * pstride + (size_t)g * BLK * HD), (short)0, BLK * HD * 2,
+            0x00020000);
+        const int off = ((sl & 3) * 16 + (lane >> 5)) * HD * 2 + (lane & 31) * 16;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rv, off, k * 1024, 0);
+            vb[k] = make_uint4(x[0], x[1], x[2], x[3]);
+        }
+    };
+
+    // one slice: stage V, scores, softmax, P V (kb / vb hold the slice's K and V rows)
+    auto slice = [&](int sl, const uint4 (&kb)[8], const uint4 (&vb)[8]) {
+        // stage V (rows past the user's length zeroed: a stale row times a zero probability could be NaN)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int row = 2 * k + (lane >> 5);
+            const uint4 v = sl * 16 + row < n ? vb[k] : make_uint4(0, 0, 0, 0);
+            *reinterpret_cast<uint4 *>(&s_v[row][(lane & 31) * 8]) = v;
+        }
+        f32x4_t sacc[QT];
+#pragma unroll
+        for (int nt = 0; nt < QT; ++nt) sacc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const bf16x8_t ak = __builtin_bit_cast(bf16x8_t, kb[j]);
+#pragma unroll
+            for (int nt = 0; nt < QT; ++nt) {
+                const bf16x8_t bq = __builtin_bit_cast(
+                    bf16x8_t, *reinterpret_cast<const uint4 *>(&s_q[l16 + 16 * nt][32 * j + 8 * lg]));
+                sacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, bq, sacc[nt], 0, 0, 0);
+            }
+        }
+        // online softmax (log2 domain) per query row over the slice's 16 rows; probabilities rounded to
+        // bf16, the running sum adds the rounded values
+        i16x4_t pb[QT];
+#pragma unroll
+        for (int nt = 0; nt < QT; ++nt) {
+            const int r0 = sl * 16 + 4 * lg;
+            float sc[4];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sc[i] = r0 + i <= lim[nt] ? sacc[nt][i] : -INFINITY;
+                mx = fmaxf(mx, sc[i]);
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float mn = fmaxf(m[nt], mx * sl2);
+            float e[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                e[i] = sc[i] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(fmaf(sc[i], sl2, -mn));
+            const uint32_t p01 = qs::cvt_pk_bf16(e[0], e[1]), p23 = qs::cvt_pk_bf16(e[2], e[3]);
+            if (__any(mn != m[nt])) {  // rescale only when some running max moved
+                const float alpha = m[nt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[nt] - mn);
+                lp[nt] *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < 16; ++dt) oacc[nt][dt] *= alpha;
+            }
+            m[nt] = mn;
+            lp[nt] += (qs::bf_lo(p01) + qs::bf_hi(p01)) + (qs::bf_lo(p23) + qs::bf_hi(p23));
+            pb[nt] = __builtin_bit_cast(i16x4_t, make_uint2(p01, p23));
+        }
+        __builtin_amdgcn_wave_barrier();
+        // O^T += V^T P^T: lane (group lg, index l16) supplies the address of V[4 lg + l16 / 4][16 dt + 4 (l16 % 4)]
+#pragma unroll
+        for (int dt = 0; dt < 16; ++dt) {
+            const i16x4_t av = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) i16x4_t *)&s_v[4 * lg + (l16 >> 2)][16 * dt + 4 * (l16 & 3)]);
+#pragma unroll
+            for (int nt = 0; nt < QT; ++nt)
+                oacc[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, pb[nt], oacc[nt][dt], 0, 0, 0);
+        }
+        __builtin_amdgcn_wave_barrier();
+    };
+    // two register buffers alternate: the next slice's K and V are in flight while a slice is computed
+    uint4 KA[8], VA[8], KB[8], VB[8];
+    int pga = s0 < s1 ? page_of(s0) : -1;
+    if (pga >= 0) {
+        load_k(pga, s0, KA);
+        load_v(pga, s0, VA);
+    }
+    for (int sl = s0; sl < s1; sl += 2) {
+        const int pgb = sl + 1 < s1 ? page_of(sl + 1) : -1;
+        if (pgb >= 0) {
+            load_k(pgb, sl + 1, KB);
+            load_v(pgb, sl + 1, VB);
+        }
+        if (pga >= 0) slice(sl, KA, VA);
+        if (sl + 1 >= s1) break;
+        pga = sl + 2 < s1 ? page_of(sl + 2) : -1;
+        if (pga >= 0) {
+            load_k(pga, sl + 2, KA);
+            load_v(pga, sl + 2, VA);
+        }
+        if (pgb >= 0) slice(sl + 1, KB, VB);
+    }
+
+    // full row sums of the wave (the 4 lane groups hold disjoint rows)
+#pragma unroll
+    for (int nt = 0; nt < QT; ++nt) {
+        lp[nt] += __shfl_xor(lp[nt], 16, 64);
+        lp[nt] += __shfl_xor(lp[nt], 32, 64);
+    }
+    // ---- merge the 4 waves: (2, 3) into (0, 1), then 1 into 0; lane layouts agree, so it is per lane
+    auto put = [&](int slot) {
+#pragma unroll
+        for (int nt = 0; nt < QT; ++nt) {
+#pragma unroll
+            for (int dt = 0; dt < 16; ++dt) s_x[((slot * QT + nt) * 16 + dt) * 64 + lane] = oacc[nt][dt];
+            s_mx[slot][nt][lane] = m[nt];
+            s_lx[slot][nt][lane] = lp[nt];
+        }
+    };
+    auto take = [&](int slot) {
+#pragma unroll
+        for (int nt = 0; nt < QT; ++nt) {
+            const float m2 = s_mx[slot][nt][lane], l2 = s_lx[slot][nt][lane];
+            const float M = fmaxf(m[nt], m2);
+            const float e1 = m[nt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[nt] - M);
+            const float e2 = m2 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m2 - M);
+#pragma unroll
+            for (int dt = 0; dt < 16; ++dt)
+                oacc[nt][dt] = oacc[nt][dt] * e1 + s_x[((slot * QT + nt) * 16 + dt) * 64 + lane] * e2;
+            lp[nt] = lp[nt] * e1 + l2 * e2;
+            m[nt] = M;
+        }
+    };
+    __syncthreads();  // the V slices are dead: s_u becomes the merge buffer
+    if (w >= 2) put(w - 2);
+    __syncthreads();
+    if (w < 2) take(w);
+    __syncthreads();
+    if (w == 1) put(0);
+    __syncthreads();
+    if (w != 0) return;
+    take(0);
+
+#pragma unroll
+    for (int nt = 0; nt < QT; ++nt) {
+        const int qr = l16 + 16 * nt;
+        if (qr >= T * G) continue;
+        const int t = qr / G, hh = qr % G;
+        const size_t row = ((size_t)b * T + t) * a.NKV + g;
+        if (a.nsplit == 1) {
+            const float inv = 1.0f / lp[nt];
+            uint16_t *op = a.o + (((size_t)b * T + t) * a.NQ + g * G + hh) * HD + 4 * lg;
+#pragma unroll
+            for (int dt = 0; dt < 16; ++dt) {
+                const f32x4_t v = oacc[nt][dt] * inv;
+                *reinterpret_cast<uint2 *>(op + 16 * dt) = make_uint2(qs::cvt_pk_bf16(v[0], v[1]), qs::cvt_pk_bf16(v[2], v[3]));
+            }
+        } else {
+            float *po = a.part_o + ((row * a.nsplit + split) * G + hh) * HD + 4 * lg;
+#pragma unroll
+            for (int dt = 0; dt < 16; ++dt) *reinterpret_cast<f32x4_t *>(po + 16 * dt) = oacc[nt][dt];
+            if (lg == 0) {
+                float *ml = a.part_ml + ((row * a.nsplit + split) * G + hh) * 2;
+                ml[0] = m[nt];
+                ml[1] = lp[nt];
+            }
+        }
+    }
+}
+
+// Merge of the splits of one output row (user, token, query head) in one memory round trip: wave w sums
+// splits w, w + 4, w + 8, ... (lane l owns head dims 4 l .. 4 l + 3), and every wave finds the global max M
+// (log2 domain, as the partials store it) and the sum L from all splits' (m, l), whose loads are in flight
+// together with the partials. The 4 waves' sums are added in wave order through LDS; every reduction runs
+// in a fixed order, so the result is identical run to run. (The leader side of the reference: global max,
+// rescale, sum, normalise, kernels/attn_leader_writer.cpp:86-106, kernels/attn_leader_compute.cpp:42-79.)
 constexpr int MAX_SPLITS = 1024;
+constexpr int MCH = 8;  // splits per wave per batch of loads
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, int G) {
-    constexpr int CH = 16;
-    __shared__ float s_wt[MAX_SPLITS];
+    __shared__ float4 s_part[4][64];
     const int rowh = blockIdx.x;  // ((b * T + t) * NKV + g) * G + h
     const int h = rowh % G, row = rowh / G;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int ns = a.nsplit;
     const size_t sstride = (size_t)G * HD;  // floats between consecutive splits of one row
     const float *ml = a.part_ml + ((size_t)row * ns * G + h) * 2;
-    const float *po = a.part_o + ((size_t)row * ns * G + h) * HD + tid;
-    float x[CH];
+    const float *po = a.part_o + ((size_t)row * ns * G + h) * HD + 4 * lane;
+    auto mlv = [&](int sp) { return *reinterpret_cast<const float2 *>(ml + (size_t)sp * G * 2); };
+    float4 x[MCH];
+    float2 mw[MCH];
 #pragma unroll
-    for (int k = 0; k < CH; ++k) x[k] = po[(size_t)min(k, ns - 1) * sstride];
-    if (tid < 64) {
-        float M = -INFINITY;
-        for (int sp = tid; sp < ns; sp += 64) M = fmaxf(M, ml[(size_t)sp * G * 2]);
-        M = qs::wave_max(M);
-        float L = 0.f;
-        for (int sp = tid; sp < ns; sp += 64) {
-            const float m = ml[(size_t)sp * G * 2];
-            const float e = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
-            s_wt[sp] = e;
-            L += e * ml[(size_t)sp * G * 2 + 1];
+    for (int k = 0; k < MCH; ++k) {
+        const int sp = min(w + 4 * k, ns - 1);
+        x[k] = *reinterpret_cast<const float4 *>(po + sp * sstride);
+        mw[k] = mlv(sp);
+    }
+    // global max and sum over all splits: lane l covers splits l, l + 64, ...
+    float M = -INFINITY;
+    float2 mg[MAX_SPLITS / 64];
+#pragma unroll
+    for (int j = 0; j < MAX_SPLITS / 64; ++j) {
+        mg[j] = make_float2(-INFINITY, 0.f);
+        if (lane + 64 * j < ns) mg[j] = mlv(lane + 64 * j);
+        M = fmaxf(M, mg[j].x);
+    }
+    M = qs::wave_max(M);
+    float L = 0.f;
+#pragma unroll
+    for (int j = 0; j < MAX_SPLITS / 64; ++j)
+        if (mg[j].x != -INFINITY) L += __builtin_amdgcn_exp2f(mg[j].x - M) * mg[j].y;
+    L = qs::wave_sum(L);
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto acc = [&](int sp, const float4 &v, float m) {
+        if (sp < ns && m != -INFINITY) {
+            const float e = __builtin_amdgcn_exp2f(m - M);
+            O.x += e * v.x, O.y += e * v.y, O.z += e * v.z, O.w += e * v.w;
         }
-        L = qs::wave_sum(L);
-        for (int sp = tid; sp < ns; sp += 64) s_wt[sp] /= L;
+    };
+#pragma unroll
+    for (int k = 0; k < MCH; ++k) acc(w + 4 * k, x[k], mw[k].x);
+    for (int s0 = 4 * MCH; s0 < ns; s0 += 4 * MCH) {  // further splits, a batch of loads at a time
+#pragma unroll
+        for (int k = 0; k < MCH; ++k) {
+            const int sp = min(s0 + w + 4 * k, ns - 1);
+            x[k] = *reinterpret_cast<const float4 *>(po + sp * sstride);
+            mw[k] = mlv(sp);
+        }
+#pragma unroll
+        for (int k = 0; k < MCH; ++k) acc(s0 + w + 4 * k, x[k], mw[k].x);
     }
+    s_part[w][lane] = O;
     __syncthreads();
-    float O = 0.f;
-#pragma unroll
-    for (int k = 0; k < CH; ++k)
-        if (k < ns) O += s_wt[k] * x[k];
-    // further splits in chunks of CH, each chunk's loads all in flight before its first use
-    for (int s0 = CH; s0 < ns; s0 += CH) {
-#pragma unroll
-        for (int k = 0; k < CH; ++k) x[k] = po[(size_t)min(s0 + k, ns - 1) * sstride];
-#pragma unroll
-        for (int k = 0; k < CH; ++k)
-            if (s0 + k < ns) O += s_wt[s0 + k] * x[k];
-    }
+    if (w != 0) return;
+    const float4 p1 = s_part[1][lane], p2 = s_part[2][lane], p3 = s_part[3][lane];
+    const float inv = 1.0f / L;
+    const float r0 = (((O.x + p1.x) + p2.x) + p3.x) * inv, r1 = (((O.y + p1.y) + p2.y) + p3.y) * inv;
+    const float r2 = (((O.z + p1.z) + p2.z) + p3.z) * inv, r3 = (((O.w + p1.w) + p2.w) + p3.w) * inv;
     const int g = row % a.NKV, bt = row / a.NKV;
-    a.o[((size_t)bt * a.NQ + g * G + h) * HD + tid] = (uint16_t)qs::f2bf(O);
+    *reinterpret_cast<uint2 *>(a.o + ((size_t)bt * a.NQ + g * G + h) * HD + 4 * lane) =
+        make_uint2(qs::cvt_pk_bf16(r0, r1), qs::cvt_pk_bf16(r2, r3));
 }
 
 int nsplit_of(int max_blocks, int pps) { return (max_blocks + pps - 1) / pps; }
@@ -448,6 +758,29 @@ extern "C" int qs_paged_gqa_decode(const uint16_t *q, const uint16_t *k_new, con
     const dim3 grid(B * NKV * ns);
     hipStream_t st = QS_STREAM(stream);
     const int TT = T >= 2 ? 2 : 1;  // query tokens per pass over the pages (4 would spill registers)
+    // verify rows (T >= 2) with at most 32 query rows per KV head run on MFMA
+    static const bool mfma_t1 = getenv("QS_ATTN_MFMA") && atoi(getenv("QS_ATTN_MFMA")) == 1;
+    if ((T >= 2 || mfma_t1) && T * G <= 32) {
+        const int QT = (T * G + 15) / 16;
+#define QS_MFMA_LAUNCH(GG)                                                       \
+    if (QT == 1) attn_mfma_kernel<GG, 1><<<grid, 256, 0, st>>>(a);               \
+    else attn_mfma_kernel<GG, 2><<<grid, 256, 0, st>>>(a);
+        switch (G) {
+            case 1: QS_MFMA_LAUNCH(1) break;
+            case 2: QS_MFMA_LAUNCH(2) break;
+            case 4: QS_MFMA_LAUNCH(4) break;
+            case 6: QS_MFMA_LAUNCH(6) break;
+            case 8: QS_MFMA_LAUNCH(8) break;
+            default: QS_REQUIRE(false, "qs_paged_gqa_decode: group size NQ/NKV = %d not in {1, 2, 4, 6, 8}", G);
+        }
+#undef QS_MFMA_LAUNCH
+        if (int e = qs::launch_status("qs_paged_gqa_decode")) return e;
+        if (ns > 1) {
+            attn_merge_kernel<<<B * T * NKV * G, 256, 0, st>>>(a, G);
+            return qs::launch_status("qs_paged_gqa_decode (merge)");
+        }
+        return QS_OK;
+    }
 #define QS_ATTN_LAUNCH(GG)                                                      \
     if (TT == 1) attn_kernel<GG, 1><<<grid, 256, 0, st>>>(a);                   \
     else attn_kernel<GG, 2><<<grid, 256, 0, st>>>(a);

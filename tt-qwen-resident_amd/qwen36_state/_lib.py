@@ -23,6 +23,11 @@ SIGNATURES = {
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _F, _P],
     ),
+    "qs_gdn_verify_step_slots": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _F, _P],
+    ),
+    "qs_verify_accept": (_I, [_P, _P, _P, _P, _I, _I, _P]),
     "qs_gdn_rollback": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "qs_gdn_rollback_layers": (
         _I, [_P, _Z, _P, _Z, _P, _Z, _P, _Z, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),

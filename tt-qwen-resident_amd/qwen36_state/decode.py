@@ -133,31 +133,44 @@ class StatePathStep:
 class VerifyStep:
     """The MTP verify step of the 64-layer state path: T tokens per user (1 accepted + T - 1 drafts) through
     every layer — GDN layers keep all T intermediate states and conv histories, attention layers append T
-    rows and attend causally among them — then the rollback to a seeded accepted length per user: state and
-    conv history restored from snapshot a - 1 (bit-exact copies) and the KV length truncated to base + a.
+    rows and attend causally among them — then the acceptance of a seeded length a per user.
 
-    The reference verify step is the 2-row form of the same protocol (model.py:426-456, README.md:413-421;
-    acceptance kernels/mlp_hub.cpp:48-58)."""
+    rollback="slots" (default, the reference's scheme: slot select, no copy, README.md:413-421): two snapshot
+    sets alternate; step k writes set k % 2 and reads each user's input from slot a - 1 of the other set,
+    so accepting is slot[b] = a - 1 and seq_lens[b] = base + a. rollback="copy": every GDN layer's state and
+    conv history are restored from snapshot a - 1 by bit-exact copies in one launch, and the next step
+    reads them in place.
+
+    The reference verify step is the 2-row form of the same protocol (model.py:426-456; acceptance
+    kernels/mlp_hub.cpp:48-58)."""
 
     def __init__(self, B, ctx, T=4, layers=64, interval=4, device="cuda", seed=0, num_blocks=2048,
-                 pages_per_split=2):  # fmt: skip
+                 pages_per_split=2, rollback="slots"):  # fmt: skip
+        if rollback not in ("slots", "copy"):
+            raise ValueError("rollback must be 'slots' or 'copy'")
         self.B, self.ctx, self.T, self.layers, self.interval = B, ctx, T, layers, interval
         self.device = torch.device(device)
         self.pps = pages_per_split
+        self.mode = rollback
         pages = (ctx + BLOCK - 1) // BLOCK
         self.block_table = W.block_tables(B, pages, num_blocks, self.device, seed)
         self.seq_lens = torch.full((B,), ctx, dtype=torch.int32, device=self.device)
         self.base_lens = self.seq_lens - T
         gen = torch.Generator().manual_seed(seed + 7)
         self.accept = torch.randint(1, T + 1, (B,), generator=gen, dtype=torch.int32).to(self.device)
-        # the GDN layers' states, conv histories and their T snapshots live in one tensor each (layer-major),
-        # so the rollback restores every layer in one launch
+        self.slot = torch.zeros(B, dtype=torch.int32, device=self.device)
+        self.parity = 0  # snapshot set the next verify step writes (slots mode)
+        # GDN tensors live layer-major in one tensor each: states / conv histories [n_gdn, B, ...] (copy mode)
+        # and the T snapshots [sets, n_gdn, T, B, ...] (2 sets in slots mode, whose set 1 starts out holding
+        # the initial state in slot 0)
         n_gdn = sum(not is_attn(l, interval) for l in range(layers))
         f32, bf = torch.float32, torch.bfloat16
-        self.g_state = torch.empty(n_gdn, B, NV, DK, DV, dtype=f32, device=self.device)
-        self.g_conv = torch.empty(n_gdn, B, W.C_QKV, CONV_K - 1, dtype=bf, device=self.device)
-        self.g_states = torch.empty(n_gdn, T, B, NV, DK, DV, dtype=f32, device=self.device)
-        self.g_convs = torch.empty(n_gdn, T, B, W.C_QKV, CONV_K - 1, dtype=bf, device=self.device)
+        sets = 2 if rollback == "slots" else 1
+        self.g_states = torch.empty(sets, n_gdn, T, B, NV, DK, DV, dtype=f32, device=self.device)
+        self.g_convs = torch.empty(sets, n_gdn, T, B, W.C_QKV, CONV_K - 1, dtype=bf, device=self.device)
+        if rollback == "copy":
+            self.g_state = torch.empty(n_gdn, B, NV, DK, DV, dtype=f32, device=self.device)
+            self.g_conv = torch.empty(n_gdn, B, W.C_QKV, CONV_K - 1, dtype=bf, device=self.device)
         self.layer = []
         gi = 0
         for l in range(layers):
@@ -168,11 +181,16 @@ class VerifyStep:
                 d["attn"] = True
             else:
                 d = W.gdn_layer(B, self.device, seed=seed + l, T=T)
-                self.g_state[gi].copy_(d["state"])
-                self.g_conv[gi].copy_(d["conv_state"])
-                d["state"], d["conv_state"] = self.g_state[gi], self.g_conv[gi]
+                if rollback == "copy":
+                    self.g_state[gi].copy_(d["state"])
+                    self.g_conv[gi].copy_(d["conv_state"])
+                    d["state"], d["conv_state"] = self.g_state[gi], self.g_conv[gi]
+                else:
+                    self.g_states[1, gi, 0].copy_(d["state"])
+                    self.g_convs[1, gi, 0].copy_(d["conv_state"])
+                    del d["state"], d["conv_state"]
                 d["o"] = torch.empty(B, T, NV, DV, dtype=torch.bfloat16, device=self.device)
-                d["states"], d["convs"] = self.g_states[gi], self.g_convs[gi]
+                d["gi"] = gi
                 d["attn"] = False
                 gi += 1
             self.layer.append(d)
@@ -181,34 +199,55 @@ class VerifyStep:
         self.graph = None
 
     def verify(self):
-        """All layers of the verify step (no rollback): what the target model's forward does."""
+        """All layers of the verify step (no acceptance): what the target model's forward does."""
+        p = self.parity
         for d in self.layer:
             if d["attn"]:
                 ops.paged_gqa_decode(d["q"], d["k_cache"], d["v_cache"], d["block_table"], d["seq_lens"],
                                      d["scale"], k_new=d["k_new"], v_new=d["v_new"], pages_per_split=self.pps,
                                      out=d["o"], ws=self.attn_ws)  # fmt: skip
+            elif self.mode == "slots":
+                gi = d["gi"]
+                ops.gdn_verify_step_slots(d["x"], self.g_convs[1 - p, gi], d["taps"], d["g"], d["beta"],
+                                          self.g_states[1 - p, gi], self.slot,
+                                          out=(d["o"], self.g_states[p, gi], self.g_convs[p, gi]))  # fmt: skip
             else:
+                gi = d["gi"]
                 ops.gdn_verify_step(d["x"], d["conv_state"], d["taps"], d["g"], d["beta"], d["state"],
-                                    out=(d["o"], d["states"], d["convs"]))  # fmt: skip
+                                    out=(d["o"], self.g_states[0, gi], self.g_convs[0, gi]))  # fmt: skip
 
     def rollback(self):
-        """Restore every GDN layer to its accepted snapshot and truncate the KV length, in one launch."""
-        ops.gdn_rollback_layers(self.g_states, self.g_convs, self.accept, self.g_state, self.g_conv, self.seq_lens,
-                                self.base_lens)  # fmt: skip
+        """Accept seeded lengths: select the snapshot slots (slots mode) or restore every GDN layer from its
+        snapshot in one launch (copy mode), and truncate the KV length."""
+        if self.mode == "slots":
+            ops.verify_accept(self.accept, self.T, self.slot, self.seq_lens, self.base_lens)
+            self.parity ^= 1
+        else:
+            ops.gdn_rollback_layers(self.g_states[0], self.g_convs[0], self.accept, self.g_state, self.g_conv,
+                                    self.seq_lens, self.base_lens)  # fmt: skip
 
     def step(self):
         self.verify()
         self.rollback()
+
+    def state_of(self, gi, b):
+        """The accepted (current) fp32 state and conv history of user b in GDN layer gi."""
+        if self.mode == "slots":
+            s = int(self.slot[b])
+            return self.g_states[1 - self.parity, gi, s, b], self.g_convs[1 - self.parity, gi, s, b]
+        return self.g_state[gi, b], self.g_conv[gi, b]
 
     def reset_lengths(self):
         """Undo the KV truncation so the same step can be replayed (benchmarking)."""
         self.seq_lens.copy_(self.base_lens + self.T)
 
     def bytes_per_step(self):
-        """Algorithmic bytes of the verify step (rollback by slot selection costs none; the copy this
-        build performs is rollback_bytes())."""
+        """Algorithmic bytes of the verify step (acceptance by slot selection moves none; the copy mode's
+        restore is rollback_bytes())."""
         return step_bytes(self.B, self.ctx, self.layers, self.interval, self.T)
 
     def rollback_bytes(self):
+        if self.mode == "slots":
+            return 0
         n_gdn = sum(not d["attn"] for d in self.layer)
         return n_gdn * self.B * (2 * NV * DK * DV * 4 + 2 * W.C_QKV * (CONV_K - 1) * 2)

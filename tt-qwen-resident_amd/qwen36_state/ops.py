@@ -182,6 +182,46 @@ def gdn_verify_step(x, conv_state, taps, g, beta, state, nk=NK, scale=None, eps=
     return (o, states, convs, y) if return_y else (o, states, convs)
 
 
+def gdn_verify_step_slots(x, conv_states_in, taps, g, beta, states_in, in_slot, out, nk=NK, scale=None, eps=EPS):
+    """gdn_verify_step whose per-user input is a slot of the previous verify step's snapshots (the reference's
+    slot select, kernels/gdn_head_reader.cpp:17-20): user b reads states_in[in_slot[b], b] and
+    conv_states_in[in_slot[b], b]. states_in [S, B, NV, DK, DV], conv_states_in [S, B, C, 3], in_slot [B]
+    int32 on the device; out = (o, states, conv_states) must not alias the inputs."""
+    dev = states_in.device
+    _chk(states_in, "states_in", torch.float32)
+    S, B, nv, dk, dv = states_in.shape
+    T = x.shape[1]
+    C = 2 * nk * dk + nv * dv
+    _chk(x, "x", torch.bfloat16, (B, T, C), dev)
+    _chk(conv_states_in, "conv_states_in", torch.bfloat16, (S, B, C, CONV_K - 1), dev)
+    _chk(taps, "taps", torch.bfloat16, (C, CONV_K), dev)
+    _chk(g, "g", torch.float32, (B, T, nv), dev)
+    _chk(beta, "beta", torch.float32, (B, T, nv), dev)
+    _chk(in_slot, "in_slot", torch.int32, (B,), dev)
+    o, states, convs = out
+    _chk(o, "out o", torch.bfloat16, (B, T, nv, dv), dev)
+    _chk(states, "out states", torch.float32, (T, B, nv, dk, dv), dev)
+    _chk(convs, "out conv_states", torch.bfloat16, (T, B, C, CONV_K - 1), dev)
+    scale = dk**-0.5 if scale is None else scale
+    call("qs_gdn_verify_step_slots", _p(x), _p(conv_states_in), _p(convs), _p(taps), _p(g), _p(beta), _p(states_in),
+         _p(states), _p(in_slot), S, _p(o), None, B, T, nk, nv, dk, dv, CONV_K, float(scale), float(eps),
+         _stream(dev))  # fmt: skip
+    return o, states, convs
+
+
+def verify_accept(accept_len, T, slot, seq_lens=None, base_lens=None):
+    """Acceptance by slot selection: slot <- accept_len - 1 (the snapshot the next verify step reads) and
+    seq_lens <- base_lens + accept_len when given; no state moves (kernels/mlp_hub.cpp:48-58)."""
+    dev = slot.device
+    B = slot.shape[0]
+    _chk(accept_len, "accept_len", torch.int32, (B,), dev)
+    _chk(slot, "slot", torch.int32, (B,), dev)
+    if seq_lens is not None:
+        _chk(seq_lens, "seq_lens", torch.int32, (B,), dev)
+        _chk(base_lens, "base_lens", torch.int32, (B,), dev)
+    call("qs_verify_accept", _p(accept_len), _p(slot), _p(seq_lens), _p(base_lens), B, T, _stream(dev))
+
+
 def gdn_rollback(states, conv_states, accept_len, state, conv_state, seq_lens=None, base_lens=None):
     """Restore state <- states[accept_len - 1], conv_state <- conv_states[accept_len - 1] per user (bit-exact),
     and seq_lens <- base_lens + accept_len when given (the KV truncation). accept_len [B] int32 on device,
