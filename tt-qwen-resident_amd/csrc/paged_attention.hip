@@ -94,7 +94,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     // The split's block-table entries (at most 64), one per lane, read once up front: the page walk takes
     // each page index with a readlane and never waits on a table read (a wait for one load would also
     // wait for the K/V loads in flight).
-    const int bt_pre = p0 + lane < p1 ? bt[p0 + lane] : -1;
+    const int bt_pre = p0 + lane < min(a.max_blocks, p0 + a.pps) ? bt[p0 + lane] : -1;  // issued before n is known
     auto page_at = [&](int pi) {
         const int pg = __builtin_amdgcn_readlane(bt_pre, pi - p0);
         return (pg >= 0 && pg < a.num_blocks) ? pg : -1;
@@ -117,6 +117,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             *reinterpret_cast<uint4 *>(d + dst) = *reinterpret_cast<const uint4 *>(s + src);
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();  // the rows are read by the wave that owns their 16-row slice (the branch is uniform)
     }
 
     const int kq = lane & 3;               // K: this lane's 16-byte piece of each 64-byte run of the row
@@ -155,15 +156,29 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         const int nt = min(TT, T - tg);
         const int vend = base + tg + nt;  // rows at or past vend are invalid for every token of the group
         const int pe = min(p1, (vend + BLK - 1) / BLK);
-        __syncthreads();
-        for (int idx = tid; idx < TT * G * 32; idx += 256) {
+        // q of the token group: loaded into registers here, stored to LDS by store_q; for one token the
+        // store waits until the first pages' loads are in flight, so they do not queue behind q's round trip
+        constexpr int QCH = (TT * G * 32 + 255) / 256;
+        uint4 qreg[QCH];
+#pragma unroll
+        for (int k = 0; k < QCH; ++k) {
+            const int idx = tid + 256 * k;
             const int tt = idx / (G * 32), hh = (idx / 32) % G, ch = idx & 31;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (tt < nt)
-                v = *reinterpret_cast<const uint4 *>(a.q + (((size_t)b * T + tg + tt) * a.NQ + g * G + hh) * HD + ch * 8);
-            *reinterpret_cast<uint4 *>(&s_q[tt][hh][ch * 8]) = v;
+            qreg[k] = make_uint4(0, 0, 0, 0);
+            if (idx < TT * G * 32 && tt < nt)
+                qreg[k] = *reinterpret_cast<const uint4 *>(a.q + (((size_t)b * T + tg + tt) * a.NQ + g * G + hh) * HD + ch * 8);
         }
-        __syncthreads();
+        auto store_q = [&]() {
+            __syncthreads();  // the previous group's readers of s_q are done
+#pragma unroll
+            for (int k = 0; k < QCH; ++k) {
+                const int idx = tid + 256 * k;
+                const int tt = idx / (G * 32), hh = (idx / 32) % G, ch = idx & 31;
+                if (idx < TT * G * 32) *reinterpret_cast<uint4 *>(&s_q[tt][hh][ch * 8]) = qreg[k];
+            }
+            __syncthreads();
+        };
+        if constexpr (TT != 1) store_q();
 
         // m: running max (log2 domain, wave-uniform); lp: every lane adds its row's rounded probability (so
         // the wave sum is 4x the row sum), reduced over the wave once per split
@@ -282,6 +297,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                 load_v(page_at(p0), Y);
             }
             if (p0 + 1 < pe && page_at(p0 + 1) >= 0) load_k(page_at(p0 + 1), Z);
+            store_q();
             for (int pi = p0; pi < pe; pi += 3) {
                 step(pi, X, Y);  // loads V(pi + 1) -> X, K(pi + 2) -> Y
                 if (pi + 1 >= pe) break;
@@ -434,17 +450,19 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
 
-    // query rows qr = t G + hh (zero past T G)
-    for (int idx = tid; idx < NQR * 32; idx += 256) {
-        const int qr = idx >> 5, ch = idx & 31;
-        uint4 v = make_uint4(0, 0, 0, 0);
+    // query rows qr = t G + hh (zero past T G): loaded into registers now, stored to LDS once the first
+    // slice's loads are in flight
+    constexpr int QCH = NQR * 32 / 256;
+    uint4 qreg[QCH];
+#pragma unroll
+    for (int k = 0; k < QCH; ++k) {
+        const int idx = tid + 256 * k, qr = idx >> 5, ch = idx & 31;
+        qreg[k] = make_uint4(0, 0, 0, 0);
         if (qr < T * G) {
             const int t = qr / G, hh = qr % G;
-            v = *reinterpret_cast<const uint4 *>(a.q + (((size_t)b * T + t) * a.NQ + g * G + hh) * HD + ch * 8);
+            qreg[k] = *reinterpret_cast<const uint4 *>(a.q + (((size_t)b * T + t) * a.NQ + g * G + hh) * HD + ch * 8);
         }
-        *reinterpret_cast<uint4 *>(&s_q[qr][ch * 8]) = v;
     }
-    __syncthreads();
 
     const float sl2 = a.scale * 1.4426950408889634f;  // log2 domain
     f32x4_t oacc[QT][16];
@@ -559,6 +577,12 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
         load_k(pga, s0, KA);
         load_v(pga, s0, VA);
     }
+#pragma unroll
+    for (int k = 0; k < QCH; ++k) {
+        const int idx = tid + 256 * k;
+        *reinterpret_cast<uint4 *>(&s_q[idx >> 5][(idx & 31) * 8]) = qreg[k];
+    }
+    __syncthreads();
     for (int sl = s0; sl < s1; sl += 2) {
         const int pgb = sl + 1 < s1 ? page_of(sl + 1) : -1;
         if (pgb >= 0) {
@@ -677,12 +701,12 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, int G) {
         if (lane + 64 * j < ns) mg[j] = mlv(lane + 64 * j);
         M = fmaxf(M, mg[j].x);
     }
-    M = qs::wave_max(M);
+    M = qs::wave_max_bcast(M);
     float L = 0.f;
 #pragma unroll
     for (int j = 0; j < MAX_SPLITS / 64; ++j)
         if (mg[j].x != -INFINITY) L += __builtin_amdgcn_exp2f(mg[j].x - M) * mg[j].y;
-    L = qs::wave_sum(L);
+    L = qs::wave_sum_dpp(L);
     float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
     auto acc = [&](int sp, const float4 &v, float m) {
         if (sp < ns && m != -INFINITY) {
