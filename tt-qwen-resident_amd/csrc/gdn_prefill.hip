@@ -317,8 +317,8 @@ __device__ __forceinline__ int kt_index(int d, int t) {
 // loaded into registers while the current chunk computes; reads past the sequence end return zeros through
 // the buffer descriptors' range checks and writes past it are dropped the same way.
 __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
-    constexpr int SKP = DK + 8;  // bf16 row stride of the S^T planes
-    constexpr int TP = CH + 8;   // bf16 row stride of the [.][token] planes
+    constexpr int SKP = DK + 16;  // bf16 row stride of the S^T planes (measured fastest of the 16-byte multiples)
+    constexpr int TP = CH + 16;   // bf16 row stride of the [.][token] planes (likewise)
     const int nwg = a.NV * NSLAB;
     const int lid = qs::xcd_logical(blockIdx.x, nwg);
     const int slab = lid % NSLAB, h = lid / NSLAB;
