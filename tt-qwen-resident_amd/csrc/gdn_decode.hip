@@ -164,8 +164,9 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
     constexpr int RW = DK / NW;    // rows per wave
     constexpr int RPL = RW / RG;   // rows per lane
     static_assert(RPL >= 1 && RW % RG == 0 && (VERIFY || TM == 1) && (NW == 1 || WPG == 1), "slab shape");
-    constexpr int WQ = 0;
-    constexpr int WK = NW >= 4 ? 1 : 0;
+    // conv roles by wave of the workgroup: q channels on wave 0, k on wave 1 (when there is one), the slab's v
+    // channels on wave 2 (NW = 4) or on every wave for its own slab (NW = 1)
+    constexpr int WK = (NW >= 4 || WPG >= 2) ? 1 : 0;
     constexpr int WV = NW >= 4 ? 2 : NW - 1;
     // WPG independent single-wave slab units per workgroup (NW == 1): unit = logical workgroup x WPG + wave
     const int gw = WPG > 1 ? (int)(threadIdx.x >> 6) : 0;
@@ -178,9 +179,14 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
     const int kh = h / rep;
     const int lane = threadIdx.x & 63;
     const int w = NW > 1 ? (int)(threadIdx.x >> 6) : 0;  // wave within the slab
+    const int r = NW > 1 ? w : gw;                        // wave within the workgroup
+    const bool isq = r == 0, isk = r == WK, isv = NW > 1 ? w == WV : true;
     const int cg = lane % CG, rg = lane / CG;
     const int T = VERIFY ? a.T : 1;
-    const bool kq_owner = (h % rep == 0) && (s == 0);  // writes the shared q/k channel outputs
+    // the workgroup's slab units share key head kh (12 units per key head, WPG divides 12); the workgroup
+    // holding its first unit writes the shared q/k channel outputs
+    const int u0 = lid - gw;
+    const bool kq_owner = ((u0 / NSLAB) % a.NV) % rep == 0 && u0 % NSLAB == 0;
     int slot = 0;
     if (VERIFY && a.in_slot) {
         slot = a.in_slot[b];
@@ -190,11 +196,9 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
 
     // q / k normalised per token, row r = w' RW + g + RG i stored at w' RW + g RPL + i: lane rg of wave w
     // reads its RPL rows as contiguous pieces
-    __shared__ __align__(16) float s_qn_[WPG][TM][DK];
-    __shared__ __align__(16) float s_kn_[WPG][TM][DK];
+    __shared__ __align__(16) float s_qn[TM][DK];
+    __shared__ __align__(16) float s_kn[TM][DK];
     __shared__ __align__(16) float s_v_[WPG][TM][SLAB];
-    auto &s_qn = s_qn_[gw];
-    auto &s_kn = s_kn_[gw];
     auto &s_v = s_v_[gw];
     __shared__ __align__(16) f32x4 s_red[NW > 1 ? 2 : 1][NW][2][CG];  // per token parity: wave column sums
 
@@ -205,9 +209,9 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
     const uint16_t *conv_b = CONV ? a.conv_in + user_in * a.C * (KC - 1) : nullptr;
     ConvPair<TM> inq, ink, inv;
     if (CONV) {
-        if (w == WQ) inq = conv_load<TM>(a, conv_b, b, cq, T);
-        if (w == WK) ink = conv_load<TM>(a, conv_b, b, ck, T);
-        if (w == WV) inv = conv_load<TM>(a, conv_b, b, cv, T);
+        if (isq) inq = conv_load<TM>(a, conv_b, b, cq, T);
+        if (isk) ink = conv_load<TM>(a, conv_b, b, ck, T);
+        if (isv) inv = conv_load<TM>(a, conv_b, b, cv, T);
     }
     const size_t head = (size_t)(b * a.NV + h) * DK * DV;
     const float *sp = a.s_in + (user_in * a.NV + h) * DK * DV + s * SLAB + cg * 4 + (size_t)(w * RW + rg) * DV;
@@ -227,23 +231,23 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
     float qv[2][TM], kv[2][TM], vv[2][TM];
     uint32_t yq[TM], yk[TM], yv[TM];
     if (CONV) {
-        if (w == WQ) conv_run<TM>(inq, T, qv, yq);
-        if (w == WK) conv_run<TM>(ink, T, kv, yk);
-        if (w == WV) conv_run<TM>(inv, T, vv, yv);
+        if (isq) conv_run<TM>(inq, T, qv, yq);
+        if (isk) conv_run<TM>(ink, T, kv, yk);
+        if (isv) conv_run<TM>(inv, T, vv, yv);
     } else {
 #pragma unroll
         for (int t = 0; t < TM; ++t) {
             if (t >= T) break;
             const size_t qk0 = (((size_t)b * T + t) * a.NK + kh) * DK + 2 * lane;
-            if (w == WQ) {
+            if (isq) {
                 const uint32_t q2 = *reinterpret_cast<const uint32_t *>(a.q + qk0);
                 qv[0][t] = qs::bf_lo(q2), qv[1][t] = qs::bf_hi(q2);
             }
-            if (w == WK) {
+            if (isk) {
                 const uint32_t k2 = *reinterpret_cast<const uint32_t *>(a.k + qk0);
                 kv[0][t] = qs::bf_lo(k2), kv[1][t] = qs::bf_hi(k2);
             }
-            if (w == WV) {
+            if (isv) {
                 const uint32_t v2 = *reinterpret_cast<const uint32_t *>(
                     a.v + (((size_t)b * T + t) * a.NV + h) * DV + s * SLAB + 2 * (lane & (SLAB / 2 - 1)));
                 vv[0][t] = qs::bf_lo(v2), vv[1][t] = qs::bf_hi(v2);
@@ -256,21 +260,21 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
 #pragma unroll
         for (int t = 0; t < TM; ++t) {
             if (t >= T) break;
-            if (w == WQ) {
+            if (isq) {
                 const float rq = rsqrtf(qs::wave_sum_dpp(qv[0][t] * qv[0][t] + qv[1][t] * qv[1][t]) + a.eps) * a.scale;
                 s_qn[t][p0] = qv[0][t] * rq;
                 s_qn[t][p0 + RPL] = qv[1][t] * rq;
             }
-            if (w == WK) {
+            if (isk) {
                 const float rk = rsqrtf(qs::wave_sum_dpp(kv[0][t] * kv[0][t] + kv[1][t] * kv[1][t]) + a.eps);
                 s_kn[t][p0] = kv[0][t] * rk;
                 s_kn[t][p0 + RPL] = kv[1][t] * rk;
             }
-            if (w == WV && lane < SLAB / 2)
+            if (isv && lane < SLAB / 2)
                 *reinterpret_cast<float2 *>(&s_v[t][2 * lane]) = make_float2(vv[0][t], vv[1][t]);
         }
     }
-    if (NW > 1)
+    if (NW > 1 || WPG > 1)
         __syncthreads();
     else
         __builtin_amdgcn_wave_barrier();
@@ -345,11 +349,11 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
             // in (its reads were consumed above; q and k count separately when different waves hold them)
             // and the last to arrive writes the shifted state at the end and re-arms the counter. The
             // count's return is waited for only there.
-            if (w == WV) conv_commit<VERIFY, TM>(a, inv, yv, b, cv, T, lane < SLAB / 2, lane < SLAB / 2);
-            if (w == WQ) conv_commit<VERIFY, TM>(a, inq, yq, b, cq, T, kq_owner, VERIFY && kq_owner);
-            if (w == WK) conv_commit<VERIFY, TM>(a, ink, yk, b, ck, T, kq_owner, VERIFY && kq_owner);
-            if (!VERIFY && (w == WQ || w == WK) && lane == 0)
-                arrived = atomicAdd(a.counters + (b * a.NK + kh) * 2 + (w == WQ ? 0 : 1), 1);
+            if (isv) conv_commit<VERIFY, TM>(a, inv, yv, b, cv, T, lane < SLAB / 2, lane < SLAB / 2);
+            if (isq) conv_commit<VERIFY, TM>(a, inq, yq, b, cq, T, kq_owner, VERIFY && kq_owner);
+            if (isk) conv_commit<VERIFY, TM>(a, ink, yk, b, ck, T, kq_owner, VERIFY && kq_owner);
+            if (!VERIFY && (isq || isk) && lane == 0)
+                arrived = atomicAdd(a.counters + (b * a.NK + kh) * 2 + (isq ? 0 : 1), 1);
         }
         float dl[4];
 #pragma unroll
@@ -374,12 +378,13 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
             *reinterpret_cast<uint2 *>(a.o + (size_t)gi * DV + s * SLAB + cg * 4) = pk;
         }
     }
-    if (CONV && !VERIFY && (w == WQ || w == WK)) {
-        const int last = __builtin_amdgcn_readfirstlane(arrived) == rep * NSLAB - 1;
+    if (CONV && !VERIFY && (isq || isk)) {
+        // one arrival per workgroup per counter: rep * NSLAB / WPG workgroups read key head kh's q/k history
+        const int last = __builtin_amdgcn_readfirstlane(arrived) == rep * NSLAB / WPG - 1;
         if (last) {
-            if (lane == 0) atomicExch(a.counters + (b * a.NK + kh) * 2 + (w == WQ ? 0 : 1), 0);
-            if (w == WQ) conv_commit<false, TM>(a, inq, yq, b, cq, T, false, true);
-            if (w == WK) conv_commit<false, TM>(a, ink, yk, b, ck, T, false, true);
+            if (lane == 0) atomicExch(a.counters + (b * a.NK + kh) * 2 + (isq ? 0 : 1), 0);
+            if (isq) conv_commit<false, TM>(a, inq, yq, b, cq, T, false, true);
+            if (isk) conv_commit<false, TM>(a, ink, yk, b, ck, T, false, true);
         }
     }
 }
@@ -474,9 +479,10 @@ __global__ __launch_bounds__(256) void rollback_kernel(const float *states_out, 
 }
 
 // 32-column slabs. One wave per slab when that gives at least 1024 waves (batch >= 6 at 48 value heads),
-// grouped 6 to a workgroup (at batch 8: 256 workgroups, one per CU, measured 5% faster on the same access
-// pattern than 1536 single-wave workgroups); below that each slab's rows are split over 4 waves so the
-// grid fills the chip. The choice depends on the
+// grouped 6 to a workgroup: 6 consecutive slab units are half of one key head's 12, so the q / k conv runs
+// once per workgroup (waves 0 and 1, shared through LDS) and 2 workgroups count in per key head; at batch 8
+// that is 256 workgroups, one per CU, which streams the same access pattern ~5% faster than 1536
+// single-wave workgroups. Below 1024 units each slab's rows are split over 4 waves so the grid fills the chip. The choice depends on the
 // batch only, so a one-token verify reproduces decode bit for bit at every batch. Verify kernels are
 // compiled for up to 4 and up to 8 tokens.
 template <bool CONV, bool VERIFY, int TM>
