@@ -162,6 +162,21 @@ int qs_paged_gqa_decode(const uint16_t *q, const uint16_t *k_new, const uint16_t
                         void *workspace, int B, int T, int NQ, int NKV, int HD, int block, int max_blocks,
                         int num_blocks, int pages_per_split, float scale, void *stream);
 
+/* The attention mixer of one decode / verify step around a5 + a6 (the path's edges, torch model.py:237-246):
+ *   qn = rope(rmsnorm(q) * wq), kn = bf16(rope(rmsnorm(k_new) * wk)) appended with v_new, and
+ *   o = bf16(softmax(qn K^T) V * sigmoid(gate)), causal among the T new rows as qs_paged_gqa_decode.
+ * rmsnorm(x) = x * rsqrt(mean(x^2) + eps) over the head dim; wq, wk [HD] fp32, 16-byte aligned, with the
+ * softmax scale folded into wq as the reference folds 1/sqrt(HD) (model.py:237); rope rotates the first rot
+ * dims of each head with halves paired as model.py:135-140, rope_cos / rope_sin [B, T, rot / 2] fp32 holding
+ * each token's table (model.py:128-132); rot 0 skips it. q, gate [B, T, NQ, HD] bf16 (raw projection
+ * slices), k_new, v_new [B, T, NKV, HD] bf16. Replaces the q/k norm + rope of the attention cores
+ * (kernels/attn_compute_common.hpp:153-279) and the gate of kernels/attn_leader_compute.cpp:22-79. */
+int qs_attn_mixer_decode(const uint16_t *q, const uint16_t *k_new, const uint16_t *v_new, const uint16_t *gate,
+                         const float *wq, const float *wk, const float *rope_cos, const float *rope_sin, int rot,
+                         uint16_t *k_cache, uint16_t *v_cache, const int *block_table, const int *seq_lens,
+                         uint16_t *o, void *workspace, int B, int T, int NQ, int NKV, int HD, int block,
+                         int max_blocks, int num_blocks, int pages_per_split, float eps, void *stream);
+
 /* ---------------------------------------------------------------------------------------- a8: prefill
  * Chunked gated delta rule over one sequence (WY/UT form, bf16 MFMA, fp32 state carry), L2-norm of q
  * (times scale) and k inside:

@@ -40,6 +40,10 @@ __all__ = [
     "gqa_decode",
     "attention_partials",
     "merge_partials",
+    "rmsnorm",
+    "rope_tables",
+    "rope",
+    "attn_mixer",
     "gdn_chunk_prefill",
     "gdn_chunk_prefill_wy",
 ]
@@ -332,6 +336,51 @@ def merge_partials(parts):
     L = sum(float(l) * math.exp(float(m) - M) for m, l, _ in parts)
     o = sum(o * math.exp(float(m) - M) for m, _, o in parts)
     return o / L
+
+
+# ------------------------------------------------------------------------- the attention mixer's edges
+
+
+def rmsnorm(x, w=None, eps=EPS):
+    """x * rsqrt(mean(x^2) + eps) over the last dim, times w — model.py:86-89 (EPS common.py:15)."""
+    y = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
+    return y if w is None else y * w
+
+
+def rope_tables(pos, rot=64, theta=1e7):
+    """cos, sin of position(s) ``pos`` for the first ``rot`` dims: inverse frequencies theta^(-2i/rot),
+    computed in float64 and rounded to float32 — model.py:128-132 (ROPE_THETA, ROT model.py:51-52).
+    pos: int or integer tensor of any shape -> cos, sin [..., rot // 2]."""
+    inv = 1.0 / theta ** (torch.arange(0, rot, 2, dtype=torch.float64) / rot)
+    ang = torch.as_tensor(pos, dtype=torch.float64)[..., None] * inv
+    return torch.cos(ang).float(), torch.sin(ang).float()
+
+
+def rope(t, cos, sin, rot=64):
+    """Rotary embedding of the first ``rot`` dims with the halves paired — model.py:135-140:
+    t[:h] = a cos - b sin, t[h:rot] = b cos + a sin (a = t[:h], b = t[h:rot], h = rot / 2); cos, sin
+    broadcast over the leading dims of t except the last."""
+    h = rot // 2
+    t = t.clone()
+    a, b = t[..., :h].clone(), t[..., h:rot].clone()
+    t[..., :h] = a * cos - b * sin
+    t[..., h:rot] = b * cos + a * sin
+    return t
+
+
+def attn_mixer(q, k_new, v_new, gate, wq, wk, cos, sin, k_cache, v_cache, block_table, seq_lens, rot=64, eps=EPS):
+    """The attention mixer around the paged cache for T tokens per user — model.py:237-246:
+    qn = rope(rmsnorm(q, wq)) (fp32; wq carries the softmax scale, model.py:237), kn = bf16(rope(rmsnorm(k,
+    wk))), kn and v appended at positions seq_lens - T + t (the caches are updated in place), and
+    o = bf16(softmax(qn K^T) V * sigmoid(gate)), causal among the T new rows.
+    q, gate [B, T, NQ, HD]; k_new, v_new [B, T, NKV, HD]; cos, sin [B, T, rot / 2] -> o [B, T, NQ, HD]."""
+    cq, sq = cos[:, :, None], sin[:, :, None]
+    qn = rope(rmsnorm(q.float(), wq, eps), cq, sq, rot)
+    kn = bf16(rope(rmsnorm(k_new.float(), wk, eps), cq, sq, rot))
+    T = q.shape[1]
+    paged_append(k_cache, v_cache, kn.to(k_cache.dtype), v_new, block_table, seq_lens - T)
+    o = gqa_decode(qn, k_cache, v_cache, block_table, seq_lens, 1.0)
+    return bf16(o * torch.sigmoid(gate.float()))
 
 
 # --------------------------------------------------------------------------------------------- a8: prefill

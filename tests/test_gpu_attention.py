@@ -76,3 +76,34 @@ def test_attention_repeatable(dev):
         for _ in range(3)
     ]
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
+
+
+@pytest.mark.parametrize("B,ctx,T,pps", [(2, 1000, 1, 4), (1, 2048, 3, 2), (3, 700, 2, 64)])
+def test_attn_mixer(dev, B, ctx, T, pps):
+    """q/k RMSNorm + partial RoPE and the sigmoid gate around the paged attention (model.py:237-246), one
+    token (VALU kernel), three verify rows (MFMA kernel) and one split (no merge): the appended K rows within
+    one bf16 ulp of the oracle's (rsqrt and the rotation differ in the last fp32 bits between libraries), V
+    rows bit-exact, the output rtol 2e-2."""
+    from conftest import bf16_ulp_mismatch
+
+    d = W.attn_layer(B, ctx, "cpu", seed=ctx + T, T=T, num_blocks=64)
+    gen = torch.Generator().manual_seed(ctx)
+    gate = torch.randn(d["q"].shape, generator=gen).bfloat16()
+    wq = (1 + 0.1 * torch.randn(256, generator=gen)) / 16.0
+    wk = 1 + 0.1 * torch.randn(256, generator=gen)
+    pos = (d["seq_lens"] - T)[:, None] + torch.arange(T)[None]
+    cos, sin = O.rope_tables(pos + 5000)
+    g = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in d.items()}
+    o = ops.attn_mixer_decode(g["q"], g["k_new"], g["v_new"], gate.to(dev), wq.to(dev), wk.to(dev), cos.to(dev),
+                              sin.to(dev), g["k_cache"], g["v_cache"], g["block_table"], g["seq_lens"],
+                              pages_per_split=pps)  # fmt: skip
+    kc, vc = d["k_cache"].clone(), d["v_cache"].clone()
+    o_ref = O.attn_mixer(d["q"], d["k_new"], d["v_new"], gate, wq, wk, cos, sin, kc, vc, d["block_table"],
+                         d["seq_lens"])  # fmt: skip
+    assert torch.equal(g["v_cache"].cpu(), vc)
+    ulps, frac = bf16_ulp_mismatch(g["k_cache"].cpu(), kc)
+    assert ulps <= 1 and frac < 1e-3, (ulps, frac)
+    assert_bf16_output(o, o_ref)
+    # the rope tables of the wrapper equal the oracle's
+    c2, s2 = ops.rope_tables(pos.to(dev) + 5000)
+    assert torch.equal(c2.cpu(), cos) and torch.equal(s2.cpu(), sin)

@@ -295,3 +295,71 @@ def test_prefill_chunked_equals_recurrence():
     # masked rows (g = 0, beta = 0) leave the state unchanged
     _, Sm = O.gdn_chunk_prefill(q[:5], k[:5], v[:5], torch.zeros(5, NV).double(), torch.zeros(5, NV).double(), S0)
     assert torch.equal(Sm, S0)
+
+
+# ------------------------------------------------------------------------- the attention mixer's edges
+
+
+def test_rmsnorm_closed_form_and_scale_invariance():
+    gen = torch.Generator().manual_seed(11)
+    x = torch.randn(5, 256, generator=gen, dtype=torch.float64)
+    y = O.rmsnorm(x, eps=1e-6)
+    ms = x.pow(2).mean(-1)
+    # mean(y^2) = mean(x^2) / (mean(x^2) + eps) exactly, and scaling x does not change y beyond the eps
+    torch.testing.assert_close(y.pow(2).mean(-1), ms / (ms + 1e-6), rtol=1e-12, atol=0)
+    torch.testing.assert_close(O.rmsnorm(7.0 * x, eps=1e-6), y, rtol=1e-6, atol=1e-9)
+    w = torch.randn(256, generator=gen, dtype=torch.float64)
+    torch.testing.assert_close(O.rmsnorm(x, w, 1e-6), y * w, rtol=0, atol=0)
+
+
+def test_rope_tables_values():
+    c, s = O.rope_tables(0)
+    assert torch.equal(c, torch.ones(32)) and torch.equal(s, torch.zeros(32))
+    c, s = O.rope_tables(torch.tensor([1, 1000]))
+    # frequency 0 is theta^0 = 1 rad per position; the last one theta^(-62/64)
+    assert abs(float(c[0, 0]) - math.cos(1.0)) < 1e-7 and abs(float(s[1, 0]) - math.sin(1000.0)) < 1e-6
+    f = 1e7 ** (-62 / 64)
+    assert abs(float(s[1, 31]) - math.sin(1000 * f)) < 1e-7
+
+
+def test_rope_is_a_rotation_of_dim_pairs():
+    gen = torch.Generator().manual_seed(12)
+    t = torch.randn(3, 256, generator=gen, dtype=torch.float64)
+    # identity at angle 0; dims past rot untouched
+    c0, s0 = torch.ones(32, dtype=torch.float64), torch.zeros(32, dtype=torch.float64)
+    assert torch.equal(O.rope(t, c0, s0), t)
+    ang_a = torch.rand(32, generator=gen, dtype=torch.float64) * 6
+    ang_b = torch.rand(32, generator=gen, dtype=torch.float64) * 6
+    ra = O.rope(t, torch.cos(ang_a), torch.sin(ang_a))
+    assert torch.equal(ra[:, 64:], t[:, 64:])
+    # each pair (d, d + 32) keeps its norm, and rotations compose by adding angles
+    torch.testing.assert_close(ra[:, :32] ** 2 + ra[:, 32:64] ** 2, t[:, :32] ** 2 + t[:, 32:64] ** 2)
+    rab = O.rope(ra, torch.cos(ang_b), torch.sin(ang_b))
+    torch.testing.assert_close(rab, O.rope(t, torch.cos(ang_a + ang_b), torch.sin(ang_a + ang_b)))
+    # the pair (a, b) turns like the complex number a + i b multiplied by e^{i angle}
+    z = torch.complex(t[:, :32], t[:, 32:64]) * torch.exp(1j * ang_a)
+    torch.testing.assert_close(ra[:, :32], z.real)
+    torch.testing.assert_close(ra[:, 32:64], z.imag)
+
+
+def test_attn_mixer_reduces_to_attention():
+    """With unit norm weights, no rotation and a gate at +30 (sigmoid = 1 in fp32) the mixer is plain
+    attention over rmsnorm(q) (scale folded into wq) with rmsnorm(k) appended; a gate of 0 halves it."""
+    d = __import__("qwen36_state.workloads", fromlist=["x"]).attn_layer(2, 300, "cpu", seed=4, T=2, num_blocks=16)
+    B, T = 2, 2
+    wq = torch.full((256,), 1 / 16.0)
+    wk = torch.ones(256)
+    cos, sin = O.rope_tables(torch.zeros(B, T, dtype=torch.long))
+    kc, vc = d["k_cache"].clone(), d["v_cache"].clone()
+    gate = torch.full(d["q"].shape, 30.0).bfloat16()
+    o = O.attn_mixer(d["q"], d["k_new"], d["v_new"], gate, wq, wk, cos, sin, kc, vc, d["block_table"],
+                     d["seq_lens"])  # fmt: skip
+    kn = O.bf16(O.rmsnorm(d["k_new"].float()))
+    kc2, vc2 = d["k_cache"].clone(), d["v_cache"].clone()
+    O.paged_append(kc2, vc2, kn.bfloat16(), d["v_new"], d["block_table"], d["seq_lens"] - T)
+    assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
+    ref = O.gqa_decode(O.rmsnorm(d["q"].float()), kc2, vc2, d["block_table"], d["seq_lens"], 1 / 16.0)
+    torch.testing.assert_close(o, O.bf16(ref), rtol=0, atol=0)
+    o0 = O.attn_mixer(d["q"], d["k_new"], d["v_new"], torch.zeros_like(gate), wq, wk, cos, sin, kc, vc,
+                      d["block_table"], d["seq_lens"])  # fmt: skip
+    torch.testing.assert_close(o0, O.bf16(ref * 0.5), rtol=0, atol=0)

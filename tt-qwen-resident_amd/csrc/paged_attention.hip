@@ -50,7 +50,59 @@ struct AttnArgs {
     float *part_ml;                     // [B, T, NKV, nsplit, G, 2]
     int B, T, NQ, NKV, max_blocks, num_blocks, pps, nsplit;
     float scale;
+    // mixer edges (qs_attn_mixer_decode; null / 0 for plain attention): q and the new k rows are
+    // RMS-normalised times wq / wk [HD] and rotated on their first rot dims with rcos / rsin
+    // [B, T, rot / 2]; the output is multiplied by sigmoid(gate [B, T, NQ, HD])
+    const uint16_t *gate;
+    const float *wq, *wk, *rcos, *rsin;
+    int rot;
+    float eps;
 };
+
+// Mixer prologue of one 8-element chunk (raw bf16 bits, chunk ch of a 256-dim row whose 32 chunks sit in 32
+// consecutive, fully active lanes): y = x * rsqrt(mean(x^2) + eps) * w, then the rotary embedding on the
+// first rot dims with the halves paired as at model.py:135-140 (d < rot/2 with d + rot/2:
+// y_d c - y_{d+h} s and y_{d+h} c + y_d s). fp32 throughout (model.py:86-89, :237-238).
+__device__ __forceinline__ void mixer_chunk(const uint4 raw, int ch, const float *w, const float *cs,
+                                            const float *sn, int rot, float eps, float y[8]) {
+    const uint32_t wd[4] = {raw.x, raw.y, raw.z, raw.w};
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        y[2 * e] = qs::bf_lo(wd[e]);
+        y[2 * e + 1] = qs::bf_hi(wd[e]);
+        ss = fmaf(y[2 * e], y[2 * e], ss);
+        ss = fmaf(y[2 * e + 1], y[2 * e + 1], ss);
+    }
+    ss += qs::dpp<0xB1>(ss);
+    ss += qs::dpp<0x4E>(ss);
+    ss += qs::dpp<0x124>(ss);
+    ss += qs::dpp<0x128>(ss);
+    ss += __shfl_xor(ss, 16, 64);  // the 32 lanes of the row
+    const float r = rsqrtf(ss * (1.0f / HD) + eps);
+    const float4 w0 = *reinterpret_cast<const float4 *>(w + ch * 8), w1 = *reinterpret_cast<const float4 *>(w + ch * 8 + 4);
+    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = y[i] * r * wv[i];
+    if (rot > 0) {
+        const int half = rot / 2, hc = half / 8;  // dims / chunks per half
+        float yp[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) yp[i] = __shfl_xor(y[i], hc, 64);
+        if (ch < 2 * hc) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int d = (ch * 8 + i) % half;
+                y[i] = ch < hc ? y[i] * cs[d] - yp[i] * sn[d] : y[i] * cs[d] + yp[i] * sn[d];
+            }
+        }
+    }
+}
+__device__ __forceinline__ uint4 pack8(const float y[8]) {
+    return make_uint4(qs::cvt_pk_bf16(y[0], y[1]), qs::cvt_pk_bf16(y[2], y[3]), qs::cvt_pk_bf16(y[4], y[5]),
+                      qs::cvt_pk_bf16(y[6], y[7]));
+}
+__device__ __forceinline__ float sigm(float g) { return 1.0f / (1.0f + expf(-g)); }
 
 // Workspace layout (bytes): part_ml | part_o, each 256-byte aligned.
 struct WsLayout {
@@ -107,17 +159,22 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     // complete before the barrier that precedes the page walk, so the walk reads every row - new ones
     // included - from the pool. No other workgroup reads these pages.
     if (a.k_new && p0 <= (n - 1) / BLK && base / BLK < p1) {
-        for (int idx = tid; idx < T * 64; idx += 256) {
+        for (int idx = tid; idx < T * 64; idx += 256) {  // whole waves: T * 64 is a multiple of 64
             const int t = idx >> 6, kv = (idx >> 5) & 1, ch = idx & 31;
             const int pos = base + t, pi = pos / BLK;
+            const size_t src = (((size_t)b * T + t) * a.NKV + g) * HD + ch * 8;
+            uint4 u = *reinterpret_cast<const uint4 *>((kv ? a.v_new : a.k_new) + src);
+            if (a.wk) {  // k rows normalised and rotated (all lanes take part in the row reductions)
+                float y[8];
+                const size_t rc = ((size_t)b * T + t) * (a.rot / 2);
+                mixer_chunk(u, ch, a.wk, a.rcos + rc, a.rsin + rc, a.rot, a.eps, y);
+                if (!kv) u = pack8(y);
+            }
             if (pi < p0 || pi >= p1) continue;
             const int pg = bt[pi];  // per thread: the new rows may straddle two pages
             if (pg < 0 || pg >= a.num_blocks) continue;
             const size_t dst = (((size_t)pg * a.NKV + g) * BLK + (pos % BLK)) * HD + ch * 8;
-            const size_t src = (((size_t)b * T + t) * a.NKV + g) * HD + ch * 8;
-            const uint16_t *s = kv ? a.v_new : a.k_new;
-            uint16_t *d = kv ? a.v_cache : a.k_cache;
-            *reinterpret_cast<uint4 *>(d + dst) = *reinterpret_cast<const uint4 *>(s + src);
+            *reinterpret_cast<uint4 *>((kv ? a.v_cache : a.k_cache) + dst) = u;
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();  // the rows are read by the wave that owns their 16-row slice (the branch is uniform)
@@ -177,7 +234,14 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             for (int k = 0; k < QCH; ++k) {
                 const int idx = tid + 256 * k;
                 const int tt = idx / (G * 32), hh = (idx / 32) % G, ch = idx & 31;
-                if (idx < TT * G * 32) *reinterpret_cast<uint4 *>(&s_q[tt][hh][ch * 8]) = qreg[k];
+                uint4 u = qreg[k];
+                if (a.wq) {  // normalised and rotated q (all lanes take part in the row reductions)
+                    float y[8];
+                    const size_t rc = ((size_t)b * T + min(tg + tt, T - 1)) * (a.rot / 2);
+                    mixer_chunk(u, ch, a.wq, a.rcos + rc, a.rsin + rc, a.rot, a.eps, y);
+                    u = pack8(y);
+                }
+                if (idx < TT * G * 32) *reinterpret_cast<uint4 *>(&s_q[tt][hh][ch * 8]) = u;
             }
             __syncthreads();
         };
@@ -360,8 +424,11 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             for (int h = 0; h < G; ++h) {
                 const float O = s_w[0][h] * s_acc[0][h][tid] + s_w[1][h] * s_acc[1][h][tid] +
                                 s_w[2][h] * s_acc[2][h][tid] + s_w[3][h] * s_acc[3][h][tid];
-                if (a.nsplit == 1)
-                    a.o[(((size_t)b * T + t) * a.NQ + g * G + h) * HD + tid] = (uint16_t)qs::f2bf(O / s_L[h]);
+                if (a.nsplit == 1) {
+                    const size_t oi = (((size_t)b * T + t) * a.NQ + g * G + h) * HD + tid;
+                    const float gt = a.gate ? sigm(qs::bf2f(a.gate[oi])) : 1.0f;
+                    a.o[oi] = (uint16_t)qs::f2bf(O / s_L[h] * gt);
+                }
                 else
                     a.part_o[((row * a.nsplit + split) * G + h) * HD + tid] = O;
             }
@@ -441,14 +508,19 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
         for (int idx = lane; idx < T * 64; idx += 64) {
             const int t = idx >> 6, kv = (idx >> 5) & 1, ch = idx & 31;
             const int pos = base + t, sl = pos / 16;
+            const size_t src = (((size_t)b * T + t) * a.NKV + g) * HD + ch * 8;
+            uint4 u = *reinterpret_cast<const uint4 *>((kv ? a.v_new : a.k_new) + src);
+            if (a.wk) {  // k rows normalised and rotated (all lanes take part in the row reductions)
+                float y[8];
+                const size_t rc = ((size_t)b * T + t) * (a.rot / 2);
+                mixer_chunk(u, ch, a.wk, a.rcos + rc, a.rsin + rc, a.rot, a.eps, y);
+                if (!kv) u = pack8(y);
+            }
             if (sl < s0 || sl >= s1) continue;
             const int pg = bt[pos / BLK];  // per lane: the new rows may straddle slices and pages
             if (pg < 0 || pg >= a.num_blocks) continue;
             const size_t dst = (((size_t)pg * a.NKV + g) * BLK + (pos % BLK)) * HD + ch * 8;
-            const size_t src = (((size_t)b * T + t) * a.NKV + g) * HD + ch * 8;
-            const uint16_t *sv = kv ? a.v_new : a.k_new;
-            uint16_t *d = kv ? a.v_cache : a.k_cache;
-            *reinterpret_cast<uint4 *>(d + dst) = *reinterpret_cast<const uint4 *>(sv + src);
+            *reinterpret_cast<uint4 *>((kv ? a.v_cache : a.k_cache) + dst) = u;
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
@@ -545,13 +617,18 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
             }
             mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float mn = fmaxf(m[nt], mx * sl2);
+            // lazy rescaling: the reference max m moves only when a score exceeds it by more than 2^8 (log2
+            // domain); probabilities up to 256 are exact in fp32 and in range for bf16, so the normalised
+            // result is unchanged while the 64 accumulators of a tile are rescaled only rarely
+            const float cand = mx * sl2;
+            const bool move = m[nt] == -INFINITY ? cand != -INFINITY : cand > m[nt] + 8.0f;
+            const float mn = move ? cand : m[nt];
             float e[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 e[i] = sc[i] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(fmaf(sc[i], sl2, -mn));
             const uint32_t p01 = qs::cvt_pk_bf16(e[0], e[1]), p23 = qs::cvt_pk_bf16(e[2], e[3]);
-            if (__any(mn != m[nt])) {  // rescale only when some running max moved
+            if (__any(move)) {
                 const float alpha = m[nt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[nt] - mn);
                 lp[nt] *= alpha;
 #pragma unroll
@@ -582,8 +659,15 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
     }
 #pragma unroll
     for (int k = 0; k < QCH; ++k) {
-        const int idx = tid + 256 * k;
-        *reinterpret_cast<uint4 *>(&s_q[idx >> 5][(idx & 31) * 8]) = qreg[k];
+        const int idx = tid + 256 * k, qr = idx >> 5, ch = idx & 31;
+        uint4 u = qreg[k];
+        if (a.wq) {  // normalised and rotated q (all lanes take part in the row reductions)
+            float y[8];
+            const size_t rc = ((size_t)b * T + min(qr / G, T - 1)) * (a.rot / 2);
+            mixer_chunk(u, ch, a.wq, a.rcos + rc, a.rsin + rc, a.rot, a.eps, y);
+            u = pack8(y);
+        }
+        *reinterpret_cast<uint4 *>(&s_q[qr][ch * 8]) = u;
     }
     __syncthreads();
     for (int sl = s0; sl < s1; sl += 2) {
@@ -650,10 +734,16 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
         const size_t row = ((size_t)b * T + t) * a.NKV + g;
         if (a.nsplit == 1) {
             const float inv = 1.0f / lp[nt];
-            uint16_t *op = a.o + (((size_t)b * T + t) * a.NQ + g * G + hh) * HD + 4 * lg;
+            const size_t oi = (((size_t)b * T + t) * a.NQ + g * G + hh) * HD + 4 * lg;
+            uint16_t *op = a.o + oi;
 #pragma unroll
             for (int dt = 0; dt < 16; ++dt) {
-                const f32x4_t v = oacc[nt][dt] * inv;
+                f32x4_t v = oacc[nt][dt] * inv;
+                if (a.gate) {
+                    const uint2 gw = *reinterpret_cast<const uint2 *>(a.gate + oi + 16 * dt);
+                    v[0] *= sigm(qs::bf_lo(gw.x)), v[1] *= sigm(qs::bf_hi(gw.x));
+                    v[2] *= sigm(qs::bf_lo(gw.y)), v[3] *= sigm(qs::bf_hi(gw.y));
+                }
                 *reinterpret_cast<uint2 *>(op + 16 * dt) = make_uint2(qs::cvt_pk_bf16(v[0], v[1]), qs::cvt_pk_bf16(v[2], v[3]));
             }
         } else {
@@ -737,8 +827,13 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, int G) {
     const float r0 = (((O.x + p1.x) + p2.x) + p3.x) * inv, r1 = (((O.y + p1.y) + p2.y) + p3.y) * inv;
     const float r2 = (((O.z + p1.z) + p2.z) + p3.z) * inv, r3 = (((O.w + p1.w) + p2.w) + p3.w) * inv;
     const int g = row % a.NKV, bt = row / a.NKV;
-    *reinterpret_cast<uint2 *>(a.o + ((size_t)bt * a.NQ + g * G + h) * HD + 4 * lane) =
-        make_uint2(qs::cvt_pk_bf16(r0, r1), qs::cvt_pk_bf16(r2, r3));
+    const size_t oi = ((size_t)bt * a.NQ + g * G + h) * HD + 4 * lane;
+    float o0 = r0, o1 = r1, o2 = r2, o3 = r3;
+    if (a.gate) {
+        const uint2 gw = *reinterpret_cast<const uint2 *>(a.gate + oi);
+        o0 *= sigm(qs::bf_lo(gw.x)), o1 *= sigm(qs::bf_hi(gw.x)), o2 *= sigm(qs::bf_lo(gw.y)), o3 *= sigm(qs::bf_hi(gw.y));
+    }
+    *reinterpret_cast<uint2 *>(a.o + oi) = make_uint2(qs::cvt_pk_bf16(o0, o1), qs::cvt_pk_bf16(o2, o3));
 }
 
 int nsplit_of(int max_blocks, int pps) { return (max_blocks + pps - 1) / pps; }
@@ -752,30 +847,23 @@ extern "C" size_t qs_paged_attention_workspace_bytes(int B, int T, int NQ, int N
     return ws_layout(B, T, NKV, NQ / NKV, ns).total;
 }
 
-extern "C" int qs_paged_gqa_decode(const uint16_t *q, const uint16_t *k_new, const uint16_t *v_new,
-                                   uint16_t *k_cache, uint16_t *v_cache, const int *block_table, const int *seq_lens,
-                                   uint16_t *o, void *workspace, int B, int T, int NQ, int NKV, int HDa, int block,
-                                   int max_blocks, int num_blocks, int pages_per_split, float scale, void *stream) {
-    QS_REQUIRE(q && k_cache && v_cache && block_table && seq_lens && o, "qs_paged_gqa_decode: null pointer");
-    QS_REQUIRE((k_new == nullptr) == (v_new == nullptr), "qs_paged_gqa_decode: give both k_new and v_new or neither");
-    QS_REQUIRE(HDa == HD, "qs_paged_gqa_decode: HD must be %d (got %d)", HD, HDa);
-    QS_REQUIRE(block == BLK, "qs_paged_gqa_decode: block must be %d (got %d)", BLK, block);
-    QS_REQUIRE(B > 0 && T >= 1 && T <= 16, "qs_paged_gqa_decode: need B > 0 and 1 <= T <= 16");
-    QS_REQUIRE(NKV > 0 && NQ > 0 && NQ % NKV == 0, "qs_paged_gqa_decode: NQ (%d) must be a multiple of NKV (%d)",
-               NQ, NKV);
-    QS_REQUIRE(max_blocks > 0 && num_blocks > 0, "qs_paged_gqa_decode: bad page counts");
-    QS_REQUIRE(pages_per_split > 0 && pages_per_split <= 64,
-               "qs_paged_gqa_decode: pages_per_split must be in [1, 64] (got %d)", pages_per_split);
+static int attn_launch(AttnArgs a, void *workspace, int HDa, int block, const char *who, void *stream) {
+    const int B = a.B, T = a.T, NQ = a.NQ, NKV = a.NKV, max_blocks = a.max_blocks, pages_per_split = a.pps;
+    QS_REQUIRE(a.q && a.k_cache && a.v_cache && a.block_table && a.seq_lens && a.o, "%s: null pointer", who);
+    QS_REQUIRE((a.k_new == nullptr) == (a.v_new == nullptr), "%s: give both k_new and v_new or neither", who);
+    QS_REQUIRE(HDa == HD, "%s: HD must be %d (got %d)", who, HD, HDa);
+    QS_REQUIRE(block == BLK, "%s: block must be %d (got %d)", who, BLK, block);
+    QS_REQUIRE(B > 0 && T >= 1 && T <= 16, "%s: need B > 0 and 1 <= T <= 16", who);
+    QS_REQUIRE(NKV > 0 && NQ > 0 && NQ % NKV == 0, "%s: NQ (%d) must be a multiple of NKV (%d)", who, NQ, NKV);
+    QS_REQUIRE(max_blocks > 0 && a.num_blocks > 0, "%s: bad page counts", who);
+    QS_REQUIRE(pages_per_split > 0 && pages_per_split <= 64, "%s: pages_per_split must be in [1, 64] (got %d)", who,
+               pages_per_split);
     const int G = NQ / NKV;
     const int ns = nsplit_of(max_blocks, pages_per_split);
-    QS_REQUIRE(ns == 1 || workspace, "qs_paged_gqa_decode: %d splits need a workspace", ns);
-    QS_REQUIRE(ns <= MAX_SPLITS, "qs_paged_gqa_decode: %d splits exceed %d (raise pages_per_split)", ns, MAX_SPLITS);
-    QS_REQUIRE((long)B * NKV * ns < (1L << 31), "qs_paged_gqa_decode: grid too large");
-    AttnArgs a{};
-    a.q = q, a.k_new = k_new, a.v_new = v_new, a.k_cache = k_cache, a.v_cache = v_cache;
-    a.block_table = block_table, a.seq_lens = seq_lens, a.o = o;
-    a.B = B, a.T = T, a.NQ = NQ, a.NKV = NKV, a.max_blocks = max_blocks, a.num_blocks = num_blocks;
-    a.pps = pages_per_split, a.nsplit = ns, a.scale = scale;
+    QS_REQUIRE(ns == 1 || workspace, "%s: %d splits need a workspace", who, ns);
+    QS_REQUIRE(ns <= MAX_SPLITS, "%s: %d splits exceed %d (raise pages_per_split)", who, ns, MAX_SPLITS);
+    QS_REQUIRE((long)B * NKV * ns < (1L << 31), "%s: grid too large", who);
+    a.nsplit = ns;
     if (workspace) {
         const WsLayout L = ws_layout(B, T, NKV, G, ns);
         char *ws = static_cast<char *>(workspace);
@@ -798,13 +886,13 @@ extern "C" int qs_paged_gqa_decode(const uint16_t *q, const uint16_t *k_new, con
             case 4: QS_MFMA_LAUNCH(4) break;
             case 6: QS_MFMA_LAUNCH(6) break;
             case 8: QS_MFMA_LAUNCH(8) break;
-            default: QS_REQUIRE(false, "qs_paged_gqa_decode: group size NQ/NKV = %d not in {1, 2, 4, 6, 8}", G);
+            default: QS_REQUIRE(false, "%s: group size NQ/NKV = %d not in {1, 2, 4, 6, 8}", who, G);
         }
 #undef QS_MFMA_LAUNCH
-        if (int e = qs::launch_status("qs_paged_gqa_decode")) return e;
+        if (int e = qs::launch_status(who)) return e;
         if (ns > 1) {
             attn_merge_kernel<<<B * T * NKV * G, 256, 0, st>>>(a, G);
-            return qs::launch_status("qs_paged_gqa_decode (merge)");
+            return qs::launch_status(who);
         }
         return QS_OK;
     }
@@ -817,13 +905,46 @@ extern "C" int qs_paged_gqa_decode(const uint16_t *q, const uint16_t *k_new, con
         case 4: QS_ATTN_LAUNCH(4) break;
         case 6: QS_ATTN_LAUNCH(6) break;
         case 8: QS_ATTN_LAUNCH(8) break;
-        default: QS_REQUIRE(false, "qs_paged_gqa_decode: group size NQ/NKV = %d not in {1, 2, 4, 6, 8}", G);
+        default: QS_REQUIRE(false, "%s: group size NQ/NKV = %d not in {1, 2, 4, 6, 8}", who, G);
     }
 #undef QS_ATTN_LAUNCH
-    if (int e = qs::launch_status("qs_paged_gqa_decode")) return e;
+    if (int e = qs::launch_status(who)) return e;
     if (ns > 1) {
         attn_merge_kernel<<<B * T * NKV * G, 256, 0, st>>>(a, G);
-        return qs::launch_status("qs_paged_gqa_decode (merge)");
+        return qs::launch_status(who);
     }
     return QS_OK;
+}
+
+extern "C" int qs_paged_gqa_decode(const uint16_t *q, const uint16_t *k_new, const uint16_t *v_new,
+                                   uint16_t *k_cache, uint16_t *v_cache, const int *block_table, const int *seq_lens,
+                                   uint16_t *o, void *workspace, int B, int T, int NQ, int NKV, int HDa, int block,
+                                   int max_blocks, int num_blocks, int pages_per_split, float scale, void *stream) {
+    AttnArgs a{};
+    a.q = q, a.k_new = k_new, a.v_new = v_new, a.k_cache = k_cache, a.v_cache = v_cache;
+    a.block_table = block_table, a.seq_lens = seq_lens, a.o = o;
+    a.B = B, a.T = T, a.NQ = NQ, a.NKV = NKV, a.max_blocks = max_blocks, a.num_blocks = num_blocks;
+    a.pps = pages_per_split, a.scale = scale;
+    return attn_launch(a, workspace, HDa, block, "qs_paged_gqa_decode", stream);
+}
+
+extern "C" int qs_attn_mixer_decode(const uint16_t *q, const uint16_t *k_new, const uint16_t *v_new,
+                                    const uint16_t *gate, const float *wq, const float *wk, const float *rope_cos,
+                                    const float *rope_sin, int rot, uint16_t *k_cache, uint16_t *v_cache,
+                                    const int *block_table, const int *seq_lens, uint16_t *o, void *workspace, int B,
+                                    int T, int NQ, int NKV, int HDa, int block, int max_blocks, int num_blocks,
+                                    int pages_per_split, float eps, void *stream) {
+    QS_REQUIRE(k_new && v_new && gate && wq && wk, "qs_attn_mixer_decode: null pointer");
+    QS_REQUIRE(rot == 0 || (rope_cos && rope_sin), "qs_attn_mixer_decode: rot > 0 needs rope_cos and rope_sin");
+    QS_REQUIRE(rot == 0 || rot == 16 || rot == 32 || rot == 64 || rot == 128 || rot == 256,
+               "qs_attn_mixer_decode: rot must be 0, 16, 32, 64, 128 or 256 (got %d)", rot);
+    QS_REQUIRE(eps > 0.f, "qs_attn_mixer_decode: eps must be positive");
+    QS_REQUIRE(((uintptr_t)wq | (uintptr_t)wk) % 16 == 0, "qs_attn_mixer_decode: wq and wk must be 16-byte aligned");
+    AttnArgs a{};
+    a.q = q, a.k_new = k_new, a.v_new = v_new, a.k_cache = k_cache, a.v_cache = v_cache;
+    a.block_table = block_table, a.seq_lens = seq_lens, a.o = o;
+    a.B = B, a.T = T, a.NQ = NQ, a.NKV = NKV, a.max_blocks = max_blocks, a.num_blocks = num_blocks;
+    a.pps = pages_per_split, a.scale = 1.0f;  // the softmax scale is folded into wq (model.py:237)
+    a.gate = gate, a.wq = wq, a.wk = wk, a.rcos = rope_cos, a.rsin = rope_sin, a.rot = rot, a.eps = eps;
+    return attn_launch(a, workspace, HDa, block, "qs_attn_mixer_decode", stream);
 }

@@ -38,6 +38,10 @@ SIGNATURES = {
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _F, _P],
     ),
+    "qs_attn_mixer_decode": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _F, _P],
+    ),
     "qs_gdn_chunk_prefill_workspace_bytes": (_Z, [_I, _I, _I, _I, _I, _I]),
     "qs_gdn_chunk_prefill": (
         _I,

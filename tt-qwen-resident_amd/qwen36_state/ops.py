@@ -13,6 +13,7 @@ from ._lib import call, lib
 
 NK, NV, DK, DV, CONV_K = 16, 48, 128, 128, 4  # model.py:48
 NQ, NKV, HD = 24, 4, 256  # model.py:50
+ROT, ROPE_THETA = 64, 1e7  # model.py:51-52
 BLOCK = 64  # vLLM block size, tt-model.yaml:41
 EPS = 1e-6  # model.py:264-267
 
@@ -399,3 +400,47 @@ def chunk_gated_delta_rule(q, k, v, g, beta, *, scale=None, initial_state=None, 
     if output_head_major:
         o = o.transpose(0, 1).contiguous()
     return o, (S if output_final_state else None)
+
+
+# ------------------------------------------------------------------------------ the attention mixer's edges
+
+
+def rope_tables(positions, rot=ROT, theta=ROPE_THETA):
+    """cos, sin [..., rot / 2] fp32 of integer positions (any shape, on the positions' device), computed in
+    float64 as model.py:128-132 does."""
+    inv = 1.0 / theta ** (torch.arange(0, rot, 2, dtype=torch.float64, device=positions.device) / rot)
+    ang = positions.to(torch.float64)[..., None] * inv
+    return torch.cos(ang).float().contiguous(), torch.sin(ang).float().contiguous()
+
+
+def attn_mixer_decode(q, k_new, v_new, gate, wq, wk, cos, sin, k_cache, v_cache, block_table, seq_lens,
+                      pages_per_split=4, eps=EPS, rot=ROT, out=None, ws=None):  # fmt: skip
+    """The attention mixer of a decode (T = 1) or verify (T > 1) step around the paged cache (model.py:237-246):
+    qn = rope(rmsnorm(q) * wq), kn = bf16(rope(rmsnorm(k_new) * wk)) appended with v_new at positions
+    seq_lens - T + t, o = bf16(softmax(qn K^T) V * sigmoid(gate)).
+
+    q, gate [B, T, NQ, HD] bf16; k_new, v_new [B, T, NKV, HD] bf16; wq, wk [HD] fp32 (wq carries the softmax
+    scale, model.py:237); cos, sin [B, T, rot / 2] fp32 (``rope_tables``); the rest as ``paged_gqa_decode``."""
+    dev = k_cache.device
+    nb, nkv, block, hd = _pool_dims(k_cache, v_cache, dev)
+    B, T, nq, _ = q.shape
+    _chk(q, "q", torch.bfloat16, (B, T, nq, hd), dev)
+    _chk(gate, "gate", torch.bfloat16, (B, T, nq, hd), dev)
+    _chk(k_new, "k_new", torch.bfloat16, (B, T, nkv, hd), dev)
+    _chk(v_new, "v_new", torch.bfloat16, (B, T, nkv, hd), dev)
+    _chk(wq, "wq", torch.float32, (hd,), dev)
+    _chk(wk, "wk", torch.float32, (hd,), dev)
+    if rot:
+        _chk(cos, "cos", torch.float32, (B, T, rot // 2), dev)
+        _chk(sin, "sin", torch.float32, (B, T, rot // 2), dev)
+    _chk(block_table, "block_table", torch.int32, None, dev)
+    _chk(seq_lens, "seq_lens", torch.int32, (B,), dev)
+    mb = block_table.shape[1]
+    o = torch.empty(B, T, nq, hd, dtype=torch.bfloat16, device=dev) if out is None else out
+    if ws is None:
+        ws = attention_workspace(B, T, nq, nkv, mb, pages_per_split, dev)
+    call("qs_attn_mixer_decode", _p(q), _p(k_new), _p(v_new), _p(gate), _p(wq), _p(wk),
+         _p(cos if rot else None), _p(sin if rot else None), rot, _p(k_cache), _p(v_cache), _p(block_table),
+         _p(seq_lens), _p(o), _p(ws), B, T, nq, nkv, hd, block, mb, nb, pages_per_split, float(eps),
+         _stream(dev))  # fmt: skip
+    return o
