@@ -79,6 +79,13 @@ int qs_gdn_decode_fused(const uint16_t *x, uint16_t *conv_state, const uint16_t 
                         const float *beta, float *state, uint16_t *o, uint16_t *y_out, void *workspace, int B,
                         int NK, int NV, int DK, int DV, int K, float scale, float eps, void *stream);
 
+/* Gated RMSNorm epilogue of the GDN mixer (the path's edge, torch model.py:274-275): for each row of DV
+ * values, out = bf16(o * rsqrt(mean(o^2) + eps) * norm_w * silu(z)). o, z, out [rows, DV] bf16 (rows = B * NV,
+ * or B * T * NV after a verify step; z is the projection's z slice), norm_w [DV] fp32. Replaces steps 7-8
+ * of the GDN head cores (kernels/gdn_head_compute.cpp:320-346). */
+int qs_gdn_gated_norm(const uint16_t *o, const uint16_t *z, const float *norm_w, uint16_t *out, int rows, int DV,
+                      float eps, void *stream);
+
 /* ---------------------------------------------------------------------------------------- a7: verify
  * T tokens per user (1 <= T <= 8) through conv + delta rule in sequence, keeping every intermediate:
  *   x [B, T, C] bf16; conv_state_in [B, C, K-1]; g, beta [B, T, NV]; state_in [B, NV, DK, DV]

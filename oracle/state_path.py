@@ -41,6 +41,7 @@ __all__ = [
     "attention_partials",
     "merge_partials",
     "rmsnorm",
+    "gdn_gated_norm",
     "rope_tables",
     "rope",
     "attn_mixer",
@@ -345,6 +346,11 @@ def rmsnorm(x, w=None, eps=EPS):
     """x * rsqrt(mean(x^2) + eps) over the last dim, times w — model.py:86-89 (EPS common.py:15)."""
     y = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
     return y if w is None else y * w
+
+
+def gdn_gated_norm(o, z, norm_w, eps=EPS):
+    """The GDN mixer's epilogue per value head — model.py:274-275: bf16(rmsnorm(o, norm_w) * silu(z))."""
+    return bf16(rmsnorm(o.float(), norm_w, eps) * F.silu(z.float()))
 
 
 def rope_tables(pos, rot=64, theta=1e7):

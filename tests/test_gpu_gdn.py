@@ -188,3 +188,16 @@ def test_verify_slots_equals_copy_rollback(dev):
     bad = torch.tensor([0, 5, 2], dtype=torch.int32, device=dev)
     ops.verify_accept(bad, T, slot, seq_s, base)
     assert slot.cpu().tolist() == [1, 2, 1] and seq_s.cpu().tolist() == [12, 23, 32]
+
+
+def test_gdn_gated_norm(dev):
+    """The GDN mixer's gated RMSNorm epilogue (model.py:274-275) for a batch-8 decode and a T = 4 verify
+    output: within one bf16 ulp of the oracle (rsqrt and exp differ in the last fp32 bits)."""
+    gen = torch.Generator().manual_seed(61)
+    for shape in ((8, NV, DV), (1, 4, NV, DV)):
+        o = torch.randn(shape, generator=gen).bfloat16()
+        z = (2 * torch.randn(shape, generator=gen)).bfloat16()
+        w = 1 + 0.1 * torch.randn(DV, generator=gen)
+        y = ops.gdn_gated_norm(o.to(dev), z.to(dev), w.to(dev))
+        ulps, frac = bf16_ulp_mismatch(y, O.gdn_gated_norm(o, z, w))
+        assert ulps <= 1 and frac < 1e-2, (ulps, frac)

@@ -7,6 +7,7 @@ import os
 import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
 
 from oracle import state_path as O
 
@@ -363,3 +364,18 @@ def test_attn_mixer_reduces_to_attention():
     o0 = O.attn_mixer(d["q"], d["k_new"], d["v_new"], torch.zeros_like(gate), wq, wk, cos, sin, kc, vc,
                       d["block_table"], d["seq_lens"])  # fmt: skip
     torch.testing.assert_close(o0, O.bf16(ref * 0.5), rtol=0, atol=0)
+
+
+def test_gdn_gated_norm_special_cases():
+    """The reference's own prefill check (test_pp_kernels.py:181-194 pattern, w = 1): on = o rsqrt(mean o^2
+    + eps), out = on silu(z); silu(0) = 0 zeroes the output, and a constant row normalises to +-1."""
+    gen = torch.Generator().manual_seed(13)
+    o = torch.randn(4, 128, generator=gen)
+    z = torch.randn(4, 128, generator=gen).bfloat16()
+    w = torch.ones(128)
+    ref = o * torch.rsqrt(o.pow(2).mean(-1, keepdim=True) + 1e-6) * F.silu(z.float())
+    torch.testing.assert_close(O.gdn_gated_norm(o, z, w), O.bf16(ref), rtol=0, atol=0)
+    assert torch.equal(O.gdn_gated_norm(o, torch.zeros_like(z), w), torch.zeros(4, 128))
+    c = torch.full((1, 128), -3.0)
+    big = torch.full((1, 128), 30.0).bfloat16()  # silu(30) = 30 in fp32
+    torch.testing.assert_close(O.gdn_gated_norm(c, big, w), O.bf16(torch.full((1, 128), -30.0 / math.sqrt(1 + 1e-6 / 9))))

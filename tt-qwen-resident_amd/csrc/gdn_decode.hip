@@ -411,6 +411,26 @@ __global__ __launch_bounds__(256) void conv1d_update_kernel(const uint16_t *x, u
     st[2] = (uint16_t)xr;
 }
 
+// -------------------------------------------------------------------------------------------- gated norm
+
+// Gated RMSNorm of the delta rule's output, per row of DV values (torch model.py:274-275; the head cores'
+// step 7-8, kernels/gdn_head_compute.cpp:320-346): out = bf16(o * rsqrt(mean(o^2) + eps) * w * silu(z)).
+// One wave per row, two values per lane; the mean is a fixed-order wave reduction.
+__global__ __launch_bounds__(256) void gated_norm_kernel(const uint16_t *o, const uint16_t *z, const float *w,
+                                                         uint16_t *out, int rows, float eps) {
+    const int row = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    if (row >= rows) return;  // the whole wave
+    const int lane = threadIdx.x & 63;
+    const uint32_t o2 = reinterpret_cast<const uint32_t *>(o + (size_t)row * DV)[lane];
+    const uint32_t z2 = reinterpret_cast<const uint32_t *>(z + (size_t)row * DV)[lane];
+    const float2 w2 = reinterpret_cast<const float2 *>(w)[lane];
+    const float a = qs::bf_lo(o2), b = qs::bf_hi(o2);
+    const float r = rsqrtf(qs::wave_sum_dpp(a * a + b * b) * (1.0f / DV) + eps);
+    const float ya = a * r * w2.x * qs::silu(qs::bf_lo(z2));
+    const float yb = b * r * w2.y * qs::silu(qs::bf_hi(z2));
+    reinterpret_cast<uint32_t *>(out + (size_t)row * DV)[lane] = qs::cvt_pk_bf16(ya, yb);
+}
+
 // -------------------------------------------------------------------------------------------- gates
 
 __global__ __launch_bounds__(256) void gates_kernel(const uint16_t *a, const uint16_t *bb, const float *dt,
@@ -531,6 +551,17 @@ extern "C" int qs_conv1d_update(const uint16_t *x, uint16_t *conv_state, const u
     const int n = B * C;
     conv1d_update_kernel<<<(n + 255) / 256, 256, 0, QS_STREAM(stream)>>>(x, conv_state, taps, y, B, C);
     return qs::launch_status("qs_conv1d_update");
+}
+
+extern "C" int qs_gdn_gated_norm(const uint16_t *o, const uint16_t *z, const float *norm_w, uint16_t *out, int rows,
+                                 int DVa, float eps, void *stream) {
+    QS_REQUIRE(o && z && norm_w && out, "qs_gdn_gated_norm: null pointer");
+    QS_REQUIRE(rows > 0 && DVa == DV, "qs_gdn_gated_norm: need rows > 0 and DV = %d (got %d, %d)", DV, rows, DVa);
+    QS_REQUIRE(eps > 0.f, "qs_gdn_gated_norm: eps must be positive");
+    QS_REQUIRE(((uintptr_t)o | (uintptr_t)z | (uintptr_t)out) % 4 == 0 && (uintptr_t)norm_w % 8 == 0,
+               "qs_gdn_gated_norm: o, z, out must be 4-byte and norm_w 8-byte aligned");
+    gated_norm_kernel<<<(rows + 3) / 4, 256, 0, QS_STREAM(stream)>>>(o, z, norm_w, out, rows, eps);
+    return qs::launch_status("qs_gdn_gated_norm");
 }
 
 extern "C" int qs_gdn_gates(const uint16_t *a, const uint16_t *b, const float *dt_bias, const float *neg_a, float *g,

@@ -150,6 +150,20 @@ def gdn_decode_fused(x, conv_state, taps, g, beta, state, nk=NK, scale=None, eps
 # ------------------------------------------------------------------------------------------- a7
 
 
+def gdn_gated_norm(o, z, norm_w, eps=EPS, out=None):
+    """The GDN mixer's gated RMSNorm epilogue (model.py:274-275): bf16(rmsnorm(o) * norm_w * silu(z)) per head.
+    o, z [..., DV] bf16 (same shape); norm_w [DV] fp32."""
+    dev = o.device
+    _chk(o, "o", torch.bfloat16)
+    _chk(z, "z", torch.bfloat16, tuple(o.shape), dev)
+    dv = o.shape[-1]
+    _chk(norm_w, "norm_w", torch.float32, (dv,), dev)
+    y = torch.empty_like(o) if out is None else out
+    _chk(y, "out", torch.bfloat16, tuple(o.shape), dev)
+    call("qs_gdn_gated_norm", _p(o), _p(z), _p(norm_w), _p(y), o.numel() // dv, dv, float(eps), _stream(dev))
+    return y
+
+
 def gdn_verify_step(x, conv_state, taps, g, beta, state, nk=NK, scale=None, eps=EPS, return_y=False, out=None):
     """T tokens per user through conv + delta rule, keeping every intermediate (the verify rows of the
     reference GDN head cores, kernels/gdn_head_reader.cpp:149-187, gdn_head_writer.cpp:60-66).
