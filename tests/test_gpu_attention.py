@@ -38,6 +38,8 @@ def run_case(dev, d, pps, fused=True):
         (1, 8192, 4, 8),  # verify: 4 new rows, causal among them
         (1, 32768, 1, 1),  # 512 splits: 3-level merge tree
         (2, 4096, 1, 64),  # one split: no merge
+        (2, 3000, 6, 4),  # 36 query rows per KV head: the VALU kernel (two tokens per pass over the pages)
+        (1, 700, 7, 64),  # VALU kernel, odd token count, one split
     ],
 )
 def test_attention(dev, B, ctx, T, pps):
@@ -78,10 +80,10 @@ def test_attention_repeatable(dev):
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
 
 
-@pytest.mark.parametrize("B,ctx,T,pps", [(2, 1000, 1, 4), (1, 2048, 3, 2), (3, 700, 2, 64)])
+@pytest.mark.parametrize("B,ctx,T,pps", [(2, 1000, 1, 4), (1, 2048, 3, 2), (3, 700, 2, 64), (1, 900, 6, 4)])
 def test_attn_mixer(dev, B, ctx, T, pps):
     """q/k RMSNorm + partial RoPE and the sigmoid gate around the paged attention (model.py:237-246), one
-    token (VALU kernel), three verify rows (MFMA kernel) and one split (no merge): the appended K rows within
+    token and three verify rows (MFMA kernel), one split (no merge), six rows (VALU kernel): the appended K rows within
     one bf16 ulp of the oracle's (rsqrt and the rotation differ in the last fp32 bits between libraries), V
     rows bit-exact, the output rtol 2e-2."""
     from conftest import bf16_ulp_mismatch

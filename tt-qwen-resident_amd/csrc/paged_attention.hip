@@ -18,8 +18,6 @@
 // kernels/attn_leader_compute.cpp:42-79), so results are identical run to run. The merge is a separate
 // launch: a merge by the last split to finish runs serially in one workgroup and measured slower, and an
 // in-kernel fan-in through release / acquire fences writes back and invalidates the whole L2 of each XCD.
-#include <stdlib.h>
-
 #include "qs_common.h"
 
 namespace {
@@ -216,8 +214,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         const int nt = min(TT, T - tg);
         const int vend = base + tg + nt;  // rows at or past vend are invalid for every token of the group
         const int pe = min(p1, (vend + BLK - 1) / BLK);
-        // q of the token group: loaded into registers here, stored to LDS by store_q; for one token the
-        // store waits until the first pages' loads are in flight, so they do not queue behind q's round trip
+        // q of the token group: loaded into registers, then stored to LDS (normalised and rotated for the mixer)
         constexpr int QCH = (TT * G * 32 + 255) / 256;
         uint4 qreg[QCH];
 #pragma unroll
@@ -245,7 +242,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             }
             __syncthreads();
         };
-        if constexpr (TT != 1) store_q();
+        store_q();
 
         // m: running max (log2 domain, wave-uniform); lp: every lane adds its row's rounded probability (so
         // the wave sum is 4x the row sum), reduced over the wave once per split
@@ -344,49 +341,19 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             __builtin_amdgcn_wave_barrier();
         };
 
-        if constexpr (TT == 1) {
-            // Three page buffers rotate through the roles K(pi), V(pi) and K(pi + 1) in flight: after the
-            // scores of page pi its K buffer takes V(pi + 1), after its P V its V buffer takes K(pi + 2), so
-            // each load has about a page of compute to arrive in.
-            uint4 X[8], Y[8], Z[8];
-            auto step = [&](int pi, uint4 (&kb)[8], uint4 (&vb)[8]) {
-                const bool ok = page_at(pi) >= 0;
-                if (ok) scores_tt(pi, 0, kb);
-                if (pi + 1 < pe && page_at(pi + 1) >= 0) load_v(page_at(pi + 1), kb);
-                if (ok) {
-                    mask_v(pi, vb);
-                    pv_tt(0, vb);
-                }
-                if (pi + 2 < pe && page_at(pi + 2) >= 0) load_k(page_at(pi + 2), vb);
-            };
-            if (p0 < pe && page_at(p0) >= 0) {
-                load_k(page_at(p0), X);
-                load_v(page_at(p0), Y);
-            }
-            if (p0 + 1 < pe && page_at(p0 + 1) >= 0) load_k(page_at(p0 + 1), Z);
-            store_q();
-            for (int pi = p0; pi < pe; pi += 3) {
-                step(pi, X, Y);  // loads V(pi + 1) -> X, K(pi + 2) -> Y
-                if (pi + 1 >= pe) break;
-                step(pi + 1, Z, X);  // loads V(pi + 2) -> Z, K(pi + 3) -> X
-                if (pi + 2 >= pe) break;
-                step(pi + 2, Y, Z);  // loads V(pi + 3) -> Y, K(pi + 4) -> Z
-            }
-        } else {
-            // verify rows: the accumulators of TT tokens leave no registers for pages in flight
-            for (int pi = p0; pi < pe; ++pi) {
-                const int pg = page_at(pi);
-                if (pg < 0) continue;
-                uint4 X[8], Y[8];
-                load_k(pg, X);
-                load_v(pg, Y);
-                mask_v(pi, Y);
+        // the accumulators of TT tokens leave no registers for pages in flight
+        for (int pi = p0; pi < pe; ++pi) {
+            const int pg = page_at(pi);
+            if (pg < 0) continue;
+            uint4 X[8], Y[8];
+            load_k(pg, X);
+            load_v(pg, Y);
+            mask_v(pi, Y);
 #pragma unroll
-                for (int tt = 0; tt < TT; ++tt) {
-                    if (tt >= nt) break;
-                    scores_tt(pi, tt, X);
-                    pv_tt(tt, Y);
-                }
+            for (int tt = 0; tt < TT; ++tt) {
+                if (tt >= nt) break;
+                scores_tt(pi, tt, X);
+                pv_tt(tt, Y);
             }
         }
 
@@ -444,29 +411,24 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 
 // ------------------------------------------------------------------------------ MFMA kernel (verify rows)
 // For T query tokens the T * G query rows of a KV head form a dense [T G x 256] x [256 x rows] product, so
-// the multi-token (verify) step runs it on MFMA. One workgroup per (user, KV head, split of pps pages); the
-// split's 4 pps 16-row page slices are divided into 4 contiguous runs, one per wave, each wave keeping its
-// own online softmax; the 4 waves are merged in LDS at the end (fixed tree order), so a split still leaves
-// one partial. Per slice (16 rows) and 16-query-row tile:
-//   S^T [16 rows x 16 q] = K [16 x 256] Q^T      8 x v_mfma_f32_16x16x32_bf16; lane l holds K row l % 16,
-//                                                 dims 32 j + 8 (l / 16) .. + 7 (one 16-byte load per j)
-//   softmax over the slice's rows, in the accumulator layout (lane: q row l % 16, rows 4 (l / 16) + i)
-//   O^T [256 x 16 q] += V^T [256 x 16 rows] P^T  16 x v_mfma_f32_16x16x16_bf16; P^T is the score
-//                                                 accumulator itself (bf16), V^T comes from the slice staged
-//                                                 in LDS through the transposing read ds_read_b64_tr_b16
-// Every lane's O^T values belong to one query row, so a rescale by the running max is per lane.
+// the multi-token (verify) step runs it on MFMA. One workgroup per (user, KV head, split of pps pages),
+// walking its pages in order. Per page, in two phases separated by a barrier:
+//   scores  wave w takes rows 16 w .. 16 w + 15 (a 16-row slice): S^T [16 rows x 16 q] = K Q^T on 8
+//           v_mfma_f32_16x16x32_bf16 per 16-query-row tile (lane l holds K row l % 16, dims 32 j + 8 (l / 16)
+//           .. + 7: one 16-byte load per j), the slice's own max m_s per query row (log2 domain), P^T =
+//           2^(s - m_s) rounded to bf16 and its row sums l_s into LDS; the slice's V rows into LDS;
+//   P V     every wave adds the 4 slices in order to O^T [its 64 head dims x 16 q] on
+//           v_mfma_f32_16x16x16_bf16 (V^T read from LDS with the transposing ds_read_b64_tr_b16, P^T as
+//           written), scaled by 2^(m_s - M) against the running max M; M moves only when a slice max exceeds
+//           it by 2^8, so the accumulators are rarely rescaled.
+// All waves see the same slice maxima in the same order, so M and the sum L agree across waves, and the
+// 4 waves' head dims are disjoint: the split's partial needs no cross-wave merge.
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int QPAD = HD + 8;   // s_q row pitch (bf16): 16-byte skew between rows
 constexpr int VPAD = HD + 16;  // s_v row pitch (bf16): 32-byte skew between rows
-
-template <int QT>
-struct MfmaLds {
-    static constexpr int VBYTES = 4 * 16 * VPAD * 2;         // per-wave V slices
-    static constexpr int XBYTES = 2 * QT * 16 * 64 * 16;     // merge: two waves' O^T (float4 per lane)
-    static constexpr int UBYTES = VBYTES > XBYTES ? VBYTES : XBYTES;
-};
+constexpr int PPAD = 16 + 4;   // s_p row pitch (bf16)
 
 template <int G, int QT>
 __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
@@ -481,33 +443,29 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
     const int T = a.T;
 
     __shared__ __align__(16) uint16_t s_q[NQR][QPAD];
-    __shared__ __align__(16) unsigned char s_u[MfmaLds<QT>::UBYTES];  // V slices, then the merge buffers
-    __shared__ float s_mx[2][QT][64], s_lx[2][QT][64];
-    uint16_t(*s_v)[VPAD] = reinterpret_cast<uint16_t(*)[VPAD]>(s_u) + 16 * w;  // this wave's 16 rows
-    f32x4_t *s_x = reinterpret_cast<f32x4_t *>(s_u);
+    __shared__ __align__(16) uint16_t s_v[4][16][VPAD];     // the page's V rows, slice by slice
+    __shared__ __align__(16) uint16_t s_p[4][QT][16][PPAD];  // P^T of each slice: [query row][slice row]
+    __shared__ float s_m[4][NQR], s_l[4][NQR];              // slice max (log2 domain) and row sum
 
     int n = a.seq_lens[b];
     n = n < T ? T : (n > a.max_blocks * BLK ? a.max_blocks * BLK : n);
     const int base = n - T;  // first new position
-    const int nsl = (n + 15) / 16;  // valid slices of this user
-    const int p0 = split * a.pps;
-    const int s0 = 4 * p0 + w * a.pps, s1 = min(nsl, s0 + a.pps);  // this wave's slices [s0, s1)
+    const int npages = (n + BLK - 1) / BLK;
+    const int p0 = split * a.pps, p1 = min(npages, p0 + a.pps);
     const int *bt = a.block_table + (size_t)b * a.max_blocks;
-    // the wave's block-table entries (at most 64 pages), one per lane
-    const int pw0 = s0 / 4;
-    const int bt_pre = pw0 + lane < a.max_blocks ? bt[pw0 + lane] : -1;  // a wave spans <= 17 pages
-    auto page_of = [&](int sl) {
-        const int pg = __builtin_amdgcn_readlane(bt_pre, sl / 4 - pw0);
+    const int bt_pre = p0 + lane < min(a.max_blocks, p0 + a.pps) ? bt[p0 + lane] : -1;  // issued before n is known
+    auto page_at = [&](int pi) {
+        const int pg = __builtin_amdgcn_readlane(bt_pre, pi - p0);
         return (pg >= 0 && pg < a.num_blocks) ? pg : -1;
     };
     const size_t pstride = (size_t)a.NKV * BLK * HD;  // elements per page
 
-    // Fused append, first: the new rows that fall in this wave's slices go into the pools and are waited
-    // for, so the slice loads read them back from the pool. No other wave reads these slices.
-    if (a.k_new && s0 < s1 && base / 16 < s1 && (n - 1) / 16 >= s0) {
+    // Fused append, first: wave w writes the new rows of its 16-row slices in this split's pages and waits
+    // for them, so its slice loads read them back from the pool. No other wave reads these slices.
+    if (a.k_new && p0 < p1 && base / BLK < p1 && (n - 1) / BLK >= p0) {
         for (int idx = lane; idx < T * 64; idx += 64) {
             const int t = idx >> 6, kv = (idx >> 5) & 1, ch = idx & 31;
-            const int pos = base + t, sl = pos / 16;
+            const int pos = base + t, pi = pos / BLK;
             const size_t src = (((size_t)b * T + t) * a.NKV + g) * HD + ch * 8;
             uint4 u = *reinterpret_cast<const uint4 *>((kv ? a.v_new : a.k_new) + src);
             if (a.wk) {  // k rows normalised and rotated (all lanes take part in the row reductions)
@@ -516,8 +474,8 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
                 mixer_chunk(u, ch, a.wk, a.rcos + rc, a.rsin + rc, a.rot, a.eps, y);
                 if (!kv) u = pack8(y);
             }
-            if (sl < s0 || sl >= s1) continue;
-            const int pg = bt[pos / BLK];  // per lane: the new rows may straddle slices and pages
+            if (pi < p0 || pi >= p1 || (pos % BLK) / 16 != w) continue;
+            const int pg = bt[pi];
             if (pg < 0 || pg >= a.num_blocks) continue;
             const size_t dst = (((size_t)pg * a.NKV + g) * BLK + (pos % BLK)) * HD + ch * 8;
             *reinterpret_cast<uint4 *>((kv ? a.v_cache : a.k_cache) + dst) = u;
@@ -526,7 +484,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
     }
 
     // query rows qr = t G + hh (zero past T G): loaded into registers now, stored to LDS once the first
-    // slice's loads are in flight
+    // page's loads are in flight
     constexpr int QCH = NQR * 32 / 256;
     uint4 qreg[QCH];
 #pragma unroll
@@ -540,39 +498,29 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
     }
 
     const float sl2 = a.scale * 1.4426950408889634f;  // log2 domain
-    f32x4_t oacc[QT][16];
-    float m[QT], lp[QT];
-#pragma unroll
-    for (int nt = 0; nt < QT; ++nt) {
-        m[nt] = -INFINITY;
-        lp[nt] = 0.f;
-#pragma unroll
-        for (int dt = 0; dt < 16; ++dt) oacc[nt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    }
-    // each lane's causal limit per query-row tile: token (l16 + 16 nt) / G sees positions <= base + token
-    int lim[QT];
+    int lim[QT];  // the lane's causal limit per query-row tile: token qr / G sees positions <= base + token
 #pragma unroll
     for (int nt = 0; nt < QT; ++nt) {
         const int qr = l16 + 16 * nt;
         lim[nt] = qr < T * G ? base + qr / G : -1;
     }
 
-    auto load_k = [&](int pg, int sl, uint4 (&kb)[8]) {
+    auto load_k = [&](int pg, uint4 (&kb)[8]) {
         const auto rk = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint16_t *>(a.k_cache + (size_t)pg * pstride + (size_t)g * BLK * HD), (short)0, BLK * HD * 2,
             0x00020000);
-        const int off = ((sl & 3) * 16 + l16) * HD * 2 + lg * 16;
+        const int off = (16 * w + l16) * HD * 2 + lg * 16;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, off, j * 64, NT);
             kb[j] = make_uint4(x[0], x[1], x[2], x[3]);
         }
     };
-    auto load_v = [&](int pg, int sl, uint4 (&vb)[8]) {
+    auto load_v = [&](int pg, uint4 (&vb)[8]) {
         const auto rv = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint16_t *>(a.v_cache + (size_t)pg * pstride + (size_t)g * BLK * HD), (short)0, BLK * HD * 2,
             0x00020000);
-        const int off = ((sl & 3) * 16 + (lane >> 5)) * HD * 2 + (lane & 31) * 16;
+        const int off = (16 * w + (lane >> 5)) * HD * 2 + (lane & 31) * 16;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rv, off, k * 1024, NT);
@@ -580,15 +528,33 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
         }
     };
 
-    // one slice: stage V, scores, softmax, P V (kb / vb hold the slice's K and V rows)
-    auto slice = [&](int sl, const uint4 (&kb)[8], const uint4 (&vb)[8]) {
-        // stage V (rows past the user's length zeroed: a stale row times a zero probability could be NaN)
+    f32x4_t oacc[QT][4];  // O^T of head dims 64 w + 16 dd + 4 lg + i (dd < 4), query row l16 + 16 nt
+    float M[QT], L[QT];
+#pragma unroll
+    for (int nt = 0; nt < QT; ++nt) {
+        M[nt] = -INFINITY;
+        L[nt] = 0.f;
+#pragma unroll
+        for (int dd = 0; dd < 4; ++dd) oacc[nt][dd] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // one page: scores of this wave's slice into LDS, barrier, every slice's P V into this wave's dims, barrier
+    // one page: scores of this wave's slice into LDS, barrier, every slice's P V into this wave's dims,
+    // barrier. kb / vb hold the page's K and V rows; each is refilled with the next page's rows as soon as
+    // it has been consumed (V after staging, K after the score MFMAs), so one buffer of each suffices.
+    auto page = [&](int pi, uint4 (&kb)[8], uint4 (&vb)[8]) {
+        const int pgn = pi + 1 < p1 ? page_at(pi + 1) : -1;
+        const bool ok = page_at(pi) >= 0;
+        const int r0w = pi * BLK + 16 * w;  // first position of this wave's slice
+        // V rows (zero where the page is invalid or past the user's length: a stale row times a zero
+        // probability could be NaN)
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const int row = 2 * k + (lane >> 5);
-            const uint4 v = sl * 16 + row < n ? vb[k] : make_uint4(0, 0, 0, 0);
-            *reinterpret_cast<uint4 *>(&s_v[row][(lane & 31) * 8]) = v;
+            const uint4 v = ok && r0w + row < n ? vb[k] : make_uint4(0, 0, 0, 0);
+            *reinterpret_cast<uint4 *>(&s_v[w][row][(lane & 31) * 8]) = v;
         }
+        if (pgn >= 0) load_v(pgn, vb);
         f32x4_t sacc[QT];
 #pragma unroll
         for (int nt = 0; nt < QT; ++nt) sacc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -602,60 +568,70 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
                 sacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, bq, sacc[nt], 0, 0, 0);
             }
         }
-        // online softmax (log2 domain) per query row over the slice's 16 rows; probabilities rounded to
-        // bf16, the running sum adds the rounded values
-        i16x4_t pb[QT];
+        if (pgn >= 0) load_k(pgn, kb);
 #pragma unroll
         for (int nt = 0; nt < QT; ++nt) {
-            const int r0 = sl * 16 + 4 * lg;
             float sc[4];
             float mx = -INFINITY;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                sc[i] = r0 + i <= lim[nt] ? sacc[nt][i] : -INFINITY;
+                sc[i] = ok && r0w + 4 * lg + i <= lim[nt] ? sacc[nt][i] : -INFINITY;
                 mx = fmaxf(mx, sc[i]);
             }
             mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            // lazy rescaling: the reference max m moves only when a score exceeds it by more than 2^8 (log2
-            // domain); probabilities up to 256 are exact in fp32 and in range for bf16, so the normalised
-            // result is unchanged while the 64 accumulators of a tile are rescaled only rarely
-            const float cand = mx * sl2;
-            const bool move = m[nt] == -INFINITY ? cand != -INFINITY : cand > m[nt] + 8.0f;
-            const float mn = move ? cand : m[nt];
+            const float ms = mx * sl2;  // -inf when no row of the slice is visible to this query row
             float e[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                e[i] = sc[i] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(fmaf(sc[i], sl2, -mn));
+            for (int i = 0; i < 4; ++i) e[i] = sc[i] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(fmaf(sc[i], sl2, -ms));
             const uint32_t p01 = qs::cvt_pk_bf16(e[0], e[1]), p23 = qs::cvt_pk_bf16(e[2], e[3]);
-            if (__any(move)) {
-                const float alpha = m[nt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[nt] - mn);
-                lp[nt] *= alpha;
-#pragma unroll
-                for (int dt = 0; dt < 16; ++dt) oacc[nt][dt] *= alpha;
+            *reinterpret_cast<uint2 *>(&s_p[w][nt][l16][4 * lg]) = make_uint2(p01, p23);
+            float ls = (qs::bf_lo(p01) + qs::bf_hi(p01)) + (qs::bf_lo(p23) + qs::bf_hi(p23));
+            ls += __shfl_xor(ls, 16, 64);
+            ls += __shfl_xor(ls, 32, 64);
+            if (lg == 0) {
+                s_m[w][l16 + 16 * nt] = ms;
+                s_l[w][l16 + 16 * nt] = ls;
             }
-            m[nt] = mn;
-            lp[nt] += (qs::bf_lo(p01) + qs::bf_hi(p01)) + (qs::bf_lo(p23) + qs::bf_hi(p23));
-            pb[nt] = __builtin_bit_cast(i16x4_t, make_uint2(p01, p23));
         }
-        __builtin_amdgcn_wave_barrier();
-        // O^T += V^T P^T: lane (group lg, index l16) supplies the address of V[4 lg + l16 / 4][16 dt + 4 (l16 % 4)]
+        __syncthreads();
+        // P V: the 4 slices in order into this wave's head dims
 #pragma unroll
-        for (int dt = 0; dt < 16; ++dt) {
-            const i16x4_t av = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) i16x4_t *)&s_v[4 * lg + (l16 >> 2)][16 * dt + 4 * (l16 & 3)]);
+        for (int q = 0; q < 4; ++q) {
+            i16x4_t av[4];
 #pragma unroll
-            for (int nt = 0; nt < QT; ++nt)
-                oacc[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, pb[nt], oacc[nt][dt], 0, 0, 0);
+            for (int dd = 0; dd < 4; ++dd)
+                av[dd] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t *)&s_v[q][4 * lg + (l16 >> 2)][16 * (4 * w + dd) + 4 * (l16 & 3)]);
+#pragma unroll
+            for (int nt = 0; nt < QT; ++nt) {
+                const float ms = s_m[q][l16 + 16 * nt], ls = s_l[q][l16 + 16 * nt];
+                const bool move = M[nt] == -INFINITY ? ms != -INFINITY : ms > M[nt] + 8.0f;
+                const float Mn = move ? ms : M[nt];
+                if (__any(move)) {
+                    const float alpha = M[nt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M[nt] - Mn);
+                    L[nt] *= alpha;
+#pragma unroll
+                    for (int dd = 0; dd < 4; ++dd) oacc[nt][dd] *= alpha;
+                }
+                M[nt] = Mn;
+                const float es = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - Mn);
+                L[nt] = fmaf(es, ls, L[nt]);
+                const i16x4_t pb = __builtin_bit_cast(i16x4_t, *reinterpret_cast<const uint2 *>(&s_p[q][nt][l16][4 * lg]));
+#pragma unroll
+                for (int dd = 0; dd < 4; ++dd) {
+                    const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+                    const f32x4_t pv = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av[dd], pb, z, 0, 0, 0);
+                    oacc[nt][dd] += es * pv;
+                }
+            }
         }
-        __builtin_amdgcn_wave_barrier();
+        __syncthreads();  // the next page's scores overwrite s_v, s_p, s_m, s_l
     };
-    // two register buffers alternate: the next slice's K and V are in flight while a slice is computed
-    uint4 KA[8], VA[8], KB[8], VB[8];
-    int pga = s0 < s1 ? page_of(s0) : -1;
-    if (pga >= 0) {
-        load_k(pga, s0, KA);
-        load_v(pga, s0, VA);
+
+    uint4 KA[8], VA[8];
+    if (p0 < p1 && page_at(p0) >= 0) {
+        load_k(page_at(p0), KA);
+        load_v(page_at(p0), VA);
     }
 #pragma unroll
     for (int k = 0; k < QCH; ++k) {
@@ -670,62 +646,9 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
         *reinterpret_cast<uint4 *>(&s_q[qr][ch * 8]) = u;
     }
     __syncthreads();
-    for (int sl = s0; sl < s1; sl += 2) {
-        const int pgb = sl + 1 < s1 ? page_of(sl + 1) : -1;
-        if (pgb >= 0) {
-            load_k(pgb, sl + 1, KB);
-            load_v(pgb, sl + 1, VB);
-        }
-        if (pga >= 0) slice(sl, KA, VA);
-        if (sl + 1 >= s1) break;
-        pga = sl + 2 < s1 ? page_of(sl + 2) : -1;
-        if (pga >= 0) {
-            load_k(pga, sl + 2, KA);
-            load_v(pga, sl + 2, VA);
-        }
-        if (pgb >= 0) slice(sl + 1, KB, VB);
-    }
+    for (int pi = p0; pi < p1; ++pi) page(pi, KA, VA);
 
-    // full row sums of the wave (the 4 lane groups hold disjoint rows)
-#pragma unroll
-    for (int nt = 0; nt < QT; ++nt) {
-        lp[nt] += __shfl_xor(lp[nt], 16, 64);
-        lp[nt] += __shfl_xor(lp[nt], 32, 64);
-    }
-    // ---- merge the 4 waves: (2, 3) into (0, 1), then 1 into 0; lane layouts agree, so it is per lane
-    auto put = [&](int slot) {
-#pragma unroll
-        for (int nt = 0; nt < QT; ++nt) {
-#pragma unroll
-            for (int dt = 0; dt < 16; ++dt) s_x[((slot * QT + nt) * 16 + dt) * 64 + lane] = oacc[nt][dt];
-            s_mx[slot][nt][lane] = m[nt];
-            s_lx[slot][nt][lane] = lp[nt];
-        }
-    };
-    auto take = [&](int slot) {
-#pragma unroll
-        for (int nt = 0; nt < QT; ++nt) {
-            const float m2 = s_mx[slot][nt][lane], l2 = s_lx[slot][nt][lane];
-            const float M = fmaxf(m[nt], m2);
-            const float e1 = m[nt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[nt] - M);
-            const float e2 = m2 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m2 - M);
-#pragma unroll
-            for (int dt = 0; dt < 16; ++dt)
-                oacc[nt][dt] = oacc[nt][dt] * e1 + s_x[((slot * QT + nt) * 16 + dt) * 64 + lane] * e2;
-            lp[nt] = lp[nt] * e1 + l2 * e2;
-            m[nt] = M;
-        }
-    };
-    __syncthreads();  // the V slices are dead: s_u becomes the merge buffer
-    if (w >= 2) put(w - 2);
-    __syncthreads();
-    if (w < 2) take(w);
-    __syncthreads();
-    if (w == 1) put(0);
-    __syncthreads();
-    if (w != 0) return;
-    take(0);
-
+    // this wave's head dims of the split's partial (or of the output)
 #pragma unroll
     for (int nt = 0; nt < QT; ++nt) {
         const int qr = l16 + 16 * nt;
@@ -733,27 +656,27 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
         const int t = qr / G, hh = qr % G;
         const size_t row = ((size_t)b * T + t) * a.NKV + g;
         if (a.nsplit == 1) {
-            const float inv = 1.0f / lp[nt];
-            const size_t oi = (((size_t)b * T + t) * a.NQ + g * G + hh) * HD + 4 * lg;
-            uint16_t *op = a.o + oi;
+            const float inv = 1.0f / L[nt];
+            const size_t oi = (((size_t)b * T + t) * a.NQ + g * G + hh) * HD + 64 * w + 4 * lg;
 #pragma unroll
-            for (int dt = 0; dt < 16; ++dt) {
-                f32x4_t v = oacc[nt][dt] * inv;
+            for (int dd = 0; dd < 4; ++dd) {
+                f32x4_t v = oacc[nt][dd] * inv;
                 if (a.gate) {
-                    const uint2 gw = *reinterpret_cast<const uint2 *>(a.gate + oi + 16 * dt);
+                    const uint2 gw = *reinterpret_cast<const uint2 *>(a.gate + oi + 16 * dd);
                     v[0] *= sigm(qs::bf_lo(gw.x)), v[1] *= sigm(qs::bf_hi(gw.x));
                     v[2] *= sigm(qs::bf_lo(gw.y)), v[3] *= sigm(qs::bf_hi(gw.y));
                 }
-                *reinterpret_cast<uint2 *>(op + 16 * dt) = make_uint2(qs::cvt_pk_bf16(v[0], v[1]), qs::cvt_pk_bf16(v[2], v[3]));
+                *reinterpret_cast<uint2 *>(a.o + oi + 16 * dd) =
+                    make_uint2(qs::cvt_pk_bf16(v[0], v[1]), qs::cvt_pk_bf16(v[2], v[3]));
             }
         } else {
-            float *po = a.part_o + ((row * a.nsplit + split) * G + hh) * HD + 4 * lg;
+            float *po = a.part_o + ((row * a.nsplit + split) * G + hh) * HD + 64 * w + 4 * lg;
 #pragma unroll
-            for (int dt = 0; dt < 16; ++dt) *reinterpret_cast<f32x4_t *>(po + 16 * dt) = oacc[nt][dt];
-            if (lg == 0) {
+            for (int dd = 0; dd < 4; ++dd) *reinterpret_cast<f32x4_t *>(po + 16 * dd) = oacc[nt][dd];
+            if (w == 0 && lg == 0) {
                 float *ml = a.part_ml + ((row * a.nsplit + split) * G + hh) * 2;
-                ml[0] = m[nt];
-                ml[1] = lp[nt];
+                ml[0] = M[nt];
+                ml[1] = L[nt];
             }
         }
     }
@@ -872,10 +795,9 @@ static int attn_launch(AttnArgs a, void *workspace, int HDa, int block, const ch
     }
     const dim3 grid(B * NKV * ns);
     hipStream_t st = QS_STREAM(stream);
-    const int TT = T >= 2 ? 2 : 1;  // query tokens per pass over the pages (4 would spill registers)
-    // verify rows (T >= 2) with at most 32 query rows per KV head run on MFMA
-    static const bool mfma_t1 = getenv("QS_ATTN_MFMA") && atoi(getenv("QS_ATTN_MFMA")) == 1;
-    if ((T >= 2 || mfma_t1) && T * G <= 32) {
+    // up to 32 query rows per KV head (every one-token decode, and verify steps with T G <= 32) run on MFMA;
+    // more rows take the VALU kernel, two query tokens per pass over the pages
+    if (T * G <= 32) {
         const int QT = (T * G + 15) / 16;
 #define QS_MFMA_LAUNCH(GG)                                                       \
     if (QT == 1) attn_mfma_kernel<GG, 1><<<grid, 256, 0, st>>>(a);               \
@@ -896,9 +818,7 @@ static int attn_launch(AttnArgs a, void *workspace, int HDa, int block, const ch
         }
         return QS_OK;
     }
-#define QS_ATTN_LAUNCH(GG)                                                      \
-    if (TT == 1) attn_kernel<GG, 1><<<grid, 256, 0, st>>>(a);                   \
-    else attn_kernel<GG, 2><<<grid, 256, 0, st>>>(a);
+#define QS_ATTN_LAUNCH(GG) attn_kernel<GG, 2><<<grid, 256, 0, st>>>(a);
     switch (G) {
         case 1: QS_ATTN_LAUNCH(1) break;
         case 2: QS_ATTN_LAUNCH(2) break;
