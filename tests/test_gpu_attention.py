@@ -109,3 +109,27 @@ def test_attn_mixer(dev, B, ctx, T, pps):
     # the rope tables of the wrapper equal the oracle's
     c2, s2 = ops.rope_tables(pos.to(dev) + 5000)
     assert torch.equal(c2.cpu(), cos) and torch.equal(s2.cpu(), sin)
+
+
+def test_in_launch_merge_counters_rearm(dev):
+    """Up to 16 splits are merged inside the attention launch by the last workgroup to arrive. The arrival
+    counters at the workspace head read zero after every call, so one workspace serves repeated calls and
+    calls of other shapes (here batch 8 one token, then batch 3 four verify rows, twice each): outputs repeat
+    bit-exactly and match the oracle."""
+    L = ops.lib()
+    ws = torch.zeros(L.qs_paged_attention_workspace_bytes(8, 4, 24, 4, 256, 64, 4), dtype=torch.uint8, device=dev)
+    cases = [(8, 4096, 1), (3, 2000, 4)]
+    data = [W.attn_layer(B, ctx, "cpu", seed=B + T, T=T, num_blocks=1024) for B, ctx, T in cases]
+    outs = []
+    for rep in range(2):
+        for d in data:
+            g = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in d.items()}
+            o = ops.paged_gqa_decode(g["q"], g["k_cache"], g["v_cache"], g["block_table"], g["seq_lens"], d["scale"],
+                                     pages_per_split=4, ws=ws)  # fmt: skip
+            torch.cuda.synchronize()
+            assert int(ws[:65536].view(torch.int32).abs().sum()) == 0, "counters not re-armed"
+            outs.append(o.cpu())
+    assert torch.equal(outs[0], outs[2]) and torch.equal(outs[1], outs[3])
+    for d, o in zip(data, outs):
+        ref = O.gqa_decode(d["q"], d["k_cache"], d["v_cache"], d["block_table"], d["seq_lens"], d["scale"])
+        assert_bf16_output(o, O.bf16(ref))

@@ -44,8 +44,9 @@ struct AttnArgs {
     const int *block_table;             // [B, max_blocks]
     const int *seq_lens;                // [B]
     uint16_t *o;                        // [B, T, NQ, HD]
-    float *part_o;                      // [B, T, NKV, nsplit, G, HD]
-    float *part_ml;                     // [B, T, NKV, nsplit, G, 2]
+    float *part_o;                      // [B, NKV, nsplit, T G, HD]: split partials (unnormalised O)
+    float *part_ml;                     // [B, NKV, nsplit, T G, 2]: their (max, sum), log2 domain
+    int *cnt;                           // [B, NKV] arrival counters of the in-launch merge (kept zero)
     int B, T, NQ, NKV, max_blocks, num_blocks, pps, nsplit;
     float scale;
     // mixer edges (qs_attn_mixer_decode; null / 0 for plain attention): q and the new k rows are
@@ -102,17 +103,26 @@ __device__ __forceinline__ uint4 pack8(const float y[8]) {
 }
 __device__ __forceinline__ float sigm(float g) { return 1.0f / (1.0f + expf(-g)); }
 
-// Workspace layout (bytes): part_ml | part_o, each 256-byte aligned.
+// Workspace layout (bytes): arrival counters | part_ml | part_o, each 256-byte aligned. The counters sit in
+// a fixed block at the head, so a workspace reused for another shape never finds partial data where its
+// counters are (they must read zero).
+constexpr size_t CNT_BYTES = 65536;  // room for B NKV <= 16384 counters
 struct WsLayout {
-    size_t ml, po, total;
+    size_t cnt, ml, po, total;
 };
 __host__ __device__ inline WsLayout ws_layout(int B, int T, int NKV, int G, int nsplit) {
     auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
     WsLayout l;
-    l.ml = 0;
-    l.po = up((size_t)B * T * NKV * nsplit * G * 2 * 4);
+    l.cnt = 0;
+    l.ml = CNT_BYTES;
+    l.po = l.ml + up((size_t)B * T * NKV * nsplit * G * 2 * 4);
     l.total = l.po + up((size_t)B * T * NKV * nsplit * G * HD * 4);
     return l;
+}
+// Row of the partial of query row qr (= t G + h) of split sp for user b, KV head g: one workgroup's rows
+// are contiguous.
+__device__ __forceinline__ size_t prow(const AttnArgs &a, int G, int b, int g, int sp, int qr) {
+    return (((size_t)b * a.NKV + g) * a.nsplit + sp) * (size_t)(a.T * G) + qr;
 }
 
 // One workgroup per (user, KV head, split); the 4 waves work on the same page at a time, wave w owning
@@ -386,7 +396,6 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                 s_L[tid] = L;
             }
             __syncthreads();
-            const size_t row = ((size_t)b * T + t) * a.NKV + g;
 #pragma unroll
             for (int h = 0; h < G; ++h) {
                 const float O = s_w[0][h] * s_acc[0][h][tid] + s_w[1][h] * s_acc[1][h][tid] +
@@ -397,10 +406,10 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                     a.o[oi] = (uint16_t)qs::f2bf(O / s_L[h] * gt);
                 }
                 else
-                    a.part_o[((row * a.nsplit + split) * G + h) * HD + tid] = O;
+                    a.part_o[prow(a, G, b, g, split, t * G + h) * HD + tid] = O;
             }
             if (a.nsplit > 1 && tid < G) {
-                float *ml = a.part_ml + ((row * a.nsplit + split) * G + tid) * 2;
+                float *ml = a.part_ml + prow(a, G, b, g, split, t * G + tid) * 2;
                 ml[0] = s_M[tid];
                 ml[1] = s_L[tid];
             }
@@ -429,6 +438,81 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int QPAD = HD + 8;   // s_q row pitch (bf16): 16-byte skew between rows
 constexpr int VPAD = HD + 16;  // s_v row pitch (bf16): 32-byte skew between rows
 constexpr int PPAD = 16 + 4;   // s_p row pitch (bf16)
+
+// Split merge inside the attention launch (nsplit <= MERGE_MAX). Every workgroup of (user b, KV head g) has
+// stored its partial with agent-coherent stores (sc1: written through the XCD's L2); each thread waits for
+// its stores to complete, then one thread counts the workgroup in. The workgroup that completes the count
+// re-arms the counter and merges: wave w takes query rows w, w + 4, ... (two at a time), lane l owns head
+// dims 4 l .. 4 l + 3, and every split's partial and (m, l) are read with agent-coherent loads in one round
+// trip. Global max M (log2 domain) and sum L over the splits, weights 2^(m_s - M), O = sum_s w_s O_s / L in
+// split order, so the result does not depend on which workgroup finished last. No L2-wide writeback or
+// invalidate is needed because only sc1 accesses touch the shared data. (The leader side of the
+// reference: kernels/attn_leader_writer.cpp:86-106, kernels/attn_leader_compute.cpp:42-79.)
+constexpr int MERGE_MAX = 16;
+template <int G>
+__device__ __forceinline__ void merge_in_launch(const AttnArgs &a, int b, int g, int tid) {
+    __shared__ int s_last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+        int *c = a.cnt + (size_t)b * a.NKV + g;
+        const int last = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.nsplit - 1;
+        if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = last;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    asm volatile("" ::: "memory");
+    const int lane = tid & 63, w = tid >> 6;
+    const int T = a.T, R = T * G, ns = a.nsplit;
+    const auto ro = __builtin_amdgcn_make_buffer_rsrc(qs::uniform_ptr(a.part_o + prow(a, G, b, g, 0, 0) * HD),
+                                                      (short)0, ns * R * HD * 4, 0x00020000);
+    const auto rm = __builtin_amdgcn_make_buffer_rsrc(qs::uniform_ptr(a.part_ml + prow(a, G, b, g, 0, 0) * 2),
+                                                      (short)0, ns * R * 8, 0x00020000);
+    for (int r0 = w; r0 < R; r0 += 8) {
+        f32x4_t x[2][MERGE_MAX];
+        float2 ml[2];
+        uint2 gw[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int qr = r0 + 4 * j;
+            if (qr >= R) continue;
+#pragma unroll
+            for (int sp = 0; sp < MERGE_MAX; ++sp)
+                if (sp < ns)
+                    x[j][sp] = __builtin_bit_cast(
+                        f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ro, ((sp * R + qr) * HD + 4 * lane) * 4, 0,
+                                                                        qs::CP_SC1));
+            ml[j] = make_float2(-INFINITY, 0.f);
+            if (lane < ns) {
+                const u32x2 u = __builtin_amdgcn_raw_buffer_load_b64(rm, (lane * R + qr) * 8, 0, qs::CP_SC1);
+                ml[j] = make_float2(__uint_as_float(u[0]), __uint_as_float(u[1]));
+            }
+            if (a.gate)
+                gw[j] = *reinterpret_cast<const uint2 *>(
+                    a.gate + (((size_t)b * T + qr / G) * a.NQ + g * G + qr % G) * HD + 4 * lane);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int qr = r0 + 4 * j;
+            if (qr >= R) continue;
+            const float M = qs::wave_max_bcast(ml[j].x);
+            const float e = ml[j].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml[j].x - M);
+            const float L = qs::wave_sum_dpp(e * ml[j].y);
+            f32x4_t O = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int sp = 0; sp < MERGE_MAX; ++sp)
+                if (sp < ns) O += qs::lane_val(e, sp) * x[j][sp];
+            O *= 1.0f / L;
+            if (a.gate) {
+                O[0] *= sigm(qs::bf_lo(gw[j].x)), O[1] *= sigm(qs::bf_hi(gw[j].x));
+                O[2] *= sigm(qs::bf_lo(gw[j].y)), O[3] *= sigm(qs::bf_hi(gw[j].y));
+            }
+            *reinterpret_cast<uint2 *>(a.o + (((size_t)b * T + qr / G) * a.NQ + g * G + qr % G) * HD + 4 * lane) =
+                make_uint2(qs::cvt_pk_bf16(O[0], O[1]), qs::cvt_pk_bf16(O[2], O[3]));
+        }
+    }
+}
 
 template <int G, int QT>
 __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
@@ -648,13 +732,17 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
     __syncthreads();
     for (int pi = p0; pi < p1; ++pi) page(pi, KA, VA);
 
-    // this wave's head dims of the split's partial (or of the output)
+    // this wave's head dims of the split's partial (or of the output); the partials are written through
+    // to the agent-coherent level (sc1), where another workgroup of this launch or the merge launch reads them
+    const auto rpo = __builtin_amdgcn_make_buffer_rsrc(a.part_o + prow(a, G, b, g, split, 0) * HD, (short)0,
+                                                       T * G * HD * 4, 0x00020000);
+    const auto rpm = __builtin_amdgcn_make_buffer_rsrc(a.part_ml + prow(a, G, b, g, split, 0) * 2, (short)0,
+                                                       T * G * 8, 0x00020000);
 #pragma unroll
     for (int nt = 0; nt < QT; ++nt) {
         const int qr = l16 + 16 * nt;
         if (qr >= T * G) continue;
         const int t = qr / G, hh = qr % G;
-        const size_t row = ((size_t)b * T + t) * a.NKV + g;
         if (a.nsplit == 1) {
             const float inv = 1.0f / L[nt];
             const size_t oi = (((size_t)b * T + t) * a.NQ + g * G + hh) * HD + 64 * w + 4 * lg;
@@ -670,16 +758,16 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
                     make_uint2(qs::cvt_pk_bf16(v[0], v[1]), qs::cvt_pk_bf16(v[2], v[3]));
             }
         } else {
-            float *po = a.part_o + ((row * a.nsplit + split) * G + hh) * HD + 64 * w + 4 * lg;
 #pragma unroll
-            for (int dd = 0; dd < 4; ++dd) *reinterpret_cast<f32x4_t *>(po + 16 * dd) = oacc[nt][dd];
-            if (w == 0 && lg == 0) {
-                float *ml = a.part_ml + ((row * a.nsplit + split) * G + hh) * 2;
-                ml[0] = M[nt];
-                ml[1] = L[nt];
-            }
+            for (int dd = 0; dd < 4; ++dd)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, oacc[nt][dd]), rpo,
+                                                       (qr * HD + 64 * w + 16 * dd + 4 * lg) * 4, 0, qs::CP_SC1);
+            if (w == 0 && lg == 0)
+                __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(M[nt]), __float_as_uint(L[nt])}, rpm,
+                                                      qr * 8, 0, qs::CP_SC1);
         }
     }
+    if (a.nsplit > 1 && a.nsplit <= MERGE_MAX) merge_in_launch<G>(a, b, g, tid);
 }
 
 // Merge of the splits of one output row (user, token, query head) in one memory round trip: wave w sums
@@ -694,12 +782,14 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, int G) {
     __shared__ float4 s_part[4][64];
     const int rowh = blockIdx.x;  // ((b * T + t) * NKV + g) * G + h
     const int h = rowh % G, row = rowh / G;
+    const int g = row % a.NKV, bt = row / a.NKV;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int ns = a.nsplit;
-    const size_t sstride = (size_t)G * HD;  // floats between consecutive splits of one row
-    const float *ml = a.part_ml + ((size_t)row * ns * G + h) * 2;
-    const float *po = a.part_o + ((size_t)row * ns * G + h) * HD + 4 * lane;
-    auto mlv = [&](int sp) { return *reinterpret_cast<const float2 *>(ml + (size_t)sp * G * 2); };
+    const int ns = a.nsplit, R = a.T * G;
+    const size_t pr = prow(a, G, bt / a.T, g, 0, (bt % a.T) * G + h);
+    const size_t sstride = (size_t)R * HD;  // floats between consecutive splits of one row
+    const float *ml = a.part_ml + pr * 2;
+    const float *po = a.part_o + pr * HD + 4 * lane;
+    auto mlv = [&](int sp) { return *reinterpret_cast<const float2 *>(ml + (size_t)sp * R * 2); };
     float4 x[MCH];
     float2 mw[MCH];
 #pragma unroll
@@ -749,7 +839,6 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, int G) {
     const float inv = 1.0f / L;
     const float r0 = (((O.x + p1.x) + p2.x) + p3.x) * inv, r1 = (((O.y + p1.y) + p2.y) + p3.y) * inv;
     const float r2 = (((O.z + p1.z) + p2.z) + p3.z) * inv, r3 = (((O.w + p1.w) + p2.w) + p3.w) * inv;
-    const int g = row % a.NKV, bt = row / a.NKV;
     const size_t oi = ((size_t)bt * a.NQ + g * G + h) * HD + 4 * lane;
     float o0 = r0, o1 = r1, o2 = r2, o3 = r3;
     if (a.gate) {
@@ -786,10 +875,13 @@ static int attn_launch(AttnArgs a, void *workspace, int HDa, int block, const ch
     QS_REQUIRE(ns == 1 || workspace, "%s: %d splits need a workspace", who, ns);
     QS_REQUIRE(ns <= MAX_SPLITS, "%s: %d splits exceed %d (raise pages_per_split)", who, ns, MAX_SPLITS);
     QS_REQUIRE((long)B * NKV * ns < (1L << 31), "%s: grid too large", who);
+    QS_REQUIRE((size_t)B * NKV * sizeof(int) <= CNT_BYTES, "%s: B NKV = %d exceeds %d", who, B * NKV,
+               (int)(CNT_BYTES / sizeof(int)));
     a.nsplit = ns;
     if (workspace) {
         const WsLayout L = ws_layout(B, T, NKV, G, ns);
         char *ws = static_cast<char *>(workspace);
+        a.cnt = reinterpret_cast<int *>(ws + L.cnt);
         a.part_ml = reinterpret_cast<float *>(ws + L.ml);
         a.part_o = reinterpret_cast<float *>(ws + L.po);
     }
@@ -812,7 +904,7 @@ static int attn_launch(AttnArgs a, void *workspace, int HDa, int block, const ch
         }
 #undef QS_MFMA_LAUNCH
         if (int e = qs::launch_status(who)) return e;
-        if (ns > 1) {
+        if (ns > MERGE_MAX) {  // fewer splits are merged inside the attention launch
             attn_merge_kernel<<<B * T * NKV * G, 256, 0, st>>>(a, G);
             return qs::launch_status(who);
         }

@@ -103,6 +103,21 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
+// A pointer made wave-uniform (its value in the first active lane), for buffer descriptors built from a
+// per-wave base.
+template <class T>
+__device__ __forceinline__ T *uniform_ptr(T *p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+    return reinterpret_cast<T *>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Cache-policy bits of the buffer load / store builtins on gfx950: nt = streaming (the line is not kept),
+// sc1 = coherent at agent scope (stores write through the XCD's L2, loads miss in it). Data that another
+// workgroup of the same launch reads back is stored and loaded with sc1, so it needs no L2 writeback.
+constexpr int CP_NT = 2, CP_SC1 = 16;
+
 // Workgroup i is dispatched to XCD i % 8. Map hardware ids so that consecutive logical ids land on one XCD
 // (and share its L2): logical = (hw % 8) * (n / 8) + hw / 8. Identity when n is not a multiple of 8.
 __device__ __forceinline__ int xcd_logical(int hw, int n) {
