@@ -11,37 +11,61 @@
 //   S  = gamma_C S0 + K^T diag(r_k gamma_C / gamma) d
 // (the chunked gated delta rule of Yang et al., "Gated Delta Networks", as FLA's chunk_gated_delta_rule
 // computes it). Two kernels:
-//   chunk_prep  one workgroup per (chunk, key head), fully parallel: K K^T and Q K^T on MFMA from the raw
-//               bf16 rows (exact products, fp32 sums), then for each of the key head's value heads A, P,
-//               the triangular inverse Tm (16 x 16 diagonal blocks by forward substitution, then the 32 x 32
-//               and 64 x 64 levels of the block recursion [T1 0; -T2 A21 T1  T2] on fp32 MFMA) and the
-//               per-token scalars, into the workspace (Tm and P as bf16 hi + lo planes);
+//   chunk_prep  one workgroup per (chunk, value head), fully parallel: K K^T and Q K^T on MFMA from the raw
+//               bf16 rows (exact products, fp32 sums), A and P from the accumulators, the triangular inverse
+//               Tm (16 x 16 diagonal blocks by forward substitution, then the 32 x 32 and 64 x 64 levels of
+//               the block recursion [T1 0; -T2 A21 T1  T2] on fp32 MFMA) and the per-token scalars into the
+//               workspace (Tm and P as bf16 hi + lo planes);
 //   chunk_walk  one workgroup per (value head, 32-column slab of S): the 128 x 32 fp32 state slab stays
 //               on chip while the workgroup walks the chunks in order. Every product that touches S or d
 //               splits the fp32 operand into bf16 hi + lo halves (two MFMAs, three for Tm x X), so the
 //               state keeps fp32-level accuracy.
+//
+// Row order of the prep's MFMA tiles: row r of a 16-row tile t stands for token sig(t, r) = 32 (t / 2) +
+// 8 (r / 4) + 4 (t % 2) + r % 4; with the chunk swizzle sw16 of the K / Q images the 16 rows of any tile read
+// 16 different 16-byte bank groups.
 // MFMA: v_mfma_f32_16x16x32_bf16; lane l holds A[l % 16][8 (l / 16) + j], B[8 (l / 16) + j][l % 16] (j < 8)
 // and C[4 (l / 16) + i][l % 16] (i < 4).
 #include "qs_common.h"
 
 namespace {
 
-constexpr int CH = 64;   // chunk
+constexpr int CH = 64;  // chunk
 constexpr int DK = 128;
 constexpr int DV = 128;
-constexpr int SLAB = 32;
+constexpr int FP = CH + 1;  // fp32 row stride of the 64 x 64 matrices of the inverse in LDS
+constexpr int SLAB = 32;    // state columns per walk workgroup
 constexpr int NSLAB = DV / SLAB;
-constexpr int KP = DK + 8;  // bf16 row stride of the K / Q chunk tiles in LDS (272 bytes)
-constexpr int FP = CH + 1;  // fp32 row stride of the 64 x 64 matrices in LDS
+constexpr int KP = DK + 8;  // bf16 row stride of the walk's K / Q chunk tiles in LDS (272 bytes)
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
+__device__ __forceinline__ bf16x8 frag(const void *p) {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(p));
+}
 __device__ __forceinline__ bf16x8 as_frag(uint4 u) { return __builtin_bit_cast(bf16x8, u32x4{u.x, u.y, u.z, u.w}); }
+
+// physical row of MFMA row r of tile t
+__device__ __forceinline__ int sig(int t, int r) { return 32 * (t >> 1) + 8 * (r >> 2) + 4 * (t & 1) + (r & 3); }
+// 16-byte chunk swizzle of the prep's K / Q images: chunk c of token row p sits at position c ^ sw16(p).
+// Over the 16 rows sig(t, 0 .. 15) of any tile, sw16 takes 16 distinct values, so the 16 lanes of a fragment
+// read hit 16 different 16-byte bank groups.
+__device__ __forceinline__ int sw16(int p) { return ((p & 3) << 2) | ((p >> 3) & 3); }
+
+// a buffer descriptor over n bytes from p: reads past the range return zeros, writes past it are dropped
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *p, int n) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, n, 0x00020000);
+}
+// 16 bytes per lane from byte offset off of r into LDS at lds + 16 lane (lds is wave-uniform)
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void *lds, int off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 16, off, 0, 0, 0);
+}
 
 struct PrefillArgs {
     const uint16_t *q, *k, *v;  // [T, NK, DK], [T, NK, DK], [T, NV, DV]
@@ -73,217 +97,225 @@ __device__ __forceinline__ void put16(float *D, int ds, f32x4 c, int lane) {
 }
 
 __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
-    const int c = blockIdx.x / a.NK, kh = blockIdx.x % a.NK;
-    const int rep = a.NV / a.NK;
-    const int t0 = c * CH;
-    const int nval = min(CH, a.T - t0);
+    const int lid = qs::xcd_logical(blockIdx.x, a.nch * a.NV);
+    const int c = lid / a.NV, h = lid % a.NV;  // the value heads of one key head on consecutive ids
+    const int rep = a.NV / a.NK, kh = h / rep;
+    const int t0 = c * CH, nval = min(CH, a.T - t0);
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int fr = lane & 15, g = lane >> 4;
 
-    // the K / Q tiles are dead once K K^T, Q K^T and the q norms exist: A and Tm reuse their space, which
-    // keeps the workgroup at 70 KB of LDS (two per CU)
-    __shared__ __align__(16) char s_kq[CH * KP * 2 * 2];
-    __shared__ float sKK[CH][FP], sQK[CH][FP];
+    // the K / Q images are dead once K K^T, Q K^T and the norms exist: A and Tm reuse their space,
+    // which keeps the workgroup at 38 KB of LDS (four per CU)
+    __shared__ __align__(16) char s_u[2 * CH * FP * 4];
     __shared__ float s_rk[CH], s_rq[CH], s_G[CH], s_b[CH];
     __shared__ float sM[4][16][16];
-    uint16_t(*sK)[KP] = reinterpret_cast<uint16_t(*)[KP]>(s_kq);
-    uint16_t(*sQ)[KP] = reinterpret_cast<uint16_t(*)[KP]>(s_kq + CH * KP * 2);
-    float(*sA)[FP] = reinterpret_cast<float(*)[FP]>(s_kq);
-    float(*sT)[FP] = reinterpret_cast<float(*)[FP]>(s_kq + CH * FP * 4);
-    static_assert(2 * CH * FP * 4 <= CH * KP * 2 * 2, "A and Tm must fit in the K / Q tiles");
+    const uint16_t *sK = reinterpret_cast<const uint16_t *>(s_u);
+    const uint16_t *sQ = sK + CH * DK;
+    float(*sA)[FP] = reinterpret_cast<float(*)[FP]>(s_u);
+    float(*sT)[FP] = reinterpret_cast<float(*)[FP]>(s_u + CH * FP * 4);
+    static_assert(2 * CH * DK * 2 <= 2 * CH * FP * 4, "the K / Q images must fit in the A / Tm space");
 
-    // 1. the chunk's raw q, k rows of key head kh (zeros past the sequence)
-    for (int idx = tid; idx < CH * (DK / 8); idx += 256) {
-        const int r = idx / (DK / 8), ch = idx % (DK / 8);
-        uint4 kv = make_uint4(0, 0, 0, 0), qv = make_uint4(0, 0, 0, 0);
-        if (r < nval) {
-            const size_t off = ((size_t)(t0 + r) * a.NK + kh) * DK + ch * 8;
-            kv = *reinterpret_cast<const uint4 *>(a.k + off);
-            qv = *reinterpret_cast<const uint4 *>(a.q + off);
+    // 1. the chunk's raw k, q rows of key head kh into swizzled LDS images (zeros past the sequence); the
+    //    gates of value head h (wave 0: lane = token, g = 0 and beta = 0 past the sequence)
+    {
+        const size_t krow = (size_t)a.NK * DK * 2;  // bytes per token
+        const auto rk = rsrc(a.k + (size_t)t0 * a.NK * DK, (int)(nval * krow));
+        const auto rq = rsrc(a.q + (size_t)t0 * a.NK * DK, (int)(nval * krow));
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int e = 256 * m + tid, p = e >> 4;
+            const int off = (int)(p * krow) + (kh * DK + ((e & 15) ^ sw16(p)) * 8) * 2;
+            dma16(rk, s_u + 4096 * m + 1024 * w, off);
+            dma16(rq, s_u + CH * DK * 2 + 4096 * m + 1024 * w, off);
         }
-        *reinterpret_cast<uint4 *>(&sK[r][ch * 8]) = kv;
-        *reinterpret_cast<uint4 *>(&sQ[r][ch * 8]) = qv;
     }
+    float gi = 0.f, bi = 0.f;
+    if (w == 0 && lane < nval) {
+        gi = a.g[(size_t)(t0 + lane) * a.NV + h];
+        bi = a.beta[(size_t)(t0 + lane) * a.NV + h];
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
 
-    // 2. K K^T and Q K^T (exact bf16 products, fp32 sums): wave w owns row tile w
-    const int fr = lane & 15, fk = (lane >> 4) * 8;
-#pragma unroll
-    for (int tc = 0; tc < 4; ++tc) {
-        f32x4 ckk = {0.f, 0.f, 0.f, 0.f}, cqk = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < DK / 32; ++ks) {
-            const bf16x8 ak = as_frag(*reinterpret_cast<const uint4 *>(&sK[16 * w + fr][ks * 32 + fk]));
-            const bf16x8 aq = as_frag(*reinterpret_cast<const uint4 *>(&sQ[16 * w + fr][ks * 32 + fk]));
-            const bf16x8 bk = as_frag(*reinterpret_cast<const uint4 *>(&sK[16 * tc + fr][ks * 32 + fk]));
-            ckk = mfma(ak, bk, ckk);
-            cqk = mfma(aq, bk, cqk);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = 16 * w + (lane >> 4) * 4 + i, col = 16 * tc + fr;
-            sKK[row][col] = ckk[i];
-            sQK[row][col] = cqk[i];
-        }
-    }
-    // 3. q norms: 4 lanes per row, 32 dims each
+    // 2. row norms (4 lanes per row; the sum runs over the row's chunks in stored order); cumulative log
+    //    decay (wave 0, inclusive scan over the 64 tokens)
     {
         const int r = tid >> 2, part = tid & 3;
-        float ss = 0.f;
+        float kk = 0.f, qq = 0.f;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const uint4 qv = *reinterpret_cast<const uint4 *>(&sQ[r][part * 32 + u * 8]);
-            const uint32_t wd[4] = {qv.x, qv.y, qv.z, qv.w};
+            const uint4 kv = *reinterpret_cast<const uint4 *>(sK + r * DK + (part * 4 + u) * 8);
+            const uint4 qv = *reinterpret_cast<const uint4 *>(sQ + r * DK + (part * 4 + u) * 8);
+            const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w}, qw[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float lo = qs::bf_lo(wd[e]), hi = qs::bf_hi(wd[e]);
-                ss = fmaf(lo, lo, ss);
-                ss = fmaf(hi, hi, ss);
+                kk = fmaf(qs::bf_lo(kw[e]), qs::bf_lo(kw[e]), kk);
+                kk = fmaf(qs::bf_hi(kw[e]), qs::bf_hi(kw[e]), kk);
+                qq = fmaf(qs::bf_lo(qw[e]), qs::bf_lo(qw[e]), qq);
+                qq = fmaf(qs::bf_hi(qw[e]), qs::bf_hi(qw[e]), qq);
             }
         }
-        ss += qs::dpp<0xB1>(ss);
-        ss += qs::dpp<0x4E>(ss);
-        if (part == 0) s_rq[r] = rsqrtf(ss + a.eps) * a.scale;
+        kk += qs::dpp<0xB1>(kk);
+        kk += qs::dpp<0x4E>(kk);
+        qq += qs::dpp<0xB1>(qq);
+        qq += qs::dpp<0x4E>(qq);
+        if (part == 0) {
+            s_rk[r] = rsqrtf(kk + a.eps);
+            s_rq[r] = rsqrtf(qq + a.eps) * a.scale;
+        }
+    }
+    if (w == 0) {
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const float up = __shfl_up(gi, d, 64);
+            if (lane >= d) gi += up;
+        }
+        s_G[lane] = gi;
+        s_b[lane] = bi;
+    }
+
+    // 3. K K^T and Q K^T in row order sig (exact bf16 products, fp32 sums): wave w owns row tile w; element
+    //    (4 g + i, fr) of column tile tc pairs tokens sig(w, 4 g + i) and sig(tc, fr)
+    f32x4 ckk[4], cqk[4];
+    {
+        const int pa = sig(w, fr);
+        bf16x8 ak[4], aq[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const int off = pa * DK + (((4 * ks + g) ^ sw16(pa)) << 3);
+            ak[ks] = frag(sK + off);
+            aq[ks] = frag(sQ + off);
+        }
+#pragma unroll
+        for (int tc = 0; tc < 4; ++tc) {
+            const int pb = sig(tc, fr);
+            ckk[tc] = f32x4{0.f, 0.f, 0.f, 0.f};
+            cqk[tc] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const bf16x8 bk = frag(sK + pb * DK + (((4 * ks + g) ^ sw16(pb)) << 3));
+                ckk[tc] = mfma(ak[ks], bk, ckk[tc]);
+                cqk[tc] = mfma(aq[ks], bk, cqk[tc]);
+            }
+        }
+    }
+    __syncthreads();  // every read of the K / Q images is done before A overwrites them
+
+    // 4. A (strictly lower) and P (lower with the diagonal, bf16 hi and lo planes) from the accumulators into
+    //    LDS; P is staged in the space Tm takes later and leaves in 16-byte rows
+    uint16_t(*sPh)[CH] = reinterpret_cast<uint16_t(*)[CH]>(s_u + CH * FP * 4);
+    uint16_t(*sPl)[CH] = reinterpret_cast<uint16_t(*)[CH]>(s_u + CH * FP * 4 + CH * CH * 2);
+    static_assert(2 * CH * CH * 2 <= CH * FP * 4, "P's planes must fit in the Tm space");
+    {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ti = sig(w, 4 * g + i);
+            const float Gi = s_G[ti], rqi = s_rq[ti], bki = s_b[ti] * s_rk[ti];
+#pragma unroll
+            for (int tc = 0; tc < 4; ++tc) {
+                const int tj = sig(tc, fr);
+                float av = 0.f, p = 0.f;
+                if (ti >= tj) {
+                    // e^(G_i - G_j) as 2^((G_i - G_j) log2 e) on the hardware exponential (the rounding of
+                    // G_i - G_j dominates the error either way)
+                    const float rkj = s_rk[tj] * __builtin_amdgcn_exp2f((Gi - s_G[tj]) * 1.4426950408889634f);
+                    if (ti > tj) av = bki * rkj * ckk[tc][i];
+                    p = rqi * rkj * cqk[tc][i];
+                }
+                sA[ti][tj] = av;
+                const uint32_t ph = qs::cvt_pk_bf16(p, 0.f) & 0xffffu;
+                sPh[ti][tj] = (uint16_t)ph;
+                sPl[ti][tj] = (uint16_t)qs::cvt_pk_bf16(p - qs::bf2f(ph), 0.f);
+            }
+        }
     }
     __syncthreads();
-    if (tid < CH) s_rk[tid] = rsqrtf(sKK[tid][tid] + a.eps);  // k . k from the exact K K^T diagonal
-    // (the barrier after the gates below also orders every sK / sQ read before the first write of sA)
+    {
+        uint16_t *Pd = a.P + ((size_t)c * a.NV + h) * 2 * CH * CH;
+        const int i = tid >> 2, j0 = (tid & 3) * 16;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            *reinterpret_cast<uint4 *>(Pd + i * CH + j0 + 8 * u) = *reinterpret_cast<const uint4 *>(&sPh[i][j0 + 8 * u]);
+            *reinterpret_cast<uint4 *>(Pd + CH * CH + i * CH + j0 + 8 * u) = *reinterpret_cast<const uint4 *>(&sPl[i][j0 + 8 * u]);
+        }
+    }
+    __syncthreads();  // P's staging space becomes Tm's
 
-    // gates of the first value head, requested now (wave 0: lane = token)
-    float gnext = 0.f, bnext = 0.f;
-    auto fetch_gates = [&](int hv) {
-        if (w == 0 && lane < nval) {
-            gnext = a.g[(size_t)(t0 + lane) * a.NV + hv];
-            bnext = a.beta[(size_t)(t0 + lane) * a.NV + hv];
+    // 5. Tm = (I + A)^-1 by 16 x 16 blocks.
+    //  (a) diagonal blocks by forward substitution, wave 0, one column per lane (16 lanes per block):
+    //      t_i = [i == col] - sum_{k < i} A_ik t_k, the column held in registers;
+    if (w == 0) {
+        const int b0 = 16 * (lane >> 4), col = lane & 15;
+        float t[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float s = i == col ? 1.f : 0.f;
+#pragma unroll
+            for (int k = 0; k < i; ++k) s = fmaf(-sA[b0 + i][b0 + k], t[k], s);
+            t[i] = s;
         }
-    };
-    fetch_gates(kh * rep);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sT[b0 + i][b0 + col] = t[i];
+    }
+    __syncthreads();
+    //  (b) 32 x 32 diagonal blocks: T_10 = -T_11 (A_10 T_00) and T_32 = -T_33 (A_32 T_22), waves 0 and 1;
+    if (w < 2) {
+        const int b = 32 * w;
+        f32x4 m = {0.f, 0.f, 0.f, 0.f};
+        mm16(m, &sA[b + 16][b], FP, &sT[b][b], FP, lane);
+        put16(&sM[w][0][0], 16, m, lane);
+    }
+    __syncthreads();
+    if (w < 2) {
+        const int b = 32 * w;
+        f32x4 r = {0.f, 0.f, 0.f, 0.f};
+        mm16(r, &sT[b + 16][b + 16], FP, &sM[w][0][0], 16, lane);
+        put16(&sT[b + 16][b], FP, -r, lane);
+    }
+    __syncthreads();
+    //  (c) the lower-left 32 x 32 quarter: X_IJ = sum_{K=J}^{1} A_IK T_KJ, then T_IJ = -sum_{K=2}^{I} T_IK X_KJ,
+    //      wave w owns block (I, J) = (2 + w / 2, w % 2). MFMA 16x16x4 fp32: exact fp32 products.
+    const int I = 2 + (w >> 1), J = w & 1;
+    {
+        f32x4 x = {0.f, 0.f, 0.f, 0.f};
+        for (int K = J; K < 2; ++K) mm16(x, &sA[16 * I][16 * K], FP, &sT[16 * K][16 * J], FP, lane);
+        put16(&sM[w][0][0], 16, x, lane);
+    }
+    __syncthreads();
+    {
+        f32x4 r = {0.f, 0.f, 0.f, 0.f};
+        for (int K = 2; K <= I; ++K) mm16(r, &sT[16 * I][16 * K], FP, &sM[2 * (K - 2) + J][0][0], 16, lane);
+        put16(&sT[16 * I][16 * J], FP, -r, lane);
+    }
+    __syncthreads();
 
-    for (int j = 0; j < rep; ++j) {
-        const int hv = kh * rep + j;
-        // 4. gates of value head hv: cumulative log decay (inclusive scan over the 64 tokens)
-        if (w == 0) {
-            float gi = gnext;
-            const float bi = bnext;
+    // 6. Tm (bf16 hi and lo planes, zero above the diagonal) and the per-token scalars to the workspace
+    const size_t mat = ((size_t)c * a.NV + h) * CH * CH;
+    {
+        const int i = tid >> 2, j0 = (tid & 3) * 16;
+        uint32_t th[8], tl[8];
 #pragma unroll
-            for (int d = 1; d < 64; d <<= 1) {
-                const float up = __shfl_up(gi, d, 64);
-                if (lane >= d) gi += up;
-            }
-            s_G[lane] = gi;
-            s_b[lane] = bi;
-            if (j + 1 < rep) fetch_gates(hv + 1);
+        for (int u = 0; u < 16; u += 2) {
+            const float v0 = i >= j0 + u ? sT[i][j0 + u] : 0.f, v1 = i >= j0 + u + 1 ? sT[i][j0 + u + 1] : 0.f;
+            th[u / 2] = qs::cvt_pk_bf16(v0, v1);
+            tl[u / 2] = qs::cvt_pk_bf16(v0 - qs::bf_lo(th[u / 2]), v1 - qs::bf_hi(th[u / 2]));
         }
-        __syncthreads();
-        // 5. A (strictly lower) into LDS; P (lower incl. diagonal) to the workspace as bf16 hi and lo planes.
-        //    Thread: row i = tid / 4, columns 16 (tid % 4) .. + 15.
-        const size_t mat = ((size_t)c * a.NV + hv) * CH * CH;
-        {
-            const int i = tid >> 2, j0 = (tid & 3) * 16;
-            const float Gi = s_G[i], rqi = s_rq[i], bki = s_b[i] * s_rk[i];
-            uint32_t ph[8], pl[8];
-#pragma unroll
-            for (int u = 0; u < 16; u += 2) {
-                float pv[2];
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const int jj = j0 + u + e;
-                    float av = 0.f, p = 0.f;
-                    if (i >= jj) {
-                        const float rkj = s_rk[jj] * expf(Gi - s_G[jj]);
-                        if (i > jj) av = bki * rkj * sKK[i][jj];
-                        p = rqi * rkj * sQK[i][jj];
-                    }
-                    sA[i][jj] = av;
-                    pv[e] = p;
-                }
-                const uint32_t h0 = qs::f2bf(pv[0]), h1 = qs::f2bf(pv[1]);
-                ph[u / 2] = h0 | (h1 << 16);
-                pl[u / 2] = qs::f2bf(pv[0] - qs::bf2f(h0)) | (qs::f2bf(pv[1] - qs::bf2f(h1)) << 16);
-            }
-            uint4 *dh = reinterpret_cast<uint4 *>(a.P + 2 * mat + i * CH + j0);
-            uint4 *dl = reinterpret_cast<uint4 *>(a.P + 2 * mat + CH * CH + i * CH + j0);
-            dh[0] = make_uint4(ph[0], ph[1], ph[2], ph[3]);
-            dh[1] = make_uint4(ph[4], ph[5], ph[6], ph[7]);
-            dl[0] = make_uint4(pl[0], pl[1], pl[2], pl[3]);
-            dl[1] = make_uint4(pl[4], pl[5], pl[6], pl[7]);
-        }
-        __syncthreads();
-        // 6. Tm = (I + A)^-1 by 16 x 16 blocks.
-        //  (a) diagonal blocks by forward substitution, wave 0, one column per lane (16 lanes per block):
-        //      t_i = [i == col] - sum_{k < i} A_ik t_k, the column held in registers;
-        if (w == 0) {
-            const int b0 = 16 * (lane >> 4), col = lane & 15;
-            float t[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                float s = i == col ? 1.f : 0.f;
-#pragma unroll
-                for (int k = 0; k < i; ++k) s = fmaf(-sA[b0 + i][b0 + k], t[k], s);
-                t[i] = s;
-            }
-#pragma unroll
-            for (int i = 0; i < 16; ++i) sT[b0 + i][b0 + col] = t[i];
-        }
-        __syncthreads();
-        //  (b) 32 x 32 diagonal blocks: T_10 = -T_11 (A_10 T_00) and T_32 = -T_33 (A_32 T_22), waves 0 and 1;
-        if (w < 2) {
-            const int b = 32 * w;
-            f32x4 m = {0.f, 0.f, 0.f, 0.f};
-            mm16(m, &sA[b + 16][b], FP, &sT[b][b], FP, lane);
-            put16(&sM[w][0][0], 16, m, lane);
-        }
-        __syncthreads();
-        if (w < 2) {
-            const int b = 32 * w;
-            f32x4 r = {0.f, 0.f, 0.f, 0.f};
-            mm16(r, &sT[b + 16][b + 16], FP, &sM[w][0][0], 16, lane);
-            put16(&sT[b + 16][b], FP, -r, lane);
-        }
-        __syncthreads();
-        //  (c) the lower-left 32 x 32 quarter: X_IJ = sum_{K=J}^{1} A_IK T_KJ, then T_IJ = -sum_{K=2}^{I} T_IK X_KJ,
-        //      wave w owns block (I, J) = (2 + w / 2, w % 2). MFMA 16x16x4 fp32: exact fp32 products.
-        const int I = 2 + (w >> 1), J = w & 1;
-        {
-            f32x4 x = {0.f, 0.f, 0.f, 0.f};
-            for (int K = J; K < 2; ++K) mm16(x, &sA[16 * I][16 * K], FP, &sT[16 * K][16 * J], FP, lane);
-            put16(&sM[w][0][0], 16, x, lane);
-        }
-        __syncthreads();
-        {
-            f32x4 r = {0.f, 0.f, 0.f, 0.f};
-            for (int K = 2; K <= I; ++K) mm16(r, &sT[16 * I][16 * K], FP, &sM[2 * (K - 2) + J][0][0], 16, lane);
-            put16(&sT[16 * I][16 * J], FP, -r, lane);
-        }
-        __syncthreads();
-        // 7. Tm (bf16 hi and lo planes, zero above the diagonal) and the per-token scalars to the workspace
-        {
-            const int i = tid >> 2, j0 = (tid & 3) * 16;
-            uint32_t th[8], tl[8];
-#pragma unroll
-            for (int u = 0; u < 16; u += 2) {
-                const float v0 = i >= j0 + u ? sT[i][j0 + u] : 0.f, v1 = i >= j0 + u + 1 ? sT[i][j0 + u + 1] : 0.f;
-                const uint32_t h0 = qs::f2bf(v0), h1 = qs::f2bf(v1);
-                th[u / 2] = h0 | (h1 << 16);
-                tl[u / 2] = qs::f2bf(v0 - qs::bf2f(h0)) | (qs::f2bf(v1 - qs::bf2f(h1)) << 16);
-            }
-            uint4 *dh = reinterpret_cast<uint4 *>(a.Tm + 2 * mat + i * CH + j0);
-            uint4 *dl = reinterpret_cast<uint4 *>(a.Tm + 2 * mat + CH * CH + i * CH + j0);
-            dh[0] = make_uint4(th[0], th[1], th[2], th[3]);
-            dh[1] = make_uint4(th[4], th[5], th[6], th[7]);
-            dl[0] = make_uint4(tl[0], tl[1], tl[2], tl[3]);
-            dl[1] = make_uint4(tl[4], tl[5], tl[6], tl[7]);
-        }
-        if (tid < CH) {
-            const int i = tid;
-            const float gam = expf(s_G[i]);
-            float *scp = a.sc + ((size_t)c * a.NV + hv) * 5 * CH;
-            scp[0 * CH + i] = s_b[i];
-            scp[1 * CH + i] = s_b[i] * gam * s_rk[i];
-            scp[2 * CH + i] = s_rq[i] * gam;
-            scp[3 * CH + i] = s_rk[i] * expf(s_G[CH - 1] - s_G[i]);
-            scp[4 * CH + i] = expf(s_G[CH - 1]);
-        }
-        __syncthreads();
+        uint4 *dh = reinterpret_cast<uint4 *>(a.Tm + 2 * mat + i * CH + j0);
+        uint4 *dl = reinterpret_cast<uint4 *>(a.Tm + 2 * mat + CH * CH + i * CH + j0);
+        dh[0] = make_uint4(th[0], th[1], th[2], th[3]);
+        dh[1] = make_uint4(th[4], th[5], th[6], th[7]);
+        dl[0] = make_uint4(tl[0], tl[1], tl[2], tl[3]);
+        dl[1] = make_uint4(tl[4], tl[5], tl[6], tl[7]);
+    }
+    if (tid < CH) {
+        const int i = tid;
+        const float gam = expf(s_G[i]);
+        float *scp = a.sc + ((size_t)c * a.NV + h) * 5 * CH;
+        scp[0 * CH + i] = s_b[i];
+        scp[1 * CH + i] = s_b[i] * gam * s_rk[i];
+        scp[2 * CH + i] = s_rq[i] * gam;
+        scp[3 * CH + i] = s_rk[i] * expf(s_G[CH - 1] - s_G[i]);
+        scp[4 * CH + i] = expf(s_G[CH - 1]);
     }
 }
 
@@ -416,7 +448,7 @@ __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
         for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                __builtin_amdgcn_raw_buffer_store_b16((unsigned short)qs::f2bf(opend[nt][i]), ro,
+                __builtin_amdgcn_raw_buffer_store_b16((unsigned short)qs::cvt_pk_bf16(opend[nt][i], 0.f), ro,
                                                       (int)((r0 + i) * vrow) + (h * DV + SLAB * slab + nt * 16 + fr) * 2, 0,
                                                       0);
     };
@@ -621,7 +653,7 @@ PrefillWs prefill_ws(int T, int NV) {
     const size_t nch = (size_t)(T + CH - 1) / CH;
     PrefillWs l;
     l.tm = 0;
-    l.p = up(nch * NV * CH * CH * 4);
+    l.p = up(nch * NV * 2 * CH * CH * 2);
     l.sc = l.p + up(nch * NV * 2 * CH * CH * 2);
     l.total = l.sc + up(nch * NV * 5 * CH * 4);
     return l;
@@ -644,6 +676,8 @@ extern "C" int qs_gdn_chunk_prefill(const uint16_t *q, const uint16_t *k, const 
     QS_REQUIRE(DKa == DK && DVa == DV, "qs_gdn_chunk_prefill: DK and DV must be 128 (got %d, %d)", DKa, DVa);
     QS_REQUIRE(NK > 0 && NV > 0 && NV % NK == 0, "qs_gdn_chunk_prefill: NV (%d) must be a multiple of NK (%d)", NV, NK);
     QS_REQUIRE(chunk == CH, "qs_gdn_chunk_prefill: only chunk %d is built (got %d)", CH, chunk);
+    QS_REQUIRE((long)(T + CH) * NV * DV * 2 < (1L << 31) && (long)(T + CH) * NK * DK * 2 < (1L << 31),
+               "qs_gdn_chunk_prefill: T = %d tokens exceed the 2 GB buffer range", T);
     const PrefillWs L = prefill_ws(T, NV);
     char *ws = static_cast<char *>(workspace);
     PrefillArgs a{};
@@ -653,7 +687,7 @@ extern "C" int qs_gdn_chunk_prefill(const uint16_t *q, const uint16_t *k, const 
     a.sc = reinterpret_cast<float *>(ws + L.sc);
     a.T = T, a.NK = NK, a.NV = NV, a.nch = (T + CH - 1) / CH, a.scale = scale, a.eps = eps;
     hipStream_t st = QS_STREAM(stream);
-    chunk_prep_kernel<<<a.nch * NK, 256, 0, st>>>(a);
+    chunk_prep_kernel<<<a.nch * NV, 256, 0, st>>>(a);
     if (int e = qs::launch_status("qs_gdn_chunk_prefill (prep)")) return e;
     chunk_walk_kernel<<<NV * NSLAB, 256, 0, st>>>(a);
     return qs::launch_status("qs_gdn_chunk_prefill (walk)");
