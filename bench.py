@@ -11,7 +11,8 @@ Inputs are seeded synthetic tensors already resident in HBM; the step moves 4,63
 
 Other workloads (one JSON line each): gdn-layer (one GDN layer, batch 1), attn-layer (one attention layer
 at 32768 positions, batch 1), verify-step (MTP verify at batch 1, 8192 positions, 4 tokens, 64 layers +
-rollback), prefill (chunked gated delta rule over 8192 tokens + the paged K/V fill).
+rollback), prefill (chunked gated delta rule over 8192 tokens + the paged K/V fill), conv-prefill (the
+prompt conv with its carry over 8192 tokens).
 
 value = algorithmic bytes / time (GB/s); roofline = the dominant kernel's per-launch algorithmic bytes /
 its average launch time (HIP events over back-to-back launches on the stream they run on); cpu_baseline =
@@ -244,6 +245,37 @@ def bench_prefill(args, torch):
                 roofline("gdn_chunk_prefill", nbytes, ms), dict(flops=71.94e9, tflops=round(71.94e9 / ms / 1e9, 1)))
 
 
+def bench_conv_prefill(args, torch):
+    """The prompt conv with its carry over 8192 tokens of the 10240 q | k | v channels, read from a
+    projection output with 128 further columns; two prompts rotate (1.3 GB per loop) so each launch reads
+    and writes HBM rather than the Infinity Cache."""
+    from qwen36_state import ops, workloads as W
+
+    T, C, ldx = 8192, W.C_QKV, W.C_QKV + 128
+    CQ, CV = ops.NK * ops.DK, ops.NV * ops.DV
+    bufs = []
+    for i in range(2):
+        gen = W._gen("cuda:0", i)
+        bufs.append(dict(
+            x=W._randn((T, ldx), gen, "cuda:0", torch.bfloat16),
+            taps=W._randn((C, 4), gen, "cuda:0", torch.bfloat16, std=0.5),
+            cs=W._randn((C, 3), gen, "cuda:0", torch.bfloat16),
+            q=torch.empty(T, CQ, dtype=torch.bfloat16, device="cuda:0"),
+            k=torch.empty(T, CQ, dtype=torch.bfloat16, device="cuda:0"),
+            v=torch.empty(T, CV, dtype=torch.bfloat16, device="cuda:0"),
+            out=torch.empty(C, 3, dtype=torch.bfloat16, device="cuda:0"),
+        ))  # fmt: skip
+
+    def calls(st):
+        return [("qs_conv1d_prefill", (_p(b["x"]), ldx, _p(b["cs"]), _p(b["taps"]), _p(b["q"]), _p(b["k"]),
+                                       _p(b["v"]), _p(b["out"]), T, CQ, CV, 4, st)) for b in bufs]  # fmt: skip
+
+    ms = kernel_time(torch, calls, args.kernel_reps)
+    nbytes = 2 * T * C * 2 + C * 4 * 2 + 2 * C * 3 * 2  # x in, q | k | v out, taps, carry in and out
+    return line(args, "prompt conv1d + SiLU with carry, 8192 tokens x 10240 channels (q | k | v of a 10368-column "
+                "projection), conv state handed to the decode", nbytes, ms, roofline("conv1d_prefill", nbytes, ms))
+
+
 def cpu_baseline(step, torch, n_gdn=2, n_attn=1, reps=3):
     """The CPU oracle on a bounded sample of the step (n_gdn GDN + n_attn attention layers at the real
     shapes), scaled to the full step by layer count; median of reps after one warm-up."""
@@ -294,6 +326,7 @@ WORKLOADS = {
     "attn-layer": bench_attn_layer,
     "verify-step": bench_verify,
     "prefill": bench_prefill,
+    "conv-prefill": bench_conv_prefill,
 }
 
 

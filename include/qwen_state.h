@@ -196,6 +196,22 @@ int qs_gdn_chunk_prefill(const uint16_t *q, const uint16_t *k, const uint16_t *v
                          void *workspace, int T, int NK, int NV, int DK, int DV, int chunk, float scale,
                          float eps, void *stream);
 
+/* ---------------------------------------------------------------------------------------- f2: prefill conv
+ * Causal depthwise conv1d + SiLU over the T prompt tokens of one sequence, carry in and out: the window of
+ * channel c is [carry (3, oldest first; zeros when conv_state_in is null), x[0..T-1]], y is written to
+ * the q | k | v planes the channels belong to, and conv_state_out receives the last 3 window inputs (bits
+ * unchanged), i.e. the decode conv state of the sequence. Same tap-sum order as qs_conv1d_update, so y
+ * equals T successive decode conv steps bit for bit. T = 0 copies the carry (x, q, k, v may then be null).
+ *   x [T, ldx] bf16 (conv channels in columns [0, 2 CQ + CV)); conv_state_in, conv_state_out [C, K-1]
+ *   (may be the same buffer); taps [C, K] -> q, k [T, CQ], v [T, CV] bf16. K == 4; every buffer 16-byte
+ *   aligned; CQ, CV, ldx multiples of 8.
+ * Replaces the prefill conv with its carry update (prefill/pp_prefill.py:384-445, prefill/kernels/
+ * conv_compute.cpp:1-12) and the conv-history handoff to the decode (prefill/pp_prefill.py:1128-1175,
+ * prefill/kernels/hist_scatter.cpp:1-12). */
+int qs_conv1d_prefill(const uint16_t *x, int ldx, const uint16_t *conv_state_in, const uint16_t *taps, uint16_t *q,
+                      uint16_t *k, uint16_t *v, uint16_t *conv_state_out, int T, int CQ, int CV, int K,
+                      void *stream);
+
 #ifdef __cplusplus
 }
 #endif

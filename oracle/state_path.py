@@ -24,6 +24,7 @@ __all__ = [
     "bf16",
     "conv1d_update",
     "conv1d_update_loops",
+    "conv1d_prefill",
     "l2norm",
     "gdn_gates",
     "gdn_step",
@@ -78,6 +79,29 @@ def conv1d_update(x, conv_state, taps):
         acc = acc + win[..., j] * t[:, j]
     y = bf16(F.silu(acc))
     return y, win[..., 1:].clone()
+
+
+def conv1d_prefill(x, conv_state, taps):
+    """Causal depthwise conv1d + SiLU over the T prompt tokens of one sequence, with the carry.
+
+    Restates the prefill conv (prefill/kernels/conv_compute.cpp:4-10, its statement in the reference test
+    tests/test_pp_kernels.py:135-140): ``win = cat([carry, x])`` oldest first, ``y_t = bf16(silu(sum_j
+    win[t + j] taps[:, j]))`` with the tap sum in the decode order (tap 0 first), and the new carry is
+    ``win[T : T + K - 1]``, the last K - 1 inputs (bits unchanged).
+
+    x [T, C]; conv_state [C, K-1] or None (zeros); taps [C, K] (bf16-valued float tensors)
+    returns y [T, C] (bf16-valued fp32), new conv state [C, K-1]
+    """
+    T, C = x.shape
+    K = taps.shape[1]
+    carry = torch.zeros(C, K - 1) if conv_state is None else conv_state.float()
+    win = torch.cat([carry.t(), x.float()], dim=0)  # [T + K - 1, C]
+    t = taps.float()
+    acc = win[0:T] * t[:, 0]
+    for j in range(1, K):
+        acc = acc + win[j : j + T] * t[:, j]
+    y = bf16(F.silu(acc))
+    return y, win[T : T + K - 1].t().contiguous()
 
 
 def conv1d_update_loops(x, conv_state, taps):

@@ -92,6 +92,46 @@ def test_conv_shift_invariant():
     assert torch.equal(cs, torch.stack(xs, -1))
 
 
+@pytest.mark.parametrize("T", [0, 1, 2, 3, 7, 40])
+def test_conv_prefill_equals_decode_steps(T):
+    """The prompt conv equals T decode conv steps from the same carry: every output bit for bit, and the
+    carry it leaves is the decode conv state (the reference's carry check, tests/test_pp_kernels.py:137-142,
+    for full, partial and 1-row chunks)."""
+    g = torch.Generator().manual_seed(10 + T)
+    C = 24
+    x, cs, taps = bfr(T, C, gen=g), bfr(C, 3, gen=g), bfr(C, 4, gen=g, std=0.5)
+    y, ns = O.conv1d_prefill(x, cs, taps)
+    st = cs[None].clone()
+    for t in range(T):
+        yt, st = O.conv1d_update(x[t][None], st, taps)
+        assert torch.equal(y[t], yt[0])
+    assert torch.equal(ns, st[0])
+    assert y.shape == (T, C)
+
+
+def test_conv_prefill_impulse_carry_and_split():
+    """An impulse at token s with a zero carry gives silu(tap 3 - j) at token s + j (tap 0 on the oldest);
+    no carry means a zero carry; prefill of a prompt in two pieces, the second from the first's carry,
+    equals the prefill of the whole prompt."""
+    taps = torch.tensor([[0.5, -0.25, 2.0, 1.5]])
+    x = torch.zeros(9, 1)
+    x[3, 0] = 1.0
+    y, ns = O.conv1d_prefill(x, None, taps)
+    silu = lambda v: float(O.bf16(F.silu(torch.tensor(v))))
+    assert [float(v) for v in y[:, 0]] == [0.0, 0.0, 0.0, silu(1.5), silu(2.0), silu(-0.25), silu(0.5), 0.0, 0.0]
+    assert ns.tolist() == [[0.0, 0.0, 0.0]]
+    g = torch.Generator().manual_seed(3)
+    x, taps = bfr(50, 16, gen=g), bfr(16, 4, gen=g)
+    y, ns = O.conv1d_prefill(x, None, taps)
+    y0, ns0 = O.conv1d_prefill(x, torch.zeros(16, 3), taps)
+    assert torch.equal(y, y0) and torch.equal(ns, ns0)
+    for cut in (1, 2, 17):
+        ya, ca = O.conv1d_prefill(x[:cut], None, taps)
+        yb, cb = O.conv1d_prefill(x[cut:], ca, taps)
+        assert torch.equal(torch.cat([ya, yb]), y) and torch.equal(cb, ns)
+    assert torch.equal(ns, x[-3:].t())
+
+
 # ------------------------------------------------------------------------------------------- a2 / a3
 
 

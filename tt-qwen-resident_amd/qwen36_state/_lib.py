@@ -48,6 +48,7 @@ SIGNATURES = {
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _F, _P],
     ),
+    "qs_conv1d_prefill": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
 }
 
 _lib = None

@@ -383,6 +383,37 @@ def paged_gqa_decode(q, k_cache, v_cache, block_table, seq_lens, scale, k_new=No
 # ------------------------------------------------------------------------------------------- a8
 
 
+def causal_conv1d_prefill(x, taps, conv_state=None, conv_state_out=None, nk=NK, nv=NV):
+    """silu(causal conv1d) of a prompt's q | k | v columns into q, k, v with the carry
+    (prefill/pp_prefill.py:384-445; the conv history handed to the decode, prefill/pp_prefill.py:1128-1175).
+
+    x [T, >= C] bf16 with unit column stride (the projection output; its first C = 2 nk DK + nv DV columns
+    are the conv channels), taps [C, K] bf16, conv_state [C, K-1] bf16 or None (a fresh prompt: zeros).
+    conv_state_out [C, K-1] receives the last K-1 inputs (the decode conv state; it may be conv_state
+    itself, a new tensor when None). Returns (q [T, nk, DK], k [T, nk, DK], v [T, nv, DV], conv_state_out)."""
+    dev = x.device
+    CQ, CV = nk * DK, nv * DV
+    C = 2 * CQ + CV
+    if not isinstance(x, torch.Tensor) or x.dim() != 2 or not x.is_cuda or x.dtype != torch.bfloat16:
+        raise ValueError("x must be a 2-D bf16 tensor on a GPU")
+    T = x.shape[0]
+    if x.shape[1] < C or (T > 1 and x.stride(1) != 1):
+        raise ValueError(f"x must hold the {C} conv channels in unit-stride columns (got {tuple(x.shape)})")
+    ldx = x.stride(0) if T > 1 else C
+    _chk(taps, "taps", torch.bfloat16, (C, CONV_K), dev)
+    if conv_state is not None:
+        _chk(conv_state, "conv_state", torch.bfloat16, (C, CONV_K - 1), dev)
+    if conv_state_out is None:
+        conv_state_out = torch.empty(C, CONV_K - 1, dtype=torch.bfloat16, device=dev)
+    _chk(conv_state_out, "conv_state_out", torch.bfloat16, (C, CONV_K - 1), dev)
+    q = torch.empty(T, nk, DK, dtype=torch.bfloat16, device=dev)
+    k = torch.empty(T, nk, DK, dtype=torch.bfloat16, device=dev)
+    v = torch.empty(T, nv, DV, dtype=torch.bfloat16, device=dev)
+    call("qs_conv1d_prefill", _p(x), ldx, _p(conv_state), _p(taps), _p(q), _p(k), _p(v), _p(conv_state_out), T, CQ,
+         CV, CONV_K, _stream(dev))  # fmt: skip
+    return q, k, v, conv_state_out
+
+
 def chunk_gated_delta_rule(q, k, v, g, beta, *, scale=None, initial_state=None, output_final_state=True,
                            chunk_size=64, output_head_major=False, eps=EPS, ws=None):  # fmt: skip
     """``chunk_gated_delta_rule(q, k, v, g, beta, scale, initial_state, output_final_state, chunk_size,
