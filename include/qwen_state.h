@@ -152,6 +152,16 @@ int qs_paged_kv_fill(const uint16_t *k, const uint16_t *v, uint16_t *k_cache, ui
                      const int *page_table, int T, int start, int NKV, int HD, int block, int table_len,
                      int num_blocks, void *stream);
 
+/* The inverse of qs_paged_kv_fill: positions start .. start+T-1 of one sequence, read from its pages into
+ * contiguous k, v [NKV, T, HD] (either pair may be null). A position whose table entry is outside
+ * [0, num_blocks) reads zeros. With qs_paged_kv_fill it converts between the paged pools and the
+ * per-sequence row layout in both directions, bit-exact.
+ * Replaces the KV part of the prefill-to-decode export (prefill/pp_prefill.py:1241-1249, the paged-to-rows
+ * page copies of prefill/kernels/handoff.cpp:4-8). */
+int qs_paged_kv_gather(const uint16_t *k_cache, const uint16_t *v_cache, const int *page_table, uint16_t *k,
+                       uint16_t *v, int T, int start, int NKV, int HD, int block, int table_len, int num_blocks,
+                       void *stream);
+
 /* ---------------------------------------------------------------------------------------- a6: attention
  * Paged GQA decode attention with split-K over block-table pages and an ordered merge launch.
  *   q [B, T, NQ, HD] bf16; seq_lens [B] = positions valid after this step's T tokens; query t of user b

@@ -58,6 +58,9 @@ def test_rejects_bad_arguments():
     # fill: a table too short for the tokens
     assert L.qs_paged_kv_fill(FAKE, FAKE, FAKE, FAKE, FAKE, 200, 0, 4, 256, 64, 3, 2048, S) == -1
     assert L.qs_paged_kv_append(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1, 1, 4, 250, 64, 8, 8, S) == -1
+    # gather: a table too short for the positions, a pool without its output
+    assert L.qs_paged_kv_gather(FAKE, FAKE, FAKE, FAKE, FAKE, 200, 0, 4, 256, 64, 3, 2048, S) == -1
+    assert L.qs_paged_kv_gather(FAKE, FAKE, FAKE, NUL, FAKE, 100, 0, 4, 256, 64, 3, 2048, S) == -1
     # prompt conv: taps, ldx below C or not a multiple of 8, CQ not a multiple of 8, misalignment, null x
     conv = lambda x, ldx, T, cq, k: (x, ldx, NUL, FAKE, FAKE, FAKE, FAKE, FAKE, T, cq, 6144, k, S)
     assert L.qs_conv1d_prefill(*conv(FAKE, 10240, 5, 2048, 3)) == -1

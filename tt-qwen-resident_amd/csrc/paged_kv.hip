@@ -1,5 +1,5 @@
-// Paged KV-cache movement on gfx950: decode append (T rows per user through the block table) and prefill
-// fill (paged_fill_cache). Pure byte copies in 16-byte units; page indices read from device memory are
+// Paged KV-cache movement on gfx950: decode append (T rows per user through the block table), prefill
+// fill (paged_fill_cache) and its inverse, the gather of a sequence's pages into contiguous rows. Pure byte copies in 16-byte units; page indices read from device memory are
 // range-checked in the kernel (a row whose page is out of range is skipped, never written out of bounds).
 #include "qs_common.h"
 
@@ -32,10 +32,13 @@ __global__ __launch_bounds__(256) void append_kernel(const uint16_t *k, const ui
     if (v) *reinterpret_cast<uint4 *>(vc + dst) = *reinterpret_cast<const uint4 *>(v + src);
 }
 
-// x [NKV, T, HD]: thread i copies chunk (i % cpr) of token ((i / cpr) % T), kv head (i / cpr / T)
+// x [NKV, T, HD]: thread i copies chunk (i % cpr) of token ((i / cpr) % T), kv head (i / cpr / T), from x
+// into its page (fill) or from its page into x (gather; a token whose page is out of range reads zeros)
+template <bool GATHER>
 __global__ __launch_bounds__(256) void fill_kernel(const uint16_t *k, const uint16_t *v, uint16_t *kc, uint16_t *vc,
-                                                   const int *page_table, int T, int start, int NKV, int HD,
-                                                   int block, int table_len, int num_blocks) {
+                                                   uint16_t *ko, uint16_t *vo, const int *page_table, int T,
+                                                   int start, int NKV, int HD, int block, int table_len,
+                                                   int num_blocks) {
     const int cpr = HD / 8;
     const long i = (long)blockIdx.x * 256 + threadIdx.x;
     const long total = (long)NKV * T * cpr;
@@ -46,13 +49,18 @@ __global__ __launch_bounds__(256) void fill_kernel(const uint16_t *k, const uint
     const int hk = (int)(r / T);
     const int p = start + tok;
     const int bi = p / block;
-    if (bi >= table_len) return;
-    const int page = page_table[bi];
-    if (page < 0 || page >= num_blocks) return;
-    const size_t dst = (((size_t)page * NKV + hk) * block + p % block) * HD + ch * 8;
-    const size_t src = (size_t)r * HD + ch * 8;
-    if (k) *reinterpret_cast<uint4 *>(kc + dst) = *reinterpret_cast<const uint4 *>(k + src);
-    if (v) *reinterpret_cast<uint4 *>(vc + dst) = *reinterpret_cast<const uint4 *>(v + src);
+    const int page = bi < table_len ? page_table[bi] : -1;
+    const bool ok = page >= 0 && page < num_blocks;
+    const size_t pg = (((size_t)page * NKV + hk) * block + p % block) * HD + ch * 8;
+    const size_t x = (size_t)r * HD + ch * 8;
+    if (GATHER) {
+        const uint4 z = make_uint4(0, 0, 0, 0);
+        if (ko) *reinterpret_cast<uint4 *>(ko + x) = ok ? *reinterpret_cast<const uint4 *>(kc + pg) : z;
+        if (vo) *reinterpret_cast<uint4 *>(vo + x) = ok ? *reinterpret_cast<const uint4 *>(vc + pg) : z;
+    } else if (ok) {
+        if (k) *reinterpret_cast<uint4 *>(kc + pg) = *reinterpret_cast<const uint4 *>(k + x);
+        if (v) *reinterpret_cast<uint4 *>(vc + pg) = *reinterpret_cast<const uint4 *>(v + x);
+    }
 }
 
 }  // namespace
@@ -84,7 +92,26 @@ extern "C" int qs_paged_kv_fill(const uint16_t *k, const uint16_t *v, uint16_t *
                "qs_paged_kv_fill: %d tokens from %d need more than the %d table entries", T, start, table_len);
     const long total = (long)NKV * T * (HD / 8);
     if (total == 0) return QS_OK;
-    fill_kernel<<<(unsigned)((total + 255) / 256), 256, 0, QS_STREAM(stream)>>>(
-        k, v, k_cache, v_cache, page_table, T, start, NKV, HD, block, table_len, num_blocks);
+    fill_kernel<false><<<(unsigned)((total + 255) / 256), 256, 0, QS_STREAM(stream)>>>(
+        k, v, k_cache, v_cache, nullptr, nullptr, page_table, T, start, NKV, HD, block, table_len, num_blocks);
     return qs::launch_status("qs_paged_kv_fill");
+}
+
+extern "C" int qs_paged_kv_gather(const uint16_t *k_cache, const uint16_t *v_cache, const int *page_table,
+                                  uint16_t *k, uint16_t *v, int T, int start, int NKV, int HD, int block,
+                                  int table_len, int num_blocks, void *stream) {
+    QS_REQUIRE(page_table, "qs_paged_kv_gather: null page table");
+    QS_REQUIRE((k == nullptr) == (k_cache == nullptr) && (v == nullptr) == (v_cache == nullptr) && (k || v),
+               "qs_paged_kv_gather: give k with k_cache and/or v with v_cache");
+    QS_REQUIRE(T >= 0 && start >= 0 && NKV > 0 && block > 0 && table_len > 0 && num_blocks > 0,
+               "qs_paged_kv_gather: bad sizes");
+    QS_REQUIRE(HD > 0 && HD % 8 == 0, "qs_paged_kv_gather: HD must be a multiple of 8 (got %d)", HD);
+    QS_REQUIRE((long)(start + T + block - 1) / block <= table_len,
+               "qs_paged_kv_gather: %d tokens from %d need more than the %d table entries", T, start, table_len);
+    const long total = (long)NKV * T * (HD / 8);
+    if (total == 0) return QS_OK;
+    fill_kernel<true><<<(unsigned)((total + 255) / 256), 256, 0, QS_STREAM(stream)>>>(
+        nullptr, nullptr, const_cast<uint16_t *>(k_cache), const_cast<uint16_t *>(v_cache), k, v, page_table, T,
+        start, NKV, HD, block, table_len, num_blocks);
+    return qs::launch_status("qs_paged_kv_gather");
 }

@@ -34,6 +34,7 @@ SIGNATURES = {
         _I, [_P, _Z, _P, _Z, _P, _Z, _P, _Z, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "qs_paged_kv_append": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "qs_paged_kv_fill": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "qs_paged_kv_gather": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "qs_paged_attention_workspace_bytes": (_Z, [_I, _I, _I, _I, _I, _I, _I]),
     "qs_paged_gqa_decode": (
         _I,

@@ -323,6 +323,21 @@ def paged_kv_fill(k, v, k_cache, v_cache, page_table, start=0):
          block, page_table.shape[0], nb, _stream(dev))  # fmt: skip
 
 
+def paged_kv_gather(k_cache, v_cache, page_table, n, start=0):
+    """Positions start .. start+n-1 of one sequence out of the pools into contiguous K, V [NKV, n, HD]: the
+    inverse of paged_kv_fill (the KV export of prefill/pp_prefill.py:1241-1249). page_table [m] int32."""
+    dev = k_cache.device
+    nb, nkv, block, hd = _pool_dims(k_cache, v_cache, dev)
+    _chk(page_table, "page_table", torch.int32, None, dev)
+    if page_table.dim() != 1:
+        raise ValueError("page_table must be one sequence's [n] table")
+    k = torch.empty(nkv, n, hd, dtype=torch.bfloat16, device=dev)
+    v = torch.empty_like(k)
+    call("qs_paged_kv_gather", _p(k_cache), _p(v_cache), _p(page_table), _p(k), _p(v), int(n), int(start), nkv, hd,
+         block, page_table.shape[0], nb, _stream(dev))  # fmt: skip
+    return k, v
+
+
 def paged_fill_cache(cache, x, page_table, batch_idx=0):
     """``ttnn.experimental.paged_fill_cache(cache, x, page_table, batch_idx)`` (prefill/pp_prefill.py:826-827).
 
@@ -415,12 +430,14 @@ def causal_conv1d_prefill(x, taps, conv_state=None, conv_state_out=None, nk=NK, 
 
 
 def chunk_gated_delta_rule(q, k, v, g, beta, *, scale=None, initial_state=None, output_final_state=True,
-                           chunk_size=64, output_head_major=False, eps=EPS, ws=None):  # fmt: skip
+                           chunk_size=64, output_head_major=False, eps=EPS, ws=None, final_state=None):  # fmt: skip
     """``chunk_gated_delta_rule(q, k, v, g, beta, scale, initial_state, output_final_state, chunk_size,
     output_head_major)`` as the reference prefill calls it (prefill/pp_prefill.py:791-807): q, k [T, NK*DK]
     or [T, NK, DK] bf16 token-major (L2-normalised inside, q times scale), v [T, NV*DV] or [T, NV, DV] bf16,
     g, beta [T, NV] fp32, initial_state [NV, DK, DV] fp32. Returns (o, final_state): o [T, NV, DV] bf16
-    ([NV, T, DV] with output_head_major), final_state [NV, DK, DV] fp32 (None unless output_final_state)."""
+    ([NV, T, DV] with output_head_major), final_state [NV, DK, DV] fp32 (None unless output_final_state).
+    final_state, when given, is written in place (it may be initial_state, or one user's slot of the decode
+    state [B, NV, DK, DV], which hands the prompt's state to the decode without a copy)."""
     dev = q.device
     T = q.shape[0]
     nv = g.shape[1]
@@ -436,7 +453,8 @@ def chunk_gated_delta_rule(q, k, v, g, beta, *, scale=None, initial_state=None, 
     _chk(initial_state, "initial_state", torch.float32, (nv, DK, DV), dev)
     scale = DK**-0.5 if scale is None else scale
     o = torch.empty(T, nv, DV, dtype=torch.bfloat16, device=dev)
-    S = torch.empty(nv, DK, DV, dtype=torch.float32, device=dev)
+    S = torch.empty(nv, DK, DV, dtype=torch.float32, device=dev) if final_state is None else final_state
+    _chk(S, "final_state", torch.float32, (nv, DK, DV), dev)
     if ws is None:
         nbytes = lib().qs_gdn_chunk_prefill_workspace_bytes(T, nk, nv, DK, DV, chunk_size)
         ws = workspace(("prefill", chunk_size), nbytes, dev)
