@@ -7,18 +7,19 @@
 // fp32), so y equals T successive decode conv steps bit for bit, and the carry is the decode conv state
 // those steps leave.
 //
-// One thread per 8 adjacent channels (16-byte rows) and R = 16 tokens: it loads the 19 window rows it needs
-// (the 3 before its block from x, or from the carry for the first block), then writes 16 output rows into
+// One thread per 8 adjacent channels (16-byte rows) and R = 8 tokens: it loads the 11 window rows it needs
+// (the 3 before its block from x, or from the carry for the first block), then writes 8 output rows into
 // the q, k or v plane its channels belong to (channels [0, CQ) -> q, [CQ, 2 CQ) -> k, [2 CQ, 2 CQ + CV) -> v).
 // The threads of the first token block also write the new carry; they are the only readers of the carry
 // in, so the carry may be updated in place. Lanes run over channel groups, so every row access is a
-// contiguous 1 KB per wave.
+// contiguous 1 KB per wave. Measured at 8192 tokens: 62.6 us, 5.37 TB/s of algorithmic bytes, HBM reads
+// 1.10x the input (the halo rows of wave 0).
 #include "qs_common.h"
 
 namespace {
 
 constexpr int KC = 4;  // conv taps
-constexpr int R = 16;  // tokens per thread
+constexpr int R = 8;  // tokens per thread (4, 16, 24, 32, or 4 blocks of 16 in sequence measured slower)
 
 struct ConvPrefillArgs {
     const uint16_t *x;       // [T, ldx], conv channels in columns [0, 2 CQ + CV)
@@ -35,9 +36,13 @@ __device__ __forceinline__ uint32_t half_of(const uint4 &r, int c) {
 }
 
 __global__ __launch_bounds__(256) void conv_prefill_kernel(ConvPrefillArgs a) {
-    const int gid = blockIdx.x * 256 + (int)threadIdx.x;
-    const int cg = gid % a.ngroups, tb = gid / a.ngroups;
-    if (tb >= a.ntb) return;
+    // workgroup = 64 channel groups (lanes) x 4 consecutive token blocks (waves): the 3 rows before the
+    // block of waves 1-3 are rows the wave before loads, so only wave 0's come from another workgroup;
+    // consecutive workgroups run across the channel spans, so the running ones stream whole rows
+    const int nspan = (a.ngroups + 63) / 64;
+    const int span = (int)blockIdx.x % nspan, quad = (int)blockIdx.x / nspan;
+    const int cg = span * 64 + (int)(threadIdx.x & 63), tb = quad * 4 + (int)(threadIdx.x >> 6);
+    if (tb >= a.ntb || cg >= a.ngroups) return;
     const int c0 = cg * 8, t0 = tb * R;
 
     uint4 tw[4];  // taps of channels c0 .. c0 + 7, 4 per channel
@@ -152,8 +157,8 @@ extern "C" int qs_conv1d_prefill(const uint16_t *x, int ldx, const uint16_t *con
     ConvPrefillArgs a{};
     a.x = x, a.st_in = conv_state_in, a.taps = taps, a.q = q, a.k = k, a.v = v, a.st_out = conv_state_out;
     a.ldx = ldx, a.T = T, a.CQ = CQ, a.CV = CV, a.ngroups = C / 8, a.ntb = T > 0 ? (T + R - 1) / R : 1;
-    const long threads = (long)a.ngroups * a.ntb;
-    QS_REQUIRE(threads < (1L << 31) - 256, "qs_conv1d_prefill: T = %d tokens are too many for one launch", T);
-    conv_prefill_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, QS_STREAM(stream)>>>(a);
+    const long wgs = (long)((a.ngroups + 63) / 64) * ((a.ntb + 3) / 4);
+    QS_REQUIRE(wgs < (1L << 31), "qs_conv1d_prefill: T = %d tokens are too many for one launch", T);
+    conv_prefill_kernel<<<(unsigned)wgs, 256, 0, QS_STREAM(stream)>>>(a);
     return qs::launch_status("qs_conv1d_prefill");
 }

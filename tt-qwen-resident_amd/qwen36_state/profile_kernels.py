@@ -2,6 +2,7 @@
 
     python tt-qwen-resident_amd/qwen36_state/profile_kernels.py gdn    # fused GDN decode, batch 8, 48 layers
     python tt-qwen-resident_amd/qwen36_state/profile_kernels.py attn   # paged GQA decode, batch 8, 4096 pos, 16 layers
+    python tt-qwen-resident_amd/qwen36_state/profile_kernels.py conv   # prompt conv with carry, 8192 tokens
     python tt-qwen-resident_amd/qwen36_state/profile_kernels.py copy   # 1 GiB device copy (counter calibration)
 
 Each mode runs its launches `--reps` times over distinct per-layer buffers (so the dispatches read HBM, not
@@ -16,7 +17,7 @@ sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("mode", choices=["gdn", "attn", "copy"])
+    ap.add_argument("mode", choices=["gdn", "attn", "conv", "copy"])
     ap.add_argument("--reps", type=int, default=3)
     ap.add_argument("--pps", type=int, default=4)
     args = ap.parse_args()
@@ -34,6 +35,19 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(f"copy: {src.numel() * 4} bytes read and written per dispatch")
+        return
+    if args.mode == "conv":
+        T, C = 8192, W.C_QKV
+        bufs = []
+        for i in range(2):
+            gen = W._gen(dev, i)
+            bufs.append((W._randn((T, C + 128), gen, dev, torch.bfloat16), W._randn((C, 4), gen, dev, torch.bfloat16),
+                         W._randn((C, 3), gen, dev, torch.bfloat16)))  # fmt: skip
+        for _ in range(args.reps):
+            for x, taps, cs in bufs:
+                ops.causal_conv1d_prefill(x[:, :C], taps, cs)
+        torch.cuda.synchronize()
+        print(f"conv1d_prefill: {2 * T * C * 2 + C * 8 + C * 12} algorithmic bytes per dispatch")
         return
     if args.mode == "gdn":
         layers = [W.gdn_layer(8, dev, seed=i) for i in range(48)]
