@@ -531,42 +531,12 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
     __shared__ __align__(16) uint16_t s_p[4][QT][16][PPAD];  // P^T of each slice: [query row][slice row]
     __shared__ float s_m[4][NQR], s_l[4][NQR];              // slice max (log2 domain) and row sum
 
-    int n = a.seq_lens[b];
-    n = n < T ? T : (n > a.max_blocks * BLK ? a.max_blocks * BLK : n);
-    const int base = n - T;  // first new position
-    const int npages = (n + BLK - 1) / BLK;
-    const int p0 = split * a.pps, p1 = min(npages, p0 + a.pps);
+    // Issued first, in this order: the split's block-table entries, the user's length and the query rows.
+    // The first page's K / V loads then wait only for the table entries, not for the length.
+    const int p0 = split * a.pps;
     const int *bt = a.block_table + (size_t)b * a.max_blocks;
-    const int bt_pre = p0 + lane < min(a.max_blocks, p0 + a.pps) ? bt[p0 + lane] : -1;  // issued before n is known
-    auto page_at = [&](int pi) {
-        const int pg = __builtin_amdgcn_readlane(bt_pre, pi - p0);
-        return (pg >= 0 && pg < a.num_blocks) ? pg : -1;
-    };
-    const size_t pstride = (size_t)a.NKV * BLK * HD;  // elements per page
-
-    // Fused append, first: wave w writes the new rows of its 16-row slices in this split's pages and waits
-    // for them, so its slice loads read them back from the pool. No other wave reads these slices.
-    if (a.k_new && p0 < p1 && base / BLK < p1 && (n - 1) / BLK >= p0) {
-        for (int idx = lane; idx < T * 64; idx += 64) {
-            const int t = idx >> 6, kv = (idx >> 5) & 1, ch = idx & 31;
-            const int pos = base + t, pi = pos / BLK;
-            const size_t src = (((size_t)b * T + t) * a.NKV + g) * HD + ch * 8;
-            uint4 u = *reinterpret_cast<const uint4 *>((kv ? a.v_new : a.k_new) + src);
-            if (a.wk) {  // k rows normalised and rotated (all lanes take part in the row reductions)
-                float y[8];
-                const size_t rc = ((size_t)b * T + t) * (a.rot / 2);
-                mixer_chunk(u, ch, a.wk, a.rcos + rc, a.rsin + rc, a.rot, a.eps, y);
-                if (!kv) u = pack8(y);
-            }
-            if (pi < p0 || pi >= p1 || (pos % BLK) / 16 != w) continue;
-            const int pg = bt[pi];
-            if (pg < 0 || pg >= a.num_blocks) continue;
-            const size_t dst = (((size_t)pg * a.NKV + g) * BLK + (pos % BLK)) * HD + ch * 8;
-            *reinterpret_cast<uint4 *>((kv ? a.v_cache : a.k_cache) + dst) = u;
-        }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-
+    const int bt_pre = p0 + lane < min(a.max_blocks, p0 + a.pps) ? bt[p0 + lane] : -1;
+    int n = a.seq_lens[b];
     // query rows qr = t G + hh (zero past T G): loaded into registers now, stored to LDS once the first
     // page's loads are in flight
     constexpr int QCH = NQR * 32 / 256;
@@ -581,13 +551,11 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
         }
     }
 
-    const float sl2 = a.scale * 1.4426950408889634f;  // log2 domain
-    int lim[QT];  // the lane's causal limit per query-row tile: token qr / G sees positions <= base + token
-#pragma unroll
-    for (int nt = 0; nt < QT; ++nt) {
-        const int qr = l16 + 16 * nt;
-        lim[nt] = qr < T * G ? base + qr / G : -1;
-    }
+    auto page_at = [&](int pi) {
+        const int pg = __builtin_amdgcn_readlane(bt_pre, pi - p0);
+        return (pg >= 0 && pg < a.num_blocks) ? pg : -1;
+    };
+    const size_t pstride = (size_t)a.NKV * BLK * HD;  // elements per page
 
     auto load_k = [&](int pg, uint4 (&kb)[8]) {
         const auto rk = __builtin_amdgcn_make_buffer_rsrc(
@@ -611,6 +579,55 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
             vb[k] = make_uint4(x[0], x[1], x[2], x[3]);
         }
     };
+
+    // the first page's rows, before the length is known: a page in the pool's range that turns out to lie
+    // past the user's length is simply not used
+    uint4 KA[8], VA[8];
+    const int pg0 = p0 < a.max_blocks ? page_at(p0) : -1;
+    if (pg0 >= 0) {
+        load_k(pg0, KA);
+        load_v(pg0, VA);
+    }
+
+    n = n < T ? T : (n > a.max_blocks * BLK ? a.max_blocks * BLK : n);
+    const int base = n - T;  // first new position
+    const int npages = (n + BLK - 1) / BLK;
+    const int p1 = min(npages, p0 + a.pps);
+
+    // Fused append, first: wave w writes the new rows of its 16-row slices in this split's pages and waits
+    // for them, so its slice loads read them back from the pool. No other wave reads these slices.
+    if (a.k_new && p0 < p1 && base / BLK < p1 && (n - 1) / BLK >= p0) {
+        for (int idx = lane; idx < T * 64; idx += 64) {
+            const int t = idx >> 6, kv = (idx >> 5) & 1, ch = idx & 31;
+            const int pos = base + t, pi = pos / BLK;
+            const size_t src = (((size_t)b * T + t) * a.NKV + g) * HD + ch * 8;
+            uint4 u = *reinterpret_cast<const uint4 *>((kv ? a.v_new : a.k_new) + src);
+            if (a.wk) {  // k rows normalised and rotated (all lanes take part in the row reductions)
+                float y[8];
+                const size_t rc = ((size_t)b * T + t) * (a.rot / 2);
+                mixer_chunk(u, ch, a.wk, a.rcos + rc, a.rsin + rc, a.rot, a.eps, y);
+                if (!kv) u = pack8(y);
+            }
+            if (pi < p0 || pi >= p1 || (pos % BLK) / 16 != w) continue;
+            const int pg = bt[pi];
+            if (pg < 0 || pg >= a.num_blocks) continue;
+            const size_t dst = (((size_t)pg * a.NKV + g) * BLK + (pos % BLK)) * HD + ch * 8;
+            *reinterpret_cast<uint4 *>((kv ? a.v_cache : a.k_cache) + dst) = u;
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (pg0 >= 0 && base / BLK <= p0) {  // new rows landed in the first page: read it again
+            load_k(pg0, KA);
+            load_v(pg0, VA);
+        }
+    }
+
+    const float sl2 = a.scale * 1.4426950408889634f;  // log2 domain
+    int lim[QT];  // the lane's causal limit per query-row tile: token qr / G sees positions <= base + token
+#pragma unroll
+    for (int nt = 0; nt < QT; ++nt) {
+        const int qr = l16 + 16 * nt;
+        lim[nt] = qr < T * G ? base + qr / G : -1;
+    }
 
     f32x4_t oacc[QT][4];  // O^T of head dims 64 w + 16 dd + 4 lg + i (dd < 4), query row l16 + 16 nt
     float M[QT], L[QT];
@@ -712,11 +729,6 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
         __syncthreads();  // the next page's scores overwrite s_v, s_p, s_m, s_l
     };
 
-    uint4 KA[8], VA[8];
-    if (p0 < p1 && page_at(p0) >= 0) {
-        load_k(page_at(p0), KA);
-        load_v(page_at(p0), VA);
-    }
 #pragma unroll
     for (int k = 0; k < QCH; ++k) {
         const int idx = tid + 256 * k, qr = idx >> 5, ch = idx & 31;
