@@ -135,8 +135,8 @@ template <int CG>
 __device__ __forceinline__ float sum_row_groups(float x) {
     if (CG == 4) x += __shfl_xor(x, 4, 64);
     x += qs::dpp<0x128>(x);  // xor 8 (row_ror:8)
-    x += __shfl_xor(x, 16, 64);
-    x += __shfl_xor(x, 32, 64);
+    x = qs::xor16_sum(x);
+    x = qs::xor32_sum(x);
     return x;
 }
 

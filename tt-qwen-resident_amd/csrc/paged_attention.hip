@@ -77,7 +77,7 @@ __device__ __forceinline__ void mixer_chunk(const uint4 raw, int ch, const float
     ss += qs::dpp<0x4E>(ss);
     ss += qs::dpp<0x124>(ss);
     ss += qs::dpp<0x128>(ss);
-    ss += __shfl_xor(ss, 16, 64);  // the 32 lanes of the row
+    ss = qs::xor16_sum(ss);  // the 32 lanes of the row
     const float r = rsqrtf(ss * (1.0f / HD) + eps);
     const float4 w0 = *reinterpret_cast<const float4 *>(w + ch * 8), w1 = *reinterpret_cast<const float4 *>(w + ch * 8 + 4);
     const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
@@ -679,8 +679,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
                 sc[i] = ok && r0w + 4 * lg + i <= lim[nt] ? sacc[nt][i] : -INFINITY;
                 mx = fmaxf(mx, sc[i]);
             }
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            mx = qs::xor32_max(qs::xor16_max(mx));
             const float ms = mx * sl2;  // -inf when no row of the slice is visible to this query row
             float e[4];
 #pragma unroll
@@ -688,8 +687,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
             const uint32_t p01 = qs::cvt_pk_bf16(e[0], e[1]), p23 = qs::cvt_pk_bf16(e[2], e[3]);
             *reinterpret_cast<uint2 *>(&s_p[w][nt][l16][4 * lg]) = make_uint2(p01, p23);
             float ls = (qs::bf_lo(p01) + qs::bf_hi(p01)) + (qs::bf_lo(p23) + qs::bf_hi(p23));
-            ls += __shfl_xor(ls, 16, 64);
-            ls += __shfl_xor(ls, 32, 64);
+            ls = qs::xor32_sum(qs::xor16_sum(ls));
             if (lg == 0) {
                 s_m[w][l16 + 16 * nt] = ms;
                 s_l[w][l16 + 16 * nt] = ls;

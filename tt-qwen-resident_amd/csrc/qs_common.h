@@ -34,15 +34,44 @@ __device__ __forceinline__ float silu_fast(float x) {
     return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
+// v op (v of lane ^ 16) and v op (v of lane ^ 32) on the VALU (gfx950 v_permlane16_swap / v_permlane32_swap,
+// no LDS round trip). With both operands v, the swap returns, in every lane, the values of the lower and
+// the upper lane of its pair (row pair 2r, 2r + 1 of 16 lanes, or the two 32-lane halves), so both lanes
+// of a pair compute the same lower op upper.
+__device__ __forceinline__ float xor16_sum(float v) {
+    const uint32_t u = __float_as_uint(v);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+    const uint32_t u = __float_as_uint(v);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float v) {
+    const uint32_t u = __float_as_uint(v);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+    const uint32_t u = __float_as_uint(v);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // sum / max over the 64 lanes of a wavefront (butterfly: every lane ends with the result)
 __device__ __forceinline__ float wave_sum(float v) {
+    v = xor32_sum(v);
+    v = xor16_sum(v);
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    for (int m = 8; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
     return v;
 }
 __device__ __forceinline__ float wave_max(float v) {
+    v = xor32_max(v);
+    v = xor16_max(v);
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    for (int m = 8; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
     return v;
 }
 
