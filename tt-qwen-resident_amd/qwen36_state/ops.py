@@ -412,7 +412,7 @@ def causal_conv1d_prefill(x, taps, conv_state=None, conv_state_out=None, nk=NK, 
     if not isinstance(x, torch.Tensor) or x.dim() != 2 or not x.is_cuda or x.dtype != torch.bfloat16:
         raise ValueError("x must be a 2-D bf16 tensor on a GPU")
     T = x.shape[0]
-    if x.shape[1] < C or (T > 1 and x.stride(1) != 1):
+    if x.shape[1] < C or (T > 0 and x.stride(1) != 1):
         raise ValueError(f"x must hold the {C} conv channels in unit-stride columns (got {tuple(x.shape)})")
     ldx = x.stride(0) if T > 1 else C
     _chk(taps, "taps", torch.bfloat16, (C, CONV_K), dev)
