@@ -72,3 +72,36 @@ def test_prefill_repeatable(dev):
     a = run(dev, d, 300)
     b = run(dev, d, 300)
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_prefill_4485_tokens(dev):
+    """4485 tokens = 71 chunks, the last one of 5 tokens, against the WY oracle."""
+    d = W.prefill(4485, "cpu", seed=8)
+    o, S = run(dev, d, 4485)
+    o_ref, S_ref = ref(d, 4485, wy=True)
+    assert_state(S, S_ref.float())
+    assert_bf16_output(o, O.bf16(o_ref.float()))
+
+
+def test_prefill_graph_replays(dev):
+    """The prefill captured into a HIP graph, replayed three times with eager work in between: every replay
+    equals the eager result bit for bit."""
+    d = W.prefill(4485, "cpu", seed=9)
+    g = {k: v.to(dev) for k, v in d.items()}
+    ws = ops.workspace(("prefill-graph", 64), ops.lib().qs_gdn_chunk_prefill_workspace_bytes(4485, 16, 48, 128, 128, 64),
+                       dev)  # fmt: skip
+    eager = ops.chunk_gated_delta_rule(g["q"], g["k"], g["v"], g["g"], g["beta"], initial_state=g["S0"], ws=ws)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            out = ops.chunk_gated_delta_rule(g["q"], g["k"], g["v"], g["g"], g["beta"], initial_state=g["S0"], ws=ws)
+    torch.cuda.current_stream().wait_stream(s)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out[0], eager[0]) and torch.equal(out[1], eager[1])
+        g["q"].add_(0)  # eager work between the replays
+        torch.cuda.synchronize()
