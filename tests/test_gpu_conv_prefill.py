@@ -108,3 +108,19 @@ def test_prompt_then_decode_equals_token_by_token(dev):
     assert torch.equal(conv_state, conv_ref)
     assert_state(state, state_ref.cpu())
     assert_bf16_output(o, o_ref.cpu())
+
+
+def test_conv_prefill_other_head_counts(dev):
+    """2 key / 6 value heads (q, k 256 channels each, v 768): the q | k | v split follows the head counts;
+    outputs and carry equal 33 decode conv launches bit for bit."""
+    nk, nv, T = 2, 6, 33
+    Cs = 2 * nk * DK + nv * DV
+    gen = torch.Generator().manual_seed(77)
+    xp = W._randn((T, Cs + 16), gen, "cpu", torch.bfloat16).to(dev)
+    cs = W._randn((Cs, 3), gen, "cpu", torch.bfloat16).to(dev)
+    taps = W._randn((Cs, 4), gen, "cpu", torch.bfloat16, std=0.5).to(dev)
+    q, k, v, out = ops.causal_conv1d_prefill(xp[:, :Cs], taps, cs, nk=nk, nv=nv)
+    assert q.shape == (T, nk, DK) and v.shape == (T, nv, DV)
+    st = cs[None].clone()
+    ys = torch.cat([ops.causal_conv1d_update(xp[t : t + 1, :Cs].contiguous(), st, taps) for t in range(T)])
+    assert torch.equal(qkv_cat(q, k, v), ys) and torch.equal(out, st[0])
