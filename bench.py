@@ -1,35 +1,47 @@
 #!/usr/bin/env python
 """Decode-time state path of the hybrid Gated-DeltaNet / attention Qwen3.6-27B engine on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--workload step]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--workload all|step|gdn-layer|attn-layer|
+                     verify-step|prefill|conv-prefill] [--profile-family gdn|attn|conv|copy]
 
-Default workload (the headline): the batch-8 decode step at 4096 positions per user — 48 Gated-DeltaNet
-layers (conv1d update + L2-norm + gated delta rule on fp32 [8, 48, 128, 128] states, in place) and 16
-attention layers (append of one token's K/V into block-64 pages + paged GQA decode, 24 q heads / 4 KV heads
-x 256, over a shared 2048-page pool through per-user random block tables), replayed as one HIP graph.
-Inputs are seeded synthetic tensors already resident in HBM; the step moves 4,631,478,272 algorithmic bytes.
+Default (``--workload all``): one JSON line whose top level is the headline workload — the batch-8 decode
+step at 4096 positions per user: 48 Gated-DeltaNet layers (conv1d update + L2-norm + gated delta rule on
+fp32 [8, 48, 128, 128] states, in place) and 16 attention layers (append of one token's K/V into block-64
+pages + paged GQA decode, 24 q heads / 4 KV heads x 256, over a shared 2048-page pool through per-user
+random block tables), replayed as one HIP graph that also advances every user's position — and whose
+``configs`` key holds the other workloads, each with its own roofline and CPU baseline:
+  gdn-layer     one GDN layer, batch 1 (48 layers' distinct buffers rotate, 313 MB per loop)
+  attn-layer    one attention layer at 32768 positions, batch 1 (4 layers' distinct pools rotate)
+  verify-step   MTP verify at batch 1, 8192 positions, 4 tokens, 64 layers + acceptance by slot
+  prefill       chunked gated delta rule over 8192 tokens + the paged K/V fill
+  conv-prefill  the prompt conv with its carry over 8192 tokens (the prefill -> decode handoff)
+Inputs are seeded synthetic tensors resident in HBM before the timed region.
 
-Other workloads (one JSON line each): gdn-layer (one GDN layer, batch 1), attn-layer (one attention layer
-at 32768 positions, batch 1), verify-step (MTP verify at batch 1, 8192 positions, 4 tokens, 64 layers +
-rollback), prefill (chunked gated delta rule over 8192 tokens + the paged K/V fill), conv-prefill (the
-prompt conv with its carry over 8192 tokens).
+Timing: K timed replays (``--steps``) bracketed by synchronisation, each replay between its own pair of HIP
+events on the replay stream (the length rewind that keeps the context fixed runs between replays, outside
+the events); ``ms_per_step`` is their mean. A second pass of max(K, 200) replays gives the median, p10 and
+p90. SCLK, MCLK and power are sampled during it. value = algorithmic bytes / ms_per_step (GB/s).
+roofline = the dominant kernel's per-launch algorithmic bytes / its average launch time (HIP events around
+back-to-back launches on the stream they run on). cpu_baseline = the CPU oracle on a bounded sample of the
+same workload on the host's cores (and on one thread), median of >= 5 runs after one warm-up.
 
-value = algorithmic bytes / time (GB/s); roofline = the dominant kernel's per-launch algorithmic bytes /
-its average launch time (HIP events over back-to-back launches on the stream they run on); cpu_baseline =
-the CPU oracle timed on a bounded sample of the same workload (step workload only).
+``--profile-family`` launches one kernel family back to back (for rocprofv3 counter runs) and exits.
 """
 import argparse
 import ctypes
+import glob
 import json
 import os
 import statistics
 import sys
+import threading
 import time
 
 REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(REPO, "tt-qwen-resident_amd"))
 
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 METRIC = "decode-step state-path µs and achieved HBM GB/s (% of peak) at batch 1/8"
 
 
@@ -41,8 +53,83 @@ def _p(t):
     return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
 
 
-def graph_time(torch, fn, steps, warmup):
-    """ms per call of fn, replayed as a HIP graph: W untimed replays, then HIP events around K replays."""
+# ------------------------------------------------------------------------------------------------ telemetry
+
+
+class Telemetry:
+    """Samples the GPU's current SCLK / MCLK (pp_dpm_sclk / pp_dpm_mclk, the starred level) and power
+    (hwmon power1_average or power1_input) from sysfs every 20 ms while active."""
+
+    def __init__(self):
+        self.card = None
+        for c in sorted(glob.glob("/sys/class/drm/card*/device")):
+            if os.path.exists(os.path.join(c, "pp_dpm_sclk")):
+                self.card = c
+                break
+        self.samples = []
+        self._stop = threading.Event()
+        self._t = None
+
+    @staticmethod
+    def _dpm(path):
+        try:
+            with open(path) as f:
+                for line in f:
+                    if "*" in line:
+                        return float(line.split(":")[1].strip().rstrip("*").strip().lower().replace("mhz", ""))
+        except (OSError, ValueError, IndexError):
+            return None
+        return None
+
+    def _power(self):
+        for name in ("power1_average", "power1_input"):
+            for p in glob.glob(os.path.join(self.card, "hwmon", "hwmon*", name)):
+                try:
+                    with open(p) as f:
+                        return float(f.read()) / 1e6
+                except (OSError, ValueError):
+                    pass
+        return None
+
+    def sample(self):
+        if self.card is None:
+            return
+        self.samples.append((self._dpm(os.path.join(self.card, "pp_dpm_sclk")),
+                             self._dpm(os.path.join(self.card, "pp_dpm_mclk")), self._power()))  # fmt: skip
+
+    def __enter__(self):
+        self.samples = []
+        self._stop.clear()
+
+        def run():
+            while not self._stop.is_set():
+                self.sample()
+                time.sleep(0.02)
+
+        self._t = threading.Thread(target=run, daemon=True)
+        self._t.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        self._t.join()
+
+    def summary(self):
+        if self.card is None:
+            return dict(available=False)
+
+        def stats(i):
+            v = [s[i] for s in self.samples if s[i] is not None]
+            return dict(mean=round(statistics.mean(v), 1), max=round(max(v), 1)) if v else None
+
+        return dict(samples=len(self.samples), sclk_mhz=stats(0), mclk_mhz=stats(1), power_w=stats(2))
+
+
+# ------------------------------------------------------------------------------------------------ timing
+
+
+def capture(torch, fn):
+    """fn recorded into a HIP graph on a side stream (run once eagerly first, so every buffer exists)."""
     fn()
     torch.cuda.synchronize()
     s = torch.cuda.Stream()
@@ -52,22 +139,73 @@ def graph_time(torch, fn, steps, warmup):
         with torch.cuda.graph(g, stream=s):
             fn()
     torch.cuda.current_stream().wait_stream(s)
-    for _ in range(warmup):
-        g.replay()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
-        g.replay()
-    e1.record()
+    return g
+
+
+def capture_calls(torch, make_calls):
+    """C-ABI launches (pre-built argument tuples) recorded into a HIP graph on a side stream: make_calls(stream)
+    returns the (entry, args) list; the launches run once eagerly first."""
+    from qwen36_state._lib import lib
+
+    L = lib()
+    s = torch.cuda.Stream()
+    fns = [(getattr(L, name), args) for name, args in make_calls(ctypes.c_void_p(s.cuda_stream))]
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for f, a in fns:
+            assert f(*a) == 0, L.qs_last_error()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps, g
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for f, a in fns:
+            f(*a)
+    torch.cuda.synchronize()
+    return g
+
+
+def replay_times(torch, replay, n, between=None):
+    """Per-replay times (ms): each replay between its own pair of HIP events on the current stream (the
+    stream the graphs launch on); ``between`` (untimed) runs after each replay's end event. Synchronised on
+    both sides."""
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for e0, e1 in evs:
+        e0.record()
+        replay()
+        e1.record()
+        if between is not None:
+            between()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return [e0.elapsed_time(e1) for e0, e1 in evs], wall
+
+
+def timed(torch, args, replay, between=None, tel=None):
+    """W untimed replays, K timed replays (the contract's step count) and a statistics pass of max(K, 200)
+    replays with telemetry. Returns (ms mean over K, stats dict)."""
+    for _ in range(args.warmup):
+        replay()
+        if between is not None:
+            between()
+    ts, wall = replay_times(torch, replay, args.steps, between)
+    n = max(args.steps, 200)
+    if tel is not None:
+        with tel:
+            st, _ = replay_times(torch, replay, n, between)
+    else:
+        st, _ = replay_times(torch, replay, n, between)
+    q = statistics.quantiles(st, n=10)
+    stats = dict(replays=n, median_ms=round(statistics.median(st), 5), p10_ms=round(q[0], 5),
+                 p90_ms=round(q[-1], 5), timed_wall_s=round(wall, 4))  # fmt: skip
+    return statistics.mean(ts), stats
 
 
 def kernel_time(torch, make_calls, reps):
     """Average ms of one launch: reps x len(calls) back-to-back C-ABI launches (pre-built argument tuples)
-    captured into a HIP graph on a side stream, replayed once untimed and once between HIP events, so no
-    host work sits between the launches. make_calls(stream) returns the (entry point, args) list."""
+    captured into a HIP graph on a side stream, replayed once untimed and once between HIP events on that
+    stream, so no host work sits between the launches. make_calls(stream) returns the (entry, args) list."""
     from qwen36_state._lib import lib
 
     L = lib()
@@ -85,9 +223,10 @@ def kernel_time(torch, make_calls, reps):
     g.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    g.replay()
-    e1.record()
+    with torch.cuda.stream(s):
+        e0.record(s)
+        g.replay()
+        e1.record(s)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / (reps * len(fns))
 
@@ -102,92 +241,192 @@ def gdn_call(d, B, ws, stream, out):
     )  # fmt: skip
 
 
-def attn_call(d, B, T, pps, ws, stream, out):
+def attn_call(d, table, lens, B, T, pps, ws, stream, out):
     from qwen36_state.ops import HD, NKV, NQ
 
     return "qs_paged_gqa_decode", (
-        _p(d["q"]), _p(d["k_new"]), _p(d["v_new"]), _p(d["k_cache"]), _p(d["v_cache"]), _p(d["block_table"]),
-        _p(d["seq_lens"]), _p(out), _p(ws), B, T, NQ, NKV, HD, 64, d["block_table"].shape[1],
-        d["k_cache"].shape[0], pps, ctypes.c_float(d["scale"]), stream,
+        _p(d["q"]), _p(d["k_new"]), _p(d["v_new"]), _p(d["k_cache"]), _p(d["v_cache"]), _p(table), _p(lens),
+        _p(out), _p(ws), B, T, NQ, NKV, HD, 64, table.shape[1], d["k_cache"].shape[0], pps,
+        ctypes.c_float(d["scale"]), ctypes.c_void_p(0), stream,
     )  # fmt: skip
 
 
-def roofline(name, nbytes, ms):
+def roofline(name, nbytes, ms, traffic_key=None, flops=None):
     achieved = nbytes / (ms * 1e-3) / 1e9
     traffic = None
     tf = os.path.join(REPO, "profiles", "pmc_traffic.json")
     if os.path.exists(tf):
         with open(tf) as f:
-            traffic = json.load(f).get(name, {}).get("hbm_bytes_per_launch")
-    return dict(kernel=name, bound="hbm", achieved=round(achieved, 1), peak=PEAK_HBM_GBS, unit="GB/s",
-                frac=round(achieved / PEAK_HBM_GBS, 4), traffic=traffic, bytes_per_launch=nbytes,
-                us_per_launch=round(ms * 1e3, 2))  # fmt: skip
+            traffic = json.load(f).get(traffic_key or name, {}).get("hbm_bytes_per_launch")
+    out = dict(kernel=name, bound="hbm", achieved=round(achieved, 1), peak=PEAK_HBM_GBS, unit="GB/s",
+               frac=round(achieved / PEAK_HBM_GBS, 4), traffic=traffic, bytes_per_launch=nbytes,
+               us_per_launch=round(ms * 1e3, 2))  # fmt: skip
+    if flops is not None:
+        out["mfma"] = dict(tflops=round(flops / (ms * 1e-3) / 1e12, 1), peak=PEAK_BF16_TFLOPS,
+                           frac=round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4))  # fmt: skip
+    return out
 
 
-def line(args, workload, nbytes, ms, dom, extra=None):
+def entry(workload, nbytes, ms, stats, dom, extra=None):
     gbs = nbytes / (ms * 1e-3) / 1e9
-    out = dict(
-        metric=METRIC, value=round(gbs, 1), unit="GB/s", n_gpus=1, steps=args.steps, warmup=args.warmup,
-        ms_per_step=round(ms, 4), us_per_step=round(ms * 1e3, 1), frac_of_peak=round(gbs / PEAK_HBM_GBS, 4),
-        higher_is_better=True, scaling="weak", vs_baseline=None, dtype="fp32-state/bf16-kv", data="synthetic",
-        config=dict(workload=workload, bytes_per_step=nbytes), roofline=dom,
-    )  # fmt: skip
+    out = dict(value=round(gbs, 1), unit="GB/s", us_per_step=round(ms * 1e3, 2), frac_of_peak=round(gbs / PEAK_HBM_GBS, 4),
+               median_us=round(stats["median_ms"] * 1e3, 2), p10_us=round(stats["p10_ms"] * 1e3, 2),
+               p90_us=round(stats["p90_ms"] * 1e3, 2), replays=stats["replays"], workload=workload,
+               bytes_per_step=nbytes, roofline=dom)  # fmt: skip
     if extra:
         out.update(extra)
     return out
 
 
+# ------------------------------------------------------------------------------------------------ CPU baseline
+
+
+def cpu_threads():
+    try:
+        share = len(os.sched_getaffinity(0))
+    except AttributeError:
+        share = os.cpu_count() or 1
+    return max(1, min(share, 16))
+
+
+def cpu_time(torch, fn, reps=5):
+    """Median seconds of fn over reps runs after one warm-up, on the host's cores and on one thread."""
+    out = {}
+    for threads in (cpu_threads(), 1):
+        torch.set_num_threads(threads)
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        out[threads] = statistics.median(ts)
+    torch.set_num_threads(cpu_threads())
+    return out
+
+
+def cpu_entry(torch, nbytes, t, unit_note, reps=5):
+    """cpu_baseline dict from {threads: seconds per unit of work} scaled to the workload's bytes."""
+    n = cpu_threads()
+    return dict(value=round(nbytes / t[n] / 1e9, 3), unit="GB/s", cores=n, kind="port",
+                os_cpu_count=os.cpu_count(), torch_threads=n, one_thread_value=round(nbytes / t[1] / 1e9, 3),
+                ms=round(t[n] * 1e3, 2), one_thread_ms=round(t[1] * 1e3, 2), sample=unit_note + f" (median of {reps} "
+                "after a warm-up)")  # fmt: skip
+
+
+def _oracle():
+    sys.path.insert(0, REPO)
+    from oracle import state_path as O
+
+    return O
+
+
+def cpu_step(torch, step):
+    """2 GDN + 1 attention layers of the batch-8 step at the real shapes, scaled to 48 + 16 layers."""
+    O = _oracle()
+    from qwen36_state.ops import DK, DV, NK, NV
+
+    gl, al = step.gdn_layers(), step.attn_layers()
+    gdn = [{k: v.cpu() for k, v in step.layer[l].items() if torch.is_tensor(v)} for l in gl[:2]]
+    a = {k: v.cpu() for k, v in step.layer[al[0]].items() if torch.is_tensor(v)}
+    table, lens = step.block_table.cpu(), step.lens.cpu() + 1
+    scale = step.layer[al[0]]["scale"]
+
+    def run():
+        for d in gdn:
+            O.gdn_decode(d["x"].float(), d["conv_state"].float(), d["taps"].float(), d["g"], d["beta"], d["state"],
+                         NK, NV, DK, DV)  # fmt: skip
+        O.paged_append(a["k_cache"], a["v_cache"], a["k_new"], a["v_new"], table, lens - 1)
+        O.gqa_decode(a["q"], a["k_cache"], a["v_cache"], table, lens, scale)
+
+    t = cpu_time(torch, run)
+    # per step: 24 x (2 GDN layers) + 16 x (1 attention layer), the GDN / attention split measured separately
+    t_g = cpu_time(torch, lambda: [O.gdn_decode(d["x"].float(), d["conv_state"].float(), d["taps"].float(), d["g"],
+                                                d["beta"], d["state"], NK, NV, DK, DV) for d in gdn])  # fmt: skip
+    scaled = {n: len(gl) / 2 * t_g[n] + len(al) * (t[n] - t_g[n]) for n in t}
+    return cpu_entry(torch, step.bytes_per_step(), scaled,
+                     f"2 GDN + 1 attention layers of the batch-{step.B} step at {step.ctx} positions, scaled to "
+                     f"{len(gl)} + {len(al)} layers")  # fmt: skip
+
+
 # ------------------------------------------------------------------------------------------------ workloads
 
 
-def bench_step(args, torch):
+def bench_step(args, torch, tel):
     from qwen36_state.decode import StatePathStep, layer_bytes
 
     log(f"building the {args.layers}-layer step: batch {args.batch}, {args.ctx} positions")
-    step = StatePathStep(args.batch, args.ctx, args.layers, device="cuda:0", pages_per_split=args.pps)
+    step = StatePathStep.synthetic(args.batch, args.ctx, args.layers, device="cuda:0", pages_per_split=args.pps)
     gl, al = step.gdn_layers(), step.attn_layers()
-    ms, _ = graph_time(torch, step.step, args.steps, args.warmup)
+    step.step()
+    step.rewind()
+    g = step.capture()
+    ms, stats = timed(torch, args, g.replay, between=step.rewind, tel=tel)
     nbytes = step.bytes_per_step()
-    log(f"step: {ms * 1e3:.1f} µs, {nbytes / ms / 1e6:.0f} GB/s")
+    log(f"step: {ms * 1e3:.1f} µs mean, {stats['median_ms'] * 1e3:.1f} µs median, {nbytes / ms / 1e6:.0f} GB/s")
+    lens1 = step.lens + 1  # the lengths the step's attention layers see
     t_gdn = kernel_time(torch, lambda st: [gdn_call(step.layer[l], step.B, step.gdn_ws, st, step.layer[l]["o"])
                                            for l in gl], args.kernel_reps)  # fmt: skip
-    t_att = kernel_time(torch, lambda st: [attn_call(step.layer[l], step.B, 1, step.pps, step.attn_ws, st,
-                                                     step.layer[l]["o"]) for l in al], args.kernel_reps)  # fmt: skip
+    t_att = kernel_time(torch, lambda st: [attn_call(step.layer[l], step.block_table, lens1, step.B, 1, step.pps,
+                                                     step.attn_ws, st, step.layer[l]["o"]) for l in al],
+                        args.kernel_reps)  # fmt: skip
     b_gdn, b_att = layer_bytes(args.batch, args.ctx), layer_bytes(args.batch, args.ctx, attn=True)
     kern = {"gdn_decode_fused": (t_gdn, b_gdn, len(gl)), "paged_gqa_decode": (t_att, b_att, len(al))}
     for k, (t, b, n) in kern.items():
         log(f"{k}: {t * 1e3:.2f} µs per launch, {b / t / 1e6:.0f} GB/s, {n} launches per step")
     dom = max(kern, key=lambda k: kern[k][0] * kern[k][2])
-    out = line(args, f"decode-step state path: {len(gl)} GDN + {len(al)} paged-attention layers, batch "
-               f"{args.batch}, {args.ctx} positions per user, block 64, HIP-graph replay", nbytes, ms,
-               roofline(dom, kern[dom][1], kern[dom][0]),
-               dict(kernels={k: dict(us_per_launch=round(t * 1e3, 2), bytes_per_launch=b,
-                                     gbs=round(b / t / 1e6, 1), launches_per_step=n) for k, (t, b, n) in kern.items()}))  # fmt: skip
-    out["config"].update(batch=args.batch, context=args.ctx, layers=args.layers, pages_per_split=args.pps)
+    work = (f"decode-step state path: {len(gl)} GDN + {len(al)} paged-attention layers, batch {args.batch}, "
+            f"{args.ctx} positions per user, block 64, HIP-graph replay with the position advance")  # fmt: skip
+    out = entry(work, nbytes, ms, stats, roofline(dom, kern[dom][1], kern[dom][0]),
+                dict(kernels={k: dict(us_per_launch=round(t * 1e3, 2), bytes_per_launch=b, gbs=round(b / t / 1e6, 1),
+                                      launches_per_step=n) for k, (t, b, n) in kern.items()}))  # fmt: skip
+    out.update(batch=args.batch, context=args.ctx, layers=args.layers, pages_per_split=args.pps)
     if not args.no_cpu:
         log("timing the CPU oracle on a sample of the step")
-        out["cpu_baseline"] = cpu_baseline(step, torch)
+        out["cpu_baseline"] = cpu_step(torch, step)
+    del step, g
+    torch.cuda.empty_cache()
     return out
 
 
-def bench_gdn_layer(args, torch):
-    """One GDN layer at batch 1; the timed loop walks 48 layers' distinct buffers (313 MB, more than the
-    256 MB Infinity Cache) so every launch reads its state from HBM."""
+def bench_gdn_layer(args, torch, tel):
+    """One GDN layer at batch 1; the graph walks 48 layers' distinct buffers (313 MB, more than the 256 MB
+    Infinity Cache) 4 times, so every launch reads its state from HBM; per launch = replay / 192."""
     from qwen36_state import ops, workloads as W
     from qwen36_state.decode import layer_bytes
 
     layers = [W.gdn_layer(1, "cuda:0", seed=i) for i in range(48)]
     outs = [torch.empty(1, 48, 128, dtype=torch.bfloat16, device="cuda:0") for _ in layers]
-    ws = ops.workspace("bench-gdn", ops.lib().qs_gdn_workspace_bytes(1, 16), "cuda:0")
-    ms = kernel_time(torch, lambda st: [gdn_call(d, 1, ws, st, o) for d, o in zip(layers, outs)], args.kernel_reps)
+    ws = torch.zeros(ops.lib().qs_gdn_workspace_bytes(1, 16), dtype=torch.uint8, device="cuda:0")
+
+    R = 4  # passes over the 48 layers per replay, so the graph's start-up is spread over 192 launches
+
+    def fn():
+        for _ in range(R):
+            for d, o in zip(layers, outs):
+                ops.gdn_decode_fused(d["x"], d["conv_state"], d["taps"], d["g"], d["beta"], d["state"], out=o, ws=ws)
+
+    g = capture(torch, fn)
+    msr, stats = timed(torch, args, g.replay, tel=tel)
+    ms = msr / (48 * R)
+    stats = {k: (v / (48 * R) if k.endswith("_ms") else v) for k, v in stats.items()}
     nbytes = layer_bytes(1, 0)
-    return line(args, "one GDN layer decode, batch 1: conv1d update (10240 channels) + L2-norm + gated delta "
-                "rule on fp32 [1, 48, 128, 128]", nbytes, ms, roofline("gdn_decode_fused", nbytes, ms))
+    out = entry("one GDN layer decode, batch 1: conv1d update (10240 channels) + L2-norm + gated delta rule on fp32 "
+                "[1, 48, 128, 128] (48 layers' buffers rotate)", nbytes, ms, stats,
+                roofline("gdn_decode_fused", nbytes, ms, "gdn_decode_fused_b1"))  # fmt: skip
+    if not args.no_cpu:
+        O = _oracle()
+        c = {k: v.cpu() for k, v in layers[0].items()}
+        t = cpu_time(torch, lambda: O.gdn_decode(c["x"].float(), c["conv_state"].float(), c["taps"].float(), c["g"],
+                                                 c["beta"], c["state"], 16, 48, 128, 128))  # fmt: skip
+        out["cpu_baseline"] = cpu_entry(torch, nbytes, t, "one GDN layer at batch 1")
+    return out
 
 
-def bench_attn_layer(args, torch):
+def bench_attn_layer(args, torch, tel):
     """One attention layer at 32768 positions, batch 1; 4 layers with their own pools rotate (each launch
-    reads 134 MB of pages that no other launch in the loop touches)."""
+    reads 134 MB of pages that no other launch in the loop touches), 10 times per replay; per launch =
+    replay / 40."""
     from qwen36_state import ops, workloads as W
     from qwen36_state.decode import layer_bytes
 
@@ -195,60 +434,118 @@ def bench_attn_layer(args, torch):
     layers = [W.attn_layer(1, 32768, "cuda:0", seed=i) for i in range(4)]
     outs = [torch.empty(1, 1, 24, 256, dtype=torch.bfloat16, device="cuda:0") for _ in layers]
     ws = ops.attention_workspace(1, 1, 24, 4, 512, pps, "cuda:0")
-    ms = kernel_time(torch, lambda st: [attn_call(d, 1, 1, pps, ws, st, o) for d, o in zip(layers, outs)],
-                     args.kernel_reps)  # fmt: skip
-    nbytes = layer_bytes(1, 32768, attn=True)
-    return line(args, f"one attention layer decode, batch 1, 32768 positions: append + paged GQA (24/4 heads x "
-                f"256, block 64, 512 random pages of 2048), split {pps} pages + merge", nbytes, ms,
-                roofline("paged_gqa_decode", nbytes, ms), dict(pages_per_split=pps))  # fmt: skip
 
-
-def bench_verify(args, torch):
-    """The MTP verify step with acceptance by slot selection: the graph holds two consecutive steps (the
-    two snapshot sets alternate), each with its KV lengths restored for the replay; time per step = half."""
-    from qwen36_state.decode import VerifyStep
-
-    vs = VerifyStep(1, 8192, T=4, device="cuda:0", pages_per_split=args.pps_verify)
+    R = 10  # passes over the 4 layers per replay, so the graph's start-up is spread over 40 launches
 
     def fn():
-        for _ in range(2):
-            vs.verify()
-            vs.rollback()
-            vs.reset_lengths()
+        for _ in range(R):
+            for d, o in zip(layers, outs):
+                ops.paged_gqa_decode(d["q"], d["k_cache"], d["v_cache"], d["block_table"], d["seq_lens"], d["scale"],
+                                     k_new=d["k_new"], v_new=d["v_new"], pages_per_split=pps, out=o, ws=ws)  # fmt: skip
 
-    ms2, _ = graph_time(torch, fn, args.steps, args.warmup)
-    ms = ms2 / 2
-    nbytes = vs.bytes_per_step()
-    return line(args, "MTP verify step, batch 1, 8192 positions, 1 + 3 draft tokens through 48 GDN + 16 attention "
-                "layers, then acceptance of a seeded length by snapshot-slot selection", nbytes, ms,
+    g = capture(torch, fn)
+    msr, stats = timed(torch, args, g.replay, tel=tel)
+    ms = msr / (4 * R)
+    stats = {k: (v / (4 * R) if k.endswith("_ms") else v) for k, v in stats.items()}
+    nbytes = layer_bytes(1, 32768, attn=True)
+    out = entry(f"one attention layer decode, batch 1, 32768 positions: append + paged GQA (24/4 heads x 256, block "
+                f"64, 512 random pages of 2048), {pps} pages per split", nbytes, ms, stats,
+                roofline("paged_gqa_decode", nbytes, ms, "paged_gqa_decode_b1_32k"), dict(pages_per_split=pps))  # fmt: skip
+    if not args.no_cpu:
+        O = _oracle()
+        c = {k: (v.cpu() if torch.is_tensor(v) else v) for k, v in layers[0].items()}
+
+        def run():
+            O.paged_append(c["k_cache"], c["v_cache"], c["k_new"], c["v_new"], c["block_table"], c["seq_lens"] - 1)
+            O.gqa_decode(c["q"], c["k_cache"], c["v_cache"], c["block_table"], c["seq_lens"], c["scale"])
+
+        out["cpu_baseline"] = cpu_entry(torch, nbytes, cpu_time(torch, run), "one attention layer at 32768 positions")
+    return out
+
+
+def bench_verify(args, torch, tel):
+    """The MTP verify step with acceptance by slot selection; the lengths are set back to the rows cached
+    before the step between replays (outside the timed events), so every replay verifies at 8192."""
+    from qwen36_state.decode import VerifyStep
+
+    vs = VerifyStep.synthetic(1, 8192, T=4, device="cuda:0", pages_per_split=args.pps_verify)
+    vs.step()
+    vs.rewind()
+    vs.capture()
+    ms, stats = timed(torch, args, vs.replay, between=vs.rewind, tel=tel)
+    nbytes = vs.bytes_per_step(8192)
+    out = entry("MTP verify step, batch 1, 8192 positions, 1 + 3 draft tokens through 48 GDN + 16 attention layers, "
+                "then acceptance of a seeded length by snapshot-slot selection", nbytes, ms, stats,
                 roofline("verify_step", nbytes, ms),
                 dict(rollback_copy_bytes=vs.rollback_bytes(), accept=vs.accept.tolist(), pages_per_split=vs.pps))  # fmt: skip
+    if not args.no_cpu:
+        O = _oracle()
+        gl = next(d for d in vs.layer if not d["attn"])
+        al = next(d for d in vs.layer if d["attn"])
+        c = {k: v.cpu() for k, v in gl.items() if torch.is_tensor(v)}
+        S0, cs0 = (t.cpu() for t in vs.state_of(gl["gi"], 0))
+        a = {k: v.cpu() for k, v in al.items() if torch.is_tensor(v)}
+        table, lens = vs.block_table.cpu(), vs.base.cpu() + 4
+
+        def run_g():
+            O.gdn_verify(c["x"].float(), cs0[None].float(), c["taps"].float(), c["g"], c["beta"], S0[None], 16, 48,
+                         128, 128)  # fmt: skip
+
+        def run_a():
+            O.paged_append(a["k_cache"], a["v_cache"], a["k_new"], a["v_new"], table, lens - 4)
+            O.gqa_decode(a["q"], a["k_cache"], a["v_cache"], table, lens, al["scale"])
+
+        tg, ta = cpu_time(torch, run_g), cpu_time(torch, run_a)
+        out["cpu_baseline"] = cpu_entry(torch, nbytes, {n: 48 * tg[n] + 16 * ta[n] for n in tg},
+                                        "1 GDN verify layer + 1 attention layer (T 4, 8192 positions), scaled to "
+                                        "48 + 16 layers")  # fmt: skip
+    del vs
+    torch.cuda.empty_cache()
+    return out
 
 
-def bench_prefill(args, torch):
+PREFILL_BYTES = 344982016
+PREFILL_FLOPS = 71.94e9
+
+
+def bench_prefill(args, torch, tel):
     from qwen36_state import ops, workloads as W
 
     d = W.prefill(8192, "cuda:0", seed=0)
     kc = torch.zeros(2048, 4, 64, 256, dtype=torch.bfloat16, device="cuda:0")
     vc = torch.zeros_like(kc)
     nbytes_ws = ops.lib().qs_gdn_chunk_prefill_workspace_bytes(8192, 16, 48, 128, 128, 64)
-    ws = ops.workspace(("bench-prefill", 64), nbytes_ws, "cuda:0")
+    ws = torch.zeros(nbytes_ws, dtype=torch.uint8, device="cuda:0")
+    S = torch.empty_like(d["S0"])
 
     def fn():
-        ops.chunk_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"], initial_state=d["S0"], ws=ws)
+        ops.chunk_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"], initial_state=d["S0"], ws=ws,
+                                   final_state=S)  # fmt: skip
         ops.paged_kv_fill(d["kv_k"], d["kv_v"], kc, vc, d["page_table"])
 
-    ms, _ = graph_time(torch, fn, max(3, args.steps // 10), 1)
-    nbytes = 344982016
-    return line(args, "chunked-prefill gated delta rule, 8192 tokens, chunk 64, 16/48 heads x 128 (WY form, bf16 "
-                "MFMA, fp32 state) + paged fill of 8192 tokens of K/V (4 x 256) into 128 random pages", nbytes, ms,
-                roofline("gdn_chunk_prefill", nbytes, ms), dict(flops=71.94e9, tflops=round(71.94e9 / ms / 1e9, 1)))
+    g = capture(torch, fn)
+    a2 = argparse.Namespace(**{**vars(args), "steps": max(3, args.steps // 5), "warmup": 2})
+    ms, stats = timed(torch, a2, g.replay, tel=tel)
+    out = entry("chunked-prefill gated delta rule, 8192 tokens, chunk 64, 16/48 heads x 128 (WY form, bf16 MFMA, fp32 "
+                "state) + paged fill of 8192 tokens of K/V (4 x 256) into 128 random pages", PREFILL_BYTES, ms, stats,
+                roofline("gdn_chunk_prefill", PREFILL_BYTES, ms, flops=PREFILL_FLOPS),
+                dict(flops=PREFILL_FLOPS, tflops=round(PREFILL_FLOPS / ms / 1e9, 1)))  # fmt: skip
+    if not args.no_cpu:
+        O = _oracle()
+        n = 1024
+        c = {k: v[:n].cpu() for k, v in d.items() if k in ("q", "k", "v", "g", "beta")}
+        S0 = d["S0"].cpu()
+        t = cpu_time(torch, lambda: O.gdn_chunk_prefill_wy(c["q"], c["k"], c["v"], c["g"], c["beta"], S0, 64))
+        out["cpu_baseline"] = cpu_entry(torch, PREFILL_BYTES, {k: v * 8192 / n for k, v in t.items()},
+                                        f"the chunked form on the first {n} of 8192 tokens, scaled by 8 (K/V fill not "
+                                        "timed)")  # fmt: skip
+    return out
 
 
-def bench_conv_prefill(args, torch):
+def bench_conv_prefill(args, torch, tel):
     """The prompt conv with its carry over 8192 tokens of the 10240 q | k | v channels, read from a
     projection output with 128 further columns; two prompts rotate (1.3 GB per loop) so each launch reads
-    and writes HBM rather than the Infinity Cache."""
+    and writes HBM rather than the Infinity Cache, 5 times per replay; per launch = replay / 10."""
     from qwen36_state import ops, workloads as W
 
     T, C, ldx = 8192, W.C_QKV, W.C_QKV + 128
@@ -256,68 +553,48 @@ def bench_conv_prefill(args, torch):
     bufs = []
     for i in range(2):
         gen = W._gen("cuda:0", i)
-        bufs.append(dict(
-            x=W._randn((T, ldx), gen, "cuda:0", torch.bfloat16),
-            taps=W._randn((C, 4), gen, "cuda:0", torch.bfloat16, std=0.5),
-            cs=W._randn((C, 3), gen, "cuda:0", torch.bfloat16),
-            q=torch.empty(T, CQ, dtype=torch.bfloat16, device="cuda:0"),
-            k=torch.empty(T, CQ, dtype=torch.bfloat16, device="cuda:0"),
-            v=torch.empty(T, CV, dtype=torch.bfloat16, device="cuda:0"),
-            out=torch.empty(C, 3, dtype=torch.bfloat16, device="cuda:0"),
-        ))  # fmt: skip
+        bufs.append(dict(x=W._randn((T, ldx), gen, "cuda:0", torch.bfloat16),
+                         taps=W._randn((C, 4), gen, "cuda:0", torch.bfloat16, std=0.5),
+                         cs=W._randn((C, 3), gen, "cuda:0", torch.bfloat16),
+                         q=torch.empty(T, CQ, dtype=torch.bfloat16, device="cuda:0"),
+                         k=torch.empty(T, CQ, dtype=torch.bfloat16, device="cuda:0"),
+                         v=torch.empty(T, CV, dtype=torch.bfloat16, device="cuda:0"),
+                         out=torch.empty(C, 3, dtype=torch.bfloat16, device="cuda:0")))  # fmt: skip
+    R = 5  # passes over the two prompts per replay
 
     def calls(st):
         return [("qs_conv1d_prefill", (_p(b["x"]), ldx, _p(b["cs"]), _p(b["taps"]), _p(b["q"]), _p(b["k"]),
-                                       _p(b["v"]), _p(b["out"]), T, CQ, CV, 4, st)) for b in bufs]  # fmt: skip
+                                       _p(b["v"]), _p(b["out"]), T, CQ, CV, 4, st)) for b in bufs] * R  # fmt: skip
 
-    ms = kernel_time(torch, calls, args.kernel_reps)
+    g = capture_calls(torch, calls)
+    msr, stats = timed(torch, args, g.replay, tel=tel)
+    ms = msr / (2 * R)
+    stats = {k: (v / (2 * R) if k.endswith("_ms") else v) for k, v in stats.items()}
     nbytes = 2 * T * C * 2 + C * 4 * 2 + 2 * C * 3 * 2  # x in, q | k | v out, taps, carry in and out
-    return line(args, "prompt conv1d + SiLU with carry, 8192 tokens x 10240 channels (q | k | v of a 10368-column "
-                "projection), conv state handed to the decode", nbytes, ms, roofline("conv1d_prefill", nbytes, ms))
+    out = entry("prompt conv1d + SiLU with carry, 8192 tokens x 10240 channels (q | k | v of a 10368-column "
+                "projection), conv state handed to the decode", nbytes, ms, stats,
+                roofline("conv1d_prefill", nbytes, ms))  # fmt: skip
+    if not args.no_cpu:
+        O = _oracle()
+        x = bufs[0]["x"][:1024, :C].cpu()
+        taps, cs = bufs[0]["taps"].cpu(), bufs[0]["cs"].cpu()
+        t = cpu_time(torch, lambda: O.conv1d_prefill(x.float(), cs.float(), taps.float()))
+        out["cpu_baseline"] = cpu_entry(torch, nbytes, {k: v * 8 for k, v in t.items()},
+                                        "the first 1024 of 8192 tokens, scaled by 8")  # fmt: skip
+    return out
 
 
-def cpu_baseline(step, torch, n_gdn=2, n_attn=1, reps=3):
-    """The CPU oracle on a bounded sample of the step (n_gdn GDN + n_attn attention layers at the real
-    shapes), scaled to the full step by layer count; median of reps after one warm-up."""
-    sys.path.insert(0, REPO)
-    from oracle import state_path as O
-    from qwen36_state.ops import DK, DV, NK, NV
-
-    gl, al = step.gdn_layers(), step.attn_layers()
-    gdn = [{k: v.cpu() for k, v in step.layer[l].items() if torch.is_tensor(v)} for l in gl[:n_gdn]]
-    att = [{k: v.cpu() for k, v in step.layer[l].items() if torch.is_tensor(v)} for l in al[:n_attn]]
-    scale = step.layer[al[0]]["scale"]
-
-    def run_gdn(d):
-        O.gdn_decode(d["x"].float(), d["conv_state"].float(), d["taps"].float(), d["g"], d["beta"], d["state"],
-                     NK, NV, DK, DV)  # fmt: skip
-
-    def run_attn(d):
-        kc, vc = d["k_cache"], d["v_cache"]
-        O.paged_append(kc, vc, d["k_new"], d["v_new"], d["block_table"], d["seq_lens"] - 1)
-        O.gqa_decode(d["q"], kc, vc, d["block_table"], d["seq_lens"], scale)
-
-    def timed(fn, ds):
-        fn(ds[0])
-        ts = []
-        for _ in range(reps):
-            t0 = time.perf_counter()
-            for d in ds:
-                fn(d)
-            ts.append((time.perf_counter() - t0) / len(ds))
-        return statistics.median(ts)
-
-    tg, ta = timed(run_gdn, gdn), timed(run_attn, att)
-    t_step = len(gl) * tg + len(al) * ta
-    return dict(
-        value=round(step.bytes_per_step() / t_step / 1e9, 3),
-        unit="GB/s",
-        cores=torch.get_num_threads(),
-        kind="port",
-        sample=f"{n_gdn} GDN + {n_attn} attention layers of the batch-{step.B} step at {step.ctx} positions "
-        f"(median of {reps}), scaled to {len(gl)} + {len(al)} layers: {t_step * 1e3:.1f} ms per step "
-        f"(GDN layer {tg * 1e3:.1f} ms, attention layer {ta * 1e3:.1f} ms)",
-    )
+def copy_ceiling(torch):
+    """Device-to-device copy of 1 GiB (torch's copy kernel): GB/s counting the read and the write."""
+    src = torch.ones(1 << 28, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    g = capture(torch, lambda: dst.copy_(src))
+    ts, _ = replay_times(torch, g.replay, 20)
+    ms = statistics.median(ts)
+    del src, dst, g
+    torch.cuda.empty_cache()
+    return dict(kernel="torch copy_ of 1 GiB", gbs=round(2 * (1 << 30) / (ms * 1e-3) / 1e9, 1),
+                frac_of_peak=round(2 * (1 << 30) / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4))  # fmt: skip
 
 
 WORKLOADS = {
@@ -328,6 +605,58 @@ WORKLOADS = {
     "prefill": bench_prefill,
     "conv-prefill": bench_conv_prefill,
 }
+CONFIG_OF = {"gdn-layer": 0, "attn-layer": 1, "step": 2, "verify-step": 3, "prefill": 4, "conv-prefill": "f2"}
+
+
+# ------------------------------------------------------------------------------------------------ profiling
+
+
+def profile_family(args, torch):
+    """One kernel family back to back over distinct per-layer buffers (so the dispatches read HBM, not the
+    Infinity Cache), for rocprofv3 counter runs; prints the algorithmic bytes of one dispatch."""
+    from qwen36_state import ops, workloads as W
+    from qwen36_state.decode import layer_bytes
+
+    dev = "cuda:0"
+    fam = args.profile_family
+    if fam == "copy":
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.reps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"copy: {src.numel() * 4} bytes read and written per dispatch")
+    elif fam == "conv":
+        C = W.C_QKV
+        bufs = [(W._randn((8192, C + 128), W._gen(dev, i), dev, torch.bfloat16),
+                 W._randn((C, 4), W._gen(dev, 10 + i), dev, torch.bfloat16),
+                 W._randn((C, 3), W._gen(dev, 20 + i), dev, torch.bfloat16)) for i in range(2)]  # fmt: skip
+        for _ in range(args.reps):
+            for x, taps, cs in bufs:
+                ops.causal_conv1d_prefill(x[:, :C], taps, cs)
+        torch.cuda.synchronize()
+        print(f"conv1d_prefill: {2 * 8192 * C * 2 + C * 8 + C * 12} algorithmic bytes per dispatch")
+    elif fam == "gdn":
+        layers = [W.gdn_layer(8, dev, seed=i) for i in range(48)]
+        for _ in range(args.reps):
+            for d in layers:
+                ops.gdn_decode_fused(d["x"], d["conv_state"], d["taps"], d["g"], d["beta"], d["state"])
+        torch.cuda.synchronize()
+        print(f"gdn_decode_fused: {layer_bytes(8, 4096)} algorithmic bytes per dispatch")
+    elif fam == "attn":
+        layers = [W.attn_layer(8, 4096, dev, seed=i) for i in range(16)]
+        for _ in range(args.reps):
+            for d in layers:
+                ops.paged_gqa_decode(d["q"], d["k_cache"], d["v_cache"], d["block_table"], d["seq_lens"], d["scale"],
+                                     k_new=d["k_new"], v_new=d["v_new"], pages_per_split=args.pps)  # fmt: skip
+        torch.cuda.synchronize()
+        print(f"paged_gqa_decode: {layer_bytes(8, 4096, attn=True)} algorithmic bytes per dispatch")
+    elif fam == "prefill":
+        d = W.prefill(8192, dev, seed=0)
+        for _ in range(args.reps):
+            ops.chunk_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"], initial_state=d["S0"])
+        torch.cuda.synchronize()
+        print(f"chunk prefill: {PREFILL_BYTES} algorithmic bytes (with the K/V fill) per prefill")
 
 
 def main():
@@ -335,7 +664,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="step")
+    ap.add_argument("--workload", choices=["all"] + sorted(WORKLOADS), default="all")
     ap.add_argument("--batch", type=int, default=8)
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--layers", type=int, default=64)
@@ -343,7 +672,9 @@ def main():
     ap.add_argument("--pps-attn1", type=int, default=4, help="pages per split (attn-layer workload)")
     ap.add_argument("--pps-verify", type=int, default=2, help="pages per split (verify-step workload)")
     ap.add_argument("--kernel-reps", type=int, default=10)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baselines")
+    ap.add_argument("--profile-family", choices=["gdn", "attn", "conv", "copy", "prefill"], default=None)
+    ap.add_argument("--reps", type=int, default=3, help="repetitions of --profile-family")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -355,7 +686,39 @@ def main():
         print("bench.py needs an MI355X", file=sys.stderr)
         sys.exit(2)
     torch.cuda.set_device(0)
-    out = WORKLOADS[args.workload](args, torch)
+    torch.set_num_threads(cpu_threads())
+    if args.profile_family:
+        profile_family(args, torch)
+        return
+    tel = Telemetry()
+    main_wl = "step" if args.workload == "all" else args.workload
+    head = WORKLOADS[main_wl](args, torch, tel)
+    head_tel = tel.summary()
+    configs = {}
+    if args.workload == "all":
+        for wl in ("gdn-layer", "attn-layer", "verify-step", "prefill", "conv-prefill"):
+            log(f"workload {wl}")
+            configs[wl] = WORKLOADS[wl](args, torch, tel)
+            configs[wl]["config"] = CONFIG_OF[wl]
+            configs[wl]["telemetry"] = tel.summary()
+            log(f"{wl}: {configs[wl]['us_per_step']} µs, {configs[wl]['value']} GB/s")
+    ceiling = copy_ceiling(torch)
+    ms = head["us_per_step"] / 1e3
+    out = dict(
+        metric=METRIC, value=head["value"], unit="GB/s", n_gpus=1, steps=args.steps, warmup=args.warmup,
+        ms_per_step=round(ms, 4), us_per_step=head["us_per_step"], frac_of_peak=head["frac_of_peak"],
+        higher_is_better=True, scaling="weak", vs_baseline=None, dtype="fp32-state/bf16-kv", data="synthetic",
+        config=dict(workload=head["workload"], config_index=CONFIG_OF[main_wl], bytes_per_step=head["bytes_per_step"],
+                    **{k: head[k] for k in ("batch", "context", "layers", "pages_per_split") if k in head}),
+        roofline=head["roofline"],
+        stats=dict(median_us=head["median_us"], p10_us=head["p10_us"], p90_us=head["p90_us"], replays=head["replays"]),
+        telemetry=head_tel, copy_ceiling=ceiling,
+    )  # fmt: skip
+    for k in ("kernels", "cpu_baseline"):
+        if k in head:
+            out[k] = head[k]
+    if configs:
+        out["configs"] = configs
     print(json.dumps(out), flush=True)
 
 

@@ -39,6 +39,15 @@ extern "C" {
 #define QS_EINVAL (-1)
 #define QS_EHIP (-2)
 
+/* Bits of the optional device status word (int32, caller-owned, zeroed by the caller; kernels OR bits into
+ * it and never clear it). Entry points that read lengths, positions, block-table entries or accept lengths
+ * from device memory take a nullable `int *status`: with it, an invalid value is reported there (the host
+ * reads the word after the step, as the reference's asserts stop a bad step, generator_vllm.py:94); with or
+ * without it the kernel handles the value in the documented, bounded way and exits normally. */
+#define QS_STATUS_LENGTH 1 /* a length or position past the block table (max_blocks * block rows) */
+#define QS_STATUS_PAGE 2   /* a block-table entry needed for a valid position outside [0, num_blocks) */
+#define QS_STATUS_ACCEPT 4 /* an accept length outside [1, T] */
+
 /* ABI version (bumped when a signature changes) and the last error message of the calling thread. */
 int qs_abi_version(void);
 const char *qs_last_error(void);
@@ -112,10 +121,10 @@ int qs_gdn_verify_step_slots(const uint16_t *x, const uint16_t *conv_states_in, 
 
 /* Acceptance without copies: slot[b] <- accept_len[b] - 1 (the snapshot the next verify step reads) and,
  * when seq_lens is non-null, seq_lens[b] <- base_lens[b] + accept_len[b] (the KV truncation), for
- * accept_len[b] in [1, T]. Replaces the hub's slot/ring advance (kernels/mlp_hub.cpp:48-58;
- * model.py:1314-1318). */
+ * accept_len[b] in [1, T]; a user with another accept length is left untouched and reported
+ * (QS_STATUS_ACCEPT). Replaces the hub's slot/ring advance (kernels/mlp_hub.cpp:48-58; model.py:1314-1318). */
 int qs_verify_accept(const int *accept_len, int *slot, int *seq_lens, const int *base_lens, int B, int T,
-                     void *stream);
+                     int *status, void *stream);
 
 /* Rollback after verify: state[b] <- states_out[accept_len[b]-1, b], conv_state[b] <- conv_states_out[...]
  * (bit-exact copies), and, when seq_lens is non-null, seq_lens[b] <- base_lens[b] + accept_len[b] (the KV
@@ -138,11 +147,22 @@ int qs_gdn_rollback_layers(const float *states_out, size_t states_out_layer_stri
 /* ---------------------------------------------------------------------------------------- a5: paged append
  * Write T new K and V rows per user at positions positions[b] + t into the paged pools (bit-exact).
  *   k, v [B, T, NKV, HD] bf16; pools [num_blocks, NKV, block, HD]; block_table [B, max_blocks]; positions [B].
+ * A negative position marks an idle slot (nothing written); a row past the table (QS_STATUS_LENGTH) or on
+ * an entry outside the pool (QS_STATUS_PAGE) is skipped and reported.
  * Replaces the tail-core append (kernels/attn_compute_common.hpp:281-341, kernels/attn_worker_writer.cpp
  * :128-143; torch model.py:245-246) with the vLLM block-table contract (block 64, tt-model.yaml:41). */
 int qs_paged_kv_append(const uint16_t *k, const uint16_t *v, uint16_t *k_cache, uint16_t *v_cache,
                        const int *block_table, const int *positions, int B, int T, int NKV, int HD, int block,
-                       int max_blocks, int num_blocks, void *stream);
+                       int max_blocks, int num_blocks, int *status, void *stream);
+
+/* The step's position advance, the first launch of a decode or verify step (ResidentModel.step moves the
+ * position by the decoded rows, model.py:1314-1351, :1499-1508): base_out[b] <- lens[b] (nullable; the
+ * verify step's acceptance adds the accept length to it) and lens[b] <- lens[b] + T, so lens goes from the
+ * rows cached before the step to the rows valid after it, which is the seq_lens the step's attention
+ * launches take. A negative length (idle slot) is left as it is. A length that passes max_len (the block
+ * table's rows: model.py's max_pos, the max_model_len assert of generator_vllm.py:94) is advanced anyway and
+ * reported (QS_STATUS_LENGTH); the attention launches then skip that user. */
+int qs_advance_lengths(int *lens, int *base_out, int B, int T, int max_len, int *status, void *stream);
 
 /* ---------------------------------------------------------------------------------------- a9: paged fill
  * paged_fill_cache for one sequence: token i of k, v [NKV, T, HD] goes to page page_table[(start+i)/block],
@@ -163,12 +183,16 @@ int qs_paged_kv_gather(const uint16_t *k_cache, const uint16_t *v_cache, const i
                        void *stream);
 
 /* ---------------------------------------------------------------------------------------- a6: attention
- * Paged GQA decode attention with split-K over block-table pages and an ordered merge launch.
+ * Paged GQA decode attention with split-K over block-table pages and an ordered merge.
  *   q [B, T, NQ, HD] bf16; seq_lens [B] = positions valid after this step's T tokens; query t of user b
  *   attends positions 0 .. seq_lens[b] - T + t (causal among the T new rows); o [B, T, NQ, HD] bf16.
- *   When k_new/v_new [B, T, NKV, HD] are non-null the T new rows are also appended (a5 fused): they are
- *   written into their pages and attended from the inputs, so no call sees a half-written row.
+ *   When k_new/v_new [B, T, NKV, HD] are non-null the T new rows are also appended (a5 fused): the
+ *   workgroup owning a new row's page writes it first and waits for the store, then reads it back with the
+ *   page, so no call sees a half-written row.
  *   pages_per_split (1..64): pages one workgroup walks (the split-K grain); the workspace holds the partials.
+ *   A user with seq_lens[b] < T is an idle slot: nothing is appended or attended and its output rows are
+ *   zero. A user with seq_lens[b] > max_blocks * block is treated the same and reported (QS_STATUS_LENGTH);
+ *   a page entry outside [0, num_blocks) is not attended and is reported (QS_STATUS_PAGE).
  * Replaces the attention leader / chunk workers / tail core (kernels/attn_worker_compute.cpp:77-270,
  * kernels/attn_leader_compute.cpp:42-105, kernels/attn_leader_writer.cpp:86-106, split schedule
  * kernels/attn_common.hpp:139-154; torch model.py:239-246). HD == 256, block == 64, NQ / NKV <= 8. */
@@ -177,7 +201,7 @@ size_t qs_paged_attention_workspace_bytes(int B, int T, int NQ, int NKV, int HD,
 int qs_paged_gqa_decode(const uint16_t *q, const uint16_t *k_new, const uint16_t *v_new, uint16_t *k_cache,
                         uint16_t *v_cache, const int *block_table, const int *seq_lens, uint16_t *o,
                         void *workspace, int B, int T, int NQ, int NKV, int HD, int block, int max_blocks,
-                        int num_blocks, int pages_per_split, float scale, void *stream);
+                        int num_blocks, int pages_per_split, float scale, int *status, void *stream);
 
 /* The attention mixer of one decode / verify step around a5 + a6 (the path's edges, torch model.py:237-246):
  *   qn = rope(rmsnorm(q) * wq), kn = bf16(rope(rmsnorm(k_new) * wk)) appended with v_new, and
@@ -192,7 +216,7 @@ int qs_attn_mixer_decode(const uint16_t *q, const uint16_t *k_new, const uint16_
                          const float *wq, const float *wk, const float *rope_cos, const float *rope_sin, int rot,
                          uint16_t *k_cache, uint16_t *v_cache, const int *block_table, const int *seq_lens,
                          uint16_t *o, void *workspace, int B, int T, int NQ, int NKV, int HD, int block,
-                         int max_blocks, int num_blocks, int pages_per_split, float eps, void *stream);
+                         int max_blocks, int num_blocks, int pages_per_split, float eps, int *status, void *stream);
 
 /* ---------------------------------------------------------------------------------------- a8: prefill
  * Chunked gated delta rule over one sequence (WY/UT form, bf16 MFMA, fp32 state carry), L2-norm of q

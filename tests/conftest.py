@@ -1,3 +1,4 @@
+import json
 import os
 import sys
 
@@ -7,6 +8,27 @@ REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 for p in (REPO, os.path.join(REPO, "tt-qwen-resident_amd")):
     if p not in sys.path:
         sys.path.insert(0, p)
+
+# Tolerances of the parity checks (the north star's rtols; the absolute floors are fractions of the
+# reference tensor's RMS, for elements near zero where a relative bound means nothing). Each floor sits a
+# few times above the largest error observed on the MI355X over the whole GPU suite, and no higher:
+#   fp32 recurrent state      rtol 1e-4, floor 1e-5 x RMS. The kernel's and the oracle's fp32 roundings
+#                             differ by a few ulp of the largest terms of each element (|decay S|, |k delta|);
+#                             observed <= 2.1e-6 x RMS after three chained steps.
+#   prefilled state           rtol 1e-4, floor 1e-4 x RMS. The chunked (WY) form reorders the recurrence's
+#                             sums over 64-token chunks and carries fp32 operands as bf16 hi + lo pairs into
+#                             the MFMAs; observed <= 2.9e-5 x RMS after 8192 tokens.
+#   GDN output o (bf16)       rtol 2e-2, floor 1e-3 x RMS. o is an fp32 dot product rounded once to bf16 on
+#                             both sides; observed <= 8.8e-5 x RMS.
+#   attention output (bf16)   rtol 2e-2, floor 1e-2 x RMS. The kernel rounds the softmax probabilities to
+#                             bf16 before P V (as a flash decode does), which moves each output by ~2^-9 x
+#                             RMS(o) whatever the element's own size; observed <= 4.4e-3 x RMS.
+STATE_RTOL, STATE_FLOOR, PREFILL_STATE_FLOOR = 1e-4, 1e-5, 1e-4
+OUT_RTOL, GDN_OUT_FLOOR, ATTN_OUT_FLOOR = 2e-2, 1e-3, 1e-2
+# Heads whose conv inputs differ from the oracle's in one bf16 ulp (the exponential inside SiLU differs in
+# the last fp32 bit between libraries) get a perturbation bound instead: one ulp of one v channel moves its
+# state column by beta |k_i| 2^-8 |v| ~ 0.5% of the state RMS (observed <= 2.9e-3 x RMS).
+PERTURBED_RTOL, PERTURBED_FLOOR = 2e-2, 1e-2
 
 
 def pytest_configure(config):
@@ -26,19 +48,62 @@ def rms(t):
     return float(t.double().pow(2).mean().sqrt())
 
 
-def assert_bf16_output(got, ref):
-    """bf16 outputs (attention / GDN o): rtol 2e-2; elements below 2% of the output RMS are held to an
-    absolute 2e-2 x RMS instead (relative error is meaningless at zero crossings)."""
+def _log(kind, got, ref, rtol, floor):
+    """With QS_TOL_LOG set, append the observed error of one check: the smallest floor (in RMS units) that
+    would have passed at this rtol, and the largest relative error among elements above 1% of the RMS."""
+    path = os.environ.get("QS_TOL_LOG")
+    if not path:
+        return
+    g, r = got.double(), ref.double()
+    s = max(rms(r), 1e-30)
+    d = (g - r).abs()
+    need = float((d - rtol * r.abs()).clamp_min(0).max()) / s
+    big = r.abs() > 0.01 * s
+    rel = float((d[big] / r[big].abs()).max()) if bool(big.any()) else 0.0
+    with open(path, "a") as f:
+        f.write(json.dumps(dict(test=os.environ.get("PYTEST_CURRENT_TEST", "?"), kind=kind, floor_needed=need,
+                                floor=floor, max_rel=rel, n=int(r.numel()))) + "\n")  # fmt: skip
+
+
+def _close(kind, got, ref, rtol, floor):
     import torch
 
-    torch.testing.assert_close(got.float().cpu(), ref.float().cpu(), rtol=2e-2, atol=2e-2 * rms(ref))
+    got, ref = got.float().cpu(), ref.float().cpu()
+    _log(kind, got, ref, rtol, floor)
+    torch.testing.assert_close(got, ref, rtol=rtol, atol=floor * rms(ref))
+
+
+def assert_bf16_output(got, ref):
+    """GDN output o (bf16): rtol 2e-2, floor 1e-3 x RMS."""
+    _close("gdn_o", got, ref, OUT_RTOL, GDN_OUT_FLOOR)
+
+
+def assert_attn_output(got, ref):
+    """Attention output (bf16): rtol 2e-2, floor 1e-2 x RMS."""
+    _close("attn_o", got, ref, OUT_RTOL, ATTN_OUT_FLOOR)
 
 
 def assert_state(got, ref):
-    """fp32 recurrent state: rtol 1e-4 (absolute floor 1e-4 x RMS for elements near zero)."""
-    import torch
+    """fp32 recurrent state: rtol 1e-4, floor 1e-5 x RMS."""
+    _close("state", got, ref, STATE_RTOL, STATE_FLOOR)
 
-    torch.testing.assert_close(got.float().cpu(), ref.float().cpu(), rtol=1e-4, atol=1e-4 * rms(ref))
+
+def assert_prefill_state(got, ref):
+    """fp32 state after a chunked prefill: rtol 1e-4, floor 1e-4 x RMS."""
+    _close("prefill_state", got, ref, STATE_RTOL, PREFILL_STATE_FLOOR)
+
+
+def assert_state_perturbed(got, ref):
+    """State of a head whose conv inputs differ from the oracle's by one bf16 ulp: rtol 2e-2, floor 1e-2 x RMS."""
+    _close("state_perturbed", got, ref, PERTURBED_RTOL, PERTURBED_FLOOR)
+
+
+def perturbed_ok(perturbed):
+    """The perturbed heads of one check are few: at most 6 or 2% of the heads, whichever is more. One
+    mismatched q or k channel perturbs the 3 value heads of its key head, so 6 is two mismatch events; in a
+    batch-1 layer one event is already 6% of the 48 heads."""
+    n = int(perturbed.sum())
+    return n <= max(6, int(0.02 * perturbed.numel()))
 
 
 def bf16_ulp_mismatch(got, ref):
@@ -49,3 +114,26 @@ def bf16_ulp_mismatch(got, ref):
     b = ref.cpu().to(torch.bfloat16).view(torch.int16).int()
     d = (a - b).abs()
     return int(d.max()), float((d != 0).float().mean())
+
+
+def conv_mismatch_heads(y_gpu, y_ref, nk, nv, dk=128, dv=128):
+    """Value heads whose conv inputs differ between the kernel and the oracle: y [B, C] (or [B, T, C], where a
+    difference at token t also marks the later tokens, whose states descend from it). Head h of user b reads
+    the q and k channels of key head h // (nv / nk) and its own v channels. Returns a bool tensor [B, nv]
+    (or [B, T, nv])."""
+    import torch
+
+    a = y_gpu.cpu().to(torch.bfloat16).view(torch.int16)
+    b = y_ref.cpu().to(torch.bfloat16).view(torch.int16)
+    diff = a != b
+    squeeze = diff.dim() == 2
+    if squeeze:
+        diff = diff[:, None]
+    B, T, _ = diff.shape
+    qd = nk * dk
+    dq = diff[..., :qd].reshape(B, T, nk, dk).any(-1)
+    dkk = diff[..., qd : 2 * qd].reshape(B, T, nk, dk).any(-1)
+    dvv = diff[..., 2 * qd : 2 * qd + nv * dv].reshape(B, T, nv, dv).any(-1)
+    heads = (dq | dkk).repeat_interleave(nv // nk, dim=2) | dvv
+    heads = torch.cummax(heads.int(), dim=1).values.bool()
+    return heads[:, 0] if squeeze else heads

@@ -29,7 +29,7 @@ def test_exports_every_declared_symbol():
         assert hasattr(L, n), n
         assert n in _lib.SIGNATURES, n
     assert set(_lib.SIGNATURES) == set(names)
-    assert L.qs_abi_version() == 1
+    assert L.qs_abi_version() == 2
 
 
 def test_rejects_bad_arguments():
@@ -49,7 +49,7 @@ def test_rejects_bad_arguments():
     assert "alias" in L.qs_last_error().decode()
     # attention: head dim, block size, group size, missing workspace
     args = lambda hd, blk, nq, mb, pps, ws: (FAKE, NUL, NUL, FAKE, FAKE, FAKE, FAKE, FAKE, ws, 1, 1, nq, 4, hd, blk,
-                                             mb, 2048, pps, 0.0625, S)  # fmt: skip
+                                             mb, 2048, pps, 0.0625, NUL, S)  # fmt: skip
     assert L.qs_paged_gqa_decode(*args(128, 64, 24, 512, 8, FAKE)) == -1
     assert L.qs_paged_gqa_decode(*args(256, 32, 24, 512, 8, FAKE)) == -1
     assert L.qs_paged_gqa_decode(*args(256, 64, 20, 512, 8, FAKE)) == -1
@@ -57,7 +57,11 @@ def test_rejects_bad_arguments():
     assert "workspace" in L.qs_last_error().decode()
     # fill: a table too short for the tokens
     assert L.qs_paged_kv_fill(FAKE, FAKE, FAKE, FAKE, FAKE, 200, 0, 4, 256, 64, 3, 2048, S) == -1
-    assert L.qs_paged_kv_append(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1, 1, 4, 250, 64, 8, 8, S) == -1
+    assert L.qs_paged_kv_append(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1, 1, 4, 250, 64, 8, 8, NUL, S) == -1
+    # the length advance: null lengths, aliasing base
+    assert L.qs_advance_lengths(NUL, NUL, 4, 1, 4096, NUL, S) == -1
+    assert L.qs_advance_lengths(FAKE, FAKE, 4, 1, 4096, NUL, S) == -1
+    assert "alias" in L.qs_last_error().decode()
     # gather: a table too short for the positions, a pool without its output
     assert L.qs_paged_kv_gather(FAKE, FAKE, FAKE, FAKE, FAKE, 200, 0, 4, 256, 64, 3, 2048, S) == -1
     assert L.qs_paged_kv_gather(FAKE, FAKE, FAKE, NUL, FAKE, 100, 0, 4, 256, 64, 3, 2048, S) == -1

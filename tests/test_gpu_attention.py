@@ -2,7 +2,7 @@
 bf16 output rtol 2e-2; the fused append leaves the pools bit-identical to the oracle's append."""
 import pytest
 import torch
-from conftest import assert_bf16_output
+from conftest import assert_attn_output
 
 from oracle import state_path as O
 from qwen36_state import ops, workloads as W
@@ -46,7 +46,7 @@ def test_attention(dev, B, ctx, T, pps):
     d = W.attn_layer(B, ctx, "cpu", seed=B + ctx + T + pps, T=T)
     o, o_ref, same = run_case(dev, d, pps)
     assert same
-    assert_bf16_output(o, o_ref)
+    assert_attn_output(o, o_ref)
 
 
 def test_attention_ragged_users(dev):
@@ -55,7 +55,7 @@ def test_attention_ragged_users(dev):
     d["seq_lens"] = torch.tensor([1, 64, 65, 700], dtype=torch.int32)
     o, o_ref, same = run_case(dev, d, pps=2)
     assert same
-    assert_bf16_output(o, o_ref)
+    assert_attn_output(o, o_ref)
     # a user with a single position attends only to its new row: o = v_new exactly (up to bf16 rounding)
     torch.testing.assert_close(o[0, 0].cpu().float(), d["v_new"][0, 0].float().repeat_interleave(6, 0), rtol=0, atol=0)
 
@@ -66,7 +66,7 @@ def test_attention_unfused_equals_fused(dev):
     o2, _, same = run_case(dev, d, pps=4, fused=False)
     assert same
     assert torch.equal(o1.cpu(), o2.cpu())
-    assert_bf16_output(o1, ref)
+    assert_attn_output(o1, ref)
 
 
 def test_attention_repeatable(dev):
@@ -105,7 +105,7 @@ def test_attn_mixer(dev, B, ctx, T, pps):
     assert torch.equal(g["v_cache"].cpu(), vc)
     ulps, frac = bf16_ulp_mismatch(g["k_cache"].cpu(), kc)
     assert ulps <= 1 and frac < 1e-3, (ulps, frac)
-    assert_bf16_output(o, o_ref)
+    assert_attn_output(o, o_ref)
     # the rope tables of the wrapper equal the oracle's
     c2, s2 = ops.rope_tables(pos.to(dev) + 5000)
     assert torch.equal(c2.cpu(), cos) and torch.equal(s2.cpu(), sin)
@@ -132,4 +132,4 @@ def test_in_launch_merge_counters_rearm(dev):
     assert torch.equal(outs[0], outs[2]) and torch.equal(outs[1], outs[3])
     for d, o in zip(data, outs):
         ref = O.gqa_decode(d["q"], d["k_cache"], d["v_cache"], d["block_table"], d["seq_lens"], d["scale"])
-        assert_bf16_output(o, O.bf16(ref))
+        assert_attn_output(o, O.bf16(ref))

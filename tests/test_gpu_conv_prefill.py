@@ -4,7 +4,7 @@ outputs within one bf16 ulp of the oracle (SiLU's exp differs in the last fp32 b
 the end-to-end prompt -> decode handoff holds the fp32 state to rtol 1e-4 and o to the bf16 rtol 2e-2."""
 import pytest
 import torch
-from conftest import assert_bf16_output, assert_state, bf16_ulp_mismatch
+from conftest import assert_bf16_output, assert_prefill_state, bf16_ulp_mismatch
 
 from oracle import state_path as O
 from qwen36_state import ops, workloads as W
@@ -106,7 +106,7 @@ def test_prompt_then_decode_equals_token_by_token(dev):
             assert torch.equal(conv_ref[0], carry)
     torch.cuda.synchronize()
     assert torch.equal(conv_state, conv_ref)
-    assert_state(state, state_ref.cpu())
+    assert_prefill_state(state, state_ref.cpu())
     assert_bf16_output(o, o_ref.cpu())
 
 

@@ -7,7 +7,7 @@ rows, conv states and other users' results bit-exact; the prompt user's fp32 sta
 against token-by-token decode."""
 import pytest
 import torch
-from conftest import assert_bf16_output, assert_state
+from conftest import assert_bf16_output, assert_prefill_state
 
 from oracle import state_path as O
 from qwen36_state import ops, workloads as W
@@ -102,7 +102,7 @@ def test_prompt_handoff_into_a_batch_slot(dev):
         assert torch.equal(state[b], st_ref[b]) and torch.equal(conv_state[b], cs_ref[b])
         assert torch.equal(o[b], o_ref[b])
     assert torch.equal(conv_state[u], c1[0])
-    assert_state(state[u], s1[0].cpu())
+    assert_prefill_state(state[u], s1[0].cpu())
     assert_bf16_output(o[u], o1[0].cpu())
     assert torch.equal(ao, ao_ref) and torch.equal(kc, kc_ref) and torch.equal(vc, vc_ref)
     krow, vrow = ops.paged_kv_gather(kc, vc, table[u].contiguous(), T + 1)

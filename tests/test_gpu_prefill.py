@@ -3,7 +3,7 @@ sequential recurrence for short sequences, its chunked WY restatement (pinned ag
 CPU) for 8192 tokens. Final fp32 state rtol 1e-4; bf16 per-token output rtol 2e-2."""
 import pytest
 import torch
-from conftest import assert_bf16_output, assert_state
+from conftest import assert_bf16_output, assert_prefill_state
 
 from oracle import state_path as O
 from qwen36_state import ops, workloads as W
@@ -30,7 +30,7 @@ def test_prefill_matches_recurrence(dev, T):
     d = W.prefill(T, "cpu", seed=T)
     o, S = run(dev, d, T)
     o_ref, S_ref = ref(d, T)
-    assert_state(S, S_ref.float())
+    assert_prefill_state(S, S_ref.float())
     assert_bf16_output(o, O.bf16(o_ref.float()))
 
 
@@ -39,7 +39,7 @@ def test_prefill_8192_tokens(dev):
     d = W.prefill(8192, "cpu", seed=4)
     o, S = run(dev, d, 8192)
     o_ref, S_ref = ref(d, 8192, wy=True)
-    assert_state(S, S_ref.float())
+    assert_prefill_state(S, S_ref.float())
     assert_bf16_output(o, O.bf16(o_ref.float()))
 
 
@@ -63,7 +63,7 @@ def test_prefill_then_decode_continues(dev):
     o1 = ops.gdn_decode_step(g["q"][129:130].contiguous(), g["k"][129:130].contiguous(), g["v"][129:130].contiguous(),
                              g["g"][129:130].contiguous(), g["beta"][129:130].contiguous(), state)  # fmt: skip
     o2, S2 = run(dev, d, 130)
-    assert_state(state[0], S2.cpu())
+    assert_prefill_state(state[0], S2.cpu())
     assert_bf16_output(o1[0], o2[129])
 
 
@@ -79,7 +79,7 @@ def test_prefill_4485_tokens(dev):
     d = W.prefill(4485, "cpu", seed=8)
     o, S = run(dev, d, 4485)
     o_ref, S_ref = ref(d, 4485, wy=True)
-    assert_state(S, S_ref.float())
+    assert_prefill_state(S, S_ref.float())
     assert_bf16_output(o, O.bf16(o_ref.float()))
 
 

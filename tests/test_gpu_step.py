@@ -1,65 +1,90 @@
-"""The batched 64-layer decode step (48 GDN + 16 attention layers, batch 8, 4096 positions): spot layers
-against their own oracle calls, and HIP-graph replays bit-identical to the eager step (replayed several
-times from a restored state, with eager work and synchronisation in between)."""
+"""Whole steps of the 64-layer state path as they are benchmarked, every layer against its own oracle call:
+
+- the decode step at batch 8, 4096 positions, 4 pages per split (the in-launch merge of 16 splits);
+- three consecutive graph replays of a decode step whose positions cross a page boundary (4095, 4096,
+  4097): each replay advances the positions on the device, and the oracle carries its own state, conv
+  history and pools from step to step;
+- the MTP verify step at batch 1, 8192 positions, T = 4, 2 pages per split, two steps in a row with the
+  seeded acceptance (the pattern of tests/test_resident_verify.py:42-72);
+- HIP-graph replays bit-identical to the eager step, and acceptance by slot selection equal to the copy
+  rollback."""
 import pytest
 import torch
-from conftest import assert_bf16_output, assert_state
+from stepcheck import OracleState, check_decode_step, check_verify_step, inputs_of
 
-from oracle import state_path as O
-from qwen36_state import ops
-from qwen36_state.decode import StatePathStep
+from qwen36_state.decode import StatePathStep, VerifyStep
 
 pytestmark = pytest.mark.gpu
-NK, NV, DK, DV = 16, 48, 128, 128
 
 
-@pytest.fixture(scope="module")
-def step(dev):
-    s = StatePathStep(8, 4096, 64, device=dev)
-    yield s
-    del s
-    torch.cuda.empty_cache()
-
-
-def test_step_layers_match_oracle(step, dev):
-    gdn = {l: {k: v.clone() for k, v in step.layer[l].items() if torch.is_tensor(v)} for l in (0, 62)}
-    cpu_in = {l: {k: v.cpu() for k, v in d.items()} for l, d in gdn.items()}
-    att3 = {k: v.cpu() for k, v in step.layer[3].items() if torch.is_tensor(v)}
-    step.step()
+def test_decode_step_as_benched(dev):
+    """StatePathStep(8, 4096, pps 4): all 48 GDN and 16 attention layers of one graph replay."""
+    step = StatePathStep.synthetic(8, 4096, device=dev, pages_per_split=4, check=True)
+    ref, inp = OracleState(step), inputs_of(step)
+    step.capture()
+    step.replay()
     torch.cuda.synchronize()
-    for l, d in gdn.items():
-        # the same launch on a copy, with the conv output exposed, reproduces the step's layer bit-exactly
-        y = torch.empty_like(d["x"])
-        o = ops.gdn_decode_fused(d["x"], d["conv_state"], d["taps"], d["g"], d["beta"], d["state"], y_out=y)
-        L, c = step.layer[l], cpu_in[l]
-        assert torch.equal(o, L["o"]) and torch.equal(d["state"], L["state"])
-        assert torch.equal(d["conv_state"], L["conv_state"])
-        _, cs = O.conv1d_update(c["x"], c["conv_state"], c["taps"])
-        assert torch.equal(L["conv_state"].cpu().float(), cs)
-        q, k, v = O.split_qkv(y.cpu().float(), NK, NV, DK, DV)
-        o_ref, S_ref = O.gdn_step(q, k, v, c["g"], c["beta"], c["state"])
-        assert_state(L["state"], S_ref)
-        assert_bf16_output(L["o"], O.bf16(o_ref))
-    # attention layer 3: append + attention over the shared block table
-    kc, vc = att3["k_cache"], att3["v_cache"]
-    O.paged_append(kc, vc, att3["k_new"], att3["v_new"], att3["block_table"], att3["seq_lens"] - 1)
-    o_ref = O.gqa_decode(att3["q"], kc, vc, att3["block_table"], att3["seq_lens"], step.layer[3]["scale"])
-    assert_bf16_output(step.layer[3]["o"], O.bf16(o_ref))
-    rows = O.paged_gather(step.layer[3]["k_cache"].cpu(), att3["block_table"][5], 4096)[:, -1]
-    assert torch.equal(rows, att3["k_new"][5, 0])
+    step.status.check()
+    check_decode_step(step, ref, inp)
 
 
-def test_graph_replay_equals_eager(step, dev):
+def test_decode_steps_cross_a_page(dev):
+    """Three graph replays from 4095 cached rows: the new rows land at positions 4095 (last row of page 63),
+    4096 and 4097 (page 64); new inputs are written into the step's buffers between replays."""
+    step = StatePathStep.synthetic(8, 4096, layers=8, device=dev, pages_per_split=4, max_blocks=68,
+                                   num_blocks=640, check=True)  # fmt: skip
+    step.capture()
+    ref = OracleState(step)
+    gen = torch.Generator().manual_seed(99)
+    for k in range(3):
+        assert int(step.lens[0]) == 4095 + k
+        if k:
+            for d in step.layer:
+                for key in (("q", "k_new", "v_new") if d["attn"] else ("x",)):
+                    d[key].copy_(torch.randn(d[key].shape, generator=gen).to(d[key].dtype))
+        inp = inputs_of(step)
+        step.replay()
+        torch.cuda.synchronize()
+        step.status.check()
+        check_decode_step(step, ref, inp)
+
+
+@pytest.mark.parametrize("steps,max_blocks", [(1, None), (2, 130)])
+def test_verify_steps_as_benched(dev, steps, max_blocks):
+    """VerifyStep(1, 8192, T 4, pps 2): all 64 layers of graph replays with the seeded acceptance. One step
+    with the benchmark's 128-page table (64 splits); two steps in a row with a 130-page table (the second
+    step's rows pass position 8191)."""
+    vs = VerifyStep.synthetic(1, 8192, T=4, device=dev, pages_per_split=2, max_blocks=max_blocks, check=True)
+
+    def cur(l):
+        gi = vs.layer[l]["gi"]
+        S, c = zip(*(vs.state_of(gi, b) for b in range(vs.B)))
+        return torch.stack(S), torch.stack(c)
+
+    ref = OracleState(vs, gdn_state_of=cur)
+    vs.capture()
+    for k in range(steps):
+        inp = inputs_of(vs)
+        vs.replay()
+        torch.cuda.synchronize()
+        vs.status.check()
+        check_verify_step(vs, ref, inp, vs.accept.cpu())
+
+
+def test_graph_replay_equals_eager(dev):
+    step = StatePathStep.synthetic(8, 4096, layers=16, device=dev, pages_per_split=4)
     snap = step.snapshot()
     step.step()
     torch.cuda.synchronize()
     ref = [(d["o"].clone(), d["state"].clone() if not d["attn"] else None) for d in step.layer]
+    lens_after = step.lens.clone()
     step.capture()
     for rep in range(3):
         step.restore(snap)
         torch.cuda.synchronize()
         step.replay()
         torch.cuda.synchronize()
+        assert torch.equal(step.lens, lens_after)
         for l, d in enumerate(step.layer):
             assert torch.equal(d["o"], ref[l][0]), (rep, l)
             if not d["attn"]:
@@ -69,17 +94,15 @@ def test_graph_replay_equals_eager(step, dev):
 
 def test_verify_step_slots_equals_copy(dev):
     """Two consecutive MTP verify steps (8 layers, batch 2, T = 3): acceptance by slot selection gives the
-    same outputs and accepted states as acceptance by copies."""
-    from qwen36_state.decode import VerifyStep
-
-    steps = {m: VerifyStep(2, 1024, T=3, layers=8, device=dev, rollback=m) for m in ("slots", "copy")}
+    same outputs, accepted states and lengths as acceptance by copies."""
+    steps = {m: VerifyStep.synthetic(2, 1024, T=3, layers=8, device=dev, rollback=m, max_blocks=20, num_blocks=64)
+             for m in ("slots", "copy")}  # fmt: skip
     for k in range(2):
         for vs in steps.values():
-            vs.verify()
-            vs.rollback()
-            vs.reset_lengths()
+            vs.step()
         torch.cuda.synchronize()
         a, c = steps["slots"], steps["copy"]
+        assert torch.equal(a.lens, c.lens)
         for la, lc in zip(a.layer, c.layer):
             assert torch.equal(la["o"], lc["o"]), (k, "o")
         for gi in range(6):

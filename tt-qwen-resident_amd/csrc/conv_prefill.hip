@@ -104,7 +104,7 @@ __global__ __launch_bounds__(256) void conv_prefill_kernel(ConvPrefillArgs a) {
             acc = acc + qs::bf2f(half_of(w[r + 1], c)) * qs::bf_hi(t01);
             acc = acc + qs::bf2f(half_of(w[r + 2], c)) * qs::bf_lo(t23);
             acc = acc + qs::bf2f(half_of(w[r + 3], c)) * qs::bf_hi(t23);
-            y[c] = qs::silu_fast(acc);
+            y[c] = qs::silu(acc);
         }
         *reinterpret_cast<uint4 *>(dst + (size_t)t * ld) =
             make_uint4(qs::cvt_pk_bf16(y[0], y[1]), qs::cvt_pk_bf16(y[2], y[3]), qs::cvt_pk_bf16(y[4], y[5]),

@@ -90,7 +90,7 @@ __device__ __forceinline__ void conv_run(const ConvPair<TM> &in, int T, float y[
             acc = acc + h1 * w1;
             acc = acc + h2 * w2;
             acc = acc + xt * w3;
-            sv[e][t] = qs::silu_fast(acc);
+            sv[e][t] = qs::silu(acc);
             h0 = h1;
             h1 = h2;
             h2 = xt;
@@ -184,8 +184,8 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
     const bool isq = r == 0, isk = r == WK, isv = NW > 1 ? w == WV : true;
     const int cg = lane % CG, rg = lane / CG;
     const int T = VERIFY ? a.T : 1;
-    // the workgroup's slab units share key head kh (12 units per key head, WPG divides 12); the workgroup
-    // holding its first unit writes the shared q/k channel outputs
+    // the workgroup's slab units share key head kh (rep * NSLAB units per key head, a multiple of WPG); the
+    // workgroup holding its first unit writes the shared q/k channel outputs
     const int u0 = lid - gw;
     const bool kq_owner = ((u0 / NSLAB) % a.NV) % rep == 0 && u0 % NSLAB == 0;
     int slot = 0;
@@ -410,7 +410,7 @@ __global__ __launch_bounds__(256) void conv1d_update_kernel(const uint16_t *x, u
     acc = acc + h1 * qs::bf_hi(tw.x);
     acc = acc + h2 * qs::bf_lo(tw.y);
     acc = acc + xt * qs::bf_hi(tw.y);
-    y[i] = (uint16_t)(qs::cvt_pk_bf16(qs::silu_fast(acc), 0.f) & 0xffffu);
+    y[i] = (uint16_t)(qs::cvt_pk_bf16(qs::silu(acc), 0.f) & 0xffffu);
     st[0] = st[1];
     st[1] = st[2];
     st[2] = (uint16_t)xr;
@@ -504,19 +504,23 @@ __global__ __launch_bounds__(256) void rollback_kernel(const float *states_out, 
 }
 
 // 32-column slabs. One wave per slab when that gives at least 1024 waves (batch >= 6 at 48 value heads),
-// grouped 6 to a workgroup: 6 consecutive slab units are half of one key head's 12, so the q / k conv runs
-// once per workgroup (waves 0 and 1, shared through LDS) and 2 workgroups count in per key head; at batch 8
-// that is 256 workgroups, one per CU, which streams the same access pattern ~5% faster than 1536
-// single-wave workgroups. Below 1024 units each slab's rows are split over 4 waves so the grid fills the chip. The choice depends on the
-// batch only, so a one-token verify reproduces decode bit for bit at every batch. Verify kernels are
-// compiled for up to 4 and up to 8 tokens.
+// grouped 6 (or 4) to a workgroup: at 3 value heads per key head, 6 consecutive slab units are half of one
+// key head's 12, so the q / k conv runs once per workgroup (waves 0 and 1, shared through LDS) and 2
+// workgroups count in per key head; at batch 8 that is 256 workgroups, one per CU, which streams the same
+// access pattern ~5% faster than 1536 single-wave workgroups. Below 1024 units each slab's rows are split
+// over 4 waves so the grid fills the chip. The choice depends on the shape only, so a one-token verify
+// reproduces decode bit for bit at every batch. Verify kernels are compiled for up to 4 and up to 8 tokens.
 template <bool CONV, bool VERIFY, int TM>
 void launch_gdn_tm(const GdnArgs &a, hipStream_t st) {
     const int units = a.B * a.NV * (DV / 32);
-    if (units >= 1024 && units % 6 == 0)  // 6 slab waves per workgroup: one workgroup per CU at batch 8
+    const int per_key_head = (a.NV / a.NK) * (DV / 32);  // consecutive slab units sharing one key head
+    // a workgroup's slab units must lie in one key head (they share its q / k conv through LDS, and the
+    // conv-state counter expects per_key_head / WPG arrivals): 6 per workgroup when 6 divides the key
+    // head's units (3 value heads per key head: one workgroup per CU at batch 8), else 4 (always divides)
+    if (units >= 1024 && per_key_head % 6 == 0)
         gdn_kernel<CONV, VERIFY, TM, 32, 1, 6><<<units / 6, 384, 0, st>>>(a);
     else if (units >= 1024)
-        gdn_kernel<CONV, VERIFY, TM, 32, 1, 1><<<units, 64, 0, st>>>(a);
+        gdn_kernel<CONV, VERIFY, TM, 32, 1, 4><<<units / 4, 256, 0, st>>>(a);
     else
         gdn_kernel<CONV, VERIFY, TM, 32, 4, 1><<<units, 256, 0, st>>>(a);
 }
@@ -653,22 +657,27 @@ extern "C" int qs_gdn_verify_step_slots(const uint16_t *x, const uint16_t *conv_
 }
 
 // Acceptance by slot selection: slot[b] <- accept[b] - 1 and seq_lens[b] <- base_lens[b] + accept[b] for
-// accept[b] in [1, T]; other users are left untouched.
-__global__ void verify_accept_kernel(const int *accept, int *slot, int *seq_lens, const int *base_lens, int B, int T) {
+// accept[b] in [1, T]; other users are left untouched and reported (QS_STATUS_ACCEPT) when status is given.
+__global__ void verify_accept_kernel(const int *accept, int *slot, int *seq_lens, const int *base_lens, int B, int T,
+                                     int *status) {
     const int b = blockIdx.x * 64 + threadIdx.x;
     if (b >= B) return;
     const int acc = accept[b];
-    if (acc < 1 || acc > T) return;
+    if (acc < 1 || acc > T) {
+        if (status) atomicOr(status, QS_STATUS_ACCEPT);
+        return;
+    }
     slot[b] = acc - 1;
     if (seq_lens) seq_lens[b] = base_lens[b] + acc;
 }
 
 extern "C" int qs_verify_accept(const int *accept_len, int *slot, int *seq_lens, const int *base_lens, int B, int T,
-                                void *stream) {
+                                int *status, void *stream) {
     QS_REQUIRE(accept_len && slot, "qs_verify_accept: null pointer");
     QS_REQUIRE(!seq_lens || base_lens, "qs_verify_accept: seq_lens needs base_lens");
     QS_REQUIRE(B > 0 && T >= 1 && T <= TMAX, "qs_verify_accept: bad shape (B %d, T %d)", B, T);
-    verify_accept_kernel<<<(B + 63) / 64, 64, 0, QS_STREAM(stream)>>>(accept_len, slot, seq_lens, base_lens, B, T);
+    verify_accept_kernel<<<(B + 63) / 64, 64, 0, QS_STREAM(stream)>>>(accept_len, slot, seq_lens, base_lens, B, T,
+                                                                      status);
     return qs::launch_status("qs_verify_accept");
 }
 

@@ -47,6 +47,7 @@ struct AttnArgs {
     float *part_o;                      // [B, NKV, nsplit, T G, HD]: split partials (unnormalised O)
     float *part_ml;                     // [B, NKV, nsplit, T G, 2]: their (max, sum), log2 domain
     int *cnt;                           // [B, NKV] arrival counters of the in-launch merge (kept zero)
+    int *status;                        // nullable: QS_STATUS_* bits of invalid lengths / table entries
     int B, T, NQ, NKV, max_blocks, num_blocks, pps, nsplit;
     float scale;
     // mixer edges (qs_attn_mixer_decode; null / 0 for plain attention): q and the new k rows are
@@ -101,7 +102,39 @@ __device__ __forceinline__ uint4 pack8(const float y[8]) {
     return make_uint4(qs::cvt_pk_bf16(y[0], y[1]), qs::cvt_pk_bf16(y[2], y[3]), qs::cvt_pk_bf16(y[4], y[5]),
                       qs::cvt_pk_bf16(y[6], y[7]));
 }
+// The rounding residues y - bf16(y) of 8 values as bf16 (hi = pack8(y)): hi + lo carries y to ~2^-17 relative,
+// so products against exact bf16 operands (K rows) keep the fp32 value of a normalised, rotated q.
+__device__ __forceinline__ uint4 pack8_lo(const float y[8], uint4 hi) {
+    const uint32_t h[4] = {hi.x, hi.y, hi.z, hi.w};
+    uint32_t lo[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) lo[e] = qs::cvt_pk_bf16(y[2 * e] - qs::bf_lo(h[e]), y[2 * e + 1] - qs::bf_hi(h[e]));
+    return make_uint4(lo[0], lo[1], lo[2], lo[3]);
+}
 __device__ __forceinline__ float sigm(float g) { return 1.0f / (1.0f + expf(-g)); }
+
+// A user's length n (positions valid after this step's T rows) is usable when T <= n <= max_blocks * BLK.
+// n < T marks an idle slot (nothing appended or attended, zero output); n past the block table is an error
+// (reported in the status word) and the user is treated as idle, never clamped onto other positions.
+__device__ __forceinline__ bool user_active(const AttnArgs &a, int n, bool report) {
+    if (n > a.max_blocks * BLK) {
+        if (report && a.status) atomicOr(a.status, QS_STATUS_LENGTH);
+        return false;
+    }
+    return n >= a.T;
+}
+__device__ __forceinline__ void report_page(const AttnArgs &a) {
+    if (a.status) atomicOr(a.status, QS_STATUS_PAGE);
+}
+// Zero output rows of an inactive user for KV head g (all T G query rows; threads of one workgroup).
+template <int G>
+__device__ __forceinline__ void zero_rows(const AttnArgs &a, int b, int g, int tid) {
+    for (int idx = tid; idx < a.T * G * 32; idx += 256) {
+        const int qr = idx >> 5, ch = idx & 31;
+        *reinterpret_cast<uint4 *>(a.o + (((size_t)b * a.T + qr / G) * a.NQ + g * G + qr % G) * HD + ch * 8) =
+            make_uint4(0, 0, 0, 0);
+    }
+}
 
 // Workspace layout (bytes): arrival counters | part_ml | part_o, each 256-byte aligned. The counters sit in
 // a fixed block at the head, so a workspace reused for another shape never finds partial data where its
@@ -130,7 +163,7 @@ __device__ __forceinline__ size_t prow(const AttnArgs &a, int G, int b, int g, i
 //   K   lane = (row 16 w + lane / 4, piece c = lane % 4): dims 32 i + 8 c .. + 7 for i < 8, 8 x 16-byte loads
 //   V   lane = head dims 4 lane .. 4 lane + 3, the wave's 16 rows (one 512-byte row per load instruction)
 // and the loaded page is reused for every query token of the group (TT tokens: the verify rows).
-template <int G, int TT>
+template <int G, int TT, bool MIX>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     constexpr int GP = (G + 3) & ~3;
     const int nwg = a.B * a.NKV * a.nsplit;
@@ -142,13 +175,17 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     const int T = a.T;
 
     __shared__ __align__(16) uint16_t s_q[TT][G][HD];
+    __shared__ __align__(16) uint16_t s_ql[MIX ? TT : 1][G][HD];  // mixer: bf16 residues of the fp32 q
     __shared__ __align__(16) uint32_t s_pp[4][8][GP];
     __shared__ __align__(16) float s_acc[4][G][HD];
     __shared__ float s_m[4][G], s_l[4][G];
     __shared__ float s_w[4][G], s_L[G], s_M[G];
 
-    int n = a.seq_lens[b];
-    n = n < T ? T : (n > a.max_blocks * BLK ? a.max_blocks * BLK : n);
+    const int n = a.seq_lens[b];
+    if (!user_active(a, n, split == 0 && g == 0 && tid == 0)) {  // uniform over the user's workgroups
+        if (split == 0) zero_rows<G>(a, b, g, tid);
+        return;
+    }
     const int base = n - T;  // first new position
     const int npages = (n + BLK - 1) / BLK;
     const int p0 = split * a.pps;
@@ -162,6 +199,9 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         const int pg = __builtin_amdgcn_readlane(bt_pre, pi - p0);
         return (pg >= 0 && pg < a.num_blocks) ? pg : -1;
     };
+    if (tid == 0)
+        for (int pi = p0; pi < p1; ++pi)
+            if (page_at(pi) < 0) report_page(a);
 
     // Fused append, first: the new rows that fall in this split's pages go into the pools, and the stores
     // complete before the barrier that precedes the page walk, so the walk reads every row - new ones
@@ -180,7 +220,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             }
             if (pi < p0 || pi >= p1) continue;
             const int pg = bt[pi];  // per thread: the new rows may straddle two pages
-            if (pg < 0 || pg >= a.num_blocks) continue;
+            if (pg < 0 || pg >= a.num_blocks) continue;  // reported with the split's pages above
             const size_t dst = (((size_t)pg * a.NKV + g) * BLK + (pos % BLK)) * HD + ch * 8;
             *reinterpret_cast<uint4 *>((kv ? a.v_cache : a.k_cache) + dst) = u;
         }
@@ -242,11 +282,12 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                 const int idx = tid + 256 * k;
                 const int tt = idx / (G * 32), hh = (idx / 32) % G, ch = idx & 31;
                 uint4 u = qreg[k];
-                if (a.wq) {  // normalised and rotated q (all lanes take part in the row reductions)
+                if constexpr (MIX) {  // normalised and rotated q (all lanes take part in the row reductions)
                     float y[8];
                     const size_t rc = ((size_t)b * T + min(tg + tt, T - 1)) * (a.rot / 2);
                     mixer_chunk(u, ch, a.wq, a.rcos + rc, a.rsin + rc, a.rot, a.eps, y);
                     u = pack8(y);
+                    if (idx < TT * G * 32) *reinterpret_cast<uint4 *>(&s_ql[tt][hh][ch * 8]) = pack8_lo(y, u);
                 }
                 if (idx < TT * G * 32) *reinterpret_cast<uint4 *>(&s_q[tt][hh][ch * 8]) = u;
             }
@@ -296,6 +337,13 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                     d = dot2(kv[i].y, qv.y, d);
                     d = dot2(kv[i].z, qv.z, d);
                     d = dot2(kv[i].w, qv.w, d);
+                    if constexpr (MIX) {
+                        const uint4 ql = *reinterpret_cast<const uint4 *>(&s_ql[tt][h][i * 32 + kq * 8]);
+                        d = dot2(kv[i].x, ql.x, d);
+                        d = dot2(kv[i].y, ql.y, d);
+                        d = dot2(kv[i].z, ql.z, d);
+                        d = dot2(kv[i].w, ql.w, d);
+                    }
                     sc[h] = d;
                 }
             }
@@ -514,7 +562,7 @@ __device__ __forceinline__ void merge_in_launch(const AttnArgs &a, int b, int g,
     }
 }
 
-template <int G, int QT>
+template <int G, int QT, bool MIX>
 __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
     constexpr int NQR = 16 * QT;
     const int nwg = a.B * a.NKV * a.nsplit;
@@ -527,6 +575,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
     const int T = a.T;
 
     __shared__ __align__(16) uint16_t s_q[NQR][QPAD];
+    __shared__ __align__(16) uint16_t s_ql[MIX ? NQR : 1][QPAD];  // mixer: bf16 residues of the fp32 q
     __shared__ __align__(16) uint16_t s_v[4][16][VPAD];     // the page's V rows, slice by slice
     __shared__ __align__(16) uint16_t s_p[4][QT][16][PPAD];  // P^T of each slice: [query row][slice row]
     __shared__ float s_m[4][NQR], s_l[4][NQR];              // slice max (log2 domain) and row sum
@@ -589,10 +638,16 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
         load_v(pg0, VA);
     }
 
-    n = n < T ? T : (n > a.max_blocks * BLK ? a.max_blocks * BLK : n);
+    if (!user_active(a, n, split == 0 && g == 0 && tid == 0)) {  // uniform over the user's workgroups
+        if (split == 0) zero_rows<G>(a, b, g, tid);
+        return;
+    }
     const int base = n - T;  // first new position
     const int npages = (n + BLK - 1) / BLK;
     const int p1 = min(npages, p0 + a.pps);
+    if (tid == 0)
+        for (int pi = p0; pi < p1; ++pi)
+            if (page_at(pi) < 0) report_page(a);
 
     // Fused append, first: wave w writes the new rows of its 16-row slices in this split's pages and waits
     // for them, so its slice loads read them back from the pool. No other wave reads these slices.
@@ -610,7 +665,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
             }
             if (pi < p0 || pi >= p1 || (pos % BLK) / 16 != w) continue;
             const int pg = bt[pi];
-            if (pg < 0 || pg >= a.num_blocks) continue;
+            if (pg < 0 || pg >= a.num_blocks) continue;  // reported with the split's pages above
             const size_t dst = (((size_t)pg * a.NKV + g) * BLK + (pos % BLK)) * HD + ch * 8;
             *reinterpret_cast<uint4 *>((kv ? a.v_cache : a.k_cache) + dst) = u;
         }
@@ -667,6 +722,11 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
                 const bf16x8_t bq = __builtin_bit_cast(
                     bf16x8_t, *reinterpret_cast<const uint4 *>(&s_q[l16 + 16 * nt][32 * j + 8 * lg]));
                 sacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, bq, sacc[nt], 0, 0, 0);
+                if constexpr (MIX) {
+                    const bf16x8_t bl = __builtin_bit_cast(
+                        bf16x8_t, *reinterpret_cast<const uint4 *>(&s_ql[l16 + 16 * nt][32 * j + 8 * lg]));
+                    sacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, bl, sacc[nt], 0, 0, 0);
+                }
             }
         }
         if (pgn >= 0) load_k(pgn, kb);
@@ -731,11 +791,12 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
     for (int k = 0; k < QCH; ++k) {
         const int idx = tid + 256 * k, qr = idx >> 5, ch = idx & 31;
         uint4 u = qreg[k];
-        if (a.wq) {  // normalised and rotated q (all lanes take part in the row reductions)
+        if constexpr (MIX) {  // normalised and rotated q (all lanes take part in the row reductions)
             float y[8];
             const size_t rc = ((size_t)b * T + min(qr / G, T - 1)) * (a.rot / 2);
             mixer_chunk(u, ch, a.wq, a.rcos + rc, a.rsin + rc, a.rot, a.eps, y);
             u = pack8(y);
+            *reinterpret_cast<uint4 *>(&s_ql[qr][ch * 8]) = pack8_lo(y, u);
         }
         *reinterpret_cast<uint4 *>(&s_q[qr][ch * 8]) = u;
     }
@@ -795,6 +856,12 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, int G) {
     const int g = row % a.NKV, bt = row / a.NKV;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int ns = a.nsplit, R = a.T * G;
+    const int n = a.seq_lens[bt / a.T];
+    if (n < a.T || n > a.max_blocks * BLK) {  // inactive user (reported by the attention launch): zero row
+        if (w == 0)
+            *reinterpret_cast<uint2 *>(a.o + ((size_t)bt * a.NQ + g * G + h) * HD + 4 * lane) = make_uint2(0, 0);
+        return;
+    }
     const size_t pr = prow(a, G, bt / a.T, g, 0, (bt % a.T) * G + h);
     const size_t sstride = (size_t)R * HD;  // floats between consecutive splits of one row
     const float *ml = a.part_ml + pr * 2;
@@ -901,9 +968,14 @@ static int attn_launch(AttnArgs a, void *workspace, int HDa, int block, const ch
     // more rows take the VALU kernel, two query tokens per pass over the pages
     if (T * G <= 32) {
         const int QT = (T * G + 15) / 16;
-#define QS_MFMA_LAUNCH(GG)                                                       \
-    if (QT == 1) attn_mfma_kernel<GG, 1><<<grid, 256, 0, st>>>(a);               \
-    else attn_mfma_kernel<GG, 2><<<grid, 256, 0, st>>>(a);
+#define QS_MFMA_LAUNCH(GG)                                                              \
+    if (a.wq) {                                                                         \
+        if (QT == 1) attn_mfma_kernel<GG, 1, true><<<grid, 256, 0, st>>>(a);            \
+        else attn_mfma_kernel<GG, 2, true><<<grid, 256, 0, st>>>(a);                    \
+    } else {                                                                            \
+        if (QT == 1) attn_mfma_kernel<GG, 1, false><<<grid, 256, 0, st>>>(a);           \
+        else attn_mfma_kernel<GG, 2, false><<<grid, 256, 0, st>>>(a);                   \
+    }
         switch (G) {
             case 1: QS_MFMA_LAUNCH(1) break;
             case 2: QS_MFMA_LAUNCH(2) break;
@@ -920,7 +992,9 @@ static int attn_launch(AttnArgs a, void *workspace, int HDa, int block, const ch
         }
         return QS_OK;
     }
-#define QS_ATTN_LAUNCH(GG) attn_kernel<GG, 2><<<grid, 256, 0, st>>>(a);
+#define QS_ATTN_LAUNCH(GG)                                \
+    if (a.wq) attn_kernel<GG, 2, true><<<grid, 256, 0, st>>>(a); \
+    else attn_kernel<GG, 2, false><<<grid, 256, 0, st>>>(a);
     switch (G) {
         case 1: QS_ATTN_LAUNCH(1) break;
         case 2: QS_ATTN_LAUNCH(2) break;
@@ -941,8 +1015,10 @@ static int attn_launch(AttnArgs a, void *workspace, int HDa, int block, const ch
 extern "C" int qs_paged_gqa_decode(const uint16_t *q, const uint16_t *k_new, const uint16_t *v_new,
                                    uint16_t *k_cache, uint16_t *v_cache, const int *block_table, const int *seq_lens,
                                    uint16_t *o, void *workspace, int B, int T, int NQ, int NKV, int HDa, int block,
-                                   int max_blocks, int num_blocks, int pages_per_split, float scale, void *stream) {
+                                   int max_blocks, int num_blocks, int pages_per_split, float scale, int *status,
+                                   void *stream) {
     AttnArgs a{};
+    a.status = status;
     a.q = q, a.k_new = k_new, a.v_new = v_new, a.k_cache = k_cache, a.v_cache = v_cache;
     a.block_table = block_table, a.seq_lens = seq_lens, a.o = o;
     a.B = B, a.T = T, a.NQ = NQ, a.NKV = NKV, a.max_blocks = max_blocks, a.num_blocks = num_blocks;
@@ -955,7 +1031,7 @@ extern "C" int qs_attn_mixer_decode(const uint16_t *q, const uint16_t *k_new, co
                                     const float *rope_sin, int rot, uint16_t *k_cache, uint16_t *v_cache,
                                     const int *block_table, const int *seq_lens, uint16_t *o, void *workspace, int B,
                                     int T, int NQ, int NKV, int HDa, int block, int max_blocks, int num_blocks,
-                                    int pages_per_split, float eps, void *stream) {
+                                    int pages_per_split, float eps, int *status, void *stream) {
     QS_REQUIRE(k_new && v_new && gate && wq && wk, "qs_attn_mixer_decode: null pointer");
     QS_REQUIRE(rot == 0 || (rope_cos && rope_sin), "qs_attn_mixer_decode: rot > 0 needs rope_cos and rope_sin");
     QS_REQUIRE(rot == 0 || rot == 16 || rot == 32 || rot == 64 || rot == 128 || rot == 256,
@@ -968,5 +1044,6 @@ extern "C" int qs_attn_mixer_decode(const uint16_t *q, const uint16_t *k_new, co
     a.B = B, a.T = T, a.NQ = NQ, a.NKV = NKV, a.max_blocks = max_blocks, a.num_blocks = num_blocks;
     a.pps = pages_per_split, a.scale = 1.0f;  // the softmax scale is folded into wq (model.py:237)
     a.gate = gate, a.wq = wq, a.wk = wk, a.rcos = rope_cos, a.rsin = rope_sin, a.rot = rot, a.eps = eps;
+    a.status = status;
     return attn_launch(a, workspace, HDa, block, "qs_attn_mixer_decode", stream);
 }

@@ -1,6 +1,8 @@
 // Paged KV-cache movement on gfx950: decode append (T rows per user through the block table), prefill
-// fill (paged_fill_cache) and its inverse, the gather of a sequence's pages into contiguous rows. Pure byte copies in 16-byte units; page indices read from device memory are
-// range-checked in the kernel (a row whose page is out of range is skipped, never written out of bounds).
+// fill (paged_fill_cache) and its inverse, the gather of a sequence's pages into contiguous rows, and the
+// step's length advance. Pure byte copies in 16-byte units; page indices read from device memory are
+// range-checked in the kernel (a row whose page is out of range is skipped, never written out of bounds,
+// and reported in the caller's status word when one is given).
 #include "qs_common.h"
 
 namespace {
@@ -9,7 +11,7 @@ namespace {
 __global__ __launch_bounds__(256) void append_kernel(const uint16_t *k, const uint16_t *v, uint16_t *kc,
                                                      uint16_t *vc, const int *block_table, const int *positions,
                                                      int B, int T, int NKV, int HD, int block, int max_blocks,
-                                                     int num_blocks) {
+                                                     int num_blocks, int *status) {
     const int cpr = HD / 8;
     const long i = (long)blockIdx.x * 256 + threadIdx.x;
     const long total = (long)B * T * NKV * cpr;
@@ -20,12 +22,19 @@ __global__ __launch_bounds__(256) void append_kernel(const uint16_t *k, const ui
     const long bt = r / NKV;
     const int t = (int)(bt % T);
     const int b = (int)(bt / T);
+    if (positions[b] < 0) return;  // idle slot
     const int p = positions[b] + t;
-    if (p < 0) return;
     const int bi = p / block;
-    if (bi >= max_blocks) return;
+    const bool report = ch == 0 && hk == 0;  // one report per row
+    if (bi >= max_blocks) {
+        if (report && status) atomicOr(status, QS_STATUS_LENGTH);
+        return;
+    }
     const int page = block_table[(long)b * max_blocks + bi];
-    if (page < 0 || page >= num_blocks) return;
+    if (page < 0 || page >= num_blocks) {
+        if (report && status) atomicOr(status, QS_STATUS_PAGE);
+        return;
+    }
     const size_t dst = (((size_t)page * NKV + hk) * block + p % block) * HD + ch * 8;
     const size_t src = (size_t)r * HD + ch * 8;
     if (k) *reinterpret_cast<uint4 *>(kc + dst) = *reinterpret_cast<const uint4 *>(k + src);
@@ -67,7 +76,7 @@ __global__ __launch_bounds__(256) void fill_kernel(const uint16_t *k, const uint
 
 extern "C" int qs_paged_kv_append(const uint16_t *k, const uint16_t *v, uint16_t *k_cache, uint16_t *v_cache,
                                   const int *block_table, const int *positions, int B, int T, int NKV, int HD,
-                                  int block, int max_blocks, int num_blocks, void *stream) {
+                                  int block, int max_blocks, int num_blocks, int *status, void *stream) {
     QS_REQUIRE(k && v && k_cache && v_cache && block_table && positions, "qs_paged_kv_append: null pointer");
     QS_REQUIRE(B > 0 && T > 0 && NKV > 0 && block > 0 && max_blocks > 0 && num_blocks > 0,
                "qs_paged_kv_append: sizes must be positive");
@@ -75,7 +84,7 @@ extern "C" int qs_paged_kv_append(const uint16_t *k, const uint16_t *v, uint16_t
     const long total = (long)B * T * NKV * (HD / 8);
     if (total == 0) return QS_OK;
     append_kernel<<<(unsigned)((total + 255) / 256), 256, 0, QS_STREAM(stream)>>>(
-        k, v, k_cache, v_cache, block_table, positions, B, T, NKV, HD, block, max_blocks, num_blocks);
+        k, v, k_cache, v_cache, block_table, positions, B, T, NKV, HD, block, max_blocks, num_blocks, status);
     return qs::launch_status("qs_paged_kv_append");
 }
 
@@ -114,4 +123,30 @@ extern "C" int qs_paged_kv_gather(const uint16_t *k_cache, const uint16_t *v_cac
         nullptr, nullptr, const_cast<uint16_t *>(k_cache), const_cast<uint16_t *>(v_cache), k, v, page_table, T,
         start, NKV, HD, block, table_len, num_blocks);
     return qs::launch_status("qs_paged_kv_gather");
+}
+
+// The step's position advance (ResidentModel.step moves every user's position by the rows it decodes,
+// model.py:1314-1351, :1499-1508): base_out[b] <- lens[b] (the cached rows before the step, nullable) and
+// lens[b] <- lens[b] + T for every user with lens[b] >= 0 (a negative length marks an idle slot and is left
+// as it is). A length that would pass max_len (the block table's capacity, model.py's max_pos and
+// generator_vllm.py:94's max_model_len assert) is still advanced, so every attention launch of the step
+// treats the user as invalid, and QS_STATUS_LENGTH is set in status.
+namespace {
+__global__ void advance_kernel(int *lens, int *base_out, int B, int T, int max_len, int *status) {
+    const int b = blockIdx.x * 64 + threadIdx.x;
+    if (b >= B) return;
+    const int n = lens[b];
+    if (base_out) base_out[b] = n;
+    if (n < 0) return;
+    if (n + T > max_len && status) atomicOr(status, QS_STATUS_LENGTH);
+    lens[b] = n + T;
+}
+}  // namespace
+
+extern "C" int qs_advance_lengths(int *lens, int *base_out, int B, int T, int max_len, int *status, void *stream) {
+    QS_REQUIRE(lens, "qs_advance_lengths: null lens");
+    QS_REQUIRE(B > 0 && T >= 1 && max_len > 0, "qs_advance_lengths: bad sizes (B %d, T %d, max_len %d)", B, T, max_len);
+    QS_REQUIRE(base_out != lens, "qs_advance_lengths: base_out must not alias lens");
+    advance_kernel<<<(B + 63) / 64, 64, 0, QS_STREAM(stream)>>>(lens, base_out, B, T, max_len, status);
+    return qs::launch_status("qs_advance_lengths");
 }

@@ -25,13 +25,17 @@ __device__ __forceinline__ uint32_t f2bf(float f) {
 }
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
-// SiLU from the hardware exponential and reciprocal (v_exp_f32, v_rcp_f32; each within 1 ulp):
-// x / (1 + 2^(-x log2 e)). Within a few fp32 ulps of x / (1 + e^-x), so its bf16 rounding agrees with the
-// correctly rounded value except on rare ties; -inf exponent arguments give -0.
-__device__ __forceinline__ float silu_fast(float x) {
-    const float e = __builtin_amdgcn_exp2f(-x * 1.4426950408889634f);
-    return x * __builtin_amdgcn_rcpf(1.0f + e);
+// SiLU as torch states it, x / (1 + e^-x): the library exponential (within 1 ulp), then the quotient from the
+// hardware reciprocal with one Newton correction (q + (x - q d) / d), which lands within about half an ulp
+// of the correctly rounded quotient for a fraction of an IEEE divide's instructions. The fp32 result is
+// within about an ulp of torch's CPU value, so its bf16 rounding agrees except where the fp32 value sits
+// within an ulp or two of a bf16 rounding boundary. When e^-x overflows (x < -88.7) the quotient is x / inf,
+// a signed zero, as in torch.
+__device__ __forceinline__ float silu(float x) {
+    const float d = 1.0f + expf(-x);
+    const float r = __builtin_amdgcn_rcpf(d);
+    const float q = x * r;
+    return __builtin_isinf(d) ? x * 0.0f : fmaf(fmaf(-q, d, x), r, q);
 }
 
 // v op (v of lane ^ 16) and v op (v of lane ^ 32) on the VALU (gfx950 v_permlane16_swap / v_permlane32_swap,

@@ -28,21 +28,22 @@ SIGNATURES = {
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _F, _P],
     ),
-    "qs_verify_accept": (_I, [_P, _P, _P, _P, _I, _I, _P]),
+    "qs_verify_accept": (_I, [_P, _P, _P, _P, _I, _I, _P, _P]),
     "qs_gdn_rollback": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "qs_gdn_rollback_layers": (
         _I, [_P, _Z, _P, _Z, _P, _Z, _P, _Z, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
-    "qs_paged_kv_append": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "qs_paged_kv_append": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P]),
+    "qs_advance_lengths": (_I, [_P, _P, _I, _I, _I, _P, _P]),
     "qs_paged_kv_fill": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "qs_paged_kv_gather": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "qs_paged_attention_workspace_bytes": (_Z, [_I, _I, _I, _I, _I, _I, _I]),
     "qs_paged_gqa_decode": (
         _I,
-        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _F, _P],
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _F, _P, _P],
     ),
     "qs_attn_mixer_decode": (
         _I,
-        [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _F, _P],
+        [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _F, _P, _P],
     ),
     "qs_gdn_chunk_prefill_workspace_bytes": (_Z, [_I, _I, _I, _I, _I, _I]),
     "qs_gdn_chunk_prefill": (

@@ -63,6 +63,47 @@ def workspace(kind, nbytes, device):
     return ws
 
 
+# ------------------------------------------------------------------------------------------- status word
+
+STATUS_LENGTH, STATUS_PAGE, STATUS_ACCEPT = 1, 2, 4  # QS_STATUS_* of include/qwen_state.h
+_STATUS_TEXT = {
+    STATUS_LENGTH: "a sequence length ran past its block table",
+    STATUS_PAGE: "a block-table entry needed by a valid position lies outside the KV pool",
+    STATUS_ACCEPT: "an accept length lies outside [1, T]",
+}
+
+
+class Status:
+    """The device status word the kernels report invalid lengths, table entries and accept lengths into
+    (an int32 the caller owns; kernels only OR bits into it). ``check()`` synchronises the device, raises
+    ValueError naming every reported condition (the reference's asserts, generator_vllm.py:94, :130) and
+    clears the word; ``peek()`` reads it without raising."""
+
+    def __init__(self, device):
+        self.word = torch.zeros(1, dtype=torch.int32, device=device)
+
+    def peek(self):
+        return int(self.word.item())
+
+    def check(self):
+        v = self.peek()
+        if v:
+            self.word.zero_()
+            raise ValueError("; ".join(t for bit, t in _STATUS_TEXT.items() if v & bit) + f" (status {v:#x})")
+
+
+def advance_lengths(lens, T, max_len, base_out=None, status=None):
+    """The step's position advance (model.py:1314-1351, :1499-1508): base_out <- lens, lens <- lens + T for
+    every user with lens >= 0 (negative = idle slot). lens [B] int32 on the device; a length past max_len is
+    reported in ``status``."""
+    dev = lens.device
+    _chk(lens, "lens", torch.int32)
+    B = lens.shape[0]
+    if base_out is not None:
+        _chk(base_out, "base_out", torch.int32, (B,), dev)
+    call("qs_advance_lengths", _p(lens), _p(base_out), B, int(T), int(max_len), _p(status), _stream(dev))
+
+
 # ------------------------------------------------------------------------------------------- a1, a3
 
 
@@ -224,9 +265,10 @@ def gdn_verify_step_slots(x, conv_states_in, taps, g, beta, states_in, in_slot, 
     return o, states, convs
 
 
-def verify_accept(accept_len, T, slot, seq_lens=None, base_lens=None):
+def verify_accept(accept_len, T, slot, seq_lens=None, base_lens=None, status=None):
     """Acceptance by slot selection: slot <- accept_len - 1 (the snapshot the next verify step reads) and
-    seq_lens <- base_lens + accept_len when given; no state moves (kernels/mlp_hub.cpp:48-58)."""
+    seq_lens <- base_lens + accept_len when given; no state moves (kernels/mlp_hub.cpp:48-58). An accept
+    length outside [1, T] leaves the user untouched and sets QS_STATUS_ACCEPT in ``status``."""
     dev = slot.device
     B = slot.shape[0]
     _chk(accept_len, "accept_len", torch.int32, (B,), dev)
@@ -234,7 +276,7 @@ def verify_accept(accept_len, T, slot, seq_lens=None, base_lens=None):
     if seq_lens is not None:
         _chk(seq_lens, "seq_lens", torch.int32, (B,), dev)
         _chk(base_lens, "base_lens", torch.int32, (B,), dev)
-    call("qs_verify_accept", _p(accept_len), _p(slot), _p(seq_lens), _p(base_lens), B, T, _stream(dev))
+    call("qs_verify_accept", _p(accept_len), _p(slot), _p(seq_lens), _p(base_lens), B, T, _p(status), _stream(dev))
 
 
 def gdn_rollback(states, conv_states, accept_len, state, conv_state, seq_lens=None, base_lens=None):
@@ -291,11 +333,12 @@ def _pool_dims(k_cache, v_cache, dev):
     return k_cache.shape
 
 
-def paged_kv_append(k, v, k_cache, v_cache, block_table, positions):
+def paged_kv_append(k, v, k_cache, v_cache, block_table, positions, status=None):
     """Write T new rows per user at positions[b] + t through the block table (bit-exact copies).
 
     k, v [B, T, NKV, HD] bf16; pools [num_blocks, NKV, block, HD]; block_table [B, max_blocks] int32;
-    positions [B] int32 (first new position)."""
+    positions [B] int32 (first new position; negative = idle slot). Rows past the table or on an entry
+    outside the pool are skipped and reported in ``status``."""
     dev = k_cache.device
     nb, nkv, block, hd = _pool_dims(k_cache, v_cache, dev)
     B, T = k.shape[:2]
@@ -306,7 +349,7 @@ def paged_kv_append(k, v, k_cache, v_cache, block_table, positions):
         raise ValueError(f"block_table must be [B={B}, max_blocks]")
     _chk(positions, "positions", torch.int32, (B,), dev)
     call("qs_paged_kv_append", _p(k), _p(v), _p(k_cache), _p(v_cache), _p(block_table), _p(positions),
-         B, T, nkv, hd, block, block_table.shape[1], nb, _stream(dev))  # fmt: skip
+         B, T, nkv, hd, block, block_table.shape[1], nb, _p(status), _stream(dev))  # fmt: skip
 
 
 def paged_kv_fill(k, v, k_cache, v_cache, page_table, start=0):
@@ -365,12 +408,14 @@ def attention_workspace(B, T, nq, nkv, max_blocks, pages_per_split, device):
 
 
 def paged_gqa_decode(q, k_cache, v_cache, block_table, seq_lens, scale, k_new=None, v_new=None,
-                     pages_per_split=8, out=None, ws=None):  # fmt: skip
+                     pages_per_split=4, out=None, ws=None, status=None):  # fmt: skip
     """Paged GQA decode attention ``softmax(q K^T scale) V`` over each user's pages (model.py:239-244).
 
     q [B, T, NQ, HD] bf16; seq_lens [B] int32 = valid positions after this step; query t of user b sees
     positions 0 .. seq_lens[b] - T + t. With k_new, v_new [B, T, NKV, HD] the new rows are appended in the
-    same launch. Returns o [B, T, NQ, HD] bf16."""
+    same launch. A user with seq_lens[b] < T is an idle slot (zero output, nothing appended); lengths past
+    the block table and table entries outside the pool are reported in ``status`` (an int32 device word,
+    ``Status``). Returns o [B, T, NQ, HD] bf16."""
     dev = k_cache.device
     nb, nkv, block, hd = _pool_dims(k_cache, v_cache, dev)
     B, T, nq = q.shape[:3]
@@ -391,7 +436,7 @@ def paged_gqa_decode(q, k_cache, v_cache, block_table, seq_lens, scale, k_new=No
         ws = attention_workspace(B, T, nq, nkv, mb, pages_per_split, dev)
     call("qs_paged_gqa_decode", _p(q), _p(k_new), _p(v_new), _p(k_cache), _p(v_cache), _p(block_table),
          _p(seq_lens), _p(o), _p(ws), B, T, nq, nkv, hd, block, mb, nb, int(pages_per_split), float(scale),
-         _stream(dev))  # fmt: skip
+         _p(status), _stream(dev))  # fmt: skip
     return o
 
 
@@ -477,7 +522,7 @@ def rope_tables(positions, rot=ROT, theta=ROPE_THETA):
 
 
 def attn_mixer_decode(q, k_new, v_new, gate, wq, wk, cos, sin, k_cache, v_cache, block_table, seq_lens,
-                      pages_per_split=4, eps=EPS, rot=ROT, out=None, ws=None):  # fmt: skip
+                      pages_per_split=4, eps=EPS, rot=ROT, out=None, ws=None, status=None):  # fmt: skip
     """The attention mixer of a decode (T = 1) or verify (T > 1) step around the paged cache (model.py:237-246):
     qn = rope(rmsnorm(q) * wq), kn = bf16(rope(rmsnorm(k_new) * wk)) appended with v_new at positions
     seq_lens - T + t, o = bf16(softmax(qn K^T) V * sigmoid(gate)).
@@ -504,6 +549,6 @@ def attn_mixer_decode(q, k_new, v_new, gate, wq, wk, cos, sin, k_cache, v_cache,
         ws = attention_workspace(B, T, nq, nkv, mb, pages_per_split, dev)
     call("qs_attn_mixer_decode", _p(q), _p(k_new), _p(v_new), _p(gate), _p(wq), _p(wk),
          _p(cos if rot else None), _p(sin if rot else None), rot, _p(k_cache), _p(v_cache), _p(block_table),
-         _p(seq_lens), _p(o), _p(ws), B, T, nq, nkv, hd, block, mb, nb, pages_per_split, float(eps),
+         _p(seq_lens), _p(o), _p(ws), B, T, nq, nkv, hd, block, mb, nb, pages_per_split, float(eps), _p(status),
          _stream(dev))  # fmt: skip
     return o
