@@ -88,6 +88,16 @@ int qs_gdn_decode_fused(const uint16_t *x, uint16_t *conv_state, const uint16_t 
                         const float *beta, float *state, uint16_t *o, uint16_t *y_out, void *workspace, int B,
                         int NK, int NV, int DK, int DV, int K, float scale, float eps, void *stream);
 
+/* qs_gdn_decode_fused for callers that cannot allocate (code under HIP graph capture, serving loops that
+ * forbid hipMalloc): the same kernels, with the conv counters in a static device array of the library
+ * (64 KB per device, held until the process ends) instead of a workspace. No counterpart in the reference.
+ * B * NK <= 8192 (QS_EINVAL beyond). No call allocates or frees device memory; the first call on a device
+ * looks the array up and clears it with a fill kernel on the given stream. Every call on one device shares
+ * the array, so calls that overlap on a device (concurrent streams) race. */
+int qs_gdn_decode_fused_noalloc(const uint16_t *x, uint16_t *conv_state, const uint16_t *taps, const float *g,
+                                const float *beta, float *state, uint16_t *o, uint16_t *y_out, int B, int NK,
+                                int NV, int DK, int DV, int K, float scale, float eps, void *stream);
+
 /* Gated RMSNorm epilogue of the GDN mixer (the path's edge, torch model.py:274-275): for each row of DV
  * values, out = bf16(o * rsqrt(mean(o^2) + eps) * norm_w * silu(z)). o, z, out [rows, DV] bf16 (rows = B * NV,
  * or B * T * NV after a verify step; z is the projection's z slice), norm_w [DV] fp32. Replaces steps 7-8

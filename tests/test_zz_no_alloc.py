@@ -1,0 +1,52 @@
+"""The allocation-free fused GDN decode (qs_gdn_decode_fused_noalloc, counters in the library's static device
+array) against the workspace entry point qs_gdn_decode_fused, both called through the C ABI: two calls in a
+row, the second with a smaller batch, each bit-identical to the workspace entry point on a copy of the same
+inputs (the same kernels run; only where the counters live differs), and an oversized batch is rejected."""
+import ctypes
+
+import pytest
+import torch
+
+from qwen36_state import ops, workloads as W
+
+pytestmark = pytest.mark.gpu
+NK, NV, DK, DV = 16, 48, 128, 128
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def run(entry, d, B, ws=None):
+    L = ops.lib()
+    o = torch.empty(B, NV, DV, dtype=torch.bfloat16, device=d["x"].device)
+    y = torch.empty_like(d["x"])
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    args = [_p(d["x"]), _p(d["conv_state"]), _p(d["taps"]), _p(d["g"]), _p(d["beta"]), _p(d["state"]), _p(o), _p(y)]
+    if ws is not None:
+        args.append(_p(ws))
+    rc = getattr(L, entry)(*args, B, NK, NV, DK, DV, 4, ctypes.c_float(DK**-0.5), ctypes.c_float(1e-6), st)
+    assert rc == 0, L.qs_last_error().decode()
+    return o, y
+
+
+@pytest.mark.parametrize("batches", [(8, 3)])
+def test_noalloc_equals_workspace_entry(dev, batches):
+    L = ops.lib()
+    for i, B in enumerate(batches):
+        d = W.gdn_layer(B, dev, seed=70 + i)
+        a = {k: v.clone() for k, v in d.items()}
+        ws = torch.zeros(L.qs_gdn_workspace_bytes(B, NK), dtype=torch.uint8, device=dev)
+        o1, y1 = run("qs_gdn_decode_fused", a, B, ws)
+        o2, y2 = run("qs_gdn_decode_fused_noalloc", d, B)
+        torch.cuda.synchronize()
+        assert torch.equal(o1, o2) and torch.equal(y1, y2), B
+        assert torch.equal(a["state"], d["state"]) and torch.equal(a["conv_state"], d["conv_state"]), B
+
+
+def test_noalloc_rejects_oversized_batch(dev):
+    L = ops.lib()
+    f = ctypes.c_void_p(0x1000)
+    rc = L.qs_gdn_decode_fused_noalloc(f, f, f, f, f, f, f, ctypes.c_void_p(0), 1024, 16, 48, 128, 128, 4,
+                                       ctypes.c_float(0.1), ctypes.c_float(1e-6), ctypes.c_void_p(0))  # fmt: skip
+    assert rc == -1 and "exceeds" in L.qs_last_error().decode()

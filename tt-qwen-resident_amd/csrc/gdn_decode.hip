@@ -9,6 +9,8 @@
 // (S^T k and S'^T q) sum a lane's rows in registers, then the row groups (lane bits 3..5) with one DPP step
 // and two lane swaps in a fixed order (bit-reproducible run to run), so no step needs a workgroup barrier.
 // The state is read once and written once per token.
+#include <mutex>
+
 #include "qs_common.h"
 
 namespace {
@@ -612,6 +614,72 @@ extern "C" int qs_gdn_decode_fused(const uint16_t *x, uint16_t *conv_state, cons
     a.B = B, a.T = 1, a.NK = NK, a.NV = NV, a.C = 2 * NK * DK + NV * DV, a.scale = scale, a.eps = eps;
     launch_gdn<true, false>(a, QS_STREAM(stream));
     return qs::launch_status("qs_gdn_decode_fused");
+}
+
+// ------------------------------------------------------------------------ allocation-free fused decode
+// qs_gdn_decode_fused with its conv counters in a file-scope device array instead of a caller workspace, for
+// callers that cannot allocate. Each device holds its own copy of the array until the process ends; host
+// code reaches it only through the address hipGetSymbolAddress returns for the current device (the array's
+// name in host code is a stand-in, not a device address). The counters self-reset like the workspace's, so
+// the array stays zero between calls; it is cleared once per device by a fill kernel at the first call.
+// Every call on one device shares the array: calls that overlap on a device (concurrent streams) race.
+namespace {
+constexpr int SCRATCH_INTS = 16384;  // 64 KB: two counters per (user, key head), B * NK <= 8192
+static __device__ __align__(256) int scratch[SCRATCH_INTS];
+
+__global__ void fill_zero_kernel(int *p, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+int *g_scratch_ptr[MAX_DEVICES] = {};
+
+// The current device's copy of `scratch` (looked up and cleared on the first call on that device).
+int scratch_of_current_device(int **out, hipStream_t st) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) {
+        qs::set_error("qs_gdn_decode_fused_noalloc: no usable current device (%d)", dev);
+        return QS_EHIP;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            qs::set_error("qs_gdn_decode_fused_noalloc: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+            return QS_EHIP;
+        }
+        fill_zero_kernel<<<SCRATCH_INTS / 256, 256, 0, st>>>(static_cast<int *>(p), SCRATCH_INTS);
+        if (int rc = qs::launch_status("qs_gdn_decode_fused_noalloc")) return rc;
+        g_scratch_ptr[dev] = static_cast<int *>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return QS_OK;
+}
+
+}  // namespace
+
+extern "C" int qs_gdn_decode_fused_noalloc(const uint16_t *x, uint16_t *conv_state, const uint16_t *taps,
+                                           const float *g, const float *beta, float *state, uint16_t *o,
+                                           uint16_t *y_out, int B, int NK, int NV, int DKa, int DVa, int K,
+                                           float scale, float eps, void *stream) {
+    QS_REQUIRE(x && conv_state && taps && g && beta && state && o, "qs_gdn_decode_fused_noalloc: null pointer");
+    if (int e = check_gdn_shapes(B, NK, NV, DKa, DVa)) return e;
+    QS_REQUIRE(K == KC, "qs_gdn_decode_fused_noalloc: only K = 4 taps are supported (got %d)", K);
+    QS_REQUIRE((long)B * NK * 2 <= SCRATCH_INTS, "qs_gdn_decode_fused_noalloc: B NK = %ld exceeds %d",
+               (long)B * NK, SCRATCH_INTS / 2);
+    if (int e = check_conv_alignment(x, conv_state, conv_state, taps, y_out)) return e;
+    int *counters = nullptr;
+    if (int e = scratch_of_current_device(&counters, QS_STREAM(stream))) return e;
+    GdnArgs a{};
+    a.x = x, a.conv_in = conv_state, a.conv_out = conv_state, a.taps = taps, a.y_out = y_out;
+    a.g = g, a.beta = beta, a.s_in = state, a.s_out = state, a.o = o;
+    a.counters = counters;
+    a.B = B, a.T = 1, a.NK = NK, a.NV = NV, a.C = 2 * NK * DK + NV * DV, a.scale = scale, a.eps = eps;
+    launch_gdn<true, false>(a, QS_STREAM(stream));
+    return qs::launch_status("qs_gdn_decode_fused_noalloc");
 }
 
 extern "C" int qs_gdn_verify_step(const uint16_t *x, const uint16_t *conv_state_in, uint16_t *conv_states_out,
