@@ -33,13 +33,15 @@ def run_case(dev, d, pps, fused=True):
 @pytest.mark.parametrize(
     "B,ctx,T,pps",
     [
-        (1, 32768, 1, 8),  # one layer at 32k context: 512 pages, 64 splits, 2-level merge tree
-        (8, 4096, 1, 8),  # batch 8 at 4k: 64 pages per user
-        (1, 8192, 4, 8),  # verify: 4 new rows, causal among them
-        (1, 32768, 1, 1),  # 512 splits: 3-level merge tree
+        (1, 32768, 1, 8),  # the 32k layer as benchmarked: 512 pages, 64 splits through the merge launch
+        (8, 4096, 1, 8),  # the batch-8 step's layer as benchmarked: 8 splits merged inside the launch
+        (8, 4096, 1, 4),  # 16 splits merged inside the launch (the limit)
+        (1, 8192, 4, 8),  # verify: 4 new rows, causal among them (24 query rows per KV head)
+        (1, 32768, 1, 1),  # 512 splits through the merge launch
         (2, 4096, 1, 64),  # one split: no merge
         (2, 3000, 6, 4),  # 36 query rows per KV head: the VALU kernel (two tokens per pass over the pages)
         (1, 700, 7, 64),  # VALU kernel, odd token count, one split
+        (3, 900, 2, 4),  # 12 query rows per KV head: two tokens on the one-tile MFMA kernel
     ],
 )
 def test_attention(dev, B, ctx, T, pps):
@@ -133,3 +135,32 @@ def test_in_launch_merge_counters_rearm(dev):
     for d, o in zip(data, outs):
         ref = O.gqa_decode(d["q"], d["k_cache"], d["v_cache"], d["block_table"], d["seq_lens"], d["scale"])
         assert_attn_output(o, O.bf16(ref))
+
+
+@pytest.mark.parametrize("ctx,pps", [(131072, 64), (131072, 2), (262144, 4)])
+def test_attention_long_context(dev, ctx, pps):
+    """128k and 256k positions at batch 1 (the reference's published long-context decode points reach 256k):
+    32 splits of the widest split (64 pages), exactly the 1024-split limit, and 1024 splits at 256k."""
+    d = W.attn_layer(1, ctx, "cpu", seed=ctx // 1024 + pps, num_blocks=ctx // 64 + 64)
+    o, o_ref, same = run_case(dev, d, pps)
+    assert same
+    assert_attn_output(o, o_ref)
+
+
+def test_attention_split_limits(dev):
+    """More than 1024 splits or more than 64 pages per split are rejected before any launch."""
+    d = W.attn_layer(1, 131072, dev, seed=1, num_blocks=2048 + 64)
+    for pps in (1, 65):
+        with pytest.raises(ValueError, match="splits|pages_per_split"):
+            ops.paged_gqa_decode(d["q"], d["k_cache"], d["v_cache"], d["block_table"], d["seq_lens"], d["scale"],
+                                 pages_per_split=pps)  # fmt: skip
+
+
+def test_attention_negative_control(dev):
+    """The check fails when the oracle drops the appended row (a missed append dependency)."""
+    d = W.attn_layer(2, 40, "cpu", seed=12, num_blocks=64)  # 40 positions: the new row carries ~1/40 of the weight
+    o, ref, _ = run_case(dev, d, 4)
+    assert_attn_output(o, ref)
+    wrong = O.bf16(O.gqa_decode(d["q"], d["k_cache"], d["v_cache"], d["block_table"], d["seq_lens"] - 1, d["scale"]))
+    with pytest.raises(AssertionError):
+        assert_attn_output(o, wrong)

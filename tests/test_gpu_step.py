@@ -1,6 +1,6 @@
 """Whole steps of the 64-layer state path as they are benchmarked, every layer against its own oracle call:
 
-- the decode step at batch 8, 4096 positions, 4 pages per split (the in-launch merge of 16 splits);
+- the decode step at batch 8, 4096 positions, 8 pages per split (the in-launch merge of 8 splits);
 - three consecutive graph replays of a decode step whose positions cross a page boundary (4095, 4096,
   4097): each replay advances the positions on the device, and the oracle carries its own state, conv
   history and pools from step to step;
@@ -18,8 +18,8 @@ pytestmark = pytest.mark.gpu
 
 
 def test_decode_step_as_benched(dev):
-    """StatePathStep(8, 4096, pps 4): all 48 GDN and 16 attention layers of one graph replay."""
-    step = StatePathStep.synthetic(8, 4096, device=dev, pages_per_split=4, check=True)
+    """StatePathStep(8, 4096, pps 8): all 48 GDN and 16 attention layers of one graph replay."""
+    step = StatePathStep.synthetic(8, 4096, device=dev, pages_per_split=8, check=True)
     ref, inp = OracleState(step), inputs_of(step)
     step.capture()
     step.replay()

@@ -841,6 +841,302 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
     if (a.nsplit > 1 && a.nsplit <= MERGE_MAX) merge_in_launch<G>(a, b, g, tid);
 }
 
+// ------------------------------------------------------------------- MFMA kernel, independent waves (decode)
+// Up to 16 query rows per KV head (a one-token decode, or T G <= 16). One workgroup per (user, KV head, split
+// of pps pages), 4 waves; wave w owns rows 16 w .. 16 w + 15 of every page of the split and walks them on its
+// own, with no workgroup barrier inside the page loop:
+//   scores  S^T [16 rows x 16 q] = K Q^T on 8 v_mfma_f32_16x16x32_bf16 (K rows loaded as whole 512-byte rows
+//           and turned into the A operand through the wave's LDS slice, Q^T held in registers for the split);
+//   softmax the slice's max per query row (log2 domain); P = 2^(s - m) rounded to bf16 lands, lane for lane,
+//           in the B-operand layout of the P V product, so P never leaves the registers;
+//   P V     O^T [256 dims x 16 q] += V^T P on 16 v_mfma_f32_16x16x16_bf16, V^T read from the same LDS slice
+//           (now holding the page's 16 V rows) with the transposing ds_read_b64_tr_b16; the running max moves only when
+//           a slice max exceeds it by 2^8, so the accumulators are rarely rescaled.
+// Each wave keeps one page of K and V in flight (refilled as soon as consumed). At the end of the split the 4
+// waves' (max, sum, O) are merged in wave order through LDS, and the split's partial (or, with one split, the
+// output) is written as attn_mfma_kernel writes it, so the in-launch and separate merges are shared.
+template <int G, bool MIX>
+__global__ __launch_bounds__(256, 2) void attn_wave_kernel(AttnArgs a) {
+    constexpr int NQR = 16;
+    const int nwg = a.B * a.NKV * a.nsplit;
+    const int lid = qs::xcd_logical(blockIdx.x, nwg);
+    const int split = lid % a.nsplit;
+    const int g = (lid / a.nsplit) % a.NKV;
+    const int b = lid / (a.nsplit * a.NKV);
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int T = a.T;
+
+    __shared__ __align__(16) uint16_t s_q[NQR][QPAD];
+    __shared__ __align__(16) uint16_t s_ql[MIX ? NQR : 1][QPAD];  // mixer: bf16 residues of the fp32 q
+    __shared__ __align__(16) uint16_t s_kv[4][16][VPAD];           // each wave's 16 K, then V rows of the page
+    // the waves' O on their way to wave 0, in the K / V slices' space (used only after every wave's loop)
+    static_assert(sizeof(float) * 2 * NQR * (HD + 4) <= sizeof(uint16_t) * 4 * 16 * VPAD, "s_o fits s_kv");
+    auto s_o = reinterpret_cast<float (*)[NQR][HD + 4]>(&s_kv[0][0][0]);
+    __shared__ float s_ml[4][NQR][2];
+
+    const int p0 = split * a.pps;
+    const int *bt = a.block_table + (size_t)b * a.max_blocks;
+    const int bt_pre = p0 + lane < min(a.max_blocks, p0 + a.pps) ? bt[p0 + lane] : -1;
+    const int n = a.seq_lens[b];
+    constexpr int QCH = NQR * 32 / 256;
+    uint4 qreg[QCH];
+#pragma unroll
+    for (int k = 0; k < QCH; ++k) {
+        const int idx = tid + 256 * k, qr = idx >> 5, ch = idx & 31;
+        qreg[k] = make_uint4(0, 0, 0, 0);
+        if (qr < T * G) {
+            const int t = qr / G, hh = qr % G;
+            qreg[k] = *reinterpret_cast<const uint4 *>(a.q + (((size_t)b * T + t) * a.NQ + g * G + hh) * HD + ch * 8);
+        }
+    }
+    auto page_at = [&](int pi) {
+        const int pg = __builtin_amdgcn_readlane(bt_pre, pi - p0);
+        return (pg >= 0 && pg < a.num_blocks) ? pg : -1;
+    };
+    const size_t pstride = (size_t)a.NKV * BLK * HD;
+    // K and V rows load alike, two whole 512-byte rows per instruction (lane: row 2 k + lane / 32, 16 bytes at
+    // (lane % 32) 16): a gather of 16-byte pieces of 16 rows per instruction streams ~20% slower
+    auto load_k = [&](int pg, uint4 (&kb)[8]) {
+        const auto rk = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t *>(a.k_cache + (size_t)pg * pstride + (size_t)g * BLK * HD), (short)0, BLK * HD * 2,
+            0x00020000);
+        const int off = (16 * w + (lane >> 5)) * HD * 2 + (lane & 31) * 16;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, off, k * 1024, NT);
+            kb[k] = make_uint4(x[0], x[1], x[2], x[3]);
+        }
+    };
+    auto load_v = [&](int pg, uint4 (&vb)[8]) {
+        const auto rv = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t *>(a.v_cache + (size_t)pg * pstride + (size_t)g * BLK * HD), (short)0, BLK * HD * 2,
+            0x00020000);
+        const int off = (16 * w + (lane >> 5)) * HD * 2 + (lane & 31) * 16;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rv, off, k * 1024, NT);
+            vb[k] = make_uint4(x[0], x[1], x[2], x[3]);
+        }
+    };
+    uint4 KA[8], VA[8];
+    const int pg0 = p0 < a.max_blocks ? page_at(p0) : -1;
+    if (pg0 >= 0) {
+        load_k(pg0, KA);
+        load_v(pg0, VA);
+    }
+
+    if (!user_active(a, n, split == 0 && g == 0 && tid == 0)) {  // uniform over the user's workgroups
+        if (split == 0) zero_rows<G>(a, b, g, tid);
+        return;
+    }
+    const int base = n - T;
+    const int npages = (n + BLK - 1) / BLK;
+    const int p1 = min(npages, p0 + a.pps);
+    if (tid == 0)
+        for (int pi = p0; pi < p1; ++pi)
+            if (page_at(pi) < 0) report_page(a);
+
+    // fused append: wave w writes the new rows of its own slices and waits for them (it alone reads them back)
+    if (a.k_new && p0 < p1 && base / BLK < p1 && (n - 1) / BLK >= p0) {
+        for (int idx = lane; idx < T * 64; idx += 64) {
+            const int t = idx >> 6, kv = (idx >> 5) & 1, ch = idx & 31;
+            const int pos = base + t, pi = pos / BLK;
+            const size_t src = (((size_t)b * T + t) * a.NKV + g) * HD + ch * 8;
+            uint4 u = *reinterpret_cast<const uint4 *>((kv ? a.v_new : a.k_new) + src);
+            if (a.wk) {
+                float y[8];
+                const size_t rc = ((size_t)b * T + t) * (a.rot / 2);
+                mixer_chunk(u, ch, a.wk, a.rcos + rc, a.rsin + rc, a.rot, a.eps, y);
+                if (!kv) u = pack8(y);
+            }
+            if (pi < p0 || pi >= p1 || (pos % BLK) / 16 != w) continue;
+            const int pg = bt[pi];
+            if (pg < 0 || pg >= a.num_blocks) continue;  // reported with the split's pages above
+            const size_t dst = (((size_t)pg * a.NKV + g) * BLK + (pos % BLK)) * HD + ch * 8;
+            *reinterpret_cast<uint4 *>((kv ? a.v_cache : a.k_cache) + dst) = u;
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (pg0 >= 0 && base / BLK <= p0) {
+            load_k(pg0, KA);
+            load_v(pg0, VA);
+        }
+    }
+
+    // q rows (normalised and rotated for the mixer) through LDS into B-operand registers, kept for the split
+#pragma unroll
+    for (int k = 0; k < QCH; ++k) {
+        const int idx = tid + 256 * k, qr = idx >> 5, ch = idx & 31;
+        uint4 u = qreg[k];
+        if constexpr (MIX) {
+            float y[8];
+            const size_t rc = ((size_t)b * T + min(qr / G, T - 1)) * (a.rot / 2);
+            mixer_chunk(u, ch, a.wq, a.rcos + rc, a.rsin + rc, a.rot, a.eps, y);
+            u = pack8(y);
+            *reinterpret_cast<uint4 *>(&s_ql[qr][ch * 8]) = pack8_lo(y, u);
+        }
+        *reinterpret_cast<uint4 *>(&s_q[qr][ch * 8]) = u;
+    }
+    __syncthreads();
+    bf16x8_t qb[8], qlo[MIX ? 8 : 1];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        qb[j] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(&s_q[l16][32 * j + 8 * lg]));
+        if constexpr (MIX) qlo[j] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(&s_ql[l16][32 * j + 8 * lg]));
+    }
+
+    const float sl2 = a.scale * 1.4426950408889634f;
+    const int lim = l16 < T * G ? base + l16 / G : -1;  // this lane's query row sees positions <= lim
+    f32x4_t oacc[16];  // O^T of head dims 16 t + 4 lg + i, query row l16
+#pragma unroll
+    for (int t = 0; t < 16; ++t) oacc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float M = -INFINITY, L = 0.f;
+
+    for (int pi = p0; pi < p1; ++pi) {
+        const int pgn = pi + 1 < p1 ? page_at(pi + 1) : -1;
+        const bool ok = page_at(pi) >= 0;
+        const int r0w = pi * BLK + 16 * w;
+        // K rows through the wave's LDS slice into the A operand (row l16, dims 32 j + 8 lg .. + 7); the next
+        // page's K is requested as soon as the rows are in LDS. Scores of masked rows are replaced below.
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+            *reinterpret_cast<uint4 *>(&s_kv[w][2 * kk + (lane >> 5)][(lane & 31) * 8]) = KA[kk];
+        if (pgn >= 0) load_k(pgn, KA);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        bf16x8_t kb[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            kb[j] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(&s_kv[w][l16][32 * j + 8 * lg]));
+        f32x4_t sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb[j], qb[j], sacc, 0, 0, 0);
+            if constexpr (MIX) sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb[j], qlo[j], sacc, 0, 0, 0);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the K reads are done before V overwrites the slice
+        // this page's V rows into the slice (zero where invalid or past the length: a stale row times a zero
+        // probability could be NaN), then the next page's V into the registers
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+            const int row = 2 * kk + (lane >> 5);
+            const uint4 v = ok && r0w + row < n ? VA[kk] : make_uint4(0, 0, 0, 0);
+            *reinterpret_cast<uint4 *>(&s_kv[w][row][(lane & 31) * 8]) = v;
+        }
+        if (pgn >= 0) load_v(pgn, VA);
+        float sc[4], mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sc[i] = ok && r0w + 4 * lg + i <= lim ? sacc[i] : -INFINITY;
+            mx = fmaxf(mx, sc[i]);
+        }
+        mx = qs::xor32_max(qs::xor16_max(mx));
+        const float ms = mx * sl2;  // -inf when no row of the slice is visible to this query row
+        float e[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) e[i] = sc[i] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(fmaf(sc[i], sl2, -ms));
+        const uint32_t p01 = qs::cvt_pk_bf16(e[0], e[1]), p23 = qs::cvt_pk_bf16(e[2], e[3]);
+        float ls = (qs::bf_lo(p01) + qs::bf_hi(p01)) + (qs::bf_lo(p23) + qs::bf_hi(p23));
+        ls = qs::xor32_sum(qs::xor16_sum(ls));
+        const bool move = M == -INFINITY ? ms != -INFINITY : ms > M + 8.0f;
+        const float Mn = move ? ms : M;
+        if (__any(move)) {
+            const float alpha = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - Mn);
+            L *= alpha;
+#pragma unroll
+            for (int t = 0; t < 16; ++t) oacc[t] *= alpha;
+        }
+        M = Mn;
+        const float es = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - Mn);
+        L = fmaf(es, ls, L);
+        const i16x4_t pb = __builtin_bit_cast(i16x4_t, make_uint2(p01, p23));
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the V staging has landed in LDS
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            const i16x4_t av = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) i16x4_t *)&s_kv[w][4 * lg + (l16 >> 2)][16 * t + 4 * (l16 & 3)]);
+            const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+            oacc[t] += es * __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, pb, z, 0, 0, 0);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the reads are done before the next page's staging
+    }
+
+    // merge the 4 waves: global max and sum per query row (in wave order), then O added in wave order
+    // through LDS
+    if (lg == 0) {
+        s_ml[w][l16][0] = M;
+        s_ml[w][l16][1] = L;
+    }
+    __syncthreads();
+    auto row_ml = [&](int r, float &Mr, float &Lr) {
+        Mr = -INFINITY;
+#pragma unroll
+        for (int ww = 0; ww < 4; ++ww) Mr = fmaxf(Mr, s_ml[ww][r][0]);
+        Lr = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < 4; ++ww) {
+            const float mw = s_ml[ww][r][0];
+            Lr += (mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - Mr)) * s_ml[ww][r][1];
+        }
+    };
+    float Ms, Ls;
+    row_ml(l16, Ms, Ls);
+    const float sw = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - Ms);
+    // O of the live query rows (lanes l16 < T G) scaled to the common max, summed as (w0 + w1) + (w2 + w3):
+    // waves 1 and 3 hand theirs to waves 0 and 2, then wave 2 hands the pair sum to wave 0 (fixed order)
+    const bool live = l16 < T * G;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) oacc[t] *= sw;
+    if ((w & 1) && live)
+#pragma unroll
+        for (int t = 0; t < 16; ++t) *reinterpret_cast<f32x4_t *>(&s_o[w >> 1][l16][16 * t + 4 * lg]) = oacc[t];
+    __syncthreads();
+    if (!(w & 1) && live)
+#pragma unroll
+        for (int t = 0; t < 16; ++t) oacc[t] += *reinterpret_cast<const f32x4_t *>(&s_o[w >> 1][l16][16 * t + 4 * lg]);
+    __syncthreads();
+    if (w == 2 && live)
+#pragma unroll
+        for (int t = 0; t < 16; ++t) *reinterpret_cast<f32x4_t *>(&s_o[0][l16][16 * t + 4 * lg]) = oacc[t];
+    __syncthreads();
+    if (w == 0 && live) {
+        // the split's partial rows (or the output): lane l16's query row, dims 16 t + 4 lg .. + 3
+#pragma unroll
+        for (int t = 0; t < 16; ++t) oacc[t] += *reinterpret_cast<const f32x4_t *>(&s_o[0][l16][16 * t + 4 * lg]);
+        const int qr = l16, tt = qr / G, hh = qr % G;
+        if (a.nsplit == 1) {
+            const float inv = 1.0f / Ls;
+            const size_t oi = (((size_t)b * T + tt) * a.NQ + g * G + hh) * HD + 4 * lg;
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                f32x4_t v = oacc[t] * inv;
+                if (a.gate) {
+                    const uint2 gw = *reinterpret_cast<const uint2 *>(a.gate + oi + 16 * t);
+                    v[0] *= sigm(qs::bf_lo(gw.x)), v[1] *= sigm(qs::bf_hi(gw.x));
+                    v[2] *= sigm(qs::bf_lo(gw.y)), v[3] *= sigm(qs::bf_hi(gw.y));
+                }
+                *reinterpret_cast<uint2 *>(a.o + oi + 16 * t) =
+                    make_uint2(qs::cvt_pk_bf16(v[0], v[1]), qs::cvt_pk_bf16(v[2], v[3]));
+            }
+        } else {
+            const auto rpo = __builtin_amdgcn_make_buffer_rsrc(a.part_o + prow(a, G, b, g, split, 0) * HD, (short)0,
+                                                               T * G * HD * 4, 0x00020000);
+#pragma unroll
+            for (int t = 0; t < 16; ++t)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, oacc[t]), rpo,
+                                                       (qr * HD + 16 * t + 4 * lg) * 4, 0, qs::CP_SC1);
+        }
+    }
+    if (a.nsplit > 1 && tid < T * G) {
+        const auto rpm = __builtin_amdgcn_make_buffer_rsrc(a.part_ml + prow(a, G, b, g, split, 0) * 2, (short)0,
+                                                           T * G * 8, 0x00020000);
+        float Mr, Lr;
+        row_ml(tid, Mr, Lr);
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(Mr), __float_as_uint(Lr)}, rpm, tid * 8, 0,
+                                              qs::CP_SC1);
+    }
+    if (a.nsplit > 1 && a.nsplit <= MERGE_MAX) merge_in_launch<G>(a, b, g, tid);
+}
+
 // Merge of the splits of one output row (user, token, query head) in one memory round trip: wave w sums
 // splits w, w + 4, w + 8, ... (lane l owns head dims 4 l .. 4 l + 3), and every wave finds the global max M
 // (log2 domain, as the partials store it) and the sum L from all splits' (m, l), whose loads are in flight
@@ -970,10 +1266,10 @@ static int attn_launch(AttnArgs a, void *workspace, int HDa, int block, const ch
         const int QT = (T * G + 15) / 16;
 #define QS_MFMA_LAUNCH(GG)                                                              \
     if (a.wq) {                                                                         \
-        if (QT == 1) attn_mfma_kernel<GG, 1, true><<<grid, 256, 0, st>>>(a);            \
+        if (QT == 1) attn_wave_kernel<GG, true><<<grid, 256, 0, st>>>(a);               \
         else attn_mfma_kernel<GG, 2, true><<<grid, 256, 0, st>>>(a);                    \
     } else {                                                                            \
-        if (QT == 1) attn_mfma_kernel<GG, 1, false><<<grid, 256, 0, st>>>(a);           \
+        if (QT == 1) attn_wave_kernel<GG, false><<<grid, 256, 0, st>>>(a);              \
         else attn_mfma_kernel<GG, 2, false><<<grid, 256, 0, st>>>(a);                   \
     }
         switch (G) {

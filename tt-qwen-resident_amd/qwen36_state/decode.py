@@ -103,7 +103,7 @@ class StatePathStep:
     device: the rows cached per user before the next step (negative = idle slot), advanced by every step.
     status: an ``ops.Status`` the kernels report invalid lengths and table entries into, or None."""
 
-    def __init__(self, layers, block_table, lens, interval=4, pages_per_split=4, status=None):
+    def __init__(self, layers, block_table, lens, interval=4, pages_per_split=8, status=None):
         self.layer = layers
         self.layers, self.interval = len(layers), interval
         self.block_table, self.lens = block_table, lens
@@ -124,7 +124,7 @@ class StatePathStep:
         self.graph = None
 
     @classmethod
-    def synthetic(cls, B, ctx, layers=64, interval=4, device="cuda", seed=0, num_blocks=2048, pages_per_split=4,
+    def synthetic(cls, B, ctx, layers=64, interval=4, device="cuda", seed=0, num_blocks=2048, pages_per_split=8,
                   max_blocks=None, check=False):  # fmt: skip
         """Seeded buffers of the decode step at ``ctx`` positions: the first step appends at position
         ctx - 1 (lens starts at ctx - 1) and attends ctx positions. Per-user tables are disjoint slices of

@@ -408,7 +408,7 @@ def attention_workspace(B, T, nq, nkv, max_blocks, pages_per_split, device):
 
 
 def paged_gqa_decode(q, k_cache, v_cache, block_table, seq_lens, scale, k_new=None, v_new=None,
-                     pages_per_split=4, out=None, ws=None, status=None):  # fmt: skip
+                     pages_per_split=8, out=None, ws=None, status=None):  # fmt: skip
     """Paged GQA decode attention ``softmax(q K^T scale) V`` over each user's pages (model.py:239-244).
 
     q [B, T, NQ, HD] bf16; seq_lens [B] int32 = valid positions after this step; query t of user b sees
@@ -522,7 +522,7 @@ def rope_tables(positions, rot=ROT, theta=ROPE_THETA):
 
 
 def attn_mixer_decode(q, k_new, v_new, gate, wq, wk, cos, sin, k_cache, v_cache, block_table, seq_lens,
-                      pages_per_split=4, eps=EPS, rot=ROT, out=None, ws=None, status=None):  # fmt: skip
+                      pages_per_split=8, eps=EPS, rot=ROT, out=None, ws=None, status=None):  # fmt: skip
     """The attention mixer of a decode (T = 1) or verify (T > 1) step around the paged cache (model.py:237-246):
     qn = rope(rmsnorm(q) * wq), kn = bf16(rope(rmsnorm(k_new) * wk)) appended with v_new at positions
     seq_lens - T + t, o = bf16(softmax(qn K^T) V * sigmoid(gate)).
