@@ -16,7 +16,7 @@
 //               Tm (16 x 16 diagonal blocks by forward substitution, then the 32 x 32 and 64 x 64 levels of
 //               the block recursion [T1 0; -T2 A21 T1  T2] on fp32 MFMA) and the per-token scalars into the
 //               workspace (Tm and P as bf16 hi + lo planes);
-//   chunk_walk  one workgroup per (value head, 32-column slab of S): the 128 x 32 fp32 state slab stays
+//   chunk_walk  one 8-wave workgroup per (value head, 32-column slab of S): the 128 x 32 fp32 state slab stays
 //               on chip while the workgroup walks the chunks in order. Every product that touches S or d
 //               splits the fp32 operand into bf16 hi + lo halves (two MFMAs, three for Tm x X), so the
 //               state keeps fp32-level accuracy.
@@ -321,8 +321,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
 
 // ------------------------------------------------------------------------------------------------ walk
 
-typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
 
 // four fp32 -> bf16 hi = rne(x), lo = rne(x - hi), each as four packed bf16 (8 bytes)
 __device__ __forceinline__ void split4(float x0, float x1, float x2, float x3, uint2 &hi, uint2 &lo) {
@@ -341,21 +340,26 @@ __device__ __forceinline__ int kt_index(int d, int t) {
     return d * CH + ((((t >> 3) ^ (d ^ (d >> 3))) & 7) << 3) + (t & 7);
 }
 
-// One workgroup (4 waves) per (value head, 32-column slab of S). The slab's fp32 state lives in registers
-// (wave w owns state rows 32 w .. 32 w + 31, the layout of its S-update MFMA tiles) and is mirrored in LDS
-// as bf16 hi + lo planes, the operand of K S0 and Q S0. Every other operand sits in LDS in the orientation
-// its MFMA fragments read (S^T, X^T, d^T [v][token], K^T [d][token], K, Q, Tm, P [token][.]) and is split
-// into bf16 hi + lo once, by the wave that produces it. The next chunk's K, Q, V, Tm, P and scalars are
-// loaded into registers while the current chunk computes; reads past the sequence end return zeros through
-// the buffer descriptors' range checks and writes past it are dropped the same way.
-__global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
-    constexpr int SKP = DK + 16;  // bf16 row stride of the S^T planes (measured fastest of the 16-byte multiples)
-    constexpr int TP = CH + 16;   // bf16 row stride of the [.][token] planes (likewise)
+// One workgroup (8 waves) per (value head, 32-column slab of S). Wave (w, nh) = (wave / 2, wave % 2) owns the
+// 16-token tile w of every chunk product and the 16-column half nh of the slab; for the state update it owns
+// state rows 32 w .. 32 w + 31 of that column half. Two waves per SIMD interleave their dependent MFMA and
+// LDS chains, and each wave's chain per chunk is half the one a 4-wave workgroup walks. The slab's fp32
+// state lives in registers and is mirrored in LDS as bf16 hi + lo planes, the operand of K S0 and Q S0.
+// Every other operand sits in LDS in the orientation its MFMA fragments read (S^T, X^T, d^T [v][token],
+// K^T [d][token], K, Q, Tm, P [token][.]) and is split into bf16 hi + lo once, by the wave that produces it.
+// The next chunk's K, Q, V, Tm, P and scalars are loaded into registers while the current chunk computes;
+// reads past the sequence end return zeros through the buffer descriptors' range checks and writes past it
+// are dropped the same way.
+constexpr int WALK_THREADS = 512;
+__global__ __launch_bounds__(WALK_THREADS) void chunk_walk_kernel(PrefillArgs a) {
+    constexpr int SKP = DK + 16;  // bf16 row stride of the S^T planes
+    constexpr int TP = CH + 16;   // bf16 row stride of the [.][token] planes
     const int nwg = a.NV * NSLAB;
     const int lid = qs::xcd_logical(blockIdx.x, nwg);
     const int slab = lid % NSLAB, h = lid / NSLAB;
     const int kh = h / (a.NV / a.NK);
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int w = wv >> 1, nh = wv & 1;
     const int fr = lane & 15, fk = (lane >> 4) * 8, fq = (lane >> 4) * 4;
 
     __shared__ __align__(16) uint16_t sS[2][SLAB][SKP];
@@ -368,38 +372,36 @@ __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
     __shared__ __align__(16) uint16_t sX[2][SLAB][TP];
     __shared__ __align__(16) uint16_t sD[2][SLAB][TP];
     __shared__ __align__(16) uint16_t sE[2][SLAB][TP];
-    __shared__ __align__(16) float s_c[5][CH];
+    __shared__ __align__(16) float s_c[5 * CH];
 
-    // state rows 32 w + 16 mt + fq + i, columns 32 slab + 16 nt + fr
-    float S[2][2][4];
-    auto mirror = [&](int mt, int nt) {
+    // state rows 32 w + 16 mt + fq + i, column 32 slab + 16 nh + fr
+    float S[2][4];
+    auto mirror = [&](int mt) {
         uint2 hi, lo;
-        split4(S[mt][nt][0], S[mt][nt][1], S[mt][nt][2], S[mt][nt][3], hi, lo);
-        const int v = 16 * nt + fr, d = 32 * w + 16 * mt + fq;
+        split4(S[mt][0], S[mt][1], S[mt][2], S[mt][3], hi, lo);
+        const int v = 16 * nh + fr, d = 32 * w + 16 * mt + fq;
         *reinterpret_cast<uint2 *>(&sS[0][v][d]) = hi;
         *reinterpret_cast<uint2 *>(&sS[1][v][d]) = lo;
     };
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                S[mt][nt][i] = a.S0[((size_t)h * DK + 32 * w + 16 * mt + fq + i) * DV + SLAB * slab + 16 * nt + fr];
-            mirror(mt, nt);
-        }
+        for (int i = 0; i < 4; ++i)
+            S[mt][i] = a.S0[((size_t)h * DK + 32 * w + 16 * mt + fq + i) * DV + SLAB * slab + 16 * nh + fr];
+        mirror(mt);
+    }
 
-    // per-thread share of a chunk: K and Q rows 2 p + (m & 1), p = pp + 4 w + 16 (m >> 1), 16 bytes at
-    // group kc (each half-wave covers 8 groups x 4 row pairs); V rows 2 (tid / 8) and 2 (tid / 8) + 1,
-    // columns 4 (tid % 8) .. + 3; Tm and P 16-byte pieces tid + 256 m of their hi | lo planes; scalars tid
-    // and 256 + tid. K, Q, V of the next chunk are requested after the first barrier after K S0, Tm, P and
-    // the scalars after the second: no prefetch register is live while K S0 and Q S0 read their operands.
-    const int kc = (lane & 7) + 8 * (lane >> 5), pp = (lane >> 3) & 3;
+    // per-thread share of a chunk: 16-byte group kc = tid % 16 of K and Q rows 2 p and 2 p + 1, p = tid / 16
+    // (16 consecutive threads read one 256-byte row); V rows 2 (tid / 16) and + 1, columns 2 (tid % 16) .. + 1;
+    // Tm and P 16-byte pieces tid + 512 m of their hi | lo planes; scalars tid < 320. K, Q, V of the next
+    // chunk are requested after the barrier that follows K S0, Tm, P and the scalars after the next one: no
+    // prefetch register is live while K S0 and Q S0 read their operands (issued earlier, measured slower).
+    const int kc = tid & 15, pp = tid >> 4;
     const size_t krow = (size_t)a.NK * DK * 2, vrow = (size_t)a.NV * DV * 2;  // bytes per token
     // (vectors, not arrays: they stay in registers whatever the unroll order)
-    u32x16 pk, pq, ptm, ppm;
-    u32x2 pv0, pv1;
-    float psc0, psc1;
+    u32x8 pk, pq, ptm, ppm;
+    uint32_t pv0, pv1;
+    float psc;
     auto fetch_kqv = [&](int c) {
         const int t0 = c * CH, nv = min(CH, a.T - t0);
         const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.k) + (size_t)t0 * a.NK * DK,
@@ -409,228 +411,191 @@ __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
         const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.v) + (size_t)t0 * a.NV * DV,
                                                           (short)0, (int)(nv * vrow), 0x00020000);
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const int r = 2 * (pp + 4 * w + 16 * (m >> 1)) + (m & 1);
-            const int off = (int)(r * krow) + (kh * DK + kc * 8) * 2;
+        for (int m = 0; m < 2; ++m) {
+            const int off = (int)((2 * pp + m) * krow) + (kh * DK + kc * 8) * 2;
             const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0);
             const u32x4 y = __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0);
 #pragma unroll
             for (int j = 0; j < 4; ++j) pk[4 * m + j] = x[j], pq[4 * m + j] = y[j];
         }
-        const int vo = (int)(2 * (tid >> 3) * vrow) + (h * DV + SLAB * slab + (tid & 7) * 4) * 2;
-        pv0 = __builtin_amdgcn_raw_buffer_load_b64(rv, vo, 0, 0);
-        pv1 = __builtin_amdgcn_raw_buffer_load_b64(rv, vo + (int)vrow, 0, 0);
+        const int vo = (int)(2 * pp * vrow) + (h * DV + SLAB * slab + kc * 2) * 2;
+        pv0 = __builtin_amdgcn_raw_buffer_load_b32(rv, vo, 0, 0);
+        pv1 = __builtin_amdgcn_raw_buffer_load_b32(rv, vo + (int)vrow, 0, 0);
     };
     auto fetch_tp = [&](int c) {
         const size_t mat = ((size_t)c * a.NV + h) * CH * CH;
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const uint4 x = *reinterpret_cast<const uint4 *>(a.Tm + 2 * mat + (tid + 256 * m) * 8);
-            const uint4 y = *reinterpret_cast<const uint4 *>(a.P + 2 * mat + (tid + 256 * m) * 8);
+        for (int m = 0; m < 2; ++m) {
+            const uint4 x = *reinterpret_cast<const uint4 *>(a.Tm + 2 * mat + (tid + WALK_THREADS * m) * 8);
+            const uint4 y = *reinterpret_cast<const uint4 *>(a.P + 2 * mat + (tid + WALK_THREADS * m) * 8);
             ptm[4 * m] = x.x, ptm[4 * m + 1] = x.y, ptm[4 * m + 2] = x.z, ptm[4 * m + 3] = x.w;
             ppm[4 * m] = y.x, ppm[4 * m + 1] = y.y, ppm[4 * m + 2] = y.z, ppm[4 * m + 3] = y.w;
         }
-        const float *scg = a.sc + ((size_t)c * a.NV + h) * 5 * CH;
-        psc0 = scg[tid];
-        psc1 = scg[256 + (tid & 63)];
+        psc = tid < 5 * CH ? a.sc[((size_t)c * a.NV + h) * 5 * CH + tid] : 0.f;
     };
     fetch_kqv(0);
     fetch_tp(0);
 
     // a chunk's output rows are stored at the start of the next chunk, after that chunk's operands have
     // been waited for, so the stores never sit in front of a prefetch in the memory counter
-    f32x4 opend[2];
+    f32x4 opend;
     auto store_o = [&](int c) {
         const int t0 = c * CH, nv = min(CH, a.T - t0), r0 = 16 * w + fq;
         const auto ro = __builtin_amdgcn_make_buffer_rsrc(a.o + (size_t)t0 * a.NV * DV, (short)0, (int)(nv * vrow),
                                                           0x00020000);
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                __builtin_amdgcn_raw_buffer_store_b16((unsigned short)qs::cvt_pk_bf16(opend[nt][i], 0.f), ro,
-                                                      (int)((r0 + i) * vrow) + (h * DV + SLAB * slab + nt * 16 + fr) * 2, 0,
-                                                      0);
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_raw_buffer_store_b16((unsigned short)qs::cvt_pk_bf16(opend[i], 0.f), ro,
+                                                  (int)((r0 + i) * vrow) + (h * DV + SLAB * slab + nh * 16 + fr) * 2, 0,
+                                                  0);
     };
 
     for (int c = 0; c < a.nch; ++c) {
         // ---- this chunk's operands from registers into LDS
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const int r = 2 * (pp + 4 * w + 16 * (m >> 1)) + (m & 1);
+        for (int m = 0; m < 2; ++m) {
+            const int r = 2 * pp + m;
             *reinterpret_cast<uint4 *>(&sK[r][kc * 8]) = make_uint4(pk[4 * m], pk[4 * m + 1], pk[4 * m + 2], pk[4 * m + 3]);
             *reinterpret_cast<uint4 *>(&sQ[r][kc * 8]) = make_uint4(pq[4 * m], pq[4 * m + 1], pq[4 * m + 2], pq[4 * m + 3]);
         }
 #pragma unroll
-        for (int m2 = 0; m2 < 2; ++m2) {  // K^T: token pairs (2 p, 2 p + 1) as one 32-bit word per d
-            const int t = 2 * (pp + 4 * w + 16 * m2);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int d = kc * 8 + 2 * e;
-                const uint32_t ev = pk[8 * m2 + e], od = pk[8 * m2 + 4 + e];
-                *reinterpret_cast<uint32_t *>(&sKt[kt_index(d, t)]) = (ev & 0xffffu) | (od << 16);
-                *reinterpret_cast<uint32_t *>(&sKt[kt_index(d + 1, t)]) = (ev >> 16) | (od & 0xffff0000u);
-            }
+        for (int e = 0; e < 4; ++e) {  // K^T: token pair (2 pp, 2 pp + 1) as one 32-bit word per d
+            const int d = kc * 8 + 2 * e;
+            const uint32_t ev = pk[e], od = pk[4 + e];
+            *reinterpret_cast<uint32_t *>(&sKt[kt_index(d, 2 * pp)]) = (ev & 0xffffu) | (od << 16);
+            *reinterpret_cast<uint32_t *>(&sKt[kt_index(d + 1, 2 * pp)]) = (ev >> 16) | (od & 0xffff0000u);
+        }
+        {  // V^T: the token pair as one 32-bit word per column
+            const int col = kc * 2, t = 2 * pp;
+            *reinterpret_cast<uint32_t *>(&sVt[col][t]) = (pv0 & 0xffffu) | (pv1 << 16);
+            *reinterpret_cast<uint32_t *>(&sVt[col + 1][t]) = (pv0 >> 16) | (pv1 & 0xffff0000u);
         }
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {  // V^T: token pairs as one 32-bit word per column
-            const int col = (tid & 7) * 4 + 2 * e, t = 2 * (tid >> 3);
-            *reinterpret_cast<uint32_t *>(&sVt[col][t]) = (pv0[e] & 0xffffu) | (pv1[e] << 16);
-            *reinterpret_cast<uint32_t *>(&sVt[col + 1][t]) = (pv0[e] >> 16) | (pv1[e] & 0xffff0000u);
-        }
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const int idx = tid + 256 * m;
+        for (int m = 0; m < 2; ++m) {
+            const int idx = tid + WALK_THREADS * m;
             *reinterpret_cast<uint4 *>(&sTm[idx >> 9][(idx >> 3) & 63][(idx & 7) * 8]) =
                 make_uint4(ptm[4 * m], ptm[4 * m + 1], ptm[4 * m + 2], ptm[4 * m + 3]);
             *reinterpret_cast<uint4 *>(&sP[idx >> 9][(idx >> 3) & 63][(idx & 7) * 8]) =
                 make_uint4(ppm[4 * m], ppm[4 * m + 1], ppm[4 * m + 2], ppm[4 * m + 3]);
         }
-        s_c[tid >> 6][tid & 63] = psc0;
-        if (tid < 64) s_c[4][tid] = psc1;
+        if (tid < 5 * CH) s_c[tid] = psc;
         if (c > 0) store_o(c - 1);
         __syncthreads();
 
-        // ---- K S0 and Q S0 for token tile w (S0 as hi + lo); every fragment is requested before the first
-        // MFMA (the scheduler barrier keeps the reads together)
-        f32x4 kacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-        f32x4 qacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        // ---- K S0 and Q S0 for token tile w, column half nh (S0 as hi + lo); every fragment is requested
+        // before the first MFMA (the scheduler barrier keeps the reads together)
+        f32x4 kacc = {0.f, 0.f, 0.f, 0.f}, qacc = {0.f, 0.f, 0.f, 0.f};
         {
-            bf16x8 ak[4], aq[4], bh[4][2], bl[4][2];
+            bf16x8 ak[4], aq[4], bh[4], bl[4];
 #pragma unroll
             for (int ks = 0; ks < DK / 32; ++ks) {
                 ak[ks] = frag(&sK[16 * w + fr][ks * 32 + fk]);
                 aq[ks] = frag(&sQ[16 * w + fr][ks * 32 + fk]);
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt) {
-                    bh[ks][nt] = frag(&sS[0][nt * 16 + fr][ks * 32 + fk]);
-                    bl[ks][nt] = frag(&sS[1][nt * 16 + fr][ks * 32 + fk]);
-                }
+                bh[ks] = frag(&sS[0][nh * 16 + fr][ks * 32 + fk]);
+                bl[ks] = frag(&sS[1][nh * 16 + fr][ks * 32 + fk]);
             }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int ks = 0; ks < DK / 32; ++ks)
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt) {
-                    kacc[nt] = mfma(ak[ks], bh[ks][nt], kacc[nt]);
-                    kacc[nt] = mfma(ak[ks], bl[ks][nt], kacc[nt]);
-                    qacc[nt] = mfma(aq[ks], bh[ks][nt], qacc[nt]);
-                    qacc[nt] = mfma(aq[ks], bl[ks][nt], qacc[nt]);
-                }
+            for (int ks = 0; ks < DK / 32; ++ks) {
+                kacc = mfma(ak[ks], bh[ks], kacc);
+                kacc = mfma(ak[ks], bl[ks], kacc);
+                qacc = mfma(aq[ks], bh[ks], qacc);
+                qacc = mfma(aq[ks], bl[ks], qacc);
+            }
         }
 
         // ---- X = beta V - (beta gamma r_k) (K S0), as X^T hi + lo
         {
             const int r0 = 16 * w + fq;
-            const float4 c0 = *reinterpret_cast<const float4 *>(&s_c[0][r0]);
-            const float4 c1 = *reinterpret_cast<const float4 *>(&s_c[1][r0]);
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                const int col = nt * 16 + fr;
-                const uint2 v4 = *reinterpret_cast<const uint2 *>(&sVt[col][r0]);
-                uint2 hi, lo;
-                split4(c0.x * qs::bf_lo(v4.x) - c1.x * kacc[nt][0], c0.y * qs::bf_hi(v4.x) - c1.y * kacc[nt][1],
-                       c0.z * qs::bf_lo(v4.y) - c1.z * kacc[nt][2], c0.w * qs::bf_hi(v4.y) - c1.w * kacc[nt][3], hi, lo);
-                *reinterpret_cast<uint2 *>(&sX[0][col][r0]) = hi;
-                *reinterpret_cast<uint2 *>(&sX[1][col][r0]) = lo;
-            }
+            const float4 c0 = *reinterpret_cast<const float4 *>(&s_c[0 * CH + r0]);
+            const float4 c1 = *reinterpret_cast<const float4 *>(&s_c[1 * CH + r0]);
+            const int col = nh * 16 + fr;
+            const uint2 v4 = *reinterpret_cast<const uint2 *>(&sVt[col][r0]);
+            uint2 hi, lo;
+            split4(c0.x * qs::bf_lo(v4.x) - c1.x * kacc[0], c0.y * qs::bf_hi(v4.x) - c1.y * kacc[1],
+                   c0.z * qs::bf_lo(v4.y) - c1.z * kacc[2], c0.w * qs::bf_hi(v4.y) - c1.w * kacc[3], hi, lo);
+            *reinterpret_cast<uint2 *>(&sX[0][col][r0]) = hi;
+            *reinterpret_cast<uint2 *>(&sX[1][col][r0]) = lo;
         }
         __syncthreads();
         if (c + 1 < a.nch) fetch_kqv(c + 1);  // lands during d, O, S and the next fill
 
         // ---- d = Tm X (hi*hi + hi*lo + lo*hi), as d^T hi + lo and e^T = (d (r_k gamma_C / gamma))^T hi + lo
         {
-            f32x4 dacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-            bf16x8 th[2], tl[2], xh[2][2], xl[2][2];
+            f32x4 dacc = {0.f, 0.f, 0.f, 0.f};
+            bf16x8 th[2], tl[2], xh[2], xl[2];
 #pragma unroll
             for (int ks = 0; ks < CH / 32; ++ks) {
                 th[ks] = frag(&sTm[0][16 * w + fr][ks * 32 + fk]);
                 tl[ks] = frag(&sTm[1][16 * w + fr][ks * 32 + fk]);
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt) {
-                    xh[ks][nt] = frag(&sX[0][nt * 16 + fr][ks * 32 + fk]);
-                    xl[ks][nt] = frag(&sX[1][nt * 16 + fr][ks * 32 + fk]);
-                }
+                xh[ks] = frag(&sX[0][nh * 16 + fr][ks * 32 + fk]);
+                xl[ks] = frag(&sX[1][nh * 16 + fr][ks * 32 + fk]);
             }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int ks = 0; ks < CH / 32; ++ks)
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt) {
-                    dacc[nt] = mfma(th[ks], xh[ks][nt], dacc[nt]);
-                    dacc[nt] = mfma(th[ks], xl[ks][nt], dacc[nt]);
-                    dacc[nt] = mfma(tl[ks], xh[ks][nt], dacc[nt]);
-                }
-            const int r0 = 16 * w + fq;
-            const float4 c3 = *reinterpret_cast<const float4 *>(&s_c[3][r0]);
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                const int col = nt * 16 + fr;
-                uint2 hi, lo;
-                split4(dacc[nt][0], dacc[nt][1], dacc[nt][2], dacc[nt][3], hi, lo);
-                *reinterpret_cast<uint2 *>(&sD[0][col][r0]) = hi;
-                *reinterpret_cast<uint2 *>(&sD[1][col][r0]) = lo;
-                split4(dacc[nt][0] * c3.x, dacc[nt][1] * c3.y, dacc[nt][2] * c3.z, dacc[nt][3] * c3.w, hi, lo);
-                *reinterpret_cast<uint2 *>(&sE[0][col][r0]) = hi;
-                *reinterpret_cast<uint2 *>(&sE[1][col][r0]) = lo;
+            for (int ks = 0; ks < CH / 32; ++ks) {
+                dacc = mfma(th[ks], xh[ks], dacc);
+                dacc = mfma(th[ks], xl[ks], dacc);
+                dacc = mfma(tl[ks], xh[ks], dacc);
             }
+            const int r0 = 16 * w + fq;
+            const float4 c3 = *reinterpret_cast<const float4 *>(&s_c[3 * CH + r0]);
+            const int col = nh * 16 + fr;
+            uint2 hi, lo;
+            split4(dacc[0], dacc[1], dacc[2], dacc[3], hi, lo);
+            *reinterpret_cast<uint2 *>(&sD[0][col][r0]) = hi;
+            *reinterpret_cast<uint2 *>(&sD[1][col][r0]) = lo;
+            split4(dacc[0] * c3.x, dacc[1] * c3.y, dacc[2] * c3.z, dacc[3] * c3.w, hi, lo);
+            *reinterpret_cast<uint2 *>(&sE[0][col][r0]) = hi;
+            *reinterpret_cast<uint2 *>(&sE[1][col][r0]) = lo;
         }
         __syncthreads();
         if (c + 1 < a.nch) fetch_tp(c + 1);
 
-        // ---- O = (gamma r_q) (Q S0) + P d  (hi*hi + hi*lo + lo*hi) and S = gamma_C S0 + K^T e, where wave w
-        // owns state rows 32 w .. 32 w + 31; the fragments of both are requested before the first MFMA
+        // ---- O = (gamma r_q) (Q S0) + P d  (hi*hi + hi*lo + lo*hi) for token tile w, column half nh, and
+        // S = gamma_C S0 + K^T e for state rows 32 w .. 32 w + 31, column half nh; the fragments of both are
+        // requested before the first MFMA
         {
-            bf16x8 ap[2], apl[2], dh[2][2], dl[2][2], ka[2][2], eh[2][2], el[2][2];
+            bf16x8 ap[2], apl[2], dh[2], dl[2], ka[2][2], eh[2], el[2];
 #pragma unroll
             for (int ks = 0; ks < CH / 32; ++ks) {
                 ap[ks] = frag(&sP[0][16 * w + fr][ks * 32 + fk]);
                 apl[ks] = frag(&sP[1][16 * w + fr][ks * 32 + fk]);
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt) {
-                    dh[ks][nt] = frag(&sD[0][nt * 16 + fr][ks * 32 + fk]);
-                    dl[ks][nt] = frag(&sD[1][nt * 16 + fr][ks * 32 + fk]);
-                    eh[ks][nt] = frag(&sE[0][nt * 16 + fr][ks * 32 + fk]);
-                    el[ks][nt] = frag(&sE[1][nt * 16 + fr][ks * 32 + fk]);
-                }
+                dh[ks] = frag(&sD[0][nh * 16 + fr][ks * 32 + fk]);
+                dl[ks] = frag(&sD[1][nh * 16 + fr][ks * 32 + fk]);
+                eh[ks] = frag(&sE[0][nh * 16 + fr][ks * 32 + fk]);
+                el[ks] = frag(&sE[1][nh * 16 + fr][ks * 32 + fk]);
 #pragma unroll
                 for (int mt = 0; mt < 2; ++mt) ka[ks][mt] = frag(&sKt[kt_index(32 * w + 16 * mt + fr, ks * 32 + fk)]);
             }
             const int r0 = 16 * w + fq;
-            const float4 c2 = *reinterpret_cast<const float4 *>(&s_c[2][r0]);
-            const float gC = s_c[4][0];
+            const float4 c2 = *reinterpret_cast<const float4 *>(&s_c[2 * CH + r0]);
+            const float gC = s_c[4 * CH];
             __builtin_amdgcn_sched_barrier(0);
-            f32x4 oacc[2];
+            f32x4 oacc;
+            oacc[0] = c2.x * qacc[0];
+            oacc[1] = c2.y * qacc[1];
+            oacc[2] = c2.z * qacc[2];
+            oacc[3] = c2.w * qacc[3];
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                oacc[nt][0] = c2.x * qacc[nt][0];
-                oacc[nt][1] = c2.y * qacc[nt][1];
-                oacc[nt][2] = c2.z * qacc[nt][2];
-                oacc[nt][3] = c2.w * qacc[nt][3];
+            for (int ks = 0; ks < CH / 32; ++ks) {
+                oacc = mfma(ap[ks], dh[ks], oacc);
+                oacc = mfma(ap[ks], dl[ks], oacc);
+                oacc = mfma(apl[ks], dh[ks], oacc);
             }
+            opend = oacc;
 #pragma unroll
-            for (int ks = 0; ks < CH / 32; ++ks)
+            for (int mt = 0; mt < 2; ++mt) {
+                f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt) {
-                    oacc[nt] = mfma(ap[ks], dh[ks][nt], oacc[nt]);
-                    oacc[nt] = mfma(ap[ks], dl[ks][nt], oacc[nt]);
-                    oacc[nt] = mfma(apl[ks], dh[ks][nt], oacc[nt]);
+                for (int ks = 0; ks < CH / 32; ++ks) {
+                    sacc = mfma(ka[ks][mt], eh[ks], sacc);
+                    sacc = mfma(ka[ks][mt], el[ks], sacc);
                 }
-            opend[0] = oacc[0], opend[1] = oacc[1];
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt) {
-                    f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int ks = 0; ks < CH / 32; ++ks) {
-                        sacc = mfma(ka[ks][mt], eh[ks][nt], sacc);
-                        sacc = mfma(ka[ks][mt], el[ks][nt], sacc);
-                    }
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) S[mt][nt][i] = fmaf(gC, S[mt][nt][i], sacc[i]);
-                    mirror(mt, nt);
-                }
+                for (int i = 0; i < 4; ++i) S[mt][i] = fmaf(gC, S[mt][i], sacc[i]);
+                mirror(mt);
+            }
         }
         __syncthreads();
     }
@@ -639,10 +604,8 @@ __global__ __launch_bounds__(256) void chunk_walk_kernel(PrefillArgs a) {
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                a.ST[((size_t)h * DK + 32 * w + 16 * mt + fq + i) * DV + SLAB * slab + 16 * nt + fr] = S[mt][nt][i];
+        for (int i = 0; i < 4; ++i)
+            a.ST[((size_t)h * DK + 32 * w + 16 * mt + fq + i) * DV + SLAB * slab + 16 * nh + fr] = S[mt][i];
 }
 
 struct PrefillWs {
@@ -689,6 +652,6 @@ extern "C" int qs_gdn_chunk_prefill(const uint16_t *q, const uint16_t *k, const 
     hipStream_t st = QS_STREAM(stream);
     chunk_prep_kernel<<<a.nch * NV, 256, 0, st>>>(a);
     if (int e = qs::launch_status("qs_gdn_chunk_prefill (prep)")) return e;
-    chunk_walk_kernel<<<NV * NSLAB, 256, 0, st>>>(a);
+    chunk_walk_kernel<<<NV * NSLAB, WALK_THREADS, 0, st>>>(a);
     return qs::launch_status("qs_gdn_chunk_prefill (walk)");
 }
