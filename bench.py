@@ -236,7 +236,8 @@ def gdn_call(d, B, ws, stream, out):
 
     return "qs_gdn_decode_fused", (
         _p(d["x"]), _p(d["conv_state"]), _p(d["taps"]), _p(d["g"]), _p(d["beta"]), _p(d["state"]), _p(out),
-        ctypes.c_void_p(0), _p(ws), B, NK, NV, DK, DV, CONV_K, ctypes.c_float(DK**-0.5), ctypes.c_float(1e-6),
+        ctypes.c_void_p(0), _p(ws), ctypes.c_void_p(0), B, NK, NV, DK, DV, CONV_K, ctypes.c_float(DK**-0.5),
+        ctypes.c_float(1e-6),
         stream,
     )  # fmt: skip
 

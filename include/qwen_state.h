@@ -83,10 +83,13 @@ size_t qs_gdn_workspace_bytes(int B, int NK);
 
 /* Conv1d update + L2-norm + delta rule of one decode step in one launch (a1+a2+a4): the GDN mixer state
  * path of torch_step model.py:255-273 behind the projection. x [B, C] is the projection's q|k|v slice
- * (C = 2 NK DK + NV DV); conv_state is shifted in place; y_out (nullable) receives the conv output. */
+ * (C = 2 NK DK + NV DV); conv_state is shifted in place; y_out (nullable) receives the conv output.
+ * lens (nullable, [B] device int32, the step's sequence lengths): a user with lens[b] < 0 is an idle slot
+ * whose state, conv history and output are left untouched. */
 int qs_gdn_decode_fused(const uint16_t *x, uint16_t *conv_state, const uint16_t *taps, const float *g,
-                        const float *beta, float *state, uint16_t *o, uint16_t *y_out, void *workspace, int B,
-                        int NK, int NV, int DK, int DV, int K, float scale, float eps, void *stream);
+                        const float *beta, float *state, uint16_t *o, uint16_t *y_out, void *workspace,
+                        const int *lens, int B, int NK, int NV, int DK, int DV, int K, float scale, float eps,
+                        void *stream);
 
 /* qs_gdn_decode_fused for callers that cannot allocate (code under HIP graph capture, serving loops that
  * forbid hipMalloc): the same kernels, with the conv counters in a static device array of the library
@@ -95,8 +98,8 @@ int qs_gdn_decode_fused(const uint16_t *x, uint16_t *conv_state, const uint16_t 
  * looks the array up and clears it with a fill kernel on the given stream. Every call on one device shares
  * the array, so calls that overlap on a device (concurrent streams) race. */
 int qs_gdn_decode_fused_noalloc(const uint16_t *x, uint16_t *conv_state, const uint16_t *taps, const float *g,
-                                const float *beta, float *state, uint16_t *o, uint16_t *y_out, int B, int NK,
-                                int NV, int DK, int DV, int K, float scale, float eps, void *stream);
+                                const float *beta, float *state, uint16_t *o, uint16_t *y_out, const int *lens,
+                                int B, int NK, int NV, int DK, int DV, int K, float scale, float eps, void *stream);
 
 /* Gated RMSNorm epilogue of the GDN mixer (the path's edge, torch model.py:274-275): for each row of DV
  * values, out = bf16(o * rsqrt(mean(o^2) + eps) * norm_w * silu(z)). o, z, out [rows, DV] bf16 (rows = B * NV,

@@ -29,7 +29,7 @@ def test_exports_every_declared_symbol():
         assert hasattr(L, n), n
         assert n in _lib.SIGNATURES, n
     assert set(_lib.SIGNATURES) == set(names)
-    assert L.qs_abi_version() == 2
+    assert L.qs_abi_version() == 3
 
 
 def test_rejects_bad_arguments():

@@ -1,0 +1,143 @@
+"""The vLLM-facing adapter of the state path against the oracle, with random vLLM-style page tables (each user a
+random set of blocks of a shared pool): two prompts prefilled into decode slots 0 and 2 (slot 1 idle), then
+three decode steps of the batch. Checked at every call: the pools on every page bit-exact against the index
+oracle's fill and appends; the prompt's conv carry bit-exact against the oracle's prompt conv; the prompt's
+GDN state against the sequential recurrence (prefill tolerance) from the kernel's own conv outputs; the decode
+steps against the oracle's decode from the raw projection slice (with the perturbed-head accounting of the
+fused GDN tests); the idle slot untouched bit for bit; a position past max_seq_len rejected."""
+import pytest
+import torch
+from conftest import (
+    assert_attn_output,
+    assert_bf16_output,
+    assert_prefill_state,
+    assert_state,
+    assert_state_perturbed,
+    conv_mismatch_heads,
+    perturbed_ok,
+)
+
+from oracle import state_path as O
+from qwen36_state import ops
+from qwen36_state.vllm_adapter import StatePathAdapter
+from qwen36_state.workloads import C_QKV
+
+pytestmark = pytest.mark.gpu
+NK, NV, DK, DV, NKV, HD, NQ = 16, 48, 128, 128, 4, 256, 24
+LAYERS, B, MAX_LEN, NUM_BLOCKS = 4, 3, 512, 40  # layers 0-2 GDN, 3 attention; 8 blocks per user
+
+
+def prompt_inputs(T, gen):
+    out = []
+    for l in range(LAYERS):
+        if (l + 1) % 4 == 0:
+            out.append(dict(k=torch.randn(NKV, T, HD, generator=gen).bfloat16(),
+                            v=torch.randn(NKV, T, HD, generator=gen).bfloat16()))  # fmt: skip
+        else:
+            g = -torch.nn.functional.softplus(torch.randn(T, NV, generator=gen)) * torch.exp(-3 * torch.rand(T, NV, generator=gen))
+            out.append(dict(x=torch.randn(T, C_QKV + 64, generator=gen).bfloat16(), g=g,
+                            beta=torch.sigmoid(torch.randn(T, NV, generator=gen))))  # fmt: skip
+    return out
+
+
+def decode_inputs(gen):
+    out = []
+    for l in range(LAYERS):
+        if (l + 1) % 4 == 0:
+            out.append(dict(q=torch.randn(B, 1, NQ, HD, generator=gen).bfloat16(),
+                            k_new=torch.randn(B, 1, NKV, HD, generator=gen).bfloat16(),
+                            v_new=torch.randn(B, 1, NKV, HD, generator=gen).bfloat16()))  # fmt: skip
+        else:
+            g = -torch.nn.functional.softplus(torch.randn(B, NV, generator=gen)) * torch.exp(-3 * torch.rand(B, NV, generator=gen))
+            out.append(dict(x=torch.randn(B, C_QKV, generator=gen).bfloat16(), g=g,
+                            beta=torch.sigmoid(torch.randn(B, NV, generator=gen))))  # fmt: skip
+    return out
+
+
+def to(xs, dev):
+    return [{k: v.to(dev) for k, v in x.items()} for x in xs]
+
+
+def test_vllm_adapter_prefill_then_decode(dev):
+    gen = torch.Generator().manual_seed(2024)
+    ad = StatePathAdapter(B, MAX_LEN, layers=LAYERS, device=dev)
+    kv = ad.allocate_kv_cache((NUM_BLOCKS, NKV, 64, HD), torch.bfloat16, 1)
+    perm = torch.randperm(NUM_BLOCKS, generator=gen).to(torch.int32)
+    tables = perm[: B * 8].view(B, 8)  # vLLM-style: each slot a random set of blocks
+    taps = [t.cpu() for t in ad.taps]
+    # oracle state: the pools (whole, on the CPU), per GDN layer the slots' states and conv histories
+    kc, vc = torch.zeros(NUM_BLOCKS, NKV, 64, HD, dtype=torch.bfloat16), torch.zeros(NUM_BLOCKS, NKV, 64, HD, dtype=torch.bfloat16)
+    S = {l: torch.zeros(B, NV, DK, DV) for l in range(3)}
+    cs = {l: torch.zeros(B, C_QKV, 3) for l in range(3)}
+    pert = {l: torch.zeros(B, NV, dtype=torch.bool) for l in range(3)}
+    lens = [-1] * B
+    for slot, T in ((0, 100), (2, 37)):
+        inp = prompt_inputs(T, gen)
+        outs = ad.prefill_forward(to(inp, dev), tables[slot : slot + 1], kv, torch.tensor([T]), slot=slot)
+        O.paged_fill(kc, inp[3]["k"], tables[slot])
+        O.paged_fill(vc, inp[3]["v"], tables[slot])
+        for l in range(3):
+            x = inp[l]
+            y_ref, carry = O.conv1d_prefill(x["x"][:, :C_QKV].float(), None, taps[l].float())
+            assert torch.equal(ad.conv_state[l, slot].cpu().float(), carry), (slot, l)
+            cs[l][slot] = carry
+            # the state from the kernel's own conv outputs (their parity with the oracle is the conv tests')
+            q, k, v, _ = ops.causal_conv1d_prefill(x["x"].to(dev), ad.taps[l])
+            o_ref, S_ref = O.gdn_chunk_prefill(q.cpu().float(), k.cpu().float(), v.cpu().float(), x["g"], x["beta"],
+                                               torch.zeros(NV, DK, DV))  # fmt: skip
+            assert_prefill_state(ad.gdn_state[l, slot], S_ref)
+            assert_bf16_output(outs[l], O.bf16(o_ref))
+            S[l][slot] = ad.gdn_state[l, slot].cpu()  # continue from the kernel's prompt state
+        lens[slot] = T
+    assert torch.equal(kv[0][0].cpu(), kc) and torch.equal(kv[0][1].cpu(), vc)
+    idle_state = (ad.gdn_state[:, 1].clone(), ad.conv_state[:, 1].clone())
+
+    for step in range(3):
+        inp = decode_inputs(gen)
+        pos = torch.tensor(lens, dtype=torch.int32)
+        outs = ad.decode_forward(to(inp, dev), pos, page_table=tables)
+        active = [b for b in range(B) if lens[b] >= 0]
+        for l in range(3):
+            x = inp[l]
+            o_ref, S2, cs2, y_ref = O.gdn_decode(x["x"][active].float(), cs[l][active], taps[l].float(), x["g"][active],
+                                                 x["beta"][active], S[l][active], NK, NV, DK, DV)  # fmt: skip
+            st = ad.conv_state[l].cpu()
+            assert torch.equal(st[active].float(), cs2), (step, l)
+            y_k = ops.causal_conv1d_update(x["x"][active].to(dev), cs[l][active].bfloat16().to(dev), ad.taps[l]).cpu()
+            pert[l][active] |= conv_mismatch_heads(y_k, y_ref, NK, NV)
+            assert perturbed_ok(pert[l])
+            got = ad.gdn_state[l].cpu()[active]
+            ok = ~pert[l][active]
+            assert_state(got[ok], S2[ok])
+            if bool((~ok).any()):
+                assert_state_perturbed(got[~ok], S2[~ok])
+            assert_bf16_output(outs[l][active], O.bf16(o_ref))
+            S[l][active], cs[l][active] = S2, cs2
+        a = inp[3]
+        pos_a = torch.tensor([lens[b] for b in active], dtype=torch.int32)
+        O.paged_append(kc, vc, a["k_new"][active], a["v_new"][active], tables[active], pos_a)
+        o_ref = O.gqa_decode(a["q"][active], kc, vc, tables[active], pos_a + 1, HD**-0.5)
+        assert_attn_output(outs[3][active], O.bf16(o_ref))
+        assert torch.count_nonzero(outs[3][1]) == 0  # the idle slot's attention output is zero
+        assert torch.equal(kv[0][0].cpu(), kc) and torch.equal(kv[0][1].cpu(), vc), step
+        assert torch.equal(ad.gdn_state[:, 1], idle_state[0]) and torch.equal(ad.conv_state[:, 1], idle_state[1])
+        lens = [p + 1 if p >= 0 else p for p in lens]
+        assert ad.lens.cpu().tolist() == lens
+
+    with pytest.raises(ValueError, match="max_seq_len"):
+        ad.decode_forward(to(decode_inputs(gen), dev), torch.tensor([MAX_LEN, -1, 40], dtype=torch.int32))
+
+
+def test_vllm_adapter_rejects_bad_calls(dev):
+    ad = StatePathAdapter(2, 256, layers=4, device=dev)
+    with pytest.raises(ValueError, match="allocate_kv_cache"):
+        ad.decode_forward([], torch.tensor([0, 0]))
+    with pytest.raises(ValueError, match="kv_cache_shape"):
+        ad.allocate_kv_cache((16, 4, 32, 256), torch.bfloat16, 1)
+    with pytest.raises(ValueError, match="attention layers"):
+        ad.allocate_kv_cache((16, 4, 64, 256), torch.bfloat16, 2)
+    kv = ad.allocate_kv_cache((16, 4, 64, 256), torch.bfloat16, 1)
+    with pytest.raises(ValueError, match="one user"):
+        ad.prefill_forward([], torch.zeros(2, 4, dtype=torch.int32), kv, torch.tensor([10]))
+    with pytest.raises(ValueError, match="blocks"):
+        ad.prefill_forward([], torch.zeros(1, 1, dtype=torch.int32), kv, torch.tensor([100]))

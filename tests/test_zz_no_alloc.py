@@ -25,6 +25,7 @@ def run(entry, d, B, ws=None):
     args = [_p(d["x"]), _p(d["conv_state"]), _p(d["taps"]), _p(d["g"]), _p(d["beta"]), _p(d["state"]), _p(o), _p(y)]
     if ws is not None:
         args.append(_p(ws))
+    args.append(ctypes.c_void_p(0))  # lens: every user active
     rc = getattr(L, entry)(*args, B, NK, NV, DK, DV, 4, ctypes.c_float(DK**-0.5), ctypes.c_float(1e-6), st)
     assert rc == 0, L.qs_last_error().decode()
     return o, y
@@ -47,6 +48,6 @@ def test_noalloc_equals_workspace_entry(dev, batches):
 def test_noalloc_rejects_oversized_batch(dev):
     L = ops.lib()
     f = ctypes.c_void_p(0x1000)
-    rc = L.qs_gdn_decode_fused_noalloc(f, f, f, f, f, f, f, ctypes.c_void_p(0), 1024, 16, 48, 128, 128, 4,
+    rc = L.qs_gdn_decode_fused_noalloc(f, f, f, f, f, f, f, ctypes.c_void_p(0), ctypes.c_void_p(0), 1024, 16, 48, 128, 128, 4,
                                        ctypes.c_float(0.1), ctypes.c_float(1e-6), ctypes.c_void_p(0))  # fmt: skip
     assert rc == -1 and "exceeds" in L.qs_last_error().decode()

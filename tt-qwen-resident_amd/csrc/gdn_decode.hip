@@ -36,6 +36,7 @@ struct GdnArgs {
     uint16_t *o;                // [B, T, NV, DV]
     int *counters;              // decode + conv: [B, NK, 2] (q, k) self-resetting
     const int *in_slot;         // verify, nullable: [B] slot of s_in / conv_in holding user b's input
+    const int *lens;            // decode, nullable: [B]; a user with lens[b] < 0 (idle slot) is left untouched
     int n_slots;                // slots in s_in / conv_in
     int B, T, NK, NV, C;
     float scale, eps;
@@ -178,6 +179,9 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
     const int s = lid % NSLAB;
     const int h = (lid / NSLAB) % a.NV;
     const int b = lid / (NSLAB * a.NV);
+    // an idle slot keeps its state, conv history and output as they are (the workgroup's units belong to one
+    // user: a user's B NV NSLAB units are a multiple of WPG, so the exit is uniform over the workgroup)
+    if (!VERIFY && a.lens && a.lens[b] < 0) return;
     const int rep = a.NV / a.NK;
     const int kh = h / rep;
     const int lane = threadIdx.x & 63;
@@ -600,8 +604,8 @@ extern "C" size_t qs_gdn_workspace_bytes(int B, int NK) { return (size_t)(B > 0 
 
 extern "C" int qs_gdn_decode_fused(const uint16_t *x, uint16_t *conv_state, const uint16_t *taps, const float *g,
                                    const float *beta, float *state, uint16_t *o, uint16_t *y_out, void *workspace,
-                                   int B, int NK, int NV, int DKa, int DVa, int K, float scale, float eps,
-                                   void *stream) {
+                                   const int *lens, int B, int NK, int NV, int DKa, int DVa, int K, float scale,
+                                   float eps, void *stream) {
     QS_REQUIRE(x && conv_state && taps && g && beta && state && o && workspace,
                "qs_gdn_decode_fused: null pointer");
     if (int e = check_gdn_shapes(B, NK, NV, DKa, DVa)) return e;
@@ -611,6 +615,7 @@ extern "C" int qs_gdn_decode_fused(const uint16_t *x, uint16_t *conv_state, cons
     a.x = x, a.conv_in = conv_state, a.conv_out = conv_state, a.taps = taps, a.y_out = y_out;
     a.g = g, a.beta = beta, a.s_in = state, a.s_out = state, a.o = o;
     a.counters = static_cast<int *>(workspace);
+    a.lens = lens;
     a.B = B, a.T = 1, a.NK = NK, a.NV = NV, a.C = 2 * NK * DK + NV * DV, a.scale = scale, a.eps = eps;
     launch_gdn<true, false>(a, QS_STREAM(stream));
     return qs::launch_status("qs_gdn_decode_fused");
@@ -663,8 +668,8 @@ int scratch_of_current_device(int **out, hipStream_t st) {
 
 extern "C" int qs_gdn_decode_fused_noalloc(const uint16_t *x, uint16_t *conv_state, const uint16_t *taps,
                                            const float *g, const float *beta, float *state, uint16_t *o,
-                                           uint16_t *y_out, int B, int NK, int NV, int DKa, int DVa, int K,
-                                           float scale, float eps, void *stream) {
+                                           uint16_t *y_out, const int *lens, int B, int NK, int NV, int DKa,
+                                           int DVa, int K, float scale, float eps, void *stream) {
     QS_REQUIRE(x && conv_state && taps && g && beta && state && o, "qs_gdn_decode_fused_noalloc: null pointer");
     if (int e = check_gdn_shapes(B, NK, NV, DKa, DVa)) return e;
     QS_REQUIRE(K == KC, "qs_gdn_decode_fused_noalloc: only K = 4 taps are supported (got %d)", K);
@@ -677,6 +682,7 @@ extern "C" int qs_gdn_decode_fused_noalloc(const uint16_t *x, uint16_t *conv_sta
     a.x = x, a.conv_in = conv_state, a.conv_out = conv_state, a.taps = taps, a.y_out = y_out;
     a.g = g, a.beta = beta, a.s_in = state, a.s_out = state, a.o = o;
     a.counters = counters;
+    a.lens = lens;
     a.B = B, a.T = 1, a.NK = NK, a.NV = NV, a.C = 2 * NK * DK + NV * DV, a.scale = scale, a.eps = eps;
     launch_gdn<true, false>(a, QS_STREAM(stream));
     return qs::launch_status("qs_gdn_decode_fused_noalloc");

@@ -150,7 +150,7 @@ class StatePathStep:
                                  ws=self.attn_ws, status=st)  # fmt: skip
         else:
             ops.gdn_decode_fused(d["x"], d["conv_state"], d["taps"], d["g"], d["beta"], d["state"], out=d["o"],
-                                 ws=self.gdn_ws)  # fmt: skip
+                                 ws=self.gdn_ws, lens=self.lens)  # fmt: skip
 
     def step(self):
         """One eager step on the current stream: the position advance, then every layer in order."""

@@ -161,12 +161,13 @@ def gdn_decode_step(q, k, v, g, beta, state, scale=None, eps=EPS, out=None):
 
 
 def gdn_decode_fused(x, conv_state, taps, g, beta, state, nk=NK, scale=None, eps=EPS, out=None, y_out=None,
-                     ws=None):  # fmt: skip
+                     ws=None, lens=None):  # fmt: skip
     """Conv1d update + L2-norm + delta rule of one decode step in one launch (model.py:255-273).
 
     x [B, C] bf16 is the projection's q|k|v slice (C = 2 nk DK + NV DV); conv_state [B, C, 3] and state
     [B, NV, DK, DV] are updated in place. Returns o [B, NV, DV] bf16 (y_out, if given, receives the conv
-    output [B, C])."""
+    output [B, C]). lens [B] int32 (optional, the step's lengths): users with lens < 0 are idle slots, left
+    untouched."""
     dev = state.device
     _chk(state, "state", torch.float32)
     B, nv, dk, dv = state.shape
@@ -183,8 +184,10 @@ def gdn_decode_fused(x, conv_state, taps, g, beta, state, nk=NK, scale=None, eps
     _chk(o, "out", torch.bfloat16, (B, nv, dv), dev)
     if ws is None:
         ws = workspace("gdn", lib().qs_gdn_workspace_bytes(B, nk), dev)
+    if lens is not None:
+        _chk(lens, "lens", torch.int32, (B,), dev)
     call("qs_gdn_decode_fused", _p(x), _p(conv_state), _p(taps), _p(g), _p(beta), _p(state), _p(o), _p(y_out),
-         _p(ws), B, nk, nv, dk, dv, CONV_K, float(scale), float(eps), _stream(dev))  # fmt: skip
+         _p(ws), _p(lens), B, nk, nv, dk, dv, CONV_K, float(scale), float(eps), _stream(dev))  # fmt: skip
     return o
 
 
