@@ -4,9 +4,11 @@
 // Grid: one workgroup per (user, KV head, split); a split is `pps` (<= 64) consecutive block-table entries.
 // Every K/V byte is loaded once for all G query heads of the KV head (GQA reuse) and, in a verify step, for
 // all query tokens of the step. Two kernels walk the pages:
-//   attn_wave_kernel  up to 32 query rows per KV head (every one-token decode, verify steps up to T = 5 at
-//                     G = 6): MFMA scores and P V, each wave on its own 16-row slices with no barrier in the
-//                     page loop, one or two pages in flight per workgroup;
+//   attn_wave_kernel  up to 16 query rows per KV head (every one-token decode): MFMA scores and P V, each
+//                     wave on its own 16-row slices with no barrier in the page loop, one or two pages in
+//                     flight per workgroup;
+//   attn_mfma_kernel  17 to 32 query rows (verify steps up to T = 5 at G = 6): MFMA, the 4 waves on the same
+//                     page, each wave owning a quarter of the head dims in P V;
 //   attn_kernel       more query rows: VALU dot products, the 4 waves on the same page.
 // The new rows are appended first, by the wave that reads them back, so every row is read from the pool.
 // The splits' partials (m, l, unnormalised O per query row) go to the workspace and are merged in split order
@@ -467,6 +469,7 @@ typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int QPAD = HD + 8;   // s_q row pitch (bf16): 16-byte skew between rows
 constexpr int VPAD = HD + 16;  // K / V slice row pitch (bf16): 32-byte skew between rows
+constexpr int PPAD = 16 + 4;   // s_p row pitch (bf16)
 
 // Split merge inside the attention launch (nsplit <= MERGE_MAX). Every workgroup of (user b, KV head g) has
 // stored its partial with agent-coherent stores (sc1: written through the XCD's L2); each thread waits for
@@ -543,28 +546,321 @@ __device__ __forceinline__ void merge_in_launch(const AttnArgs &a, int b, int g,
     }
 }
 
+// ------------------------------------------------------------------------------ MFMA kernel (verify rows)
+// For T query tokens the T * G query rows of a KV head form a dense [T G x 256] x [256 x rows] product, so
+// the multi-token (verify) step runs it on MFMA. One workgroup per (user, KV head, split of pps pages),
+// walking its pages in order. Per page, in two phases separated by a barrier:
+//   scores  wave w takes rows 16 w .. 16 w + 15 (a 16-row slice): S^T [16 rows x 16 q] = K Q^T on 8
+//           v_mfma_f32_16x16x32_bf16 per 16-query-row tile (lane l holds K row l % 16, dims 32 j + 8 (l / 16)
+//           .. + 7: one 16-byte load per j), the slice's own max m_s per query row (log2 domain), P^T =
+//           2^(s - m_s) rounded to bf16 and its row sums l_s into LDS; the slice's V rows into LDS;
+//   P V     every wave adds the 4 slices in order to O^T [its 64 head dims x 16 q] on
+//           v_mfma_f32_16x16x16_bf16 (V^T read from LDS with the transposing ds_read_b64_tr_b16, P^T as
+//           written), scaled by 2^(m_s - M) against the running max M; M moves only when a slice max exceeds
+//           it by 2^8, so the accumulators are rarely rescaled.
+// All waves see the same slice maxima in the same order, so M and the sum L agree across waves, and the
+// 4 waves' head dims are disjoint: the split's partial needs no cross-wave merge.
+template <int G, int QT, bool MIX>
+__global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
+    constexpr int NQR = 16 * QT;
+    const int nwg = a.B * a.NKV * a.nsplit;
+    const int lid = qs::xcd_logical(blockIdx.x, nwg);
+    const int split = lid % a.nsplit;
+    const int g = (lid / a.nsplit) % a.NKV;
+    const int b = lid / (a.nsplit * a.NKV);
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int T = a.T;
+
+    __shared__ __align__(16) uint16_t s_q[NQR][QPAD];
+    __shared__ __align__(16) uint16_t s_ql[MIX ? NQR : 1][QPAD];  // mixer: bf16 residues of the fp32 q
+    __shared__ __align__(16) uint16_t s_v[4][16][VPAD];     // the page's V rows, slice by slice
+    __shared__ __align__(16) uint16_t s_p[4][QT][16][PPAD];  // P^T of each slice: [query row][slice row]
+    __shared__ float s_m[4][NQR], s_l[4][NQR];              // slice max (log2 domain) and row sum
+
+    // Issued first, in this order: the split's block-table entries, the user's length and the query rows.
+    // The first page's K / V loads then wait only for the table entries, not for the length.
+    const int p0 = split * a.pps;
+    const int *bt = a.block_table + (size_t)b * a.max_blocks;
+    const int bt_pre = p0 + lane < min(a.max_blocks, p0 + a.pps) ? bt[p0 + lane] : -1;
+    int n = a.seq_lens[b];
+    // query rows qr = t G + hh (zero past T G): loaded into registers now, stored to LDS once the first
+    // page's loads are in flight
+    constexpr int QCH = NQR * 32 / 256;
+    uint4 qreg[QCH];
+#pragma unroll
+    for (int k = 0; k < QCH; ++k) {
+        const int idx = tid + 256 * k, qr = idx >> 5, ch = idx & 31;
+        qreg[k] = make_uint4(0, 0, 0, 0);
+        if (qr < T * G) {
+            const int t = qr / G, hh = qr % G;
+            qreg[k] = *reinterpret_cast<const uint4 *>(a.q + (((size_t)b * T + t) * a.NQ + g * G + hh) * HD + ch * 8);
+        }
+    }
+
+    auto page_at = [&](int pi) {
+        const int pg = __builtin_amdgcn_readlane(bt_pre, pi - p0);
+        return (pg >= 0 && pg < a.num_blocks) ? pg : -1;
+    };
+    const size_t pstride = (size_t)a.NKV * BLK * HD;  // elements per page
+
+    auto load_k = [&](int pg, uint4 (&kb)[8]) {
+        const auto rk = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t *>(a.k_cache + (size_t)pg * pstride + (size_t)g * BLK * HD), (short)0, BLK * HD * 2,
+            0x00020000);
+        const int off = (16 * w + l16) * HD * 2 + lg * 16;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, off, j * 64, NT);
+            kb[j] = make_uint4(x[0], x[1], x[2], x[3]);
+        }
+    };
+    auto load_v = [&](int pg, uint4 (&vb)[8]) {
+        const auto rv = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t *>(a.v_cache + (size_t)pg * pstride + (size_t)g * BLK * HD), (short)0, BLK * HD * 2,
+            0x00020000);
+        const int off = (16 * w + (lane >> 5)) * HD * 2 + (lane & 31) * 16;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rv, off, k * 1024, NT);
+            vb[k] = make_uint4(x[0], x[1], x[2], x[3]);
+        }
+    };
+
+    // the first page's rows, before the length is known: a page in the pool's range that turns out to lie
+    // past the user's length is simply not used
+    uint4 KA[8], VA[8];
+    const int pg0 = p0 < a.max_blocks ? page_at(p0) : -1;
+    if (pg0 >= 0) {
+        load_k(pg0, KA);
+        load_v(pg0, VA);
+    }
+
+    if (!user_active(a, n, split == 0 && g == 0 && tid == 0)) {  // uniform over the user's workgroups
+        if (split == 0) zero_rows<G>(a, b, g, tid);
+        return;
+    }
+    const int base = n - T;  // first new position
+    const int npages = (n + BLK - 1) / BLK;
+    const int p1 = min(npages, p0 + a.pps);
+    if (tid == 0)
+        for (int pi = p0; pi < p1; ++pi)
+            if (page_at(pi) < 0) report_page(a);
+
+    // Fused append, first: wave w writes the new rows of its 16-row slices in this split's pages and waits
+    // for them, so its slice loads read them back from the pool. No other wave reads these slices.
+    if (a.k_new && p0 < p1 && base / BLK < p1 && (n - 1) / BLK >= p0) {
+        for (int idx = lane; idx < T * 64; idx += 64) {
+            const int t = idx >> 6, kv = (idx >> 5) & 1, ch = idx & 31;
+            const int pos = base + t, pi = pos / BLK;
+            const size_t src = (((size_t)b * T + t) * a.NKV + g) * HD + ch * 8;
+            uint4 u = *reinterpret_cast<const uint4 *>((kv ? a.v_new : a.k_new) + src);
+            if (a.wk) {  // k rows normalised and rotated (all lanes take part in the row reductions)
+                float y[8];
+                const size_t rc = ((size_t)b * T + t) * (a.rot / 2);
+                mixer_chunk(u, ch, a.wk, a.rcos + rc, a.rsin + rc, a.rot, a.eps, y);
+                if (!kv) u = pack8(y);
+            }
+            if (pi < p0 || pi >= p1 || (pos % BLK) / 16 != w) continue;
+            const int pg = bt[pi];
+            if (pg < 0 || pg >= a.num_blocks) continue;  // reported with the split's pages above
+            const size_t dst = (((size_t)pg * a.NKV + g) * BLK + (pos % BLK)) * HD + ch * 8;
+            *reinterpret_cast<uint4 *>((kv ? a.v_cache : a.k_cache) + dst) = u;
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (pg0 >= 0 && base / BLK <= p0) {  // new rows landed in the first page: read it again
+            load_k(pg0, KA);
+            load_v(pg0, VA);
+        }
+    }
+
+    const float sl2 = a.scale * 1.4426950408889634f;  // log2 domain
+    int lim[QT];  // the lane's causal limit per query-row tile: token qr / G sees positions <= base + token
+#pragma unroll
+    for (int nt = 0; nt < QT; ++nt) {
+        const int qr = l16 + 16 * nt;
+        lim[nt] = qr < T * G ? base + qr / G : -1;
+    }
+
+    f32x4_t oacc[QT][4];  // O^T of head dims 64 w + 16 dd + 4 lg + i (dd < 4), query row l16 + 16 nt
+    float M[QT], L[QT];
+#pragma unroll
+    for (int nt = 0; nt < QT; ++nt) {
+        M[nt] = -INFINITY;
+        L[nt] = 0.f;
+#pragma unroll
+        for (int dd = 0; dd < 4; ++dd) oacc[nt][dd] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // one page: scores of this wave's slice into LDS, barrier, every slice's P V into this wave's dims, barrier
+    // one page: scores of this wave's slice into LDS, barrier, every slice's P V into this wave's dims,
+    // barrier. kb / vb hold the page's K and V rows; each is refilled with the next page's rows as soon as
+    // it has been consumed (V after staging, K after the score MFMAs), so one buffer of each suffices.
+    auto page = [&](int pi, uint4 (&kb)[8], uint4 (&vb)[8]) {
+        const int pgn = pi + 1 < p1 ? page_at(pi + 1) : -1;
+        const bool ok = page_at(pi) >= 0;
+        const int r0w = pi * BLK + 16 * w;  // first position of this wave's slice
+        // V rows (zero where the page is invalid or past the user's length: a stale row times a zero
+        // probability could be NaN)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int row = 2 * k + (lane >> 5);
+            const uint4 v = ok && r0w + row < n ? vb[k] : make_uint4(0, 0, 0, 0);
+            *reinterpret_cast<uint4 *>(&s_v[w][row][(lane & 31) * 8]) = v;
+        }
+        if (pgn >= 0) load_v(pgn, vb);
+        f32x4_t sacc[QT];
+#pragma unroll
+        for (int nt = 0; nt < QT; ++nt) sacc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const bf16x8_t ak = __builtin_bit_cast(bf16x8_t, kb[j]);
+#pragma unroll
+            for (int nt = 0; nt < QT; ++nt) {
+                const bf16x8_t bq = __builtin_bit_cast(
+                    bf16x8_t, *reinterpret_cast<const uint4 *>(&s_q[l16 + 16 * nt][32 * j + 8 * lg]));
+                sacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, bq, sacc[nt], 0, 0, 0);
+                if constexpr (MIX) {
+                    const bf16x8_t bl = __builtin_bit_cast(
+                        bf16x8_t, *reinterpret_cast<const uint4 *>(&s_ql[l16 + 16 * nt][32 * j + 8 * lg]));
+                    sacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, bl, sacc[nt], 0, 0, 0);
+                }
+            }
+        }
+        if (pgn >= 0) load_k(pgn, kb);
+#pragma unroll
+        for (int nt = 0; nt < QT; ++nt) {
+            float sc[4];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sc[i] = ok && r0w + 4 * lg + i <= lim[nt] ? sacc[nt][i] : -INFINITY;
+                mx = fmaxf(mx, sc[i]);
+            }
+            mx = qs::xor32_max(qs::xor16_max(mx));
+            const float ms = mx * sl2;  // -inf when no row of the slice is visible to this query row
+            float e[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) e[i] = sc[i] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(fmaf(sc[i], sl2, -ms));
+            const uint32_t p01 = qs::cvt_pk_bf16(e[0], e[1]), p23 = qs::cvt_pk_bf16(e[2], e[3]);
+            *reinterpret_cast<uint2 *>(&s_p[w][nt][l16][4 * lg]) = make_uint2(p01, p23);
+            float ls = (qs::bf_lo(p01) + qs::bf_hi(p01)) + (qs::bf_lo(p23) + qs::bf_hi(p23));
+            ls = qs::xor32_sum(qs::xor16_sum(ls));
+            if (lg == 0) {
+                s_m[w][l16 + 16 * nt] = ms;
+                s_l[w][l16 + 16 * nt] = ls;
+            }
+        }
+        __syncthreads();
+        // P V: the 4 slices in order into this wave's head dims
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            i16x4_t av[4];
+#pragma unroll
+            for (int dd = 0; dd < 4; ++dd)
+                av[dd] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t *)&s_v[q][4 * lg + (l16 >> 2)][16 * (4 * w + dd) + 4 * (l16 & 3)]);
+#pragma unroll
+            for (int nt = 0; nt < QT; ++nt) {
+                const float ms = s_m[q][l16 + 16 * nt], ls = s_l[q][l16 + 16 * nt];
+                const bool move = M[nt] == -INFINITY ? ms != -INFINITY : ms > M[nt] + 8.0f;
+                const float Mn = move ? ms : M[nt];
+                if (__any(move)) {
+                    const float alpha = M[nt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M[nt] - Mn);
+                    L[nt] *= alpha;
+#pragma unroll
+                    for (int dd = 0; dd < 4; ++dd) oacc[nt][dd] *= alpha;
+                }
+                M[nt] = Mn;
+                const float es = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - Mn);
+                L[nt] = fmaf(es, ls, L[nt]);
+                const i16x4_t pb = __builtin_bit_cast(i16x4_t, *reinterpret_cast<const uint2 *>(&s_p[q][nt][l16][4 * lg]));
+#pragma unroll
+                for (int dd = 0; dd < 4; ++dd) {
+                    const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+                    const f32x4_t pv = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av[dd], pb, z, 0, 0, 0);
+                    oacc[nt][dd] += es * pv;
+                }
+            }
+        }
+        __syncthreads();  // the next page's scores overwrite s_v, s_p, s_m, s_l
+    };
+
+#pragma unroll
+    for (int k = 0; k < QCH; ++k) {
+        const int idx = tid + 256 * k, qr = idx >> 5, ch = idx & 31;
+        uint4 u = qreg[k];
+        if constexpr (MIX) {  // normalised and rotated q (all lanes take part in the row reductions)
+            float y[8];
+            const size_t rc = ((size_t)b * T + min(qr / G, T - 1)) * (a.rot / 2);
+            mixer_chunk(u, ch, a.wq, a.rcos + rc, a.rsin + rc, a.rot, a.eps, y);
+            u = pack8(y);
+            *reinterpret_cast<uint4 *>(&s_ql[qr][ch * 8]) = pack8_lo(y, u);
+        }
+        *reinterpret_cast<uint4 *>(&s_q[qr][ch * 8]) = u;
+    }
+    __syncthreads();
+    for (int pi = p0; pi < p1; ++pi) page(pi, KA, VA);
+
+    // this wave's head dims of the split's partial (or of the output); the partials are written through
+    // to the agent-coherent level (sc1), where another workgroup of this launch or the merge launch reads them
+    const auto rpo = __builtin_amdgcn_make_buffer_rsrc(a.part_o + prow(a, G, b, g, split, 0) * HD, (short)0,
+                                                       T * G * HD * 4, 0x00020000);
+    const auto rpm = __builtin_amdgcn_make_buffer_rsrc(a.part_ml + prow(a, G, b, g, split, 0) * 2, (short)0,
+                                                       T * G * 8, 0x00020000);
+#pragma unroll
+    for (int nt = 0; nt < QT; ++nt) {
+        const int qr = l16 + 16 * nt;
+        if (qr >= T * G) continue;
+        const int t = qr / G, hh = qr % G;
+        if (a.nsplit == 1) {
+            const float inv = 1.0f / L[nt];
+            const size_t oi = (((size_t)b * T + t) * a.NQ + g * G + hh) * HD + 64 * w + 4 * lg;
+#pragma unroll
+            for (int dd = 0; dd < 4; ++dd) {
+                f32x4_t v = oacc[nt][dd] * inv;
+                if (a.gate) {
+                    const uint2 gw = *reinterpret_cast<const uint2 *>(a.gate + oi + 16 * dd);
+                    v[0] *= sigm(qs::bf_lo(gw.x)), v[1] *= sigm(qs::bf_hi(gw.x));
+                    v[2] *= sigm(qs::bf_lo(gw.y)), v[3] *= sigm(qs::bf_hi(gw.y));
+                }
+                *reinterpret_cast<uint2 *>(a.o + oi + 16 * dd) =
+                    make_uint2(qs::cvt_pk_bf16(v[0], v[1]), qs::cvt_pk_bf16(v[2], v[3]));
+            }
+        } else {
+#pragma unroll
+            for (int dd = 0; dd < 4; ++dd)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, oacc[nt][dd]), rpo,
+                                                       (qr * HD + 64 * w + 16 * dd + 4 * lg) * 4, 0, qs::CP_SC1);
+            if (w == 0 && lg == 0)
+                __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(M[nt]), __float_as_uint(L[nt])}, rpm,
+                                                      qr * 8, 0, qs::CP_SC1);
+        }
+    }
+    if (a.nsplit > 1 && a.nsplit <= MERGE_MAX) merge_in_launch<G>(a, b, g, tid);
+}
+
 // ------------------------------------------------------------------- MFMA kernel, independent waves
-// Up to 16 QT query rows per KV head (QT = 1: every one-token decode; QT = 2: verify steps up to T = 5 at
-// G = 6). One workgroup per (user, KV head, split of pps pages) with 4 WPP waves: wave w owns rows
+// Up to 16 query rows per KV head (every one-token decode, and verify steps with T G <= 16). One workgroup per
+// (user, KV head, split of pps pages) with 4 WPP waves: wave w owns rows
 // 16 (w % 4) .. + 15 of pages p0 + w / 4, p0 + w / 4 + WPP, ... of the split (WPP pages in flight per
 // workgroup) and walks them on its own, with no workgroup barrier inside the page loop:
-//   scores  S^T [16 rows x 16 q] = K Q^T on 8 v_mfma_f32_16x16x32_bf16 per query tile (K rows loaded as whole
-//           512-byte rows and turned into the A operand through the wave's LDS slice, Q^T held in registers);
+//   scores  S^T [16 rows x 16 q] = K Q^T on 8 v_mfma_f32_16x16x32_bf16 (K rows loaded as whole 512-byte rows
+//           and turned into the A operand through the wave's LDS slice, Q^T held in registers);
 //   softmax per query row against the wave's running max M (log2 domain): P = 2^(s - M) rounded to bf16
 //           lands, lane for lane, in the B-operand layout of the P V product, so P never leaves the
 //           registers; M moves only when a slice max exceeds it by 2^8 (the accumulators are then rescaled),
 //           so P <= 2^8;
-//   P V     O^T [256 dims x 16 q] += V^T P on 16 v_mfma_f32_16x16x16_bf16 per query tile, accumulated by the
-//           MFMA itself, V^T read from the same LDS slice (now holding the page's 16 V rows) with the
-//           transposing ds_read_b64_tr_b16.
+//   P V     O^T [256 dims x 16 q] += V^T P on 16 v_mfma_f32_16x16x16_bf16, accumulated by the MFMA itself,
+//           V^T read from the same LDS slice (now holding the page's 16 V rows) with the transposing
+//           ds_read_b64_tr_b16.
 // Each wave keeps one page of K and V in flight (refilled as soon as consumed). At the end of the split the
 // waves' (max, sum) meet in LDS and their O, scaled to the common max, is summed through LDS in a fixed order
 // ((w + 4) pairs first when WPP = 2), every wave summing and storing a share of the head dims; the split's
 // partial, or with one split the output, has the layout the in-launch and separate merges read.
 constexpr int OPAD = HD + 4;  // fp32 row pitch of the waves' O rows in LDS
-template <int G, int QT, int WPP, bool MIX>
-__global__ __launch_bounds__(256 * WPP, (QT == 1 && WPP == 1) ? 2 : 1) void attn_wave_kernel(AttnArgs a) {
-    constexpr int NQR = 16 * QT;
+template <int G, int WPP, bool MIX>
+__global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(AttnArgs a) {
+    constexpr int QT = 1, NQR = 16;
     constexpr int NWV = 4 * WPP, NTH = 64 * NWV;
     const int nwg = a.B * a.NKV * a.nsplit;
     const int lid = qs::xcd_logical(blockIdx.x, nwg);
@@ -683,25 +979,16 @@ __global__ __launch_bounds__(256 * WPP, (QT == 1 && WPP == 1) ? 2 : 1) void attn
         *reinterpret_cast<uint4 *>(&s_q[qr][ch * 8]) = u;
     }
     __syncthreads();
-    // Q^T fragments: held in registers for the split, except with two query tiles at 8 waves per workgroup
-    // (two waves per SIMD), where they are read from LDS per page to stay within 256 registers
-    constexpr bool QREG = !(QT == 2 && WPP == 2);
-    auto qfrag = [&](int nt, int j) {
-        return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(&s_q[16 * nt + l16][32 * j + 8 * lg]));
-    };
-    auto qlfrag = [&](int nt, int j) {
-        return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(&s_ql[16 * nt + l16][32 * j + 8 * lg]));
-    };
-    bf16x8_t qb[QREG ? QT : 1][8], qlo[QREG ? QT : 1][MIX ? 8 : 1];
-    if constexpr (QREG) {
+    // Q^T fragments, held in registers for the split
+    bf16x8_t qb[QT][8], qlo[QT][MIX ? 8 : 1];
 #pragma unroll
-        for (int nt = 0; nt < QT; ++nt)
+    for (int nt = 0; nt < QT; ++nt)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                qb[nt][j] = qfrag(nt, j);
-                if constexpr (MIX) qlo[nt][j] = qlfrag(nt, j);
-            }
-    }
+        for (int j = 0; j < 8; ++j) {
+            qb[nt][j] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(&s_q[16 * nt + l16][32 * j + 8 * lg]));
+            if constexpr (MIX)
+                qlo[nt][j] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(&s_ql[16 * nt + l16][32 * j + 8 * lg]));
+        }
 
     const float sl2 = a.scale * 1.4426950408889634f;
     int lim[QT];  // this lane's query row of tile nt sees positions <= lim[nt]
@@ -728,8 +1015,8 @@ __global__ __launch_bounds__(256 * WPP, (QT == 1 && WPP == 1) ? 2 : 1) void attn
             *reinterpret_cast<uint4 *>(&s_kv[w][2 * kk + (lane >> 5)][(lane & 31) * 8]) = KA[kk];
         if (pgn >= 0) load_rows(a.k_cache, pgn, KA);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        // K fragments (row l16, dims 32 j + 8 lg .. + 7) in groups of KG, each used by every query tile
-        constexpr int KG = QREG ? 8 : 4;
+        // K fragments (row l16, dims 32 j + 8 lg .. + 7), each used by every query tile
+        constexpr int KG = 8;
         f32x4_t sacc[QT];
 #pragma unroll
         for (int nt = 0; nt < QT; ++nt) sacc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -743,12 +1030,9 @@ __global__ __launch_bounds__(256 * WPP, (QT == 1 && WPP == 1) ? 2 : 1) void attn
             for (int nt = 0; nt < QT; ++nt)
 #pragma unroll
                 for (int j = 0; j < KG; ++j) {
-                    const bf16x8_t qf = QREG ? qb[QREG ? nt : 0][j0 + j] : qfrag(nt, j0 + j);
-                    sacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb[j], qf, sacc[nt], 0, 0, 0);
-                    if constexpr (MIX) {
-                        const bf16x8_t qlf = QREG ? qlo[QREG ? nt : 0][j0 + j] : qlfrag(nt, j0 + j);
-                        sacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb[j], qlf, sacc[nt], 0, 0, 0);
-                    }
+                    sacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb[j], qb[nt][j0 + j], sacc[nt], 0, 0, 0);
+                    if constexpr (MIX)
+                        sacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb[j], qlo[nt][j0 + j], sacc[nt], 0, 0, 0);
                 }
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the K reads are done before V overwrites the slice
@@ -975,11 +1259,9 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, int G) {
 }
 
 int nsplit_of(int max_blocks, int pps) { return (max_blocks + pps - 1) / pps; }
-// Pages a workgroup of the independent-wave kernel walks at once (4 waves each): two for one query tile when
-// the split has more than one page (batch 8 at 4096 positions: 26.8 against 27.7 us; batch 1 at 32768: 29.8
-// against 30.4), one for two query tiles (their 8-wave form re-reads Q^T from LDS per page to fit in 256
-// registers and measured slower: 21.8 against 19.4 us for a 4-token verify at 8192 positions).
-int attn_wpp(int pps, int QT) { return QT == 1 && pps >= 2 ? 2 : 1; }
+// Pages a workgroup of the independent-wave kernel walks at once (4 waves each): two when the split has more
+// than one page (batch 8 at 4096 positions: 26.8 against 27.7 us; batch 1 at 32768: 29.8 against 30.4).
+int attn_wpp(int pps) { return pps >= 2 ? 2 : 1; }
 
 }  // namespace
 
@@ -1023,15 +1305,15 @@ static int attn_launch(AttnArgs a, void *workspace, int HDa, int block, const ch
     if (T * G <= 32) {
         const int QT = (T * G + 15) / 16;
         // two pages in flight per workgroup (8 waves) when the split has more than one page
-        const int wpp = attn_wpp(pages_per_split, QT);
-#define QS_WAVE(GG, Q, W, MX) attn_wave_kernel<GG, Q, W, MX><<<grid, 256 * W, 0, st>>>(a)
+        const int wpp = attn_wpp(pages_per_split);
+#define QS_WAVE(GG, W, MX) attn_wave_kernel<GG, W, MX><<<grid, 256 * W, 0, st>>>(a)
 #define QS_MFMA_LAUNCH(GG)                                                              \
     if (a.wq) {                                                                         \
-        if (QT == 1) { if (wpp == 1) QS_WAVE(GG, 1, 1, true); else QS_WAVE(GG, 1, 2, true); }  \
-        else { if (wpp == 1) QS_WAVE(GG, 2, 1, true); else QS_WAVE(GG, 2, 2, true); }          \
+        if (QT == 1) { if (wpp == 1) QS_WAVE(GG, 1, true); else QS_WAVE(GG, 2, true); }  \
+        else attn_mfma_kernel<GG, 2, true><<<grid, 256, 0, st>>>(a);                    \
     } else {                                                                            \
-        if (QT == 1) { if (wpp == 1) QS_WAVE(GG, 1, 1, false); else QS_WAVE(GG, 1, 2, false); } \
-        else { if (wpp == 1) QS_WAVE(GG, 2, 1, false); else QS_WAVE(GG, 2, 2, false); }         \
+        if (QT == 1) { if (wpp == 1) QS_WAVE(GG, 1, false); else QS_WAVE(GG, 2, false); } \
+        else attn_mfma_kernel<GG, 2, false><<<grid, 256, 0, st>>>(a);                   \
     }
         switch (G) {
             case 1: QS_MFMA_LAUNCH(1) break;
