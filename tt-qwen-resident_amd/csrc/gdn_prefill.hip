@@ -36,7 +36,6 @@ constexpr int DV = 128;
 constexpr int FP = CH + 1;  // fp32 row stride of the 64 x 64 matrices of the inverse in LDS
 constexpr int SLAB = 32;    // state columns per walk workgroup
 constexpr int NSLAB = DV / SLAB;
-constexpr int KP = DK + 8;  // bf16 row stride of the walk's K / Q chunk tiles in LDS (272 bytes)
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -58,6 +57,14 @@ __device__ __forceinline__ int sig(int t, int r) { return 32 * (t >> 1) + 8 * (r
 // read hit 16 different 16-byte bank groups.
 __device__ __forceinline__ int sw16(int p) { return ((p & 3) << 2) | ((p >> 3) & 3); }
 
+// Fragment order of a matrix the walk multiplies by (its rows are the A operand of 16x16x32 MFMAs): the 16 x 32
+// block (row tile rt, column step ks) is one kilobyte, lane l = 16 g + r holding row 16 rt + r, columns
+// 32 ks + 8 g .. + 7 in its 16 bytes, blocks ordered by (rt, ks). A wave loads a block as one contiguous
+// kilobyte (whole 128-byte lines). Element offset of the 8-column group starting at (row, col):
+__device__ __forceinline__ int frag_off(int row, int col, int nks) {
+    return (((row >> 4) * nks + (col >> 5)) * 64 + ((col >> 3) & 3) * 16 + (row & 15)) * 8;
+}
+
 // a buffer descriptor over n bytes from p: reads past the range return zeros, writes past it are dropped
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *p, int n) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, n, 0x00020000);
@@ -73,8 +80,9 @@ struct PrefillArgs {
     const float *S0;            // [NV, DK, DV]
     float *ST;                  // [NV, DK, DV]
     uint16_t *o;                // [T, NV, DV]
-    uint16_t *Tm;               // workspace [nch, NV, 2, 64, 64] bf16: hi and lo planes of Tm
-    uint16_t *P;                // workspace [nch, NV, 2, 64, 64] bf16: hi and lo planes of P
+    uint16_t *Tm;               // workspace [nch, NV, 2, 64 x 64] bf16: hi and lo planes of Tm, fragment order
+    uint16_t *P;                // workspace [nch, NV, 2, 64 x 64] bf16: hi and lo planes of P, fragment order
+    uint16_t *KQ;               // workspace [nch, NK, 2, 64 x 128] bf16: the chunk's k and q rows, fragment order
     float *sc;                  // workspace [nch, NV, 5, 64]: beta | beta gamma r_k | gamma r_q | r_k gamma_C/gamma | gamma_C
     int T, NK, NV, nch;
     float scale, eps;
@@ -174,6 +182,20 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
         s_b[lane] = bi;
     }
 
+    // 2b. the first value head of each key head stores the chunk's k and q rows in fragment order for the walk
+    if (h % rep == 0) {
+        uint16_t *dst = a.KQ + ((size_t)c * a.NK + kh) * 2 * CH * DK;
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            const int idx = tid + 256 * m, mat = idx >> 10, piece = idx & 1023;
+            const int f = piece >> 6, l = piece & 63;
+            const int row = 16 * (f >> 2) + (l & 15), q = 4 * (f & 3) + (l >> 4);
+            const uint16_t *img = mat ? sQ : sK;
+            *reinterpret_cast<uint4 *>(dst + mat * CH * DK + piece * 8) =
+                *reinterpret_cast<const uint4 *>(img + row * DK + ((q ^ sw16(row)) << 3));
+        }
+    }
+
     // 3. K K^T and Q K^T in row order sig (exact bf16 products, fp32 sums): wave w owns row tile w; element
     //    (4 g + i, fr) of column tile tc pairs tokens sig(w, 4 g + i) and sig(tc, fr)
     f32x4 ckk[4], cqk[4];
@@ -235,8 +257,9 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
         const int i = tid >> 2, j0 = (tid & 3) * 16;
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            *reinterpret_cast<uint4 *>(Pd + i * CH + j0 + 8 * u) = *reinterpret_cast<const uint4 *>(&sPh[i][j0 + 8 * u]);
-            *reinterpret_cast<uint4 *>(Pd + CH * CH + i * CH + j0 + 8 * u) = *reinterpret_cast<const uint4 *>(&sPl[i][j0 + 8 * u]);
+            const int off = frag_off(i, j0 + 8 * u, CH / 32);
+            *reinterpret_cast<uint4 *>(Pd + off) = *reinterpret_cast<const uint4 *>(&sPh[i][j0 + 8 * u]);
+            *reinterpret_cast<uint4 *>(Pd + CH * CH + off) = *reinterpret_cast<const uint4 *>(&sPl[i][j0 + 8 * u]);
         }
     }
     __syncthreads();  // P's staging space becomes Tm's
@@ -300,12 +323,12 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
             th[u / 2] = qs::cvt_pk_bf16(v0, v1);
             tl[u / 2] = qs::cvt_pk_bf16(v0 - qs::bf_lo(th[u / 2]), v1 - qs::bf_hi(th[u / 2]));
         }
-        uint4 *dh = reinterpret_cast<uint4 *>(a.Tm + 2 * mat + i * CH + j0);
-        uint4 *dl = reinterpret_cast<uint4 *>(a.Tm + 2 * mat + CH * CH + i * CH + j0);
-        dh[0] = make_uint4(th[0], th[1], th[2], th[3]);
-        dh[1] = make_uint4(th[4], th[5], th[6], th[7]);
-        dl[0] = make_uint4(tl[0], tl[1], tl[2], tl[3]);
-        dl[1] = make_uint4(tl[4], tl[5], tl[6], tl[7]);
+        uint16_t *Td = a.Tm + 2 * mat;
+        const int o0 = frag_off(i, j0, CH / 32), o1 = frag_off(i, j0 + 8, CH / 32);
+        *reinterpret_cast<uint4 *>(Td + o0) = make_uint4(th[0], th[1], th[2], th[3]);
+        *reinterpret_cast<uint4 *>(Td + o1) = make_uint4(th[4], th[5], th[6], th[7]);
+        *reinterpret_cast<uint4 *>(Td + CH * CH + o0) = make_uint4(tl[0], tl[1], tl[2], tl[3]);
+        *reinterpret_cast<uint4 *>(Td + CH * CH + o1) = make_uint4(tl[4], tl[5], tl[6], tl[7]);
     }
     if (tid < CH) {
         const int i = tid;
@@ -333,23 +356,53 @@ __device__ __forceinline__ void split4(float x0, float x1, float x2, float x3, u
 
 __device__ __forceinline__ bf16x8 frag(const uint16_t *p) { return as_frag(*reinterpret_cast<const uint4 *>(p)); }
 
-// K^T [d][token] rows are 64 tokens (128 bytes) with the 16-byte token groups XOR-swizzled by
-// (d ^ d / 8) % 8: the paired-token writes of the transpose and the MFMA fragment reads are both free of
-// bank conflicts without padding.
-__device__ __forceinline__ int kt_index(int d, int t) {
-    return d * CH + ((((t >> 3) ^ (d ^ (d >> 3))) & 7) << 3) + (t & 7);
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// The walk's K image: token rows of 128 d (256 bytes), the 16-byte d groups XOR-swizzled by
+// kswz(row) = 2 (row % 4) | (row / 4) % 2. The 16-byte fragment writes (8 consecutive rows per 8 lanes) and
+// the transposing reads (4 consecutive rows x 32 bytes per 16 lanes) are both free of bank conflicts.
+__device__ __forceinline__ int kimg(int row, int d) {
+    return row * DK + ((((d >> 3) ^ (((row & 3) << 1) | ((row >> 2) & 1)))) << 3) + (d & 7);
 }
 
-// One workgroup (8 waves) per (value head, 32-column slab of S). Wave (w, nh) = (wave / 2, wave % 2) owns the
-// 16-token tile w of every chunk product and the 16-column half nh of the slab; for the state update it owns
-// state rows 32 w .. 32 w + 31 of that column half. Two waves per SIMD interleave their dependent MFMA and
-// LDS chains, and each wave's chain per chunk is half the one a 4-wave workgroup walks. The slab's fp32
-// state lives in registers and is mirrored in LDS as bf16 hi + lo planes, the operand of K S0 and Q S0.
-// Every other operand sits in LDS in the orientation its MFMA fragments read (S^T, X^T, d^T [v][token],
-// K^T [d][token], K, Q, Tm, P [token][.]) and is split into bf16 hi + lo once, by the wave that produces it.
-// The next chunk's K, Q, V, Tm, P and scalars are loaded into registers while the current chunk computes;
-// reads past the sequence end return zeros through the buffer descriptors' range checks and writes past it
-// are dropped the same way.
+// One workgroup (8 waves) per (value head, 32-column slab of S). Wave (w, role) = (wave % 4, wave / 4) works on
+// the 16-token tile w of every chunk product; the two waves of a tile share a SIMD. The k wave (role 0)
+// forms K S0 for both column halves of the slab, X = beta V - (beta gamma r_k) K S0 and d = Tm X; the q wave
+// (role 1) forms Q S0 and O = (gamma r_q) Q S0 + P d. For the state update S = gamma_C S0 + K^T e each
+// wave owns state rows 32 w .. 32 w + 31 of column half `role`; the slab's fp32 state lives in registers
+// and is mirrored in LDS as bf16 hi + lo planes (S^T [v][d]), the operand of K S0 and Q S0. Each wave loads only the fragments it multiplies
+// by, from the prep's fragment-order copies (one contiguous kilobyte per load, every byte loaded once per
+// workgroup): k wave K rows and Tm, q wave Q rows and P, one chunk ahead. What crosses waves goes through
+// LDS: the state mirror, X^T, d^T and e^T (split into bf16 hi + lo by the wave that produces them), the
+// chunk's K rows (read transposed, K^T [d][token], with ds_read_b64_tr_b16) and the per-token scalars.
+// Three barriers per chunk: after X, after d, after the state update. Reads past the sequence end return
+// zeros through the buffer descriptors' range checks and writes past it are dropped the same way.
+// The walk's X image: token rows of 32 slab columns (64 bytes, no padding), the 8-byte column groups u = v / 4
+// XOR-swizzled by xswz(t / 2) = 4 ((t / 2) % 2) + (t / 2) / 2 % 4. The 8-byte writes of 16 consecutive rows and
+// the transposing reads (4 consecutive rows x 32 bytes per 16 lanes) are both free of bank conflicts.
+__device__ __forceinline__ int ximg(int t, int v) {
+    const int m = t >> 1;
+    return t * SLAB + ((((v >> 2) ^ (((m & 1) << 2) | ((m >> 1) & 3))) << 2)) + (v & 3);
+}
+
+// A B (or A) fragment of 8 rows x 16 columns read across: lane fr of each 16-lane group receives column
+// c0 + fr of rows r0 .. r0 + 3 from p0 and of rows r0 + 4 .. r0 + 7 from p4, where each lane points p0 at
+// row r0 + fr / 4, columns c0 + 4 (fr % 4) .. + 3 (ds_read_b64_tr_b16) and p4 four rows further
+__device__ __forceinline__ bf16x8 tr_frag(const uint16_t *p0, const uint16_t *p4) {
+    const i16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4 *)p0);
+    const i16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4 *)p4);
+    return __builtin_bit_cast(bf16x8, u32x4{__builtin_bit_cast(u32x2, lo4)[0], __builtin_bit_cast(u32x2, lo4)[1],
+                                            __builtin_bit_cast(u32x2, hi4)[0], __builtin_bit_cast(u32x2, hi4)[1]});
+}
+
+// keeps a group of memory requests where it is written: neither the optimizer nor the scheduler moves code
+// across it
+__device__ __forceinline__ void fence_issue() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 constexpr int WALK_THREADS = 512;
 __global__ __launch_bounds__(WALK_THREADS) void chunk_walk_kernel(PrefillArgs a) {
     constexpr int SKP = DK + 16;  // bf16 row stride of the S^T planes
@@ -358,28 +411,23 @@ __global__ __launch_bounds__(WALK_THREADS) void chunk_walk_kernel(PrefillArgs a)
     const int lid = qs::xcd_logical(blockIdx.x, nwg);
     const int slab = lid % NSLAB, h = lid / NSLAB;
     const int kh = h / (a.NV / a.NK);
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int w = wv >> 1, nh = wv & 1;
-    const int fr = lane & 15, fk = (lane >> 4) * 8, fq = (lane >> 4) * 4;
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int w = wv & 3, role = wv >> 2;
+    const int fr = lane & 15, g = lane >> 4, fk = g * 8, fq = g * 4;
 
     __shared__ __align__(16) uint16_t sS[2][SLAB][SKP];
-    __shared__ __align__(16) uint16_t sK[CH][KP];
-    __shared__ __align__(16) uint16_t sQ[CH][KP];
-    __shared__ __align__(16) uint16_t sKt[DK * CH];
-    __shared__ __align__(16) uint16_t sVt[SLAB][CH + 4];
-    __shared__ __align__(16) uint16_t sTm[2][CH][TP];
-    __shared__ __align__(16) uint16_t sP[2][CH][TP];
-    __shared__ __align__(16) uint16_t sX[2][SLAB][TP];
+    __shared__ __align__(16) uint16_t sK[CH * DK];
+    __shared__ __align__(16) uint16_t sX[2][CH * SLAB];
     __shared__ __align__(16) uint16_t sD[2][SLAB][TP];
     __shared__ __align__(16) uint16_t sE[2][SLAB][TP];
-    __shared__ __align__(16) float s_c[5 * CH];
+    __shared__ __align__(16) float s_c[2][5][CH];
 
-    // state rows 32 w + 16 mt + fq + i, column 32 slab + 16 nh + fr
+    // state rows 32 w + 16 mt + fq + i, column 32 slab + 16 role + fr
     float S[2][4];
     auto mirror = [&](int mt) {
         uint2 hi, lo;
         split4(S[mt][0], S[mt][1], S[mt][2], S[mt][3], hi, lo);
-        const int v = 16 * nh + fr, d = 32 * w + 16 * mt + fq;
+        const int v = 16 * role + fr, d = 32 * w + 16 * mt + fq;
         *reinterpret_cast<uint2 *>(&sS[0][v][d]) = hi;
         *reinterpret_cast<uint2 *>(&sS[1][v][d]) = lo;
     };
@@ -387,203 +435,210 @@ __global__ __launch_bounds__(WALK_THREADS) void chunk_walk_kernel(PrefillArgs a)
     for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            S[mt][i] = a.S0[((size_t)h * DK + 32 * w + 16 * mt + fq + i) * DV + SLAB * slab + 16 * nh + fr];
+            S[mt][i] = a.S0[((size_t)h * DK + 32 * w + 16 * mt + fq + i) * DV + SLAB * slab + 16 * role + fr];
         mirror(mt);
     }
 
-    // per-thread share of a chunk: 16-byte group kc = tid % 16 of K and Q rows 2 p and 2 p + 1, p = tid / 16
-    // (16 consecutive threads read one 256-byte row); V rows 2 (tid / 16) and + 1, columns 2 (tid % 16) .. + 1;
-    // Tm and P 16-byte pieces tid + 512 m of their hi | lo planes; scalars tid < 320. K, Q, V of the next
-    // chunk are requested after the barrier that follows K S0, Tm, P and the scalars after the next one: no
-    // prefetch register is live while K S0 and Q S0 read their operands (issued earlier, measured slower).
-    const int kc = tid & 15, pp = tid >> 4;
-    const size_t krow = (size_t)a.NK * DK * 2, vrow = (size_t)a.NV * DV * 2;  // bytes per token
-    // (vectors, not arrays: they stay in registers whatever the unroll order)
-    u32x8 pk, pq, ptm, ppm;
-    uint32_t pv0, pv1;
-    float psc;
-    auto fetch_kqv = [&](int c) {
-        const int t0 = c * CH, nv = min(CH, a.T - t0);
-        const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.k) + (size_t)t0 * a.NK * DK,
-                                                          (short)0, (int)(nv * krow), 0x00020000);
-        const auto rq = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.q) + (size_t)t0 * a.NK * DK,
-                                                          (short)0, (int)(nv * krow), 0x00020000);
-        const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.v) + (size_t)t0 * a.NV * DV,
-                                                          (short)0, (int)(nv * vrow), 0x00020000);
+    // Registers of the chunk in flight: fA = the wave's K (role 0) or Q (role 1) fragments, column steps 0..3;
+    // fB = its Tm (role 0) or P (role 1) fragments, [plane][column step]; fV = V at row 16 w + fr, columns
+    // 16 nh + fq .. + 3 (the accumulator layout of X^T; role 1 reads an empty range); psc = row `wave` of the five
+    // per-token scalar rows (waves 0..4; the others an empty range). Every wave issues the same requests in the
+    // same order, without a branch, so the compiler's memory-counter waits are exact: a wait for one set skips
+    // every set requested after it. The fetches of chunk nch (one past the last) read empty ranges or repeat
+    // the last chunk.
+    const size_t vrow = (size_t)a.NV * DV * 2;  // bytes per token
+    u32x4 fA[4], fB[4];
+    u32x2 fV[2];
+    uint32_t psc;
+    auto fetch_a = [&](int c) {
+        const int cc = min(c, a.nch - 1);
+        const auto rs = rsrc(a.sc + ((size_t)cc * a.NV + h) * 5 * CH, wv < 5 ? 5 * CH * 4 : 0);
+        psc = __builtin_amdgcn_raw_buffer_load_b32(rs, (wv * CH + lane) * 4, 0, 0);
+        const uint16_t *src = a.KQ + (((size_t)cc * a.NK + kh) * 2 + role) * CH * DK + frag_off(16 * w + fr, fk, 4);
 #pragma unroll
-        for (int m = 0; m < 2; ++m) {
-            const int off = (int)((2 * pp + m) * krow) + (kh * DK + kc * 8) * 2;
-            const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0);
-            const u32x4 y = __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0);
+        for (int ks = 0; ks < 4; ++ks) fA[ks] = *reinterpret_cast<const u32x4 *>(src + ks * 512);
+        const int t0 = c * CH, nv = __builtin_amdgcn_readfirstlane(role == 0 ? max(0, min(CH, a.T - t0)) : 0);
+        const auto rv = rsrc(a.v + (size_t)t0 * a.NV * DV, (int)(nv * vrow));
+        const int vo = (int)((16 * w + fr) * vrow) + (h * DV + SLAB * slab + fq) * 2;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) pk[4 * m + j] = x[j], pq[4 * m + j] = y[j];
-        }
-        const int vo = (int)(2 * pp * vrow) + (h * DV + SLAB * slab + kc * 2) * 2;
-        pv0 = __builtin_amdgcn_raw_buffer_load_b32(rv, vo, 0, 0);
-        pv1 = __builtin_amdgcn_raw_buffer_load_b32(rv, vo + (int)vrow, 0, 0);
+        for (int nh = 0; nh < 2; ++nh) fV[nh] = __builtin_amdgcn_raw_buffer_load_b64(rv, vo + 32 * nh, 0, 0);
     };
-    auto fetch_tp = [&](int c) {
-        const size_t mat = ((size_t)c * a.NV + h) * CH * CH;
+    auto fetch_b = [&](int c) {
+        const int cc = min(c, a.nch - 1);
+        const uint16_t *src = (role ? a.P : a.Tm) + ((size_t)cc * a.NV + h) * 2 * CH * CH + frag_off(16 * w + fr, fk, 2);
 #pragma unroll
-        for (int m = 0; m < 2; ++m) {
-            const uint4 x = *reinterpret_cast<const uint4 *>(a.Tm + 2 * mat + (tid + WALK_THREADS * m) * 8);
-            const uint4 y = *reinterpret_cast<const uint4 *>(a.P + 2 * mat + (tid + WALK_THREADS * m) * 8);
-            ptm[4 * m] = x.x, ptm[4 * m + 1] = x.y, ptm[4 * m + 2] = x.z, ptm[4 * m + 3] = x.w;
-            ppm[4 * m] = y.x, ppm[4 * m + 1] = y.y, ppm[4 * m + 2] = y.z, ppm[4 * m + 3] = y.w;
-        }
-        psc = tid < 5 * CH ? a.sc[((size_t)c * a.NV + h) * 5 * CH + tid] : 0.f;
+        for (int pl = 0; pl < 2; ++pl)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) fB[2 * pl + ks] = *reinterpret_cast<const u32x4 *>(src + pl * CH * CH + ks * 512);
     };
-    fetch_kqv(0);
-    fetch_tp(0);
+    // output row 16 w + fr, columns 16 nh + fq .. + 3 of chunk c (q waves: O^T accumulators), or nothing (k
+    // waves: an empty range), so that every wave issues the same stores
+    auto store_o = [&](int c, const f32x4 (&o)[2]) {
+        const int t0 = c * CH, nv = __builtin_amdgcn_readfirstlane(role == 1 ? max(0, min(CH, a.T - t0)) : 0);
+        const auto ro = rsrc(a.o + (size_t)t0 * a.NV * DV, (int)(nv * vrow));
+        const int oo = (int)((16 * w + fr) * vrow) + (h * DV + SLAB * slab + fq) * 2;
+#pragma unroll
+        for (int nh = 0; nh < 2; ++nh)
+            __builtin_amdgcn_raw_buffer_store_b64(
+                u32x2{qs::cvt_pk_bf16(o[nh][0], o[nh][1]), qs::cvt_pk_bf16(o[nh][2], o[nh][3])}, ro, oo + 32 * nh, 0, 0);
+    };
 
-    // a chunk's output rows are stored at the start of the next chunk, after that chunk's operands have
-    // been waited for, so the stores never sit in front of a prefetch in the memory counter
-    f32x4 opend;
-    auto store_o = [&](int c) {
-        const int t0 = c * CH, nv = min(CH, a.T - t0), r0 = 16 * w + fq;
-        const auto ro = __builtin_amdgcn_make_buffer_rsrc(a.o + (size_t)t0 * a.NV * DV, (short)0, (int)(nv * vrow),
-                                                          0x00020000);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            __builtin_amdgcn_raw_buffer_store_b16((unsigned short)qs::cvt_pk_bf16(opend[i], 0.f), ro,
-                                                  (int)((r0 + i) * vrow) + (h * DV + SLAB * slab + nh * 16 + fr) * 2, 0,
-                                                  0);
-    };
+    // the requests in flight at the top of every chunk, oldest first: the scalars (already consumed), fA and fV
+    // of the chunk; its fB; the previous chunk's eight output stores (before the first chunk, eight with an
+    // empty range)
+    f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    fence_issue();
+    fetch_a(0);
+    fence_issue();
+    fetch_b(0);
+    fence_issue();
+    store_o(a.nch, acc);
+    fence_issue();
+    if (wv < 5) s_c[0][wv][lane] = __uint_as_float(psc);
+    __syncthreads();
 
     for (int c = 0; c < a.nch; ++c) {
-        // ---- this chunk's operands from registers into LDS
+        const int cb = c & 1;
+        // ---- k wave: the chunk's K rows into the K image; (K S0)^T = S0^T K^T (S0 as hi + lo) and X^T for both
+        // column halves, into the X image as hi + lo. q wave: (Q S0)^T for both halves, kept for O^T. The
+        // transposed products leave four consecutive columns of one token in each lane.
+        if (role == 0) {
 #pragma unroll
-        for (int m = 0; m < 2; ++m) {
-            const int r = 2 * pp + m;
-            *reinterpret_cast<uint4 *>(&sK[r][kc * 8]) = make_uint4(pk[4 * m], pk[4 * m + 1], pk[4 * m + 2], pk[4 * m + 3]);
-            *reinterpret_cast<uint4 *>(&sQ[r][kc * 8]) = make_uint4(pq[4 * m], pq[4 * m + 1], pq[4 * m + 2], pq[4 * m + 3]);
-        }
+            for (int ks = 0; ks < DK / 32; ++ks) *reinterpret_cast<u32x4 *>(&sK[kimg(16 * w + fr, 32 * ks + fk)]) = fA[ks];
+            bf16x8 bh[2][4], bl[2][4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {  // K^T: token pair (2 pp, 2 pp + 1) as one 32-bit word per d
-            const int d = kc * 8 + 2 * e;
-            const uint32_t ev = pk[e], od = pk[4 + e];
-            *reinterpret_cast<uint32_t *>(&sKt[kt_index(d, 2 * pp)]) = (ev & 0xffffu) | (od << 16);
-            *reinterpret_cast<uint32_t *>(&sKt[kt_index(d + 1, 2 * pp)]) = (ev >> 16) | (od & 0xffff0000u);
-        }
-        {  // V^T: the token pair as one 32-bit word per column
-            const int col = kc * 2, t = 2 * pp;
-            *reinterpret_cast<uint32_t *>(&sVt[col][t]) = (pv0 & 0xffffu) | (pv1 << 16);
-            *reinterpret_cast<uint32_t *>(&sVt[col + 1][t]) = (pv0 >> 16) | (pv1 & 0xffff0000u);
-        }
+            for (int nh = 0; nh < 2; ++nh)
 #pragma unroll
-        for (int m = 0; m < 2; ++m) {
-            const int idx = tid + WALK_THREADS * m;
-            *reinterpret_cast<uint4 *>(&sTm[idx >> 9][(idx >> 3) & 63][(idx & 7) * 8]) =
-                make_uint4(ptm[4 * m], ptm[4 * m + 1], ptm[4 * m + 2], ptm[4 * m + 3]);
-            *reinterpret_cast<uint4 *>(&sP[idx >> 9][(idx >> 3) & 63][(idx & 7) * 8]) =
-                make_uint4(ppm[4 * m], ppm[4 * m + 1], ppm[4 * m + 2], ppm[4 * m + 3]);
-        }
-        if (tid < 5 * CH) s_c[tid] = psc;
-        if (c > 0) store_o(c - 1);
-        __syncthreads();
-
-        // ---- K S0 and Q S0 for token tile w, column half nh (S0 as hi + lo); every fragment is requested
-        // before the first MFMA (the scheduler barrier keeps the reads together)
-        f32x4 kacc = {0.f, 0.f, 0.f, 0.f}, qacc = {0.f, 0.f, 0.f, 0.f};
-        {
-            bf16x8 ak[4], aq[4], bh[4], bl[4];
+                for (int ks = 0; ks < DK / 32; ++ks) {
+                    bh[nh][ks] = frag(&sS[0][nh * 16 + fr][ks * 32 + fk]);
+                    bl[nh][ks] = frag(&sS[1][nh * 16 + fr][ks * 32 + fk]);
+                }
 #pragma unroll
-            for (int ks = 0; ks < DK / 32; ++ks) {
-                ak[ks] = frag(&sK[16 * w + fr][ks * 32 + fk]);
-                aq[ks] = frag(&sQ[16 * w + fr][ks * 32 + fk]);
-                bh[ks] = frag(&sS[0][nh * 16 + fr][ks * 32 + fk]);
-                bl[ks] = frag(&sS[1][nh * 16 + fr][ks * 32 + fk]);
+            for (int nh = 0; nh < 2; ++nh) {
+                acc[nh] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < DK / 32; ++ks) {
+                    const bf16x8 bk = __builtin_bit_cast(bf16x8, fA[ks]);
+                    acc[nh] = mfma(bh[nh][ks], bk, acc[nh]);
+                    acc[nh] = mfma(bl[nh][ks], bk, acc[nh]);
+                }
             }
-            __builtin_amdgcn_sched_barrier(0);
+            const int t = 16 * w + fr;
+            const float c0 = s_c[cb][0][t], c1 = s_c[cb][1][t];
 #pragma unroll
-            for (int ks = 0; ks < DK / 32; ++ks) {
-                kacc = mfma(ak[ks], bh[ks], kacc);
-                kacc = mfma(ak[ks], bl[ks], kacc);
-                qacc = mfma(aq[ks], bh[ks], qacc);
-                qacc = mfma(aq[ks], bl[ks], qacc);
+            for (int nh = 0; nh < 2; ++nh) {
+                uint2 hi, lo;
+                split4(c0 * qs::bf_lo(fV[nh][0]) - c1 * acc[nh][0], c0 * qs::bf_hi(fV[nh][0]) - c1 * acc[nh][1],
+                       c0 * qs::bf_lo(fV[nh][1]) - c1 * acc[nh][2], c0 * qs::bf_hi(fV[nh][1]) - c1 * acc[nh][3], hi, lo);
+                *reinterpret_cast<uint2 *>(&sX[0][ximg(t, 16 * nh + fq)]) = hi;
+                *reinterpret_cast<uint2 *>(&sX[1][ximg(t, 16 * nh + fq)]) = lo;
             }
-        }
-
-        // ---- X = beta V - (beta gamma r_k) (K S0), as X^T hi + lo
-        {
-            const int r0 = 16 * w + fq;
-            const float4 c0 = *reinterpret_cast<const float4 *>(&s_c[0 * CH + r0]);
-            const float4 c1 = *reinterpret_cast<const float4 *>(&s_c[1 * CH + r0]);
-            const int col = nh * 16 + fr;
-            const uint2 v4 = *reinterpret_cast<const uint2 *>(&sVt[col][r0]);
-            uint2 hi, lo;
-            split4(c0.x * qs::bf_lo(v4.x) - c1.x * kacc[0], c0.y * qs::bf_hi(v4.x) - c1.y * kacc[1],
-                   c0.z * qs::bf_lo(v4.y) - c1.z * kacc[2], c0.w * qs::bf_hi(v4.y) - c1.w * kacc[3], hi, lo);
-            *reinterpret_cast<uint2 *>(&sX[0][col][r0]) = hi;
-            *reinterpret_cast<uint2 *>(&sX[1][col][r0]) = lo;
+        } else {
+            bf16x8 bh[2][4], bl[2][4];
+#pragma unroll
+            for (int nh = 0; nh < 2; ++nh)
+#pragma unroll
+                for (int ks = 0; ks < DK / 32; ++ks) {
+                    bh[nh][ks] = frag(&sS[0][nh * 16 + fr][ks * 32 + fk]);
+                    bl[nh][ks] = frag(&sS[1][nh * 16 + fr][ks * 32 + fk]);
+                }
+#pragma unroll
+            for (int nh = 0; nh < 2; ++nh) {
+                acc[nh] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < DK / 32; ++ks) {
+                    const bf16x8 bq = __builtin_bit_cast(bf16x8, fA[ks]);
+                    acc[nh] = mfma(bh[nh][ks], bq, acc[nh]);
+                    acc[nh] = mfma(bl[nh][ks], bq, acc[nh]);
+                }
+            }
         }
         __syncthreads();
-        if (c + 1 < a.nch) fetch_kqv(c + 1);  // lands during d, O, S and the next fill
+        fence_issue();
+        fetch_a(c + 1);  // the scalars land during d; fA and fV during d, O, S and the next barrier
+        fence_issue();
 
-        // ---- d = Tm X (hi*hi + hi*lo + lo*hi), as d^T hi + lo and e^T = (d (r_k gamma_C / gamma))^T hi + lo
-        {
-            f32x4 dacc = {0.f, 0.f, 0.f, 0.f};
-            bf16x8 th[2], tl[2], xh[2], xl[2];
+        // ---- k wave: d = Tm X (hi*hi + hi*lo + lo*hi) for both halves, as d^T hi + lo and
+        // e^T = (d (r_k gamma_C / gamma))^T hi + lo
+        if (role == 0) {
+            // X fragments (B: tokens 32 ks + fk .. + 7 of column 16 nh + fr) by transposing reads of the X image
+            bf16x8 xh[2][2], xl[2][2];
 #pragma unroll
-            for (int ks = 0; ks < CH / 32; ++ks) {
-                th[ks] = frag(&sTm[0][16 * w + fr][ks * 32 + fk]);
-                tl[ks] = frag(&sTm[1][16 * w + fr][ks * 32 + fk]);
-                xh[ks] = frag(&sX[0][nh * 16 + fr][ks * 32 + fk]);
-                xl[ks] = frag(&sX[1][nh * 16 + fr][ks * 32 + fk]);
-            }
-            __builtin_amdgcn_sched_barrier(0);
+            for (int nh = 0; nh < 2; ++nh)
 #pragma unroll
-            for (int ks = 0; ks < CH / 32; ++ks) {
-                dacc = mfma(th[ks], xh[ks], dacc);
-                dacc = mfma(th[ks], xl[ks], dacc);
-                dacc = mfma(tl[ks], xh[ks], dacc);
-            }
+                for (int ks = 0; ks < CH / 32; ++ks) {
+                    const int row = 32 * ks + fk + (fr >> 2), col = 16 * nh + 4 * (fr & 3);
+                    xh[nh][ks] = tr_frag(&sX[0][ximg(row, col)], &sX[0][ximg(row + 4, col)]);
+                    xl[nh][ks] = tr_frag(&sX[1][ximg(row, col)], &sX[1][ximg(row + 4, col)]);
+                }
             const int r0 = 16 * w + fq;
-            const float4 c3 = *reinterpret_cast<const float4 *>(&s_c[3 * CH + r0]);
-            const int col = nh * 16 + fr;
-            uint2 hi, lo;
-            split4(dacc[0], dacc[1], dacc[2], dacc[3], hi, lo);
-            *reinterpret_cast<uint2 *>(&sD[0][col][r0]) = hi;
-            *reinterpret_cast<uint2 *>(&sD[1][col][r0]) = lo;
-            split4(dacc[0] * c3.x, dacc[1] * c3.y, dacc[2] * c3.z, dacc[3] * c3.w, hi, lo);
-            *reinterpret_cast<uint2 *>(&sE[0][col][r0]) = hi;
-            *reinterpret_cast<uint2 *>(&sE[1][col][r0]) = lo;
+            const float4 c3 = *reinterpret_cast<const float4 *>(&s_c[cb][3][r0]);
+#pragma unroll
+            for (int nh = 0; nh < 2; ++nh) {
+                f32x4 dacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < CH / 32; ++ks) {
+                    const bf16x8 th = __builtin_bit_cast(bf16x8, fB[ks]), tl = __builtin_bit_cast(bf16x8, fB[2 + ks]);
+                    dacc = mfma(th, xh[nh][ks], dacc);
+                    dacc = mfma(th, xl[nh][ks], dacc);
+                    dacc = mfma(tl, xh[nh][ks], dacc);
+                }
+                const int col = nh * 16 + fr;
+                uint2 hi, lo;
+                split4(dacc[0], dacc[1], dacc[2], dacc[3], hi, lo);
+                *reinterpret_cast<uint2 *>(&sD[0][col][r0]) = hi;
+                *reinterpret_cast<uint2 *>(&sD[1][col][r0]) = lo;
+                split4(dacc[0] * c3.x, dacc[1] * c3.y, dacc[2] * c3.z, dacc[3] * c3.w, hi, lo);
+                *reinterpret_cast<uint2 *>(&sE[0][col][r0]) = hi;
+                *reinterpret_cast<uint2 *>(&sE[1][col][r0]) = lo;
+            }
         }
         __syncthreads();
-        if (c + 1 < a.nch) fetch_tp(c + 1);
 
-        // ---- O = (gamma r_q) (Q S0) + P d  (hi*hi + hi*lo + lo*hi) for token tile w, column half nh, and
-        // S = gamma_C S0 + K^T e for state rows 32 w .. 32 w + 31, column half nh; the fragments of both are
-        // requested before the first MFMA
+        // ---- every wave: S = gamma_C S0 + K^T e for state rows 32 w .. 32 w + 31 of column half `role`. K^T
+        // fragments: lane fr of a 16-lane group receives column d0 + fr of token rows R0 .. R0 + 3 from the
+        // transposing read. q wave: O^T = (gamma r_q) (Q S0)^T + d^T P^T (hi*hi + lo*hi + hi*lo) for both halves.
         {
-            bf16x8 ap[2], apl[2], dh[2], dl[2], ka[2][2], eh[2], el[2];
+            bf16x8 eh[2], el[2], ka[2][2];
 #pragma unroll
             for (int ks = 0; ks < CH / 32; ++ks) {
-                ap[ks] = frag(&sP[0][16 * w + fr][ks * 32 + fk]);
-                apl[ks] = frag(&sP[1][16 * w + fr][ks * 32 + fk]);
-                dh[ks] = frag(&sD[0][nh * 16 + fr][ks * 32 + fk]);
-                dl[ks] = frag(&sD[1][nh * 16 + fr][ks * 32 + fk]);
-                eh[ks] = frag(&sE[0][nh * 16 + fr][ks * 32 + fk]);
-                el[ks] = frag(&sE[1][nh * 16 + fr][ks * 32 + fk]);
+                eh[ks] = frag(&sE[0][role * 16 + fr][ks * 32 + fk]);
+                el[ks] = frag(&sE[1][role * 16 + fr][ks * 32 + fk]);
 #pragma unroll
-                for (int mt = 0; mt < 2; ++mt) ka[ks][mt] = frag(&sKt[kt_index(32 * w + 16 * mt + fr, ks * 32 + fk)]);
+                for (int mt = 0; mt < 2; ++mt) {
+                    const int row = 32 * ks + fk + (fr >> 2), col = 32 * w + 16 * mt + 4 * (fr & 3);
+                    ka[ks][mt] = tr_frag(&sK[kimg(row, col)], &sK[kimg(row + 4, col)]);
+                }
             }
-            const int r0 = 16 * w + fq;
-            const float4 c2 = *reinterpret_cast<const float4 *>(&s_c[2 * CH + r0]);
-            const float gC = s_c[4 * CH];
-            __builtin_amdgcn_sched_barrier(0);
-            f32x4 oacc;
-            oacc[0] = c2.x * qacc[0];
-            oacc[1] = c2.y * qacc[1];
-            oacc[2] = c2.z * qacc[2];
-            oacc[3] = c2.w * qacc[3];
+            if (role == 1) {
+                bf16x8 dh[2][2], dl[2][2];
 #pragma unroll
-            for (int ks = 0; ks < CH / 32; ++ks) {
-                oacc = mfma(ap[ks], dh[ks], oacc);
-                oacc = mfma(ap[ks], dl[ks], oacc);
-                oacc = mfma(apl[ks], dh[ks], oacc);
+                for (int nh = 0; nh < 2; ++nh)
+#pragma unroll
+                    for (int ks = 0; ks < CH / 32; ++ks) {
+                        dh[nh][ks] = frag(&sD[0][nh * 16 + fr][ks * 32 + fk]);
+                        dl[nh][ks] = frag(&sD[1][nh * 16 + fr][ks * 32 + fk]);
+                    }
+                // O^T = (gamma r_q) (Q S0)^T + d^T P^T: A = d^T, B = P^T (the P fragments, read as B)
+                const float c2 = s_c[cb][2][16 * w + fr];
+#pragma unroll
+                for (int nh = 0; nh < 2; ++nh) {
+                    f32x4 oacc;
+                    oacc[0] = c2 * acc[nh][0];
+                    oacc[1] = c2 * acc[nh][1];
+                    oacc[2] = c2 * acc[nh][2];
+                    oacc[3] = c2 * acc[nh][3];
+#pragma unroll
+                    for (int ks = 0; ks < CH / 32; ++ks) {
+                        const bf16x8 ph = __builtin_bit_cast(bf16x8, fB[ks]), pl = __builtin_bit_cast(bf16x8, fB[2 + ks]);
+                        oacc = mfma(dh[nh][ks], ph, oacc);
+                        oacc = mfma(dl[nh][ks], ph, oacc);
+                        oacc = mfma(dh[nh][ks], pl, oacc);
+                    }
+                    acc[nh] = oacc;
+                }
             }
-            opend = oacc;
+            const float gc = s_c[cb][4][0];
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) {
                 f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
@@ -593,32 +648,38 @@ __global__ __launch_bounds__(WALK_THREADS) void chunk_walk_kernel(PrefillArgs a)
                     sacc = mfma(ka[ks][mt], el[ks], sacc);
                 }
 #pragma unroll
-                for (int i = 0; i < 4; ++i) S[mt][i] = fmaf(gC, S[mt][i], sacc[i]);
+                for (int i = 0; i < 4; ++i) S[mt][i] = fmaf(gc, S[mt][i], sacc[i]);
                 mirror(mt);
             }
+            if (wv < 5) s_c[cb ^ 1][wv][lane] = __uint_as_float(psc);  // the next chunk's scalars
         }
+        fence_issue();
+        fetch_b(c + 1);
+        fence_issue();
+        store_o(c, acc);  // after the next operands are requested: a wait for those never waits for these
+        fence_issue();
         __syncthreads();
     }
-    store_o(a.nch - 1);
 
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            a.ST[((size_t)h * DK + 32 * w + 16 * mt + fq + i) * DV + SLAB * slab + 16 * nh + fr] = S[mt][i];
+            a.ST[((size_t)h * DK + 32 * w + 16 * mt + fq + i) * DV + SLAB * slab + 16 * role + fr] = S[mt][i];
 }
 
 struct PrefillWs {
-    size_t tm, p, sc, total;
+    size_t tm, p, sc, kq, total;
 };
-PrefillWs prefill_ws(int T, int NV) {
+PrefillWs prefill_ws(int T, int NK, int NV) {
     auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
     const size_t nch = (size_t)(T + CH - 1) / CH;
     PrefillWs l;
     l.tm = 0;
     l.p = up(nch * NV * 2 * CH * CH * 2);
     l.sc = l.p + up(nch * NV * 2 * CH * CH * 2);
-    l.total = l.sc + up(nch * NV * 5 * CH * 4);
+    l.kq = l.sc + up(nch * NV * 5 * CH * 4);
+    l.total = l.kq + up(nch * NK * 2 * CH * DK * 2);
     return l;
 }
 
@@ -626,7 +687,7 @@ PrefillWs prefill_ws(int T, int NV) {
 
 extern "C" size_t qs_gdn_chunk_prefill_workspace_bytes(int T, int NK, int NV, int DKa, int DVa, int chunk) {
     if (T <= 0 || NK <= 0 || NV <= 0 || NV % NK || DKa != DK || DVa != DV || chunk != CH) return 0;
-    return prefill_ws(T, NV).total;
+    return prefill_ws(T, NK, NV).total;
 }
 
 extern "C" int qs_gdn_chunk_prefill(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *g,
@@ -641,13 +702,14 @@ extern "C" int qs_gdn_chunk_prefill(const uint16_t *q, const uint16_t *k, const 
     QS_REQUIRE(chunk == CH, "qs_gdn_chunk_prefill: only chunk %d is built (got %d)", CH, chunk);
     QS_REQUIRE((long)(T + CH) * NV * DV * 2 < (1L << 31) && (long)(T + CH) * NK * DK * 2 < (1L << 31),
                "qs_gdn_chunk_prefill: T = %d tokens exceed the 2 GB buffer range", T);
-    const PrefillWs L = prefill_ws(T, NV);
+    const PrefillWs L = prefill_ws(T, NK, NV);
     char *ws = static_cast<char *>(workspace);
     PrefillArgs a{};
     a.q = q, a.k = k, a.v = v, a.g = g, a.beta = beta, a.S0 = initial_state, a.ST = final_state, a.o = o;
     a.Tm = reinterpret_cast<uint16_t *>(ws + L.tm);
     a.P = reinterpret_cast<uint16_t *>(ws + L.p);
     a.sc = reinterpret_cast<float *>(ws + L.sc);
+    a.KQ = reinterpret_cast<uint16_t *>(ws + L.kq);
     a.T = T, a.NK = NK, a.NV = NV, a.nch = (T + CH - 1) / CH, a.scale = scale, a.eps = eps;
     hipStream_t st = QS_STREAM(stream);
     chunk_prep_kernel<<<a.nch * NV, 256, 0, st>>>(a);
