@@ -36,6 +36,7 @@ constexpr int DV = 128;
 constexpr int FP = CH + 1;  // fp32 row stride of the 64 x 64 matrices of the inverse in LDS
 constexpr int SLAB = 32;    // state columns per walk workgroup
 constexpr int NSLAB = DV / SLAB;
+constexpr int MAXREP = 4;  // value heads per key head the prep handles (one gate scan per wave)
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -104,10 +105,12 @@ __device__ __forceinline__ void put16(float *D, int ds, f32x4 c, int lane) {
     for (int i = 0; i < 4; ++i) D[(4 * (lane >> 4) + i) * ds + (lane & 15)] = c[i];
 }
 
-__global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
-    const int lid = qs::xcd_logical(blockIdx.x, a.nch * a.NV);
-    const int c = lid / a.NV, h = lid % a.NV;  // the value heads of one key head on consecutive ids
-    const int rep = a.NV / a.NK, kh = h / rep;
+__global__ __launch_bounds__(256, 4) void chunk_prep_kernel(PrefillArgs a) {
+    // one workgroup per (chunk, key head): the k, q rows, their norms, K K^T and Q K^T are shared by the rep
+    // value heads of the key head, which then take turns for A, P and Tm
+    const int lid = qs::xcd_logical(blockIdx.x, a.nch * a.NK);
+    const int c = lid / a.NK, kh = lid % a.NK;
+    const int rep = a.NV / a.NK;
     const int t0 = c * CH, nval = min(CH, a.T - t0);
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int fr = lane & 15, g = lane >> 4;
@@ -115,7 +118,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
     // the K / Q images are dead once K K^T, Q K^T and the norms exist: A and Tm reuse their space,
     // which keeps the workgroup at 38 KB of LDS (four per CU)
     __shared__ __align__(16) char s_u[2 * CH * FP * 4];
-    __shared__ float s_rk[CH], s_rq[CH], s_G[CH], s_b[CH];
+    __shared__ float s_rk[CH], s_rq[CH], s_G[MAXREP][CH], s_b[MAXREP][CH];
     __shared__ float sM[4][16][16];
     const uint16_t *sK = reinterpret_cast<const uint16_t *>(s_u);
     const uint16_t *sQ = sK + CH * DK;
@@ -124,7 +127,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
     static_assert(2 * CH * DK * 2 <= 2 * CH * FP * 4, "the K / Q images must fit in the A / Tm space");
 
     // 1. the chunk's raw k, q rows of key head kh into swizzled LDS images (zeros past the sequence); the
-    //    gates of value head h (wave 0: lane = token, g = 0 and beta = 0 past the sequence)
+    //    gates of value head kh rep + w (waves w < rep: lane = token, g = 0 and beta = 0 past the sequence)
     {
         const size_t krow = (size_t)a.NK * DK * 2;  // bytes per token
         const auto rk = rsrc(a.k + (size_t)t0 * a.NK * DK, (int)(nval * krow));
@@ -138,15 +141,15 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
         }
     }
     float gi = 0.f, bi = 0.f;
-    if (w == 0 && lane < nval) {
-        gi = a.g[(size_t)(t0 + lane) * a.NV + h];
-        bi = a.beta[(size_t)(t0 + lane) * a.NV + h];
+    if (w < rep && lane < nval) {
+        gi = a.g[(size_t)(t0 + lane) * a.NV + kh * rep + w];
+        bi = a.beta[(size_t)(t0 + lane) * a.NV + kh * rep + w];
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
 
     // 2. row norms (4 lanes per row; the sum runs over the row's chunks in stored order); cumulative log
-    //    decay (wave 0, inclusive scan over the 64 tokens)
+    //    decay of each value head (waves w < rep, inclusive scan over the 64 tokens)
     {
         const int r = tid >> 2, part = tid & 3;
         float kk = 0.f, qq = 0.f;
@@ -172,18 +175,18 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
             s_rq[r] = rsqrtf(qq + a.eps) * a.scale;
         }
     }
-    if (w == 0) {
+    if (w < rep) {
 #pragma unroll
         for (int d = 1; d < 64; d <<= 1) {
             const float up = __shfl_up(gi, d, 64);
             if (lane >= d) gi += up;
         }
-        s_G[lane] = gi;
-        s_b[lane] = bi;
+        s_G[w][lane] = gi;
+        s_b[w][lane] = bi;
     }
 
-    // 2b. the first value head of each key head stores the chunk's k and q rows in fragment order for the walk
-    if (h % rep == 0) {
+    // 2b. the chunk's k and q rows in fragment order for the walk
+    {
         uint16_t *dst = a.KQ + ((size_t)c * a.NK + kh) * 2 * CH * DK;
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
@@ -223,122 +226,128 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
     }
     __syncthreads();  // every read of the K / Q images is done before A overwrites them
 
-    // 4. A (strictly lower) and P (lower with the diagonal, bf16 hi and lo planes) from the accumulators into
-    //    LDS; P is staged in the space Tm takes later and leaves in 16-byte rows
-    uint16_t(*sPh)[CH] = reinterpret_cast<uint16_t(*)[CH]>(s_u + CH * FP * 4);
-    uint16_t(*sPl)[CH] = reinterpret_cast<uint16_t(*)[CH]>(s_u + CH * FP * 4 + CH * CH * 2);
-    static_assert(2 * CH * CH * 2 <= CH * FP * 4, "P's planes must fit in the Tm space");
-    {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int ti = sig(w, 4 * g + i);
-            const float Gi = s_G[ti], rqi = s_rq[ti], bki = s_b[ti] * s_rk[ti];
-#pragma unroll
-            for (int tc = 0; tc < 4; ++tc) {
-                const int tj = sig(tc, fr);
-                float av = 0.f, p = 0.f;
-                if (ti >= tj) {
-                    // e^(G_i - G_j) as 2^((G_i - G_j) log2 e) on the hardware exponential (the rounding of
-                    // G_i - G_j dominates the error either way)
-                    const float rkj = s_rk[tj] * __builtin_amdgcn_exp2f((Gi - s_G[tj]) * 1.4426950408889634f);
-                    if (ti > tj) av = bki * rkj * ckk[tc][i];
-                    p = rqi * rkj * cqk[tc][i];
+#pragma unroll 1
+    for (int hv = 0; hv < rep; ++hv) {
+        const int h = kh * rep + hv;
+        const float *sG = s_G[hv], *sB = s_b[hv];
+        // 4. A (strictly lower) and P (lower with the diagonal, bf16 hi and lo planes) from the accumulators into
+        //    LDS; P is staged in the space Tm takes later and leaves in 16-byte rows
+        uint16_t(*sPh)[CH] = reinterpret_cast<uint16_t(*)[CH]>(s_u + CH * FP * 4);
+        uint16_t(*sPl)[CH] = reinterpret_cast<uint16_t(*)[CH]>(s_u + CH * FP * 4 + CH * CH * 2);
+        static_assert(2 * CH * CH * 2 <= CH * FP * 4, "P's planes must fit in the Tm space");
+        {
+    #pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int ti = sig(w, 4 * g + i);
+                const float Gi = sG[ti], rqi = s_rq[ti], bki = sB[ti] * s_rk[ti];
+    #pragma unroll
+                for (int tc = 0; tc < 4; ++tc) {
+                    const int tj = sig(tc, fr);
+                    float av = 0.f, p = 0.f;
+                    if (ti >= tj) {
+                        // e^(G_i - G_j) as 2^((G_i - G_j) log2 e) on the hardware exponential (the rounding of
+                        // G_i - G_j dominates the error either way)
+                        const float rkj = s_rk[tj] * __builtin_amdgcn_exp2f((Gi - sG[tj]) * 1.4426950408889634f);
+                        if (ti > tj) av = bki * rkj * ckk[tc][i];
+                        p = rqi * rkj * cqk[tc][i];
+                    }
+                    sA[ti][tj] = av;
+                    const uint32_t ph = qs::cvt_pk_bf16(p, 0.f) & 0xffffu;
+                    sPh[ti][tj] = (uint16_t)ph;
+                    sPl[ti][tj] = (uint16_t)qs::cvt_pk_bf16(p - qs::bf2f(ph), 0.f);
                 }
-                sA[ti][tj] = av;
-                const uint32_t ph = qs::cvt_pk_bf16(p, 0.f) & 0xffffu;
-                sPh[ti][tj] = (uint16_t)ph;
-                sPl[ti][tj] = (uint16_t)qs::cvt_pk_bf16(p - qs::bf2f(ph), 0.f);
             }
         }
-    }
-    __syncthreads();
-    {
-        uint16_t *Pd = a.P + ((size_t)c * a.NV + h) * 2 * CH * CH;
-        const int i = tid >> 2, j0 = (tid & 3) * 16;
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int off = frag_off(i, j0 + 8 * u, CH / 32);
-            *reinterpret_cast<uint4 *>(Pd + off) = *reinterpret_cast<const uint4 *>(&sPh[i][j0 + 8 * u]);
-            *reinterpret_cast<uint4 *>(Pd + CH * CH + off) = *reinterpret_cast<const uint4 *>(&sPl[i][j0 + 8 * u]);
+        __syncthreads();
+        {
+            uint16_t *Pd = a.P + ((size_t)c * a.NV + h) * 2 * CH * CH;
+            const int i = tid >> 2, j0 = (tid & 3) * 16;
+    #pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int off = frag_off(i, j0 + 8 * u, CH / 32);
+                *reinterpret_cast<uint4 *>(Pd + off) = *reinterpret_cast<const uint4 *>(&sPh[i][j0 + 8 * u]);
+                *reinterpret_cast<uint4 *>(Pd + CH * CH + off) = *reinterpret_cast<const uint4 *>(&sPl[i][j0 + 8 * u]);
+            }
         }
-    }
-    __syncthreads();  // P's staging space becomes Tm's
+        __syncthreads();  // P's staging space becomes Tm's
 
-    // 5. Tm = (I + A)^-1 by 16 x 16 blocks.
-    //  (a) diagonal blocks by forward substitution, wave 0, one column per lane (16 lanes per block):
-    //      t_i = [i == col] - sum_{k < i} A_ik t_k, the column held in registers;
-    if (w == 0) {
-        const int b0 = 16 * (lane >> 4), col = lane & 15;
-        float t[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            float s = i == col ? 1.f : 0.f;
-#pragma unroll
-            for (int k = 0; k < i; ++k) s = fmaf(-sA[b0 + i][b0 + k], t[k], s);
-            t[i] = s;
+        // 5. Tm = (I + A)^-1 by 16 x 16 blocks.
+        //  (a) diagonal blocks by forward substitution, wave 0, one column per lane (16 lanes per block):
+        //      t_i = [i == col] - sum_{k < i} A_ik t_k, the column held in registers;
+        if (w == 0) {
+            const int b0 = 16 * (lane >> 4), col = lane & 15;
+            float t[16];
+    #pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                float s = i == col ? 1.f : 0.f;
+    #pragma unroll
+                for (int k = 0; k < i; ++k) s = fmaf(-sA[b0 + i][b0 + k], t[k], s);
+                t[i] = s;
+            }
+    #pragma unroll
+            for (int i = 0; i < 16; ++i) sT[b0 + i][b0 + col] = t[i];
         }
-#pragma unroll
-        for (int i = 0; i < 16; ++i) sT[b0 + i][b0 + col] = t[i];
-    }
-    __syncthreads();
-    //  (b) 32 x 32 diagonal blocks: T_10 = -T_11 (A_10 T_00) and T_32 = -T_33 (A_32 T_22), waves 0 and 1;
-    if (w < 2) {
-        const int b = 32 * w;
-        f32x4 m = {0.f, 0.f, 0.f, 0.f};
-        mm16(m, &sA[b + 16][b], FP, &sT[b][b], FP, lane);
-        put16(&sM[w][0][0], 16, m, lane);
-    }
-    __syncthreads();
-    if (w < 2) {
-        const int b = 32 * w;
-        f32x4 r = {0.f, 0.f, 0.f, 0.f};
-        mm16(r, &sT[b + 16][b + 16], FP, &sM[w][0][0], 16, lane);
-        put16(&sT[b + 16][b], FP, -r, lane);
-    }
-    __syncthreads();
-    //  (c) the lower-left 32 x 32 quarter: X_IJ = sum_{K=J}^{1} A_IK T_KJ, then T_IJ = -sum_{K=2}^{I} T_IK X_KJ,
-    //      wave w owns block (I, J) = (2 + w / 2, w % 2). MFMA 16x16x4 fp32: exact fp32 products.
-    const int I = 2 + (w >> 1), J = w & 1;
-    {
-        f32x4 x = {0.f, 0.f, 0.f, 0.f};
-        for (int K = J; K < 2; ++K) mm16(x, &sA[16 * I][16 * K], FP, &sT[16 * K][16 * J], FP, lane);
-        put16(&sM[w][0][0], 16, x, lane);
-    }
-    __syncthreads();
-    {
-        f32x4 r = {0.f, 0.f, 0.f, 0.f};
-        for (int K = 2; K <= I; ++K) mm16(r, &sT[16 * I][16 * K], FP, &sM[2 * (K - 2) + J][0][0], 16, lane);
-        put16(&sT[16 * I][16 * J], FP, -r, lane);
-    }
-    __syncthreads();
+        __syncthreads();
+        //  (b) 32 x 32 diagonal blocks: T_10 = -T_11 (A_10 T_00) and T_32 = -T_33 (A_32 T_22), waves 0 and 1;
+        if (w < 2) {
+            const int b = 32 * w;
+            f32x4 m = {0.f, 0.f, 0.f, 0.f};
+            mm16(m, &sA[b + 16][b], FP, &sT[b][b], FP, lane);
+            put16(&sM[w][0][0], 16, m, lane);
+        }
+        __syncthreads();
+        if (w < 2) {
+            const int b = 32 * w;
+            f32x4 r = {0.f, 0.f, 0.f, 0.f};
+            mm16(r, &sT[b + 16][b + 16], FP, &sM[w][0][0], 16, lane);
+            put16(&sT[b + 16][b], FP, -r, lane);
+        }
+        __syncthreads();
+        //  (c) the lower-left 32 x 32 quarter: X_IJ = sum_{K=J}^{1} A_IK T_KJ, then T_IJ = -sum_{K=2}^{I} T_IK X_KJ,
+        //      wave w owns block (I, J) = (2 + w / 2, w % 2). MFMA 16x16x4 fp32: exact fp32 products.
+        const int I = 2 + (w >> 1), J = w & 1;
+        {
+            f32x4 x = {0.f, 0.f, 0.f, 0.f};
+            for (int K = J; K < 2; ++K) mm16(x, &sA[16 * I][16 * K], FP, &sT[16 * K][16 * J], FP, lane);
+            put16(&sM[w][0][0], 16, x, lane);
+        }
+        __syncthreads();
+        {
+            f32x4 r = {0.f, 0.f, 0.f, 0.f};
+            for (int K = 2; K <= I; ++K) mm16(r, &sT[16 * I][16 * K], FP, &sM[2 * (K - 2) + J][0][0], 16, lane);
+            put16(&sT[16 * I][16 * J], FP, -r, lane);
+        }
+        __syncthreads();
 
-    // 6. Tm (bf16 hi and lo planes, zero above the diagonal) and the per-token scalars to the workspace
-    const size_t mat = ((size_t)c * a.NV + h) * CH * CH;
-    {
-        const int i = tid >> 2, j0 = (tid & 3) * 16;
-        uint32_t th[8], tl[8];
-#pragma unroll
-        for (int u = 0; u < 16; u += 2) {
-            const float v0 = i >= j0 + u ? sT[i][j0 + u] : 0.f, v1 = i >= j0 + u + 1 ? sT[i][j0 + u + 1] : 0.f;
-            th[u / 2] = qs::cvt_pk_bf16(v0, v1);
-            tl[u / 2] = qs::cvt_pk_bf16(v0 - qs::bf_lo(th[u / 2]), v1 - qs::bf_hi(th[u / 2]));
+        // 6. Tm (bf16 hi and lo planes, zero above the diagonal) and the per-token scalars to the workspace
+        const size_t mat = ((size_t)c * a.NV + h) * CH * CH;
+        {
+            const int i = tid >> 2, j0 = (tid & 3) * 16;
+            uint32_t th[8], tl[8];
+    #pragma unroll
+            for (int u = 0; u < 16; u += 2) {
+                const float v0 = i >= j0 + u ? sT[i][j0 + u] : 0.f, v1 = i >= j0 + u + 1 ? sT[i][j0 + u + 1] : 0.f;
+                th[u / 2] = qs::cvt_pk_bf16(v0, v1);
+                tl[u / 2] = qs::cvt_pk_bf16(v0 - qs::bf_lo(th[u / 2]), v1 - qs::bf_hi(th[u / 2]));
+            }
+            uint16_t *Td = a.Tm + 2 * mat;
+            const int o0 = frag_off(i, j0, CH / 32), o1 = frag_off(i, j0 + 8, CH / 32);
+            *reinterpret_cast<uint4 *>(Td + o0) = make_uint4(th[0], th[1], th[2], th[3]);
+            *reinterpret_cast<uint4 *>(Td + o1) = make_uint4(th[4], th[5], th[6], th[7]);
+            *reinterpret_cast<uint4 *>(Td + CH * CH + o0) = make_uint4(tl[0], tl[1], tl[2], tl[3]);
+            *reinterpret_cast<uint4 *>(Td + CH * CH + o1) = make_uint4(tl[4], tl[5], tl[6], tl[7]);
         }
-        uint16_t *Td = a.Tm + 2 * mat;
-        const int o0 = frag_off(i, j0, CH / 32), o1 = frag_off(i, j0 + 8, CH / 32);
-        *reinterpret_cast<uint4 *>(Td + o0) = make_uint4(th[0], th[1], th[2], th[3]);
-        *reinterpret_cast<uint4 *>(Td + o1) = make_uint4(th[4], th[5], th[6], th[7]);
-        *reinterpret_cast<uint4 *>(Td + CH * CH + o0) = make_uint4(tl[0], tl[1], tl[2], tl[3]);
-        *reinterpret_cast<uint4 *>(Td + CH * CH + o1) = make_uint4(tl[4], tl[5], tl[6], tl[7]);
-    }
-    if (tid < CH) {
-        const int i = tid;
-        const float gam = expf(s_G[i]);
-        float *scp = a.sc + ((size_t)c * a.NV + h) * 5 * CH;
-        scp[0 * CH + i] = s_b[i];
-        scp[1 * CH + i] = s_b[i] * gam * s_rk[i];
-        scp[2 * CH + i] = s_rq[i] * gam;
-        scp[3 * CH + i] = s_rk[i] * expf(s_G[CH - 1] - s_G[i]);
-        scp[4 * CH + i] = expf(s_G[CH - 1]);
+        if (tid < CH) {
+            const int i = tid;
+            const float gam = expf(sG[i]);
+            float *scp = a.sc + ((size_t)c * a.NV + h) * 5 * CH;
+            scp[0 * CH + i] = sB[i];
+            scp[1 * CH + i] = sB[i] * gam * s_rk[i];
+            scp[2 * CH + i] = s_rq[i] * gam;
+            scp[3 * CH + i] = s_rk[i] * expf(sG[CH - 1] - sG[i]);
+            scp[4 * CH + i] = expf(sG[CH - 1]);
+        }
+        __syncthreads();  // the next head's A and P overwrite what this head's Tm store reads
     }
 }
 
@@ -405,8 +414,11 @@ __device__ __forceinline__ void fence_issue() {
 
 constexpr int WALK_THREADS = 512;
 __global__ __launch_bounds__(WALK_THREADS) void chunk_walk_kernel(PrefillArgs a) {
-    constexpr int SKP = DK + 16;  // bf16 row stride of the S^T planes
-    constexpr int TP = CH + 16;   // bf16 row stride of the [.][token] planes
+    // row strides (bf16) of the S^T planes and of the [.][token] planes: 272 and 144 bytes, 16 bytes past a
+    // multiple of 128, so the 8 lanes that share a cycle of a 16-byte fragment read (8 consecutive rows) hit
+    // 8 different 16-byte bank groups
+    constexpr int SKP = DK + 8;
+    constexpr int TP = CH + 8;
     const int nwg = a.NV * NSLAB;
     const int lid = qs::xcd_logical(blockIdx.x, nwg);
     const int slab = lid % NSLAB, h = lid / NSLAB;
@@ -686,7 +698,7 @@ PrefillWs prefill_ws(int T, int NK, int NV) {
 }  // namespace
 
 extern "C" size_t qs_gdn_chunk_prefill_workspace_bytes(int T, int NK, int NV, int DKa, int DVa, int chunk) {
-    if (T <= 0 || NK <= 0 || NV <= 0 || NV % NK || DKa != DK || DVa != DV || chunk != CH) return 0;
+    if (T <= 0 || NK <= 0 || NV <= 0 || NV % NK || NV / NK > MAXREP || DKa != DK || DVa != DV || chunk != CH) return 0;
     return prefill_ws(T, NK, NV).total;
 }
 
@@ -699,6 +711,8 @@ extern "C" int qs_gdn_chunk_prefill(const uint16_t *q, const uint16_t *k, const 
     QS_REQUIRE(T > 0, "qs_gdn_chunk_prefill: T must be positive (got %d)", T);
     QS_REQUIRE(DKa == DK && DVa == DV, "qs_gdn_chunk_prefill: DK and DV must be 128 (got %d, %d)", DKa, DVa);
     QS_REQUIRE(NK > 0 && NV > 0 && NV % NK == 0, "qs_gdn_chunk_prefill: NV (%d) must be a multiple of NK (%d)", NV, NK);
+    QS_REQUIRE(NV / NK <= MAXREP, "qs_gdn_chunk_prefill: at most %d value heads per key head are built (got %d)", MAXREP,
+               NV / NK);
     QS_REQUIRE(chunk == CH, "qs_gdn_chunk_prefill: only chunk %d is built (got %d)", CH, chunk);
     QS_REQUIRE((long)(T + CH) * NV * DV * 2 < (1L << 31) && (long)(T + CH) * NK * DK * 2 < (1L << 31),
                "qs_gdn_chunk_prefill: T = %d tokens exceed the 2 GB buffer range", T);
@@ -712,7 +726,7 @@ extern "C" int qs_gdn_chunk_prefill(const uint16_t *q, const uint16_t *k, const 
     a.KQ = reinterpret_cast<uint16_t *>(ws + L.kq);
     a.T = T, a.NK = NK, a.NV = NV, a.nch = (T + CH - 1) / CH, a.scale = scale, a.eps = eps;
     hipStream_t st = QS_STREAM(stream);
-    chunk_prep_kernel<<<a.nch * NV, 256, 0, st>>>(a);
+    chunk_prep_kernel<<<a.nch * NK, 256, 0, st>>>(a);
     if (int e = qs::launch_status("qs_gdn_chunk_prefill (prep)")) return e;
     chunk_walk_kernel<<<NV * NSLAB, WALK_THREADS, 0, st>>>(a);
     return qs::launch_status("qs_gdn_chunk_prefill (walk)");
