@@ -34,6 +34,28 @@ def test_prefill_matches_recurrence(dev, T):
     assert_bf16_output(o, O.bf16(o_ref.float()))
 
 
+@pytest.mark.parametrize("nk,nv", [(4, 4), (4, 8), (2, 8)])
+def test_prefill_head_ratios(dev, nk, nv):
+    """1, 2 and 4 value heads per key head (the prep forms K K^T and Q K^T once per key head and takes the
+    value heads in turn); 130 tokens, a partial last chunk."""
+    T = 130
+    d = W.prefill(T, "cpu", seed=7)
+    d = {"q": d["q"][:, :nk], "k": d["k"][:, :nk], "v": d["v"][:, :nv], "g": d["g"][:, :nv],
+         "beta": d["beta"][:, :nv], "S0": d["S0"][:nv]}  # fmt: skip
+    d = {n: t.contiguous() for n, t in d.items()}
+    o, S = run(dev, d, T)
+    o_ref, S_ref = ref(d, T)
+    assert_prefill_state(S, S_ref.float())
+    assert_bf16_output(o, O.bf16(o_ref.float()))
+
+
+def test_prefill_rejects_more_than_four_value_heads_per_key_head(dev):
+    d = W.prefill(64, "cpu", seed=8)
+    with pytest.raises((RuntimeError, ValueError)):
+        run(dev, {"q": d["q"][:, :1].contiguous(), "k": d["k"][:, :1].contiguous(), "v": d["v"][:, :8].contiguous(),
+                  "g": d["g"][:, :8].contiguous(), "beta": d["beta"][:, :8].contiguous(), "S0": d["S0"][:8].contiguous()}, 64)  # fmt: skip
+
+
 def test_prefill_8192_tokens(dev):
     """The prefill workload: one GDN layer over 8192 tokens (128 chunks), 16 key / 48 value heads."""
     d = W.prefill(8192, "cpu", seed=4)
