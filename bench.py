@@ -182,13 +182,26 @@ def replay_times(torch, replay, n, between=None):
     return [e0.elapsed_time(e1) for e0, e1 in evs], wall
 
 
-def timed(torch, args, replay, between=None, tel=None):
-    """W untimed replays, K timed replays (the contract's step count) and a statistics pass of max(K, 200)
-    replays with telemetry. Returns (ms mean over K, stats dict)."""
+SETTLE_MS = 150.0  # untimed replays before a per-workload line's timed replays (its first replays run slower)
+
+
+def timed(torch, args, replay, between=None, tel=None, settle_ms=0.0):
+    """W untimed replays (then more, untimed, until settle_ms of wall time have passed: the per-workload lines
+    settle the clocks this way, the headline step keeps exactly W), K timed replays (the contract's step count)
+    and a statistics pass of max(K, 200) replays with telemetry. Returns (ms mean over K, stats dict)."""
     for _ in range(args.warmup):
         replay()
         if between is not None:
             between()
+    if settle_ms > 0:
+        torch.cuda.synchronize()
+        t_end = time.perf_counter() + settle_ms / 1e3
+        while time.perf_counter() < t_end:
+            for _ in range(8):
+                replay()
+                if between is not None:
+                    between()
+            torch.cuda.synchronize()
     ts, wall = replay_times(torch, replay, args.steps, between)
     n = max(args.steps, 200)
     if tel is not None:
@@ -408,7 +421,7 @@ def bench_gdn_layer(args, torch, tel):
                 ops.gdn_decode_fused(d["x"], d["conv_state"], d["taps"], d["g"], d["beta"], d["state"], out=o, ws=ws)
 
     g = capture(torch, fn)
-    msr, stats = timed(torch, args, g.replay, tel=tel)
+    msr, stats = timed(torch, args, g.replay, tel=tel, settle_ms=SETTLE_MS)
     ms = msr / (48 * R)
     stats = {k: (v / (48 * R) if k.endswith("_ms") else v) for k, v in stats.items()}
     nbytes = layer_bytes(1, 0)
@@ -445,7 +458,7 @@ def bench_attn_layer(args, torch, tel):
                                      k_new=d["k_new"], v_new=d["v_new"], pages_per_split=pps, out=o, ws=ws)  # fmt: skip
 
     g = capture(torch, fn)
-    msr, stats = timed(torch, args, g.replay, tel=tel)
+    msr, stats = timed(torch, args, g.replay, tel=tel, settle_ms=SETTLE_MS)
     ms = msr / (4 * R)
     stats = {k: (v / (4 * R) if k.endswith("_ms") else v) for k, v in stats.items()}
     nbytes = layer_bytes(1, 32768, attn=True)
@@ -473,7 +486,7 @@ def bench_verify(args, torch, tel):
     vs.step()
     vs.rewind()
     vs.capture()
-    ms, stats = timed(torch, args, vs.replay, between=vs.rewind, tel=tel)
+    ms, stats = timed(torch, args, vs.replay, between=vs.rewind, tel=tel, settle_ms=SETTLE_MS)
     nbytes = vs.bytes_per_step(8192)
     out = entry("MTP verify step, batch 1, 8192 positions, 1 + 3 draft tokens through 48 GDN + 16 attention layers, "
                 "then acceptance of a seeded length by snapshot-slot selection", nbytes, ms, stats,
@@ -525,8 +538,8 @@ def bench_prefill(args, torch, tel):
         ops.paged_kv_fill(d["kv_k"], d["kv_v"], kc, vc, d["page_table"])
 
     g = capture(torch, fn)
-    a2 = argparse.Namespace(**{**vars(args), "steps": max(3, args.steps // 5), "warmup": 2})
-    ms, stats = timed(torch, a2, g.replay, tel=tel)
+    a2 = argparse.Namespace(**{**vars(args), "steps": max(10, args.steps // 5)})
+    ms, stats = timed(torch, a2, g.replay, tel=tel, settle_ms=SETTLE_MS)
     out = entry("chunked-prefill gated delta rule, 8192 tokens, chunk 64, 16/48 heads x 128 (WY form, bf16 MFMA, fp32 "
                 "state) + paged fill of 8192 tokens of K/V (4 x 256) into 128 random pages", PREFILL_BYTES, ms, stats,
                 roofline("gdn_chunk_prefill", PREFILL_BYTES, ms, flops=PREFILL_FLOPS),
@@ -568,7 +581,7 @@ def bench_conv_prefill(args, torch, tel):
                                        _p(b["v"]), _p(b["out"]), T, CQ, CV, 4, st)) for b in bufs] * R  # fmt: skip
 
     g = capture_calls(torch, calls)
-    msr, stats = timed(torch, args, g.replay, tel=tel)
+    msr, stats = timed(torch, args, g.replay, tel=tel, settle_ms=SETTLE_MS)
     ms = msr / (2 * R)
     stats = {k: (v / (2 * R) if k.endswith("_ms") else v) for k, v in stats.items()}
     nbytes = 2 * T * C * 2 + C * 4 * 2 + 2 * C * 3 * 2  # x in, q | k | v out, taps, carry in and out
