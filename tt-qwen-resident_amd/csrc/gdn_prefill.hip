@@ -11,11 +11,13 @@
 //   S  = gamma_C S0 + K^T diag(r_k gamma_C / gamma) d
 // (the chunked gated delta rule of Yang et al., "Gated Delta Networks", as FLA's chunk_gated_delta_rule
 // computes it). Two kernels:
-//   chunk_prep  one workgroup per (chunk, value head), fully parallel: K K^T and Q K^T on MFMA from the raw
-//               bf16 rows (exact products, fp32 sums), A and P from the accumulators, the triangular inverse
-//               Tm (16 x 16 diagonal blocks by forward substitution, then the 32 x 32 and 64 x 64 levels of
-//               the block recursion [T1 0; -T2 A21 T1  T2] on fp32 MFMA) and the per-token scalars into the
-//               workspace (Tm and P as bf16 hi + lo planes);
+//   chunk_prep  one workgroup per (chunk, key head), fully parallel: the row norms, K K^T and Q K^T on MFMA
+//               from the raw bf16 rows (exact products, fp32 sums) once for the key head, then for each of its
+//               value heads in turn A and P from the accumulators, the triangular inverse Tm (16 x 16
+//               diagonal blocks by forward substitution, then the 32 x 32 and 64 x 64 levels of the block
+//               recursion [T1 0; -T2 A21 T1  T2] on fp32 MFMA) and the per-token scalars into the workspace;
+//               Tm and P (bf16 hi + lo planes) and a copy of the chunk's k and q rows go there in MFMA
+//               fragment order, so the walk loads each fragment as one contiguous kilobyte;
 //   chunk_walk  one 8-wave workgroup per (value head, 32-column slab of S): the 128 x 32 fp32 state slab stays
 //               on chip while the workgroup walks the chunks in order. Every product that touches S or d
 //               splits the fp32 operand into bf16 hi + lo halves (two MFMAs, three for Tm x X), so the
