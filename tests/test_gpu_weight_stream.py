@@ -1,0 +1,111 @@
+"""Weight-streaming projections and the MLP half on the GPU against the oracle: the device quantizer bit for
+bit against the oracle's MXFP4 / MXFP8 quantization and layout (ties, saturation, zero and tiny blocks), the
+streamed y = h W against h times the dequantized weight (fp32 accumulation: rtol 1e-4), and the MLP half
+x + bf16(silu(h G) (h U)) D at the reference's shape (H 5120, I 17408) and at small ones."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import weight_stream as WS
+from qwen36_state import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g) * scale
+
+
+def _special_blocks(w, fmt):
+    """Blocks that exercise the encoder's edges: all zeros, exact ties at scale 1, saturation, tiny values."""
+    w[:32, 0] = 0.0
+    if fmt == 4:
+        ties = [6.0, 0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, -0.3, 0.1, -0.1, -6.0, 0.5, -2.5, -5.0]
+        w[32:64, 1] = 0.0
+        w[32 : 32 + len(ties), 1] = torch.tensor(ties)
+        w[64:96, 2] = torch.linspace(-7.9, 7.9, 32)
+    else:
+        ties = [480.0, 448.0, 1.0, 1.0625, 1.1875, 2.0**-10, 3 * 2.0**-10, -1.0, 2.0**-6, -1.0625, 300.0]
+        w[32:64, 1] = 0.0
+        w[32 : 32 + len(ties), 1] = torch.tensor(ties)
+        w[64:96, 2] = torch.linspace(-500.0, 500.0, 32)
+    w[96:128, 3] = 1e-30 * torch.arange(1, 33)
+    return w
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+def test_quantize_matches_oracle(dev, fmt):
+    K, N = 256, 64
+    w = _special_blocks(_rand((K, N), 1, 0.05), fmt)
+    packed = ops.MxWeight.quantize(w.to(dev), fmt).packed.cpu().numpy()
+    codes, e = WS.mx_quantize(w.double(), fmt)
+    np.testing.assert_array_equal(packed, WS.mx_pack(codes, e, fmt))
+
+
+def _dequantized(W):
+    codes, e = WS.mx_unpack(W.packed.cpu().numpy(), W.K, W.N, W.fmt)
+    return WS.mx_dequantize(codes, e, W.fmt)
+
+
+@pytest.mark.parametrize("fmt,K,N,B", [(4, 512, 128, 1), (4, 5120, 256, 8), (8, 1024, 64, 16), (8, 17408, 64, 1),
+                                       (4, 256, 2048, 3)])  # fmt: skip
+def test_mx_linear(dev, fmt, K, N, B):
+    w = _rand((K, N), 2, 1 / math.sqrt(K))
+    W = ops.MxWeight.quantize(w.to(dev), fmt)
+    h = _rand((B, K), 3).bfloat16()
+    y = ops.mx_linear(h.to(dev), W)
+    ref = h.double() @ _dequantized(W)
+    torch.testing.assert_close(y.cpu().double(), ref, rtol=1e-4, atol=1e-5 * ref.abs().max().item())
+
+
+def _mlp(dev, B, H, I, seed=4):
+    gate = ops.MxWeight.quantize(_rand((H, I), seed, 1 / math.sqrt(H)).to(dev), ops.MXFP4)
+    up = ops.MxWeight.quantize(_rand((H, I), seed + 1, 1 / math.sqrt(H)).to(dev), ops.MXFP4)
+    down = ops.MxWeight.quantize(_rand((I, H), seed + 2, 0.5 / math.sqrt(I)).to(dev), ops.MXFP8)
+    gamma = 1 + 0.1 * _rand((H,), seed + 3)
+    x = _rand((B, H), seed + 4)
+    return x, gamma, gate, up, down
+
+
+def _rel(a, b):
+    return ((a - b).norm() / b.norm()).item()
+
+
+@pytest.mark.parametrize("B,H,I", [(1, 256, 512), (8, 512, 1024), (16, 256, 256), (1, 5120, 17408)])
+def test_mlp_decode(dev, B, H, I):
+    x, gamma, gate, up, down = _mlp(dev, B, H, I)
+    out = ops.mlp_decode(x.to(dev), gamma.to(dev), gate, up, down).cpu().double()
+    G, U, D = _dequantized(gate), _dequantized(up), _dequantized(down)
+    ref = WS.mlp_half(x.double(), gamma.double(), G, U, D)
+    delta, dref = out - x.double(), ref - x.double()
+    # h and z are bf16: where the kernel's fp32 rmsnorm or gate product sits within an ulp of a bf16 rounding
+    # boundary it may round the other way; such elements move the output by ~2^-9 of one term
+    assert _rel(delta, dref) < 2e-3
+    torch.testing.assert_close(delta, dref, rtol=2e-2, atol=5e-3 * dref.pow(2).mean().sqrt().item())
+    # negative control: the oracle with gate and up exchanged is far off
+    assert _rel(delta, WS.mlp_half(x.double(), gamma.double(), U, G, D) - x.double()) > 0.1
+
+
+def test_mlp_decode_in_place_and_repeatable(dev):
+    x, gamma, gate, up, down = _mlp(dev, 4, 256, 512, seed=9)
+    xd = x.to(dev)
+    a = ops.mlp_decode(xd, gamma.to(dev), gate, up, down)
+    b = xd.clone()
+    ops.mlp_decode(b, gamma.to(dev), gate, up, down, out=b)
+    assert torch.equal(a, b)
+
+
+def test_rejects_bad_shapes(dev):
+    with pytest.raises(ValueError):
+        ops.MxWeight.quantize(torch.zeros(100, 16, device=dev), ops.MXFP4)
+    with pytest.raises(ValueError):
+        ops.MxWeight.quantize(torch.zeros(128, 20, device=dev), ops.MXFP8)
+    W = ops.MxWeight.quantize(torch.zeros(128, 16, device=dev), ops.MXFP4)
+    with pytest.raises(ValueError):
+        ops.mx_linear(torch.zeros(17, 128, dtype=torch.bfloat16, device=dev), W)
+    x, gamma, gate, up, down = _mlp(dev, 2, 256, 512)
+    with pytest.raises(ValueError):
+        ops.mlp_decode(x.to(dev), gamma.to(dev), up, gate, gate)  # down must be MXFP8 [I, H]

@@ -555,3 +555,73 @@ def attn_mixer_decode(q, k_new, v_new, gate, wq, wk, cos, sin, k_cache, v_cache,
          _p(seq_lens), _p(o), _p(ws), B, T, nq, nkv, hd, block, mb, nb, pages_per_split, float(eps), _p(status),
          _stream(dev))  # fmt: skip
     return o
+
+
+# ----------------------------------------------------------- weight-streaming projections and the MLP half
+
+HIDDEN, INTER = 5120, 17408  # common.py:13-14
+MXFP4, MXFP8 = 4, 8  # fmt codes of include/qwen_state.h
+
+
+class MxWeight:
+    """A weight W [K, N] (y = h W) quantized on the device to OCP MXFP4 or MXFP8 and laid out in the kernels'
+    fragment order (the reference quantizes to 4- / 8-bit block floating point on the host and lays the
+    tiles out per DRAM bank: common.py:115-116, tests/bench_resident_mlp.py:51-96)."""
+
+    def __init__(self, packed, K, N, fmt):
+        self.packed, self.K, self.N, self.fmt = packed, K, N, fmt
+
+    @classmethod
+    def quantize(cls, w, fmt):
+        """Quantize an fp32 [K, N] weight on its device (32 values along K per E8M0 scale)."""
+        dev = w.device
+        K, N = w.shape
+        _chk(w, "w", torch.float32, (K, N), dev)
+        nbytes = lib().qs_mx_packed_bytes(K, N, fmt)
+        if nbytes == 0:
+            raise ValueError(f"fmt {fmt} (4 or 8) needs N % 16 == 0 and K % {128 if fmt == MXFP4 else 64} == 0 "
+                             f"(got K {K}, N {N})")  # fmt: skip
+        packed = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        call("qs_mx_quantize", _p(w), _p(packed), K, N, int(fmt), _stream(dev))
+        return cls(packed, K, N, fmt)
+
+
+def mx_linear(h, weight, out=None, ws=None):
+    """y = h W for 1..16 rows h [B, K] bf16 and a streamed MxWeight: the reference's M = 1 projections of
+    rmsnorm'd rows through the weight ring (kernels/streamer_compute.cpp:371-449). Returns y [B, N] fp32."""
+    dev = h.device
+    B = h.shape[0]
+    _chk(h, "h", torch.bfloat16, (B, weight.K), dev)
+    if not 1 <= B <= 16:
+        raise ValueError(f"1 to 16 rows (got {B})")
+    y = torch.empty(B, weight.N, dtype=torch.float32, device=dev) if out is None else out
+    _chk(y, "out", torch.float32, (B, weight.N), dev)
+    if ws is None:
+        ws = workspace(("mx_gemv", weight.fmt), lib().qs_mx_gemv_workspace_bytes(B, weight.K, weight.N, weight.fmt), dev)
+    call("qs_mx_gemv", _p(h), _p(weight.packed), _p(y), _p(ws), B, weight.K, weight.N, int(weight.fmt), _stream(dev))
+    return y
+
+
+def mlp_decode(x, gamma, gate, up, down, eps=EPS, out=None, ws=None):
+    """The MLP half of a decoder layer for 1..16 rows (tests/bench_resident_mlp.py:98-105):
+    x + (silu(h G) * (h U)) D with h = bf16(x * rsqrt(mean(x^2) + eps) * gamma), z = silu(h G) * (h U) kept
+    in bf16. x [B, H] fp32, gamma [H] fp32; gate, up MxWeight MXFP4 [H, I]; down MxWeight MXFP8 [I, H].
+    Returns x_out [B, H] fp32 (``out`` may be ``x``)."""
+    dev = x.device
+    B, H = x.shape
+    _chk(x, "x", torch.float32, (B, H), dev)
+    _chk(gamma, "gamma", torch.float32, (H,), dev)
+    I = gate.N
+    for w, name, shape, fmt in ((gate, "gate", (H, I), MXFP4), (up, "up", (H, I), MXFP4), (down, "down", (I, H), MXFP8)):
+        if (w.K, w.N) != shape or w.fmt != fmt:
+            raise ValueError(f"{name} must be a {shape} MXFP{fmt} weight (got {(w.K, w.N)} MXFP{w.fmt})")
+    nbytes = lib().qs_mlp_decode_workspace_bytes(B, H, I)
+    if nbytes == 0:
+        raise ValueError(f"1 to 16 rows, H % 128 == 0, I % 256 == 0 (got B {B}, H {H}, I {I})")
+    y = torch.empty_like(x) if out is None else out
+    _chk(y, "out", torch.float32, (B, H), dev)
+    if ws is None:
+        ws = workspace("mlp", nbytes, dev)
+    call("qs_mlp_decode", _p(x), _p(gamma), _p(gate.packed), _p(up.packed), _p(down.packed), _p(y), _p(ws), B, H, I,
+         float(eps), _stream(dev))  # fmt: skip
+    return y
