@@ -2,7 +2,8 @@
 """Decode-time state path of the hybrid Gated-DeltaNet / attention Qwen3.6-27B engine on one MI355X.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--workload all|step|gdn-layer|attn-layer|
-                     verify-step|prefill|conv-prefill] [--profile-family gdn|attn|conv|copy]
+                     verify-step|prefill|conv-prefill|mlp-layer]
+                    [--profile-family gdn|attn|conv|copy|prefill|mlp]
 
 Default (``--workload all``): one JSON line whose top level is the headline workload — the batch-8 decode
 step at 4096 positions per user: 48 Gated-DeltaNet layers (conv1d update + L2-norm + gated delta rule on
@@ -15,6 +16,7 @@ random block tables), replayed as one HIP graph that also advances every user's 
   verify-step   MTP verify at batch 1, 8192 positions, 4 tokens, 64 layers + acceptance by slot
   prefill       chunked gated delta rule over 8192 tokens + the paged K/V fill
   conv-prefill  the prompt conv with its carry over 8192 tokens (the prefill -> decode handoff)
+  mlp-layer     the MLP half of one layer at one row, weights streamed as MXFP4 (gate | up) and MXFP8 (down)
 Inputs are seeded synthetic tensors resident in HBM before the timed region.
 
 Timing: K timed replays (``--steps``) bracketed by synchronisation, each replay between its own pair of HIP
@@ -598,6 +600,56 @@ def bench_conv_prefill(args, torch, tel):
     return out
 
 
+def mlp_bytes(B, H, I):
+    """Algorithmic HBM bytes of one MLP half: the packed gate | up (MXFP4) and down (MXFP8) weights, x in,
+    gamma, x_out."""
+    from qwen36_state._lib import lib
+
+    L = lib()
+    return 2 * L.qs_mx_packed_bytes(H, I, 4) + L.qs_mx_packed_bytes(I, H, 8) + 2 * B * H * 4 + H * 4
+
+
+def bench_mlp_layer(args, torch, tel):
+    """The MLP half of one decoder layer at one row (the reference's 1-chip MLP bench: x [1, 5120], gate | up
+    [5120, 17408] 4-bit, down [17408, 5120] 8-bit, us per layer and weight GB/s): three layers' weights
+    (560 MB, beyond the 256 MB Infinity Cache) rotate, twice per replay; per layer = replay / 6."""
+    from qwen36_state import ops, workloads as W
+
+    B, H, I = 1, ops.HIDDEN, ops.INTER
+    layers = [W.mlp_layer(B, "cuda:0", seed=i, keep_fp32=(i == 0 and not args.no_cpu)) for i in range(3)]
+    for d in layers:
+        d["out"] = torch.empty_like(d["x"])
+    ws = torch.empty(ops.lib().qs_mlp_decode_workspace_bytes(B, H, I), dtype=torch.uint8, device="cuda:0")
+    R = 2
+
+    def calls(st):
+        return [("qs_mlp_decode", (_p(d["x"]), _p(d["gamma"]), _p(d["gate"].packed), _p(d["up"].packed),
+                                   _p(d["down"].packed), _p(d["out"]), _p(ws), B, H, I, ctypes.c_float(ops.EPS),
+                                   st)) for d in layers] * R  # fmt: skip
+
+    g = capture_calls(torch, calls)
+    msr, stats = timed(torch, args, g.replay, tel=tel, settle_ms=SETTLE_MS)
+    n = len(layers) * R
+    ms = msr / n
+    stats = {k: (v / n if k.endswith("_ms") else v) for k, v in stats.items()}
+    nbytes = mlp_bytes(B, H, I)
+    out = entry("MLP half of one decoder layer, 1 row: rmsnorm + gate | up 5120 x 17408 MXFP4 with silu, down "
+                "17408 x 5120 MXFP8 in 4 K splits + residual (2 launches)", nbytes, ms, stats,
+                roofline("mlp_decode", nbytes, ms))  # fmt: skip
+    out["us_per_layer"] = out["us_per_step"]
+    if not args.no_cpu:
+        _oracle()
+        from oracle import weight_stream as WS
+
+        d = layers[0]
+        x, gamma = d["x"].cpu(), d["gamma"].cpu()
+        G, U, D = d["gate32"], d["up32"], d["down32"]
+        t = cpu_time(torch, lambda: WS.mlp_half(x, gamma, G, U, D))
+        out["cpu_baseline"] = cpu_entry(torch, nbytes, t, "the oracle's MLP half (fp32 weights, dequantization not "
+                                        "timed) at the full shape, 1 row")  # fmt: skip
+    return out
+
+
 def copy_ceiling(torch):
     """Device-to-device copy of 1 GiB (torch's copy kernel): GB/s counting the read and the write."""
     src = torch.ones(1 << 28, dtype=torch.float32, device="cuda:0")
@@ -618,8 +670,10 @@ WORKLOADS = {
     "verify-step": bench_verify,
     "prefill": bench_prefill,
     "conv-prefill": bench_conv_prefill,
+    "mlp-layer": bench_mlp_layer,
 }
-CONFIG_OF = {"gdn-layer": 0, "attn-layer": 1, "step": 2, "verify-step": 3, "prefill": 4, "conv-prefill": "f2"}
+CONFIG_OF = {"gdn-layer": 0, "attn-layer": 1, "step": 2, "verify-step": 3, "prefill": 4, "conv-prefill": "f2",
+             "mlp-layer": "f4"}
 
 
 # ------------------------------------------------------------------------------------------------ profiling
@@ -671,6 +725,13 @@ def profile_family(args, torch):
             ops.chunk_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"], initial_state=d["S0"])
         torch.cuda.synchronize()
         print(f"chunk prefill: {PREFILL_BYTES} algorithmic bytes (with the K/V fill) per prefill")
+    elif fam == "mlp":
+        layers = [W.mlp_layer(1, dev, seed=i) for i in range(3)]
+        for _ in range(args.reps):
+            for d in layers:
+                ops.mlp_decode(d["x"], d["gamma"], d["gate"], d["up"], d["down"])
+        torch.cuda.synchronize()
+        print(f"mlp_decode: {mlp_bytes(1, ops.HIDDEN, ops.INTER)} algorithmic bytes per layer")
 
 
 def main():
@@ -687,7 +748,7 @@ def main():
     ap.add_argument("--pps-verify", type=int, default=2, help="pages per split (verify-step workload)")
     ap.add_argument("--kernel-reps", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baselines")
-    ap.add_argument("--profile-family", choices=["gdn", "attn", "conv", "copy", "prefill"], default=None)
+    ap.add_argument("--profile-family", choices=["gdn", "attn", "conv", "copy", "prefill", "mlp"], default=None)
     ap.add_argument("--reps", type=int, default=3, help="repetitions of --profile-family")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -710,7 +771,7 @@ def main():
     head_tel = tel.summary()
     configs = {}
     if args.workload == "all":
-        for wl in ("gdn-layer", "attn-layer", "verify-step", "prefill", "conv-prefill"):
+        for wl in ("gdn-layer", "attn-layer", "verify-step", "prefill", "conv-prefill", "mlp-layer"):
             log(f"workload {wl}")
             configs[wl] = WORKLOADS[wl](args, torch, tel)
             configs[wl]["config"] = CONFIG_OF[wl]

@@ -275,17 +275,20 @@ int qs_mx_quantize(const float *w, uint8_t *packed, int K, int N, int fmt, void 
 
 /* y [B, N] fp32 = h [B, K] bf16 times the packed W, for 1 <= B <= 16 activation rows: the M = 1..16
  * projections of the reference's streamers (kernels/streamer_compute.cpp:371-449: rmsnorm'd rows times
- * streamed weight tiles). Large K is split over workgroups into a caller workspace of
- * qs_mx_gemv_workspace_bytes (0 when none is needed; no zeroing required), then summed. */
+ * streamed weight tiles). K is split over workgroups when the rows of one split would not fit in 24 KB of
+ * LDS or the grid would be small; the splits' partials meet in a caller workspace of
+ * qs_mx_gemv_workspace_bytes (0 when none is needed; zeroed once, like every workspace) and the last split
+ * of each 16-column tile sums them in split order, inside the launch. */
 size_t qs_mx_gemv_workspace_bytes(int B, int K, int N, int fmt);
 int qs_mx_gemv(const uint16_t *h, const uint8_t *w, float *y, void *workspace, int B, int K, int N, int fmt,
                void *stream);
 
 /* The MLP half of a decoder layer for 1 <= B <= 16 rows: h = bf16(x rsqrt(mean(x^2) + eps) gamma) per row,
  * z = bf16(silu(h G) (h U)), x_out = x + z D; gate, up packed MXFP4 [H, I], down packed MXFP8 [I, H];
- * x, x_out [B, H] fp32 (may alias), gamma [H] fp32; H % 128 == 0, I % 256 == 0. The workspace
- * (qs_mlp_decode_workspace_bytes, no zeroing required) holds h, z and the down projection's four K-split
- * partials. Replaces the streamers' MLP phase and its residual (kernels/streamer_compute.cpp:452-464,
+ * x, x_out [B, H] fp32 (may alias), gamma [H] fp32; H % 128 == 0, I % 64 == 0. Two launches for one row
+ * with H <= 5120 (the gate | up workgroups normalise the row themselves), three otherwise. The workspace
+ * (qs_mlp_decode_workspace_bytes, zeroed once) holds arrival counters, h, z and the K-split partials.
+ * Replaces the streamers' MLP phase and its residual (kernels/streamer_compute.cpp:452-464,
  * mlp_hub.cpp:309-364 all-reduce on one device; torch pattern tests/bench_resident_mlp.py:98-105). */
 size_t qs_mlp_decode_workspace_bytes(int B, int H, int I);
 int qs_mlp_decode(const float *x, const float *gamma, const uint8_t *gate, const uint8_t *up, const uint8_t *down,

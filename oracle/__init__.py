@@ -22,6 +22,9 @@ Pinning (what independently fixes each function; the tests under ``tests/test_or
                      softmax shift invariance; causal mask against per-token truncation
   gdn_chunk_prefill  the sequential recurrence (gdn_step applied T times); the chunked WY/UT form is a
                      second, independent restatement checked against it in fp64
+  weight_stream      (module ``oracle.weight_stream``) golden OCP MX encodings and block quantizations,
+                     the nearest-representable property, a hand-indexed layout case, the MLP half's closed
+                     forms (D = 0 identity, linearity in D, rmsnorm scale invariance) and scalar loops
 
 Functions whose exact rounding only the reference's third-party ops could pin (tt-metal's
 ``chunk_gated_delta_rule`` tile staging) are matched within tolerance, not bit-for-bit: parity for that

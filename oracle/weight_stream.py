@@ -15,7 +15,7 @@ The checker therefore restates:
                               reference's torch_reference with the intermediate rounded to bf16 where the
                               kernels keep it (the reference's device path also holds it in 16-bit tiles).
 
-Pinned by tests/test_oracle.py: hand-written golden vectors for both encodings and for quantization (ties,
+Pinned by tests/test_oracle_weight_stream.py: hand-written golden vectors for both encodings and for quantization (ties,
 saturation, zero blocks, scale choice), a hand-indexed layout case, and the MLP's closed forms (D = 0 is the
 identity, the delta is linear in D, rmsnorm's scale invariance).
 """

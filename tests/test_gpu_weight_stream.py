@@ -50,8 +50,11 @@ def _dequantized(W):
     return WS.mx_dequantize(codes, e, W.fmt)
 
 
+# K splits (the activation rows a workgroup stages must fit in 24 KB of LDS; more splits while the grid is
+# small): 1 for (4, 512, 128, 1); 8 for (8, 17408, 64, 1); 25 for (8, 17408, 64, 16), summed over 4 round
+# trips of the last workgroup; 6 for (4, 5120, 32, 13)
 @pytest.mark.parametrize("fmt,K,N,B", [(4, 512, 128, 1), (4, 5120, 256, 8), (8, 1024, 64, 16), (8, 17408, 64, 1),
-                                       (4, 256, 2048, 3)])  # fmt: skip
+                                       (4, 256, 2048, 3), (8, 17408, 64, 16), (4, 5120, 32, 13)])  # fmt: skip
 def test_mx_linear(dev, fmt, K, N, B):
     w = _rand((K, N), 2, 1 / math.sqrt(K))
     W = ops.MxWeight.quantize(w.to(dev), fmt)
@@ -59,6 +62,8 @@ def test_mx_linear(dev, fmt, K, N, B):
     y = ops.mx_linear(h.to(dev), W)
     ref = h.double() @ _dequantized(W)
     torch.testing.assert_close(y.cpu().double(), ref, rtol=1e-4, atol=1e-5 * ref.abs().max().item())
+    # the split sums are re-armed by each launch: a second call gives the same bits
+    assert torch.equal(ops.mx_linear(h.to(dev), W), y)
 
 
 def _mlp(dev, B, H, I, seed=4):
@@ -74,7 +79,9 @@ def _rel(a, b):
     return ((a - b).norm() / b.norm()).item()
 
 
-@pytest.mark.parametrize("B,H,I", [(1, 256, 512), (8, 512, 1024), (16, 256, 256), (1, 5120, 17408)])
+# (16, 5120, 1024): gate | up in 7 K splits, the last workgroup of a tile applying silu
+@pytest.mark.parametrize("B,H,I", [(1, 256, 512), (8, 512, 1024), (16, 256, 256), (1, 5120, 17408), (16, 5120, 1024),
+                                   (5, 1024, 2048)])  # fmt: skip
 def test_mlp_decode(dev, B, H, I):
     x, gamma, gate, up, down = _mlp(dev, B, H, I)
     out = ops.mlp_decode(x.to(dev), gamma.to(dev), gate, up, down).cpu().double()

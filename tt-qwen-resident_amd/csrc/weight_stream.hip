@@ -15,8 +15,9 @@
 // The kernels stream weights at the HBM rate; the conversions and MFMAs hide under the loads.
 //
 // MLP half (qs_mlp_decode): h = bf16(x rsqrt(mean(x^2) + eps) gamma); z = bf16(silu(h G) (h U)) in one
-// launch (gate and up tiles in the same workgroup); the down projection split four ways over K into fp32
-// partials; x_out = x + the partials' sum.
+// launch (gate and up tiles in the same workgroup; for one row the workgroups also form h themselves); the
+// down projection split over K (four ways for one row), its last split per tile adding the partials and the
+// residual: x_out = x + z D. Two launches per layer for one row.
 #include "qs_common.h"
 
 namespace {
@@ -155,170 +156,335 @@ __global__ __launch_bounds__(256) void mx_quantize_kernel(const float *w, uint8_
 
 // --------------------------------------------------------------------------------------- projections
 
-// Each workgroup (4 waves) takes NM matrices' 16-column tile t over K groups [q0, q1); wave w takes groups
-// q0 + w, q0 + w + 4, ... and the partial sums meet in LDS. Two register sets alternate: the next group's
-// blocks and activation rows are requested before the current group is converted and multiplied. A operand:
-// rows of h (bf16 [B, K]), lane (r, g) holding h[r][32 s + 8 g .. + 7] of each step; lanes of rows past B
-// request nothing and hold zeros.
-template <int FMT, int NM>
-struct Tile {
-    f32x4 acc[NM];
+constexpr int WAVES = 4;             // waves per projection workgroup
+constexpr int RING2 = 2, RING1 = 4;  // weight groups in flight per wave, with two weights / one
+constexpr int H_LDS = 24576;         // most bytes of activation rows a workgroup stages in LDS
+constexpr size_t CNT_BYTES = 65536;  // arrival counters at the head of a workspace, one per column tile
+constexpr int EPI_SUM = 0, EPI_SILU = 1, EPI_RESID = 2;
+constexpr int NX = 5;  // NORM: 16-byte pieces of x and of gamma per thread, rows up to 5120 values
+
+// a buffer descriptor over n bytes from p: reads past the range return zeros without touching memory
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *p, uint32_t n) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)n, 0x00020000);
+}
+
+struct Proj {
+    const uint8_t *W0, *W1;  // packed weights (W1: the up projection of EPI_SILU)
+    const uint16_t *h;       // activation rows [B, K] bf16
+    const float *x;          // EPI_RESID: residual rows [B, N]; NORM: the row to normalise [K]
+    const float *gamma;      // NORM: [K]
+    float eps;               // NORM
+    float *y;                // EPI_SUM, EPI_RESID: output rows [B, N] fp32 (may alias x)
+    uint16_t *z;             // EPI_SILU: output rows [B, N] bf16
+    float *part;             // nsplit > 1: partial sums [nsplit, NM, B, N] fp32
+    int *cnt;                // nsplit > 1: [N / 16] arrival counters, zero between launches
+    int B, K, N, nsplit;
+};
+
+// K groups [q0, q1) of split `split` out of nq
+__host__ __device__ inline int split_begin(int nq, int split, int nsplit) { return (int)((long)nq * split / nsplit); }
+// h row pitch in LDS (bf16 values): a split's K range plus a 16-byte skew between rows
+__host__ __device__ inline int h_pitch(int ngmax, int kg) { return ngmax * kg + 8; }
+
+// One workgroup per (16-column tile t, K split): the split's activation rows are staged in LDS once, then
+// each wave streams every 4th K group of the NM weights through a ring of RING groups held in registers
+// (requested RING groups ahead, streaming loads that do not keep the lines in the caches). The ring is
+// requested in the same order every step and requests past the split's range read zeros without a memory
+// access, so every wave issues an identical, unconditional sequence and the compiler's memory-counter waits
+// stay exact. A operand: h rows from LDS (lane (r, g) holds h[r][32 s + 8 g .. + 7] of each 32-value step;
+// rows past B repeat row B - 1 and land in output rows that are never stored). The 4 waves' sums meet in
+// LDS. With one split the workgroup applies the epilogue; otherwise it stores its partial (written through
+// to memory), counts itself in, and the workgroup that completes the tile's count re-arms the counter, sums
+// the partials in split order and applies the epilogue: EPI_SUM y = sum, EPI_RESID y = x + sum,
+// EPI_SILU z = bf16(silu(h W0) (h W1)). NORM (one row, one split, K <= 5120): the workgroup forms the
+// rmsnorm'd row h from x and gamma itself instead of reading it.
+template <int FMT, int NM, int EPI, bool NORM>
+__global__ __launch_bounds__(256, 5) void proj_kernel(Proj a) {
+    using M = Mx<FMT>;
+    extern __shared__ __align__(16) uint16_t s_h[];
+    __shared__ float s_red[WAVES - 1][NM][4][64];
+    __shared__ float s_part[WAVES];
+    __shared__ int s_last;
+    const int ntile = a.N / TILE_N;
+    const int t = blockIdx.x % ntile, split = blockIdx.x / ntile;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, r = lane & 15, g = lane >> 4;
+    const int nq = a.K / M::KG;
+    const int q0 = split_begin(nq, split, a.nsplit), ng = split_begin(nq, split + 1, a.nsplit) - q0;
+    const int P = h_pitch((nq + a.nsplit - 1) / a.nsplit, M::KG);
+
+    // 1. activation rows of the split: B x ng KG values, 16 bytes per request, up to 6 per thread; or, with
+    // NORM (one row, one split), the row of x and gamma, NX x 16 bytes of each per thread
+    constexpr int HV = NORM ? 1 : H_LDS / 16 / 256;
+    const int per_row = ng * M::KG / 8, total = a.B * per_row;
+    const auto hr = rsrc(a.h, NORM ? 0u : (uint32_t)a.B * a.K * 2);
+    u32x4 hv[HV];
+    f32x4 xv[NORM ? NX : 1], gv[NORM ? NX : 1];
+    if constexpr (NORM) {
+        const auto xr = rsrc(a.x, (uint32_t)a.K * 4), gr = rsrc(a.gamma, (uint32_t)a.K * 4);
+#pragma unroll
+        for (int c = 0; c < NX; ++c) {
+            const int i = tid + 256 * c;
+            const uint32_t off = i < a.K / 4 ? (uint32_t)i * 16 : 0xffffff00u;
+            xv[c] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+            gv[c] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(gr, off, 0, 0));
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < HV; ++c) {
+            const int i = tid + 256 * c, b = i / per_row, j = i - b * per_row;
+            const uint32_t off = i < total ? (uint32_t)((b * a.K + q0 * M::KG + 8 * j) * 2) : 0xffffff00u;
+            hv[c] = __builtin_amdgcn_raw_buffer_load_b128(hr, off, 0, 0);
+        }
+    }
+
+    // 2. the weight ring
     struct Buf {
         u32x4 v[NM];
         uint32_t sc[NM];
-        u32x4 a[Mx<FMT>::STEPS];
     };
-    __device__ __forceinline__ void run(const uint8_t *const (&W)[NM], const uint16_t *h, int B, int K, int t, int q0,
-                                        int q1, int w, int lane) {
-        using M = Mx<FMT>;
-        const int r = lane & 15, g = lane >> 4;
-        const size_t tile_off = (size_t)t * (K / M::KG) * M::BYTES;
-        const uint16_t *hrow = h + (size_t)r * K + 8 * g;
+    __amdgpu_buffer_rsrc_t wr[NM];
 #pragma unroll
-        for (int m = 0; m < NM; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-        auto load = [&](int q, Buf &b) {
+    for (int m = 0; m < NM; ++m)
+        wr[m] = rsrc((m == 0 ? a.W0 : a.W1) + ((size_t)t * nq + q0) * M::BYTES, (uint32_t)ng * M::BYTES);
+    auto load = [&](int lg, Buf &bf) {
+        const uint32_t base = (uint32_t)lg * M::BYTES;
 #pragma unroll
-            for (int m = 0; m < NM; ++m) {
-                const uint8_t *p = W[m] + tile_off + (size_t)q * M::BYTES;
-                b.v[m] = *reinterpret_cast<const u32x4 *>(p + 16 * lane);
-                b.sc[m] = FMT == FMT_FP4 ? *reinterpret_cast<const uint32_t *>(p + 1024 + 4 * r)
-                                         : (uint32_t)*reinterpret_cast<const uint16_t *>(p + 1024 + 2 * r);
-            }
+        for (int m = 0; m < NM; ++m) {
+            bf.v[m] = __builtin_amdgcn_raw_buffer_load_b128(wr[m], base + 16 * lane, 0, qs::CP_NT);
+            if constexpr (FMT == FMT_FP4)
+                bf.sc[m] = __builtin_amdgcn_raw_buffer_load_b32(wr[m], base + 1024 + 4 * r, 0, qs::CP_NT);
+            else
+                bf.sc[m] = __builtin_amdgcn_raw_buffer_load_b16(wr[m], base + 1024 + 2 * r, 0, qs::CP_NT);
+        }
+    };
+    constexpr int RING = NM == 2 ? RING2 : RING1;
+    Buf ring[RING];
+#pragma unroll
+    for (int j = 0; j < RING; ++j) load(w + WAVES * j, ring[j]);
+
+    // 3. rows into LDS (row b at b P); NORM: h = bf16(x rsqrt(mean(x^2) + eps) gamma) first, the same
+    // arithmetic as rmsnorm_kernel
+    if constexpr (NORM) {
+        float ss = 0.f;
+#pragma unroll
+        for (int c = 0; c < NX; ++c) ss += xv[c][0] * xv[c][0] + xv[c][1] * xv[c][1] + xv[c][2] * xv[c][2] + xv[c][3] * xv[c][3];
+        ss = qs::wave_sum(ss);
+        if (lane == 0) s_part[w] = ss;
+        __syncthreads();
+        const float inv = rsqrtf((s_part[0] + s_part[1] + s_part[2] + s_part[3]) / (float)a.K + a.eps);
+#pragma unroll
+        for (int c = 0; c < NX; ++c) {
+            const int i = tid + 256 * c;
+            if (i < a.K / 4)
+                *reinterpret_cast<u32x2 *>(s_h + 4 * i) =
+                    u32x2{qs::pack_bf2(xv[c][0] * inv * gv[c][0], xv[c][1] * inv * gv[c][1]),
+                          qs::pack_bf2(xv[c][2] * inv * gv[c][2], xv[c][3] * inv * gv[c][3])};
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < HV; ++c) {
+            const int i = tid + 256 * c, b = i / per_row, j = i - b * per_row;
+            if (i < total) *reinterpret_cast<u32x4 *>(s_h + b * P + 8 * j) = hv[c];
+        }
+    }
+    __syncthreads();
+
+    // 4. stream
+    f32x4 acc[NM];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const uint16_t *hrow = s_h + min(r, a.B - 1) * P + 8 * g;
+    const int iters = ((ng + WAVES - 1) / WAVES + RING - 1) / RING;
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int j = 0; j < RING; ++j) {
+            const int lg = w + WAVES * (it * RING + j);
+            bf16x8 bw[NM][M::STEPS];
+#pragma unroll
+            for (int m = 0; m < NM; ++m) dequant<FMT>(ring[j].v[m], ring[j].sc[m], bw[m]);
+            load(lg + WAVES * RING, ring[j]);
+            __builtin_amdgcn_sched_barrier(0);  // the requests leave before the multiplies
+            const uint16_t *hq = hrow + min(lg, ng - 1) * M::KG;
 #pragma unroll
             for (int s = 0; s < M::STEPS; ++s) {
-                b.a[s] = u32x4{0u, 0u, 0u, 0u};
-                if (r < B) b.a[s] = *reinterpret_cast<const u32x4 *>(hrow + q * M::KG + 32 * s);
-            }
-        };
-        auto compute = [&](const Buf &b) {
+                const bf16x8 av = *reinterpret_cast<const bf16x8 *>(hq + 32 * s);
 #pragma unroll
-            for (int m = 0; m < NM; ++m) {
-                bf16x8 bw[M::STEPS];
-                dequant<FMT>(b.v[m], b.sc[m], bw);
-#pragma unroll
-                for (int s = 0; s < M::STEPS; ++s)
-                    acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, b.a[s]), bw[s], acc[m], 0, 0, 0);
+                for (int m = 0; m < NM; ++m) acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bw[m][s], acc[m], 0, 0, 0);
             }
-        };
-        Buf b0, b1;
-        int q = q0 + w;
-        if (q < q1) load(q, b0);
-        while (q < q1) {
-            if (q + 4 < q1) load(q + 4, b1);
-            compute(b0);
-            q += 4;
-            if (q >= q1) break;
-            if (q + 4 < q1) load(q + 4, b0);
-            compute(b1);
-            q += 4;
         }
     }
-    // sum of the 4 waves' partials, left in wave 0 (acc holds rows 4 g + i, column r of the tile)
-    __device__ __forceinline__ void reduce(float (*s_red)[NM][4][64], int w, int lane) {
-        if (w > 0)
+
+    // 5. the 4 waves' sums into wave 0 (lane (r, g) holds rows 4 g + i of column r)
+    if (w > 0)
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s_red[w - 1][m][i][lane] = acc[m][i];
+    __syncthreads();
+    const int col = TILE_N * t + r;
+    if (w == 0)
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[m][i] += s_red[0][m][i][lane] + s_red[1][m][i][lane] + s_red[2][m][i][lane];
+
+    // 6. partials and the arrival count
+    if (a.nsplit > 1) {
+        if (w == 0) {
+            const auto pr = rsrc(a.part, (uint32_t)a.nsplit * NM * a.B * a.N * 4);
 #pragma unroll
             for (int m = 0; m < NM; ++m)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) s_red[w - 1][m][i][lane] = acc[m][i];
+                for (int i = 0; i < 4; ++i) {
+                    const int b = 4 * g + i;
+                    if (b < a.B)
+                        __builtin_amdgcn_raw_buffer_store_b32(
+                            __float_as_uint(acc[m][i]), pr,
+                            (uint32_t)((((split * NM + m) * a.B + b) * a.N + col) * 4), 0, qs::CP_SC1);
+                }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (w == 0)
-#pragma unroll
-            for (int m = 0; m < NM; ++m)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[m][i] += s_red[0][m][i][lane] + s_red[1][m][i][lane] + s_red[2][m][i][lane];
-    }
-};
-
-// y[split][b][n] = sum over the split's K groups of h[b][k] W[k][n] (fp32); grid (N / 16) x nsplit
-template <int FMT>
-__global__ __launch_bounds__(256) void mx_gemv_kernel(const uint8_t *W, const uint16_t *h, float *y, int B, int K,
-                                                      int N, int nsplit) {
-    __shared__ float s_red[3][1][4][64];
-    const int t = blockIdx.x % (N / TILE_N), split = blockIdx.x / (N / TILE_N);
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int nq = K / Mx<FMT>::KG;
-    const int q0 = (int)((long)nq * split / nsplit), q1 = (int)((long)nq * (split + 1) / nsplit);
-    Tile<FMT, 1> tile;
-    const uint8_t *Ws[1] = {W};
-    tile.run(Ws, h, B, K, t, q0, q1, w, lane);
-    tile.reduce(s_red, w, lane);
-    if (w == 0) {
-        const int col = TILE_N * t + (lane & 15);
+        if (tid == 0) {
+            int *c = a.cnt + t;
+            const int last = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.nsplit - 1;
+            if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = last;
+        }
+        __syncthreads();
+        if (!s_last || w != 0) return;
+        asm volatile("" ::: "memory");
+        const auto pr = rsrc(a.part, (uint32_t)a.nsplit * NM * a.B * a.N * 4);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int b = 4 * (lane >> 4) + i;
-            if (b < B) y[((size_t)split * B + b) * N + col] = tile.acc[0][i];
+            const int b = 4 * g + i;
+            if (b >= a.B) continue;
+            float v[NM] = {};
+            constexpr int PB = 8 / NM;  // splits' partials per round trip, summed in split order
+            for (int c0 = 0; c0 < a.nsplit; c0 += PB) {
+                float pv[NM][PB];
+#pragma unroll
+                for (int k = 0; k < PB; ++k)
+#pragma unroll
+                    for (int m = 0; m < NM; ++m) {
+                        const int sp = c0 + k;
+                        const uint32_t off =
+                            sp < a.nsplit ? (uint32_t)((((sp * NM + m) * a.B + b) * a.N + col) * 4) : 0xffffff00u;
+                        pv[m][k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, off, 0, qs::CP_SC1));
+                    }
+#pragma unroll
+                for (int k = 0; k < PB; ++k)
+#pragma unroll
+                    for (int m = 0; m < NM; ++m) v[m] += pv[m][k];
+            }
+#pragma unroll
+            for (int m = 0; m < NM; ++m) acc[m][i] = v[m];
         }
+    } else if (w != 0) {
+        return;
+    }
+
+    // 7. epilogue (wave 0)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int b = 4 * g + i;
+        if (b >= a.B) continue;
+        const size_t o = (size_t)b * a.N + col;
+        if constexpr (EPI == EPI_SILU)
+            a.z[o] = (uint16_t)qs::f2bf(qs::silu(acc[0][i]) * acc[NM - 1][i]);
+        else if constexpr (EPI == EPI_RESID)
+            a.y[o] = a.x[o] + acc[0][i];
+        else
+            a.y[o] = acc[0][i];
     }
 }
 
-// z[b][n] = bf16(silu(h G)[b][n] (h U)[b][n]); grid N / 16
-__global__ __launch_bounds__(256) void gate_up_kernel(const uint8_t *G, const uint8_t *U, const uint16_t *h, uint16_t *z,
-                                                      int B, int K, int N) {
-    __shared__ float s_red[3][2][4][64];
-    const int t = blockIdx.x;
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    Tile<FMT_FP4, 2> tile;
-    const uint8_t *Ws[2] = {G, U};
-    tile.run(Ws, h, B, K, t, 0, K / Mx<FMT_FP4>::KG, w, lane);
-    tile.reduce(s_red, w, lane);
-    if (w == 0) {
-        const int col = TILE_N * t + (lane & 15);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int b = 4 * (lane >> 4) + i;
-            if (b < B) z[(size_t)b * N + col] = (uint16_t)qs::f2bf(qs::silu(tile.acc[0][i]) * tile.acc[1][i]);
-        }
-    }
-}
-
-// h[b] = bf16(x[b] rsqrt(mean(x[b]^2) + eps) gamma); one workgroup per row
+// h[b] = bf16(x[b] rsqrt(mean(x[b]^2) + eps) gamma); one workgroup per row. Each chunk of 8192 values is
+// requested at once (8 x 16 bytes of x and gamma per thread); rows of one chunk are normalised from registers.
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *x, const float *gamma, uint16_t *h, int H, float eps) {
     __shared__ float s_part[4];
-    const int b = blockIdx.x, tid = threadIdx.x;
-    const float *xr = x + (size_t)b * H;
-    float ss = 0.f;
-    for (int k = tid; k < H; k += 256) ss = fmaf(xr[k], xr[k], ss);
+    constexpr int V = 8, CHUNK = 256 * V;  // float4 per thread, float4 per chunk
+    const int b = blockIdx.x, tid = threadIdx.x, n4 = H / 4;
+    const auto xr = rsrc(x + (size_t)b * H, (uint32_t)H * 4), gr = rsrc(gamma, (uint32_t)H * 4);
+    f32x4 xv[V], gv[V];
+    auto fetch = [&](int c0) {
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        for (int j = 0; j < V; ++j) {
+            const int i = c0 + tid + 256 * j;
+            const uint32_t off = i < n4 ? (uint32_t)i * 16 : 0xffffff00u;
+            xv[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+            gv[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(gr, off, 0, 0));
+        }
+    };
+    float ss = 0.f;
+    for (int c0 = 0; c0 < n4; c0 += CHUNK) {
+        fetch(c0);
+#pragma unroll
+        for (int j = 0; j < V; ++j) ss += xv[j][0] * xv[j][0] + xv[j][1] * xv[j][1] + xv[j][2] * xv[j][2] + xv[j][3] * xv[j][3];
+    }
+    ss = qs::wave_sum(ss);
     if ((tid & 63) == 0) s_part[tid >> 6] = ss;
     __syncthreads();
     const float inv = rsqrtf((s_part[0] + s_part[1] + s_part[2] + s_part[3]) / (float)H + eps);
-    for (int k = tid; k < H; k += 256) h[(size_t)b * H + k] = (uint16_t)qs::f2bf(xr[k] * inv * gamma[k]);
+    for (int c0 = 0; c0 < n4; c0 += CHUNK) {
+        if (n4 > CHUNK) fetch(c0);
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            const int i = c0 + tid + 256 * j;
+            if (i < n4)
+                *reinterpret_cast<u32x2 *>(h + (size_t)b * H + 4 * i) =
+                    u32x2{qs::pack_bf2(xv[j][0] * inv * gv[j][0], xv[j][1] * inv * gv[j][1]),
+                          qs::pack_bf2(xv[j][2] * inv * gv[j][2], xv[j][3] * inv * gv[j][3])};
+        }
+    }
 }
 
-// out[i] = (x ? x[i] : 0) + sum over splits of part[s][i]
-__global__ __launch_bounds__(256) void sum_splits_kernel(const float *x, const float *part, float *out, long n,
-                                                         int nsplit) {
-    const long i = (long)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n) return;
-    float v = x ? x[i] : 0.f;
-    for (int s = 0; s < nsplit; ++s) v += part[(size_t)s * n + i];
-    out[i] = v;
-}
-
-int gemv_splits(int K, int N, int fmt) {
-    const int nq = K / (fmt == FMT_FP4 ? Mx<FMT_FP4>::KG : Mx<FMT_FP8>::KG);
+// Splits of K for one projection: enough that a split's activation rows fit in LDS, then doubled while the
+// grid has fewer than 1024 workgroups and each split keeps at least 16 groups (4 per wave).
+int proj_splits(int B, int K, int N, int fmt) {
+    const int kg = fmt == FMT_FP4 ? Mx<FMT_FP4>::KG : Mx<FMT_FP8>::KG;
+    const int nq = K / kg;
     int s = 1;
-    while ((N / TILE_N) * s < 1024 && nq / (2 * s) >= 4) s *= 2;  // enough workgroups, >= 4 groups per split
+    while (s < nq && (size_t)B * h_pitch((nq + s - 1) / s, kg) * 2 > (size_t)H_LDS) ++s;
+    while ((N / TILE_N) * s < 1024 && nq / (2 * s) >= 16) s *= 2;
     return s;
+}
+size_t h_lds_bytes(int B, int K, int fmt, int nsplit) {
+    const int kg = fmt == FMT_FP4 ? Mx<FMT_FP4>::KG : Mx<FMT_FP8>::KG;
+    return (size_t)B * h_pitch((K / kg + nsplit - 1) / nsplit, kg) * 2;
 }
 
 bool mx_shape_ok(int K, int N, int fmt) {
     return (fmt == FMT_FP4 || fmt == FMT_FP8) && K > 0 && N > 0 && N % TILE_N == 0 &&
-           K % (fmt == FMT_FP4 ? Mx<FMT_FP4>::KG : Mx<FMT_FP8>::KG) == 0 && (long)K * MAX_ROWS * 2 < (1L << 31);
+           K % (fmt == FMT_FP4 ? Mx<FMT_FP4>::KG : Mx<FMT_FP8>::KG) == 0 && (size_t)N / TILE_N * 4 <= CNT_BYTES &&
+           (long)K * MAX_ROWS * 2 < (1L << 31) && mx_bytes(K, N, fmt) < (1UL << 32);
+}
+
+template <int FMT, int NM, int EPI, bool NORM = false>
+int launch_proj(const Proj &a, hipStream_t st, const char *what) {
+    const size_t lds = h_lds_bytes(a.B, a.K, FMT, a.nsplit);
+    proj_kernel<FMT, NM, EPI, NORM><<<(unsigned)((a.N / TILE_N) * a.nsplit), 256, lds, st>>>(a);
+    return qs::launch_status(what);
+}
+
+// workspace: counters | partials
+size_t proj_ws_bytes(int B, int N, int nm, int nsplit) {
+    return nsplit > 1 ? CNT_BYTES + (size_t)nsplit * nm * B * N * 4 : 0;
 }
 
 struct MlpWs {
     size_t h, z, part, total;
+    int sg, sd;  // K splits of gate | up and of down
 };
 MlpWs mlp_ws(int B, int H, int I) {
     auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
     MlpWs l;
-    l.h = 0;
-    l.z = up((size_t)B * H * 2);
+    l.sg = proj_splits(B, H, I, FMT_FP4);
+    l.sd = proj_splits(B, I, H, FMT_FP8);
+    l.h = CNT_BYTES;
+    l.z = l.h + up((size_t)B * H * 2);
     l.part = l.z + up((size_t)B * I * 2);
-    l.total = l.part + up((size_t)DOWN_SPLIT * B * H * 4);
+    l.total = l.part + up(std::max((size_t)l.sg * 2 * B * I, (size_t)l.sd * B * H) * 4);
     return l;
 }
 
@@ -344,8 +510,8 @@ extern "C" int qs_mx_quantize(const float *w, uint8_t *packed, int K, int N, int
 
 extern "C" size_t qs_mx_gemv_workspace_bytes(int B, int K, int N, int fmt) {
     if (!mx_shape_ok(K, N, fmt) || B <= 0 || B > MAX_ROWS) return 0;
-    const int s = gemv_splits(K, N, fmt);
-    return s > 1 ? (size_t)s * B * N * 4 : 0;
+    const size_t n = proj_ws_bytes(B, N, 1, proj_splits(B, K, N, fmt));
+    return n < (1UL << 32) ? n : 0;
 }
 
 extern "C" int qs_mx_gemv(const uint16_t *h, const uint8_t *w, float *y, void *workspace, int B, int K, int N, int fmt,
@@ -354,28 +520,23 @@ extern "C" int qs_mx_gemv(const uint16_t *h, const uint8_t *w, float *y, void *w
     QS_REQUIRE(B > 0 && B <= MAX_ROWS, "qs_mx_gemv: 1 to %d activation rows (got %d)", MAX_ROWS, B);
     QS_REQUIRE(mx_shape_ok(K, N, fmt), "qs_mx_gemv: fmt %d (4 or 8) needs N %% 16 == 0 and K %% %d == 0 (got K %d, N %d)",
                fmt, fmt == FMT_FP4 ? 128 : 64, K, N);
-    const int s = gemv_splits(K, N, fmt);
+    const int s = proj_splits(B, K, N, fmt);
+    QS_REQUIRE(proj_ws_bytes(B, N, 1, s) < (1UL << 32), "qs_mx_gemv: K %d, N %d need too many K splits", K, N);
     QS_REQUIRE(s == 1 || workspace, "qs_mx_gemv: this shape needs a workspace of qs_mx_gemv_workspace_bytes");
-    float *dst = s > 1 ? static_cast<float *>(workspace) : y;
+    Proj a{};
+    a.W0 = a.W1 = w;
+    a.h = h;
+    a.y = y;
+    a.cnt = static_cast<int *>(workspace);
+    a.part = s > 1 ? reinterpret_cast<float *>(static_cast<char *>(workspace) + CNT_BYTES) : nullptr;
+    a.B = B, a.K = K, a.N = N, a.nsplit = s;
     hipStream_t st = QS_STREAM(stream);
-    const unsigned grid = (unsigned)((N / TILE_N) * s);
-    if (fmt == FMT_FP4)
-        mx_gemv_kernel<FMT_FP4><<<grid, 256, 0, st>>>(w, h, dst, B, K, N, s);
-    else
-        mx_gemv_kernel<FMT_FP8><<<grid, 256, 0, st>>>(w, h, dst, B, K, N, s);
-    if (int e = qs::launch_status("qs_mx_gemv")) return e;
-    if (s > 1) {
-        const long n = (long)B * N;
-        sum_splits_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(nullptr, dst, y, n, s);
-        return qs::launch_status("qs_mx_gemv (sum)");
-    }
-    return QS_OK;
+    return fmt == FMT_FP4 ? launch_proj<FMT_FP4, 1, EPI_SUM>(a, st, "qs_mx_gemv")
+                          : launch_proj<FMT_FP8, 1, EPI_SUM>(a, st, "qs_mx_gemv");
 }
 
 extern "C" size_t qs_mlp_decode_workspace_bytes(int B, int H, int I) {
-    if (B <= 0 || B > MAX_ROWS || !mx_shape_ok(H, I, FMT_FP4) || !mx_shape_ok(I, H, FMT_FP8) ||
-        I % (DOWN_SPLIT * Mx<FMT_FP8>::KG) != 0)
-        return 0;
+    if (B <= 0 || B > MAX_ROWS || !mx_shape_ok(H, I, FMT_FP4) || !mx_shape_ok(I, H, FMT_FP8)) return 0;
     return mlp_ws(B, H, I).total;
 }
 
@@ -384,21 +545,27 @@ extern "C" int qs_mlp_decode(const float *x, const float *gamma, const uint8_t *
                              void *stream) {
     QS_REQUIRE(x && gamma && gate && up && down && x_out && workspace, "qs_mlp_decode: null pointer");
     QS_REQUIRE(B > 0 && B <= MAX_ROWS, "qs_mlp_decode: 1 to %d rows (got %d)", MAX_ROWS, B);
-    QS_REQUIRE(mx_shape_ok(H, I, FMT_FP4) && mx_shape_ok(I, H, FMT_FP8) && I % (DOWN_SPLIT * Mx<FMT_FP8>::KG) == 0,
-               "qs_mlp_decode: H must be a multiple of 128 and I of 256 (got H %d, I %d)", H, I);
+    QS_REQUIRE(mx_shape_ok(H, I, FMT_FP4) && mx_shape_ok(I, H, FMT_FP8),
+               "qs_mlp_decode: H must be a multiple of 128 and I of 64 (got H %d, I %d)", H, I);
     const MlpWs L = mlp_ws(B, H, I);
     char *ws = static_cast<char *>(workspace);
     uint16_t *h = reinterpret_cast<uint16_t *>(ws + L.h);
     uint16_t *z = reinterpret_cast<uint16_t *>(ws + L.z);
-    float *part = reinterpret_cast<float *>(ws + L.part);
     hipStream_t st = QS_STREAM(stream);
-    rmsnorm_kernel<<<B, 256, 0, st>>>(x, gamma, h, H, eps);
-    if (int e = qs::launch_status("qs_mlp_decode (rmsnorm)")) return e;
-    gate_up_kernel<<<I / TILE_N, 256, 0, st>>>(gate, up, h, z, B, H, I);
-    if (int e = qs::launch_status("qs_mlp_decode (gate, up)")) return e;
-    mx_gemv_kernel<FMT_FP8><<<(H / TILE_N) * DOWN_SPLIT, 256, 0, st>>>(down, z, part, B, I, H, DOWN_SPLIT);
-    if (int e = qs::launch_status("qs_mlp_decode (down)")) return e;
-    const long n = (long)B * H;
-    sum_splits_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(x, part, x_out, n, DOWN_SPLIT);
-    return qs::launch_status("qs_mlp_decode (residual)");
+    Proj a{};
+    a.cnt = static_cast<int *>(workspace);
+    a.part = reinterpret_cast<float *>(ws + L.part);
+    a.W0 = gate, a.W1 = up, a.h = h, a.z = z;
+    a.B = B, a.K = H, a.N = I, a.nsplit = L.sg;
+    if (B == 1 && L.sg == 1 && H <= 4 * 256 * NX) {  // one row: the gate | up workgroups normalise it themselves
+        a.x = x, a.gamma = gamma, a.eps = eps;
+        if (int e = launch_proj<FMT_FP4, 2, EPI_SILU, true>(a, st, "qs_mlp_decode (rmsnorm, gate, up)")) return e;
+    } else {
+        rmsnorm_kernel<<<B, 256, 0, st>>>(x, gamma, h, H, eps);
+        if (int e = qs::launch_status("qs_mlp_decode (rmsnorm)")) return e;
+        if (int e = launch_proj<FMT_FP4, 2, EPI_SILU>(a, st, "qs_mlp_decode (gate, up)")) return e;
+    }
+    a.W0 = a.W1 = down, a.h = z, a.x = x, a.y = x_out, a.z = nullptr;
+    a.K = I, a.N = H, a.nsplit = L.sd;
+    return launch_proj<FMT_FP8, 1, EPI_RESID>(a, st, "qs_mlp_decode (down, residual)");
 }

@@ -617,7 +617,7 @@ def mlp_decode(x, gamma, gate, up, down, eps=EPS, out=None, ws=None):
             raise ValueError(f"{name} must be a {shape} MXFP{fmt} weight (got {(w.K, w.N)} MXFP{w.fmt})")
     nbytes = lib().qs_mlp_decode_workspace_bytes(B, H, I)
     if nbytes == 0:
-        raise ValueError(f"1 to 16 rows, H % 128 == 0, I % 256 == 0 (got B {B}, H {H}, I {I})")
+        raise ValueError(f"1 to 16 rows, H % 128 == 0, I % 64 == 0 (got B {B}, H {H}, I {I})")
     y = torch.empty_like(x) if out is None else out
     _chk(y, "out", torch.float32, (B, H), dev)
     if ws is None:
