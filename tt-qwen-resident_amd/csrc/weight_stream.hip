@@ -212,9 +212,10 @@ __global__ __launch_bounds__(256, 5) void proj_kernel(Proj a) {
     const int q0 = split_begin(nq, split, a.nsplit), ng = split_begin(nq, split + 1, a.nsplit) - q0;
     const int P = h_pitch((nq + a.nsplit - 1) / a.nsplit, M::KG);
 
-    // 1. activation rows of the split: B x ng KG values, 16 bytes per request, up to 6 per thread; or, with
-    // NORM (one row, one split), the row of x and gamma, NX x 16 bytes of each per thread
-    constexpr int HV = NORM ? 1 : H_LDS / 16 / 256;
+    // 1. activation rows of the split: B x ng KG values, 16 bytes per request, the first HV per thread
+    // requested before the weight ring, any others after it; or, with NORM (one row, one split), the row of
+    // x and gamma, NX x 16 bytes of each per thread
+    constexpr int HV = NORM ? 1 : 6;
     const int per_row = ng * M::KG / 8, total = a.B * per_row;
     const auto hr = rsrc(a.h, NORM ? 0u : (uint32_t)a.B * a.K * 2);
     u32x4 hv[HV];
@@ -228,14 +229,23 @@ __global__ __launch_bounds__(256, 5) void proj_kernel(Proj a) {
             xv[c] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
             gv[c] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(gr, off, 0, 0));
         }
-    } else {
+    }
+    auto fetch_h = [&](int i0) {
 #pragma unroll
         for (int c = 0; c < HV; ++c) {
-            const int i = tid + 256 * c, b = i / per_row, j = i - b * per_row;
+            const int i = i0 + tid + 256 * c, b = i / per_row, j = i - b * per_row;
             const uint32_t off = i < total ? (uint32_t)((b * a.K + q0 * M::KG + 8 * j) * 2) : 0xffffff00u;
             hv[c] = __builtin_amdgcn_raw_buffer_load_b128(hr, off, 0, 0);
         }
-    }
+    };
+    auto put_h = [&](int i0) {
+#pragma unroll
+        for (int c = 0; c < HV; ++c) {
+            const int i = i0 + tid + 256 * c, b = i / per_row, j = i - b * per_row;
+            if (i < total) *reinterpret_cast<u32x4 *>(s_h + b * P + 8 * j) = hv[c];
+        }
+    };
+    if constexpr (!NORM) fetch_h(0);
 
     // 2. the weight ring
     struct Buf {
@@ -281,10 +291,10 @@ __global__ __launch_bounds__(256, 5) void proj_kernel(Proj a) {
                           qs::pack_bf2(xv[c][2] * inv * gv[c][2], xv[c][3] * inv * gv[c][3])};
         }
     } else {
-#pragma unroll
-        for (int c = 0; c < HV; ++c) {
-            const int i = tid + 256 * c, b = i / per_row, j = i - b * per_row;
-            if (i < total) *reinterpret_cast<u32x4 *>(s_h + b * P + 8 * j) = hv[c];
+        put_h(0);
+        for (int i0 = 256 * HV; i0 < total; i0 += 256 * HV) {
+            fetch_h(i0);
+            put_h(i0);
         }
     }
     __syncthreads();
