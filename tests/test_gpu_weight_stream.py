@@ -50,9 +50,10 @@ def _dequantized(W):
     return WS.mx_dequantize(codes, e, W.fmt)
 
 
-# K splits (the activation rows a workgroup stages must fit in 24 KB of LDS; more splits while the grid is
-# small): 1 for (4, 512, 128, 1); 8 for (8, 17408, 64, 1); 25 for (8, 17408, 64, 16), summed over 4 round
-# trips of the last workgroup; 6 for (4, 5120, 32, 13)
+# K splits (one row up to 7 (MXFP4) / 15 (MXFP8) rows: the rows a workgroup stages must fit in 24 KB of LDS;
+# more rows: read from L2 with each weight group; then more splits while the grid is small): 1 for
+# (4, 512, 128, 1); 16 for (8, 17408, 64, 1), summed over 2 round trips of the last workgroup; 16 for
+# (8, 17408, 64, 16) and 2 for (4, 5120, 256, 8) and (4, 5120, 32, 13) with rows from L2
 @pytest.mark.parametrize("fmt,K,N,B", [(4, 512, 128, 1), (4, 5120, 256, 8), (8, 1024, 64, 16), (8, 17408, 64, 1),
                                        (4, 256, 2048, 3), (8, 17408, 64, 16), (4, 5120, 32, 13)])  # fmt: skip
 def test_mx_linear(dev, fmt, K, N, B):
@@ -79,9 +80,10 @@ def _rel(a, b):
     return ((a - b).norm() / b.norm()).item()
 
 
-# (16, 5120, 1024): gate | up in 7 K splits, the last workgroup of a tile applying silu
+# the last workgroup of a tile applying silu after K splits: (16, 5120, 1024) gate | up in 2 splits with rows
+# from L2, (4, 5120, 2048) in 2 splits with rows staged in LDS
 @pytest.mark.parametrize("B,H,I", [(1, 256, 512), (8, 512, 1024), (16, 256, 256), (1, 5120, 17408), (16, 5120, 1024),
-                                   (5, 1024, 2048)])  # fmt: skip
+                                   (5, 1024, 2048), (4, 5120, 2048)])  # fmt: skip
 def test_mlp_decode(dev, B, H, I):
     x, gamma, gate, up, down = _mlp(dev, B, H, I)
     out = ops.mlp_decode(x.to(dev), gamma.to(dev), gate, up, down).cpu().double()

@@ -197,9 +197,10 @@ __host__ __device__ inline int h_pitch(int ngmax, int kg) { return ngmax * kg + 
 // to memory), counts itself in, and the workgroup that completes the tile's count re-arms the counter, sums
 // the partials in split order and applies the epilogue: EPI_SUM y = sum, EPI_RESID y = x + sum,
 // EPI_SILU z = bf16(silu(h W0) (h W1)). NORM (one row, one split, K <= 5120): the workgroup forms the
-// rmsnorm'd row h from x and gamma itself instead of reading it.
-template <int FMT, int NM, int EPI, bool NORM>
-__global__ __launch_bounds__(256, 5) void proj_kernel(Proj a) {
+// rmsnorm'd row h from x and gamma itself instead of reading it. HREG: no staging; each ring slot also
+// holds the group's A fragments, requested from L2 with its weights (lanes of rows past B read zeros).
+template <int FMT, int NM, int EPI, bool NORM, bool HREG>
+__global__ __launch_bounds__(256, HREG ? 4 : 5) void proj_kernel(Proj a) {
     using M = Mx<FMT>;
     extern __shared__ __align__(16) uint16_t s_h[];
     __shared__ float s_red[WAVES - 1][NM][4][64];
@@ -245,13 +246,15 @@ __global__ __launch_bounds__(256, 5) void proj_kernel(Proj a) {
             if (i < total) *reinterpret_cast<u32x4 *>(s_h + b * P + 8 * j) = hv[c];
         }
     };
-    if constexpr (!NORM) fetch_h(0);
+    if constexpr (!NORM && !HREG) fetch_h(0);
 
     // 2. the weight ring
     struct Buf {
         u32x4 v[NM];
         uint32_t sc[NM];
+        u32x4 a[HREG ? M::STEPS : 1];  // HREG: the group's activation fragments
     };
+    const auto har = rsrc(a.h, HREG ? (uint32_t)a.B * a.K * 2 : 0u);
     __amdgpu_buffer_rsrc_t wr[NM];
 #pragma unroll
     for (int m = 0; m < NM; ++m)
@@ -266,15 +269,23 @@ __global__ __launch_bounds__(256, 5) void proj_kernel(Proj a) {
             else
                 bf.sc[m] = __builtin_amdgcn_raw_buffer_load_b16(wr[m], base + 1024 + 2 * r, 0, qs::CP_NT);
         }
+        if constexpr (HREG)
+#pragma unroll
+            for (int s = 0; s < M::STEPS; ++s) {
+                const uint32_t off = r < a.B && lg < ng
+                                         ? (uint32_t)((r * a.K + (q0 + lg) * M::KG + 32 * s + 8 * g) * 2) : 0xffffff00u;
+                bf.a[s] = __builtin_amdgcn_raw_buffer_load_b128(har, off, 0, 0);
+            }
     };
-    constexpr int RING = NM == 2 ? RING2 : RING1;
+    constexpr int RING = NM == 2 || (HREG && FMT == FMT_FP4) ? RING2 : RING1;
     Buf ring[RING];
 #pragma unroll
     for (int j = 0; j < RING; ++j) load(w + WAVES * j, ring[j]);
 
     // 3. rows into LDS (row b at b P); NORM: h = bf16(x rsqrt(mean(x^2) + eps) gamma) first, the same
     // arithmetic as rmsnorm_kernel
-    if constexpr (NORM) {
+    if constexpr (HREG) {
+    } else if constexpr (NORM) {
         float ss = 0.f;
 #pragma unroll
         for (int c = 0; c < NX; ++c) ss += xv[c][0] * xv[c][0] + xv[c][1] * xv[c][1] + xv[c][2] * xv[c][2] + xv[c][3] * xv[c][3];
@@ -312,12 +323,16 @@ __global__ __launch_bounds__(256, 5) void proj_kernel(Proj a) {
             bf16x8 bw[NM][M::STEPS];
 #pragma unroll
             for (int m = 0; m < NM; ++m) dequant<FMT>(ring[j].v[m], ring[j].sc[m], bw[m]);
+            u32x4 ha[HREG ? M::STEPS : 1];
+            if constexpr (HREG)
+#pragma unroll
+                for (int s = 0; s < M::STEPS; ++s) ha[s] = ring[j].a[s];
             load(lg + WAVES * RING, ring[j]);
             __builtin_amdgcn_sched_barrier(0);  // the requests leave before the multiplies
             const uint16_t *hq = hrow + min(lg, ng - 1) * M::KG;
 #pragma unroll
             for (int s = 0; s < M::STEPS; ++s) {
-                const bf16x8 av = *reinterpret_cast<const bf16x8 *>(hq + 32 * s);
+                const bf16x8 av = HREG ? __builtin_bit_cast(bf16x8, ha[s]) : *reinterpret_cast<const bf16x8 *>(hq + 32 * s);
 #pragma unroll
                 for (int m = 0; m < NM; ++m) acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bw[m][s], acc[m], 0, 0, 0);
             }
@@ -451,11 +466,17 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *x, const floa
 
 // Splits of K for one projection: enough that a split's activation rows fit in LDS, then doubled while the
 // grid has fewer than 1024 workgroups and each split keeps at least 16 groups (4 per wave).
+// Activation rows: staged in LDS per workgroup (read by every wave; 24 KB of rows bound the K split), or,
+// from 8 rows (MXFP4) / 16 rows (MXFP8) on, requested from L2 with each weight group, where the LDS bound
+// would cut K into too many short splits (measured per layer at H 5120 / I 17408: gate | up 26.9 against
+// 30.7 us at 8 rows, down 34.8 against 38.8 us at 16 rows; slower below those counts).
+bool use_hreg(int B, int fmt) { return B >= (fmt == FMT_FP4 ? 8 : 16); }
+
 int proj_splits(int B, int K, int N, int fmt) {
     const int kg = fmt == FMT_FP4 ? Mx<FMT_FP4>::KG : Mx<FMT_FP8>::KG;
     const int nq = K / kg;
     int s = 1;
-    while (s < nq && (size_t)B * h_pitch((nq + s - 1) / s, kg) * 2 > (size_t)H_LDS) ++s;
+    while (!use_hreg(B, fmt) && s < nq && (size_t)B * h_pitch((nq + s - 1) / s, kg) * 2 > (size_t)H_LDS) ++s;
     while ((N / TILE_N) * s < 1024 && nq / (2 * s) >= 16) s *= 2;
     return s;
 }
@@ -470,10 +491,10 @@ bool mx_shape_ok(int K, int N, int fmt) {
            (long)K * MAX_ROWS * 2 < (1L << 31) && mx_bytes(K, N, fmt) < (1UL << 32);
 }
 
-template <int FMT, int NM, int EPI, bool NORM = false>
+template <int FMT, int NM, int EPI, bool NORM = false, bool HREG = false>
 int launch_proj(const Proj &a, hipStream_t st, const char *what) {
-    const size_t lds = h_lds_bytes(a.B, a.K, FMT, a.nsplit);
-    proj_kernel<FMT, NM, EPI, NORM><<<(unsigned)((a.N / TILE_N) * a.nsplit), 256, lds, st>>>(a);
+    const size_t lds = HREG ? 0 : h_lds_bytes(a.B, a.K, FMT, a.nsplit);
+    proj_kernel<FMT, NM, EPI, NORM, HREG><<<(unsigned)((a.N / TILE_N) * a.nsplit), 256, lds, st>>>(a);
     return qs::launch_status(what);
 }
 
@@ -541,6 +562,9 @@ extern "C" int qs_mx_gemv(const uint16_t *h, const uint8_t *w, float *y, void *w
     a.part = s > 1 ? reinterpret_cast<float *>(static_cast<char *>(workspace) + CNT_BYTES) : nullptr;
     a.B = B, a.K = K, a.N = N, a.nsplit = s;
     hipStream_t st = QS_STREAM(stream);
+    if (use_hreg(B, fmt))
+        return fmt == FMT_FP4 ? launch_proj<FMT_FP4, 1, EPI_SUM, false, true>(a, st, "qs_mx_gemv")
+                              : launch_proj<FMT_FP8, 1, EPI_SUM, false, true>(a, st, "qs_mx_gemv");
     return fmt == FMT_FP4 ? launch_proj<FMT_FP4, 1, EPI_SUM>(a, st, "qs_mx_gemv")
                           : launch_proj<FMT_FP8, 1, EPI_SUM>(a, st, "qs_mx_gemv");
 }
@@ -569,13 +593,16 @@ extern "C" int qs_mlp_decode(const float *x, const float *gamma, const uint8_t *
     a.B = B, a.K = H, a.N = I, a.nsplit = L.sg;
     if (B == 1 && L.sg == 1 && H <= 4 * 256 * NX) {  // one row: the gate | up workgroups normalise it themselves
         a.x = x, a.gamma = gamma, a.eps = eps;
-        if (int e = launch_proj<FMT_FP4, 2, EPI_SILU, true>(a, st, "qs_mlp_decode (rmsnorm, gate, up)")) return e;
+        if (int e = launch_proj<FMT_FP4, 2, EPI_SILU, true, false>(a, st, "qs_mlp_decode (rmsnorm, gate, up)")) return e;
     } else {
         rmsnorm_kernel<<<B, 256, 0, st>>>(x, gamma, h, H, eps);
         if (int e = qs::launch_status("qs_mlp_decode (rmsnorm)")) return e;
-        if (int e = launch_proj<FMT_FP4, 2, EPI_SILU>(a, st, "qs_mlp_decode (gate, up)")) return e;
+        const int e = use_hreg(B, FMT_FP4) ? launch_proj<FMT_FP4, 2, EPI_SILU, false, true>(a, st, "qs_mlp_decode (gate, up)")
+                                  : launch_proj<FMT_FP4, 2, EPI_SILU>(a, st, "qs_mlp_decode (gate, up)");
+        if (e) return e;
     }
     a.W0 = a.W1 = down, a.h = z, a.x = x, a.y = x_out, a.z = nullptr;
     a.K = I, a.N = H, a.nsplit = L.sd;
+    if (use_hreg(B, FMT_FP8)) return launch_proj<FMT_FP8, 1, EPI_RESID, false, true>(a, st, "qs_mlp_decode (down, residual)");
     return launch_proj<FMT_FP8, 1, EPI_RESID>(a, st, "qs_mlp_decode (down, residual)");
 }
