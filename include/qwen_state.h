@@ -285,7 +285,8 @@ int qs_mx_gemv(const uint16_t *h, const uint8_t *w, float *y, void *workspace, i
 
 /* The MLP half of a decoder layer for 1 <= B <= 16 rows: h = bf16(x rsqrt(mean(x^2) + eps) gamma) per row,
  * z = bf16(silu(h G) (h U)), x_out = x + z D; gate, up packed MXFP4 [H, I], down packed MXFP8 [I, H];
- * x, x_out [B, H] fp32 (may alias), gamma [H] fp32; H % 128 == 0, I % 64 == 0. Two launches for one row
+ * x, x_out [B, H] fp32 (may alias), gamma [H] fp32 or null when the norm weight is already folded into the
+ * rows of gate and up (the reference's weights.py:107-112 does so); H % 128 == 0, I % 64 == 0. Two launches for one row
  * with H <= 5120 (the gate | up workgroups normalise the row themselves), three otherwise. The workspace
  * (qs_mlp_decode_workspace_bytes, zeroed once) holds arrival counters, h, z and the K-split partials.
  * Replaces the streamers' MLP phase and its residual (kernels/streamer_compute.cpp:452-464,

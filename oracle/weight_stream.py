@@ -128,6 +128,7 @@ def mlp_half(x, gamma, G, U, D, eps=EPS):
     (tests/bench_resident_mlp.py:98-105; EPS common.py:15). x [B, H]; G, U [H, I]; D [I, H] (dequantized)."""
     dt = G.dtype
     x = x.to(dt)
-    h = bf16(x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * gamma.to(dt)).to(dt)
+    g = torch.ones(x.shape[-1], dtype=dt) if gamma is None else gamma.to(dt)  # None: folded into G and U
+    h = bf16(x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * g).to(dt)
     z = bf16(F.silu(h @ G) * (h @ U)).to(dt)
     return x + z @ D

@@ -110,6 +110,18 @@ def test_mlp_decode_in_place_and_repeatable(dev, B, H, I):
     assert torch.equal(a, b)
 
 
+# gamma None: the norm weight folded into the rows of gate and up, as the reference's weights.py:107-112 loads
+# them; one row (rmsnorm inside the gate | up launch) and eight (its own launch)
+@pytest.mark.parametrize("B", [1, 8])
+def test_mlp_decode_folded_gamma(dev, B):
+    x, gamma, gate, up, down = _mlp(dev, B, 512, 1024, seed=12)
+    out = ops.mlp_decode(x.to(dev), None, gate, up, down).cpu().double()
+    G, U, D = _dequantized(gate), _dequantized(up), _dequantized(down)
+    ref = WS.mlp_half(x.double(), None, G, U, D)
+    assert _rel(out - x.double(), ref - x.double()) < 2e-3
+    assert torch.equal(ops.mlp_decode(x.to(dev), torch.ones(512, device=dev), gate, up, down).cpu().double(), out)
+
+
 def test_rejects_bad_shapes(dev):
     with pytest.raises(ValueError):
         ops.MxWeight.quantize(torch.zeros(100, 16, device=dev), ops.MXFP4)

@@ -129,3 +129,11 @@ def test_mlp_half_matches_loops():
         for n in range(8):
             want = x[b, n].item() + sum(z[i] * D[i, n].item() for i in range(16))
             assert abs(out[b, n].item() - want) <= 1e-12 * (1 + abs(want))
+
+
+def test_mlp_half_folded_gamma_is_unit_gamma():
+    x, gamma, G, U, D = _mlp_weights(32, 64, seed=5)
+    assert torch.equal(WS.mlp_half(x, None, G, U, D), WS.mlp_half(x, torch.ones(32, dtype=torch.float64), G, U, D))
+    # folding gamma into the rows of G and U changes only where h is rounded to bf16
+    folded = WS.mlp_half(x, None, gamma[:, None] * G, gamma[:, None] * U, D)
+    torch.testing.assert_close(folded, WS.mlp_half(x, gamma, G, U, D), rtol=2e-2, atol=1e-2)

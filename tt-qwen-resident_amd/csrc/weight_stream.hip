@@ -172,7 +172,7 @@ struct Proj {
     const uint8_t *W0, *W1;  // packed weights (W1: the up projection of EPI_SILU)
     const uint16_t *h;       // activation rows [B, K] bf16
     const float *x;          // EPI_RESID: residual rows [B, N]; NORM: the row to normalise [K]
-    const float *gamma;      // NORM: [K]
+    const float *gamma;      // NORM: [K], or null when the norm weight is folded into the weights (unit gamma)
     float eps;               // NORM
     float *y;                // EPI_SUM, EPI_RESID: output rows [B, N] fp32 (may alias x)
     uint16_t *z;             // EPI_SILU: output rows [B, N] bf16
@@ -222,13 +222,13 @@ __global__ __launch_bounds__(256, HREG ? 4 : 5) void proj_kernel(Proj a) {
     u32x4 hv[HV];
     f32x4 xv[NORM ? NX : 1], gv[NORM ? NX : 1];
     if constexpr (NORM) {
-        const auto xr = rsrc(a.x, (uint32_t)a.K * 4), gr = rsrc(a.gamma, (uint32_t)a.K * 4);
+        const auto xr = rsrc(a.x, (uint32_t)a.K * 4), gr = rsrc(a.gamma, a.gamma ? (uint32_t)a.K * 4 : 0u);
 #pragma unroll
         for (int c = 0; c < NX; ++c) {
             const int i = tid + 256 * c;
             const uint32_t off = i < a.K / 4 ? (uint32_t)i * 16 : 0xffffff00u;
             xv[c] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
-            gv[c] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(gr, off, 0, 0));
+            gv[c] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(gr, a.gamma ? off : 0xffffff00u, 0, 0));
         }
     }
     auto fetch_h = [&](int i0) {
@@ -293,6 +293,9 @@ __global__ __launch_bounds__(256, HREG ? 4 : 5) void proj_kernel(Proj a) {
         if (lane == 0) s_part[w] = ss;
         __syncthreads();
         const float inv = rsqrtf((s_part[0] + s_part[1] + s_part[2] + s_part[3]) / (float)a.K + a.eps);
+        if (!a.gamma)
+#pragma unroll
+            for (int c = 0; c < NX; ++c) gv[c] = f32x4{1.f, 1.f, 1.f, 1.f};
 #pragma unroll
         for (int c = 0; c < NX; ++c) {
             const int i = tid + 256 * c;
@@ -424,13 +427,14 @@ __global__ __launch_bounds__(256, HREG ? 4 : 5) void proj_kernel(Proj a) {
     }
 }
 
-// h[b] = bf16(x[b] rsqrt(mean(x[b]^2) + eps) gamma); one workgroup per row. Each chunk of 8192 values is
-// requested at once (8 x 16 bytes of x and gamma per thread); rows of one chunk are normalised from registers.
+// h[b] = bf16(x[b] rsqrt(mean(x[b]^2) + eps) gamma) (gamma null: 1); one workgroup per row. Each chunk of 8192
+// values is requested at once (8 x 16 bytes of x and gamma per thread); rows of one chunk are normalised from
+// registers.
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *x, const float *gamma, uint16_t *h, int H, float eps) {
     __shared__ float s_part[4];
     constexpr int V = 8, CHUNK = 256 * V;  // float4 per thread, float4 per chunk
     const int b = blockIdx.x, tid = threadIdx.x, n4 = H / 4;
-    const auto xr = rsrc(x + (size_t)b * H, (uint32_t)H * 4), gr = rsrc(gamma, (uint32_t)H * 4);
+    const auto xr = rsrc(x + (size_t)b * H, (uint32_t)H * 4), gr = rsrc(gamma, gamma ? (uint32_t)H * 4 : 0u);
     f32x4 xv[V], gv[V];
     auto fetch = [&](int c0) {
 #pragma unroll
@@ -453,6 +457,9 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *x, const floa
     const float inv = rsqrtf((s_part[0] + s_part[1] + s_part[2] + s_part[3]) / (float)H + eps);
     for (int c0 = 0; c0 < n4; c0 += CHUNK) {
         if (n4 > CHUNK) fetch(c0);
+        if (!gamma)
+#pragma unroll
+            for (int j = 0; j < V; ++j) gv[j] = f32x4{1.f, 1.f, 1.f, 1.f};
 #pragma unroll
         for (int j = 0; j < V; ++j) {
             const int i = c0 + tid + 256 * j;
@@ -577,7 +584,7 @@ extern "C" size_t qs_mlp_decode_workspace_bytes(int B, int H, int I) {
 extern "C" int qs_mlp_decode(const float *x, const float *gamma, const uint8_t *gate, const uint8_t *up,
                              const uint8_t *down, float *x_out, void *workspace, int B, int H, int I, float eps,
                              void *stream) {
-    QS_REQUIRE(x && gamma && gate && up && down && x_out && workspace, "qs_mlp_decode: null pointer");
+    QS_REQUIRE(x && gate && up && down && x_out && workspace, "qs_mlp_decode: null pointer");
     QS_REQUIRE(B > 0 && B <= MAX_ROWS, "qs_mlp_decode: 1 to %d rows (got %d)", MAX_ROWS, B);
     QS_REQUIRE(mx_shape_ok(H, I, FMT_FP4) && mx_shape_ok(I, H, FMT_FP8),
                "qs_mlp_decode: H must be a multiple of 128 and I of 64 (got H %d, I %d)", H, I);

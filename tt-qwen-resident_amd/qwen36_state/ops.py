@@ -605,12 +605,14 @@ def mx_linear(h, weight, out=None, ws=None):
 def mlp_decode(x, gamma, gate, up, down, eps=EPS, out=None, ws=None):
     """The MLP half of a decoder layer for 1..16 rows (tests/bench_resident_mlp.py:98-105):
     x + (silu(h G) * (h U)) D with h = bf16(x * rsqrt(mean(x^2) + eps) * gamma), z = silu(h G) * (h U) kept
-    in bf16. x [B, H] fp32, gamma [H] fp32; gate, up MxWeight MXFP4 [H, I]; down MxWeight MXFP8 [I, H].
+    in bf16. x [B, H] fp32, gamma [H] fp32 or None when the norm weight is folded into the rows of gate and up
+    (weights.py:107-112); gate, up MxWeight MXFP4 [H, I]; down MxWeight MXFP8 [I, H].
     Returns x_out [B, H] fp32 (``out`` may be ``x``)."""
     dev = x.device
     B, H = x.shape
     _chk(x, "x", torch.float32, (B, H), dev)
-    _chk(gamma, "gamma", torch.float32, (H,), dev)
+    if gamma is not None:
+        _chk(gamma, "gamma", torch.float32, (H,), dev)
     I = gate.N
     for w, name, shape, fmt in ((gate, "gate", (H, I), MXFP4), (up, "up", (H, I), MXFP4), (down, "down", (I, H), MXFP8)):
         if (w.K, w.N) != shape or w.fmt != fmt:
