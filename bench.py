@@ -11,10 +11,10 @@ fp32 [8, 48, 128, 128] states, in place) and 16 attention layers (append of one 
 pages + paged GQA decode, 24 q heads / 4 KV heads x 256, over a shared 2048-page pool through per-user
 random block tables), replayed as one HIP graph that also advances every user's position — and whose
 ``configs`` key holds the other workloads, each with its own roofline and CPU baseline:
-  gdn-layer     one GDN layer, batch 1 (48 layers' distinct buffers rotate, 313 MB per loop)
+  gdn-layer     one GDN layer, batch 1 (96 layers' distinct buffers rotate, 627 MB per loop)
   attn-layer    one attention layer at 32768 positions, batch 1 (4 layers' distinct pools rotate)
   verify-step   MTP verify at batch 1, 8192 positions, 4 tokens, 64 layers + acceptance by slot
-  prefill       chunked gated delta rule over 8192 tokens + the paged K/V fill
+  prefill       chunked gated delta rule over 8192 tokens + the paged K/V fill (two prompts rotate)
   conv-prefill  the prompt conv with its carry over 8192 tokens (the prefill -> decode handoff)
   mlp-layer     the MLP half of one layer at one row, weights streamed as MXFP4 (gate | up) and MXFP8 (down)
 Inputs are seeded synthetic tensors resident in HBM before the timed region.
@@ -406,16 +406,16 @@ def bench_step(args, torch, tel):
 
 
 def bench_gdn_layer(args, torch, tel):
-    """One GDN layer at batch 1; the graph walks 48 layers' distinct buffers (313 MB, more than the 256 MB
-    Infinity Cache) 4 times, so every launch reads its state from HBM; per launch = replay / 192."""
+    """One GDN layer at batch 1; the graph walks 96 layers' distinct buffers (627 MB, more than twice the
+    256 MB Infinity Cache) twice, so every launch reads its state from HBM; per launch = replay / 192."""
     from qwen36_state import ops, workloads as W
     from qwen36_state.decode import layer_bytes
 
-    layers = [W.gdn_layer(1, "cuda:0", seed=i) for i in range(48)]
+    layers = [W.gdn_layer(1, "cuda:0", seed=i) for i in range(96)]
     outs = [torch.empty(1, 48, 128, dtype=torch.bfloat16, device="cuda:0") for _ in layers]
     ws = torch.zeros(ops.lib().qs_gdn_workspace_bytes(1, 16), dtype=torch.uint8, device="cuda:0")
 
-    R = 4  # passes over the 48 layers per replay, so the graph's start-up is spread over 192 launches
+    R = 2  # passes over the 96 layers per replay, so the graph's start-up is spread over 192 launches
 
     def fn():
         for _ in range(R):
@@ -424,8 +424,8 @@ def bench_gdn_layer(args, torch, tel):
 
     g = capture(torch, fn)
     msr, stats = timed(torch, args, g.replay, tel=tel, settle_ms=SETTLE_MS)
-    ms = msr / (48 * R)
-    stats = {k: (v / (48 * R) if k.endswith("_ms") else v) for k, v in stats.items()}
+    ms = msr / (len(layers) * R)
+    stats = {k: (v / (len(layers) * R) if k.endswith("_ms") else v) for k, v in stats.items()}
     nbytes = layer_bytes(1, 0)
     out = entry("one GDN layer decode, batch 1: conv1d update (10240 channels) + L2-norm + gated delta rule on fp32 "
                 "[1, 48, 128, 128] (48 layers' buffers rotate)", nbytes, ms, stats,
@@ -525,23 +525,31 @@ PREFILL_FLOPS = 71.94e9
 
 
 def bench_prefill(args, torch, tel):
+    """The chunked rule over one 8192-token prompt plus its paged K/V fill; two prompts rotate (each ~300 MB
+    of inputs, outputs and pages besides the workspace), so each call reads them from HBM; per call =
+    replay / 2."""
     from qwen36_state import ops, workloads as W
 
-    d = W.prefill(8192, "cuda:0", seed=0)
+    prompts = [W.prefill(8192, "cuda:0", seed=i) for i in range(2)]
     kc = torch.zeros(2048, 4, 64, 256, dtype=torch.bfloat16, device="cuda:0")
     vc = torch.zeros_like(kc)
     nbytes_ws = ops.lib().qs_gdn_chunk_prefill_workspace_bytes(8192, 16, 48, 128, 128, 64)
     ws = torch.zeros(nbytes_ws, dtype=torch.uint8, device="cuda:0")
-    S = torch.empty_like(d["S0"])
+    finals = [torch.empty_like(d["S0"]) for d in prompts]
 
     def fn():
-        ops.chunk_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"], initial_state=d["S0"], ws=ws,
-                                   final_state=S)  # fmt: skip
-        ops.paged_kv_fill(d["kv_k"], d["kv_v"], kc, vc, d["page_table"])
+        for d, S in zip(prompts, finals):
+            ops.chunk_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"], initial_state=d["S0"], ws=ws,
+                                       final_state=S)  # fmt: skip
+            ops.paged_kv_fill(d["kv_k"], d["kv_v"], kc, vc, d["page_table"])
 
     g = capture(torch, fn)
     a2 = argparse.Namespace(**{**vars(args), "steps": max(10, args.steps // 5)})
-    ms, stats = timed(torch, a2, g.replay, tel=tel, settle_ms=SETTLE_MS)
+    msr, stats = timed(torch, a2, g.replay, tel=tel, settle_ms=SETTLE_MS)
+    n = len(prompts)
+    ms = msr / n
+    stats = {k: (v / n if k.endswith("_ms") else v) for k, v in stats.items()}
+    d = prompts[0]
     out = entry("chunked-prefill gated delta rule, 8192 tokens, chunk 64, 16/48 heads x 128 (WY form, bf16 MFMA, fp32 "
                 "state) + paged fill of 8192 tokens of K/V (4 x 256) into 128 random pages", PREFILL_BYTES, ms, stats,
                 roofline("gdn_chunk_prefill", PREFILL_BYTES, ms, flops=PREFILL_FLOPS),
