@@ -3,7 +3,7 @@
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--workload all|step|gdn-layer|attn-layer|
                      verify-step|prefill|conv-prefill|mlp-layer]
-                    [--profile-family gdn|attn|conv|copy|prefill|mlp]
+                    [--profile-family gdn|gdn1|attn|attn1|verify|conv|copy|prefill|mlp]
 
 Default (``--workload all``): one JSON line whose top level is the headline workload — the batch-8 decode
 step at 4096 positions per user: 48 Gated-DeltaNet layers (conv1d update + L2-norm + gated delta rule on
@@ -729,10 +729,37 @@ def profile_family(args, torch):
         print(f"paged_gqa_decode: {layer_bytes(8, 4096, attn=True)} algorithmic bytes per dispatch")
     elif fam == "prefill":
         d = W.prefill(8192, dev, seed=0)
+        kc = torch.zeros(2048, 4, 64, 256, dtype=torch.bfloat16, device=dev)
+        vc = torch.zeros_like(kc)
         for _ in range(args.reps):
             ops.chunk_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"], initial_state=d["S0"])
+            ops.paged_kv_fill(d["kv_k"], d["kv_v"], kc, vc, d["page_table"])
         torch.cuda.synchronize()
         print(f"chunk prefill: {PREFILL_BYTES} algorithmic bytes (with the K/V fill) per prefill")
+    elif fam == "gdn1":
+        layers = [W.gdn_layer(1, dev, seed=i) for i in range(96)]
+        for _ in range(args.reps):
+            for d in layers:
+                ops.gdn_decode_fused(d["x"], d["conv_state"], d["taps"], d["g"], d["beta"], d["state"])
+        torch.cuda.synchronize()
+        print(f"gdn_decode_fused: {layer_bytes(1, 0)} algorithmic bytes per dispatch")
+    elif fam == "attn1":
+        layers = [W.attn_layer(1, 32768, dev, seed=i) for i in range(4)]
+        for _ in range(args.reps):
+            for d in layers:
+                ops.paged_gqa_decode(d["q"], d["k_cache"], d["v_cache"], d["block_table"], d["seq_lens"], d["scale"],
+                                     k_new=d["k_new"], v_new=d["v_new"], pages_per_split=args.pps_attn1)  # fmt: skip
+        torch.cuda.synchronize()
+        print(f"paged_gqa_decode: {layer_bytes(1, 32768, attn=True)} algorithmic bytes per call (main + merge)")
+    elif fam == "verify":
+        from qwen36_state.decode import VerifyStep
+
+        vs = VerifyStep.synthetic(1, 8192, T=4, device=dev, pages_per_split=args.pps_verify)
+        for _ in range(args.reps):
+            vs.step()
+            vs.rewind()
+        torch.cuda.synchronize()
+        print(f"verify step: {vs.bytes_per_step(8192)} algorithmic bytes per step")
     elif fam == "mlp":
         layers = [W.mlp_layer(1, dev, seed=i) for i in range(3)]
         for _ in range(args.reps):
@@ -756,7 +783,8 @@ def main():
     ap.add_argument("--pps-verify", type=int, default=2, help="pages per split (verify-step workload)")
     ap.add_argument("--kernel-reps", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baselines")
-    ap.add_argument("--profile-family", choices=["gdn", "attn", "conv", "copy", "prefill", "mlp"], default=None)
+    ap.add_argument("--profile-family", choices=["gdn", "gdn1", "attn", "attn1", "verify", "conv", "copy", "prefill", "mlp"],
+                    default=None)
     ap.add_argument("--reps", type=int, default=3, help="repetitions of --profile-family")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
