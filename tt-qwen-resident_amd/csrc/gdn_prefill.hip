@@ -431,6 +431,9 @@ __global__ __launch_bounds__(WALK_THREADS) void chunk_walk_kernel(PrefillArgs a)
     const int kh = h / (a.NV / a.NK);
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int w = wv & 3, role = wv >> 2;
+    // the k waves issue ahead of the q waves on a shared SIMD: their X, d and Tm requests lead every chunk's
+    // chain (the reverse order measured 25% slower, this one 0.5% faster than equal priority)
+    if (role == 0) __builtin_amdgcn_s_setprio(1);
     const int fr = lane & 15, g = lane >> 4, fk = g * 8, fq = g * 4;
 
     __shared__ __align__(16) uint16_t sS[2][SLAB][SKP];
