@@ -209,6 +209,10 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
     auto &s_v = s_v_[gw];
     __shared__ __align__(16) f32x4 s_red[NW > 1 ? 2 : 1][NW][2][CG];  // per token parity: wave column sums
 
+    // the q / k conv waves of a multi-slab workgroup issue first: their conv inputs then leave ahead of the other
+    // waves' state loads and the norms every slab waits for are ready sooner (the 64-layer batch-8 step:
+    // 936.5 -> 928.5 us; at batch 1, with the rows of a slab split over 4 waves, it measured slower)
+    if (CONV && NW == 1 && (isq || isk)) __builtin_amdgcn_s_setprio(2);
     // 1. Loads. Conv inputs (raw bits, untouched until used), this wave's state rows, the gates.
     const int qd = a.NK * DK;
     const int cq = kh * DK + 2 * lane, ck = qd + cq;                           // q, k channel pairs
@@ -286,6 +290,7 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
     else
         __builtin_amdgcn_wave_barrier();
 
+    if (CONV && NW == 1 && (isq || isk)) __builtin_amdgcn_s_setprio(0);
     // 3. Delta rule, token by token, on the rows held in registers.
     int arrived = 0;
     for (int t = 0; t < T; ++t) {
