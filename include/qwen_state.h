@@ -101,6 +101,12 @@ int qs_gdn_decode_fused_noalloc(const uint16_t *x, uint16_t *conv_state, const u
                                 const float *beta, float *state, uint16_t *o, uint16_t *y_out, const int *lens,
                                 int B, int NK, int NV, int DK, int DV, int K, float scale, float eps, void *stream);
 
+/* Diagnostics of qs_gdn_decode_fused_noalloc (no counterpart in the reference; for tests and for callers that
+ * want to check the library's counters are at rest between calls): copies the first n (1 <= n <= 16384)
+ * ints of the current device's static counter array into dst (device memory) on the stream. Allocates
+ * nothing. */
+int qs_gdn_noalloc_scratch_read(int *dst, int n, void *stream);
+
 /* Gated RMSNorm epilogue of the GDN mixer (the path's edge, torch model.py:274-275): for each row of DV
  * values, out = bf16(o * rsqrt(mean(o^2) + eps) * norm_w * silu(z)). o, z, out [rows, DV] bf16 (rows = B * NV,
  * or B * T * NV after a verify step; z is the projection's z slice), norm_w [DV] fp32. Replaces steps 7-8
@@ -113,35 +119,41 @@ int qs_gdn_gated_norm(const uint16_t *o, const uint16_t *z, const float *norm_w,
  *   x [B, T, C] bf16; conv_state_in [B, C, K-1]; g, beta [B, T, NV]; state_in [B, NV, DK, DV]
  *   -> conv_states_out [T, B, C, K-1], states_out [T, B, NV, DK, DV], o [B, T, NV, DV], y_out (nullable)
  *   [B, T, C]. Inputs are not modified.
+ * lens (nullable, [B] device int32, the step's lengths): a user with lens[b] < 0 is an idle slot, for which
+ * nothing is computed or written.
  * Replaces the verify rows of the GDN head cores (kernels/gdn_head_reader.cpp:149-187,
  * gdn_head_writer.cpp:60-66, :109) and the conv pair-slot ring (kernels/streamer_common.hpp:38-44). */
 int qs_gdn_verify_step(const uint16_t *x, const uint16_t *conv_state_in, uint16_t *conv_states_out,
                        const uint16_t *taps, const float *g, const float *beta, const float *state_in,
-                       float *states_out, uint16_t *o, uint16_t *y_out, int B, int T, int NK, int NV, int DK,
-                       int DV, int K, float scale, float eps, void *stream);
+                       float *states_out, uint16_t *o, uint16_t *y_out, const int *lens, int B, int T, int NK,
+                       int NV, int DK, int DV, int K, float scale, float eps, void *stream);
 
 /* The verify step reading each user's input from a slot of the previous verify step's snapshots, so a
  * rollback costs no copy (the reference's slot select: kernels/gdn_head_reader.cpp:17-20, :149-187, the
  * conv pair slots kernels/streamer_common.hpp:38-44): user b's state and conv history are slot in_slot[b]
  * of states_in [n_slots, B, NV, DK, DV] and conv_states_in [n_slots, B, C, K-1]; in_slot [B] int32 is
  * device memory (a slot outside [0, n_slots) reads slot 0). Outputs as qs_gdn_verify_step; they must not
- * alias the inputs (callers alternate two snapshot sets). */
+ * alias the inputs (callers alternate two snapshot sets). An idle slot (lens non-null, lens[b] < 0) verifies
+ * no token: its input state and conv history are copied unchanged into the same slot of the outputs (when
+ * that slot is below T), which the next step reads, since the acceptance leaves an idle slot's slot as it is. */
 int qs_gdn_verify_step_slots(const uint16_t *x, const uint16_t *conv_states_in, uint16_t *conv_states_out,
                              const uint16_t *taps, const float *g, const float *beta, const float *states_in,
                              float *states_out, const int *in_slot, int n_slots, uint16_t *o, uint16_t *y_out,
-                             int B, int T, int NK, int NV, int DK, int DV, int K, float scale, float eps,
-                             void *stream);
+                             const int *lens, int B, int T, int NK, int NV, int DK, int DV, int K, float scale,
+                             float eps, void *stream);
 
 /* Acceptance without copies: slot[b] <- accept_len[b] - 1 (the snapshot the next verify step reads) and,
  * when seq_lens is non-null, seq_lens[b] <- base_lens[b] + accept_len[b] (the KV truncation), for
  * accept_len[b] in [1, T]; a user with another accept length is left untouched and reported
- * (QS_STATUS_ACCEPT). Replaces the hub's slot/ring advance (kernels/mlp_hub.cpp:48-58; model.py:1314-1318). */
+ * (QS_STATUS_ACCEPT). An idle slot (base_lens non-null, base_lens[b] < 0) keeps its slot and length.
+ * Replaces the hub's slot/ring advance (kernels/mlp_hub.cpp:48-58; model.py:1314-1318). */
 int qs_verify_accept(const int *accept_len, int *slot, int *seq_lens, const int *base_lens, int B, int T,
                      int *status, void *stream);
 
 /* Rollback after verify: state[b] <- states_out[accept_len[b]-1, b], conv_state[b] <- conv_states_out[...]
  * (bit-exact copies), and, when seq_lens is non-null, seq_lens[b] <- base_lens[b] + accept_len[b] (the KV
- * truncation; no KV bytes move). accept_len is device memory, 1 <= accept_len[b] <= T.
+ * truncation; no KV bytes move). accept_len is device memory, 1 <= accept_len[b] <= T; an idle slot
+ * (base_lens non-null, base_lens[b] < 0) is left untouched.
  * Replaces the slot/ring advance of the hub (kernels/mlp_hub.cpp:48-58; model.py:1314-1318). */
 int qs_gdn_rollback(const float *states_out, float *state, const uint16_t *conv_states_out, uint16_t *conv_state,
                     const int *accept_len, int *seq_lens, const int *base_lens, int B, int T, int NV, int DK,
@@ -236,6 +248,9 @@ int qs_attn_mixer_decode(const uint16_t *q, const uint16_t *k_new, const uint16_
  * (times scale) and k inside:
  *   q, k [T, NK, DK] bf16; v [T, NV, DV] bf16; g, beta [T, NV] fp32; initial_state [NV, DK, DV] fp32
  *   -> o [T, NV, DV] bf16 (token-major), final_state [NV, DK, DV] fp32 (may alias initial_state).
+ * chunk: 32 (the reference prefill's chunk_size, prefill/pp_prefill.py:56, :801) or 64. The chunked form
+ * equals the token-by-token recurrence for every chunk size, so both run the kernels' 64-token chunks;
+ * any other value is rejected.
  * Replaces ttnn.transformer.chunk_gated_delta_rule as called at prefill/pp_prefill.py:791-807. */
 size_t qs_gdn_chunk_prefill_workspace_bytes(int T, int NK, int NV, int DK, int DV, int chunk);
 int qs_gdn_chunk_prefill(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *g,

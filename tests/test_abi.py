@@ -29,7 +29,7 @@ def test_exports_every_declared_symbol():
         assert hasattr(L, n), n
         assert n in _lib.SIGNATURES, n
     assert set(_lib.SIGNATURES) == set(names)
-    assert L.qs_abi_version() == 3
+    assert L.qs_abi_version() == 4
 
 
 def test_rejects_bad_arguments():
@@ -42,9 +42,9 @@ def test_rejects_bad_arguments():
     assert L.qs_gdn_decode_step(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1, 16, 40, 128, 128, 0.1, 1e-6, S) == -1
     assert "multiple" in L.qs_last_error().decode()
     assert L.qs_conv1d_update(FAKE, FAKE, FAKE, FAKE, 1, 10240, 3, S) == -1
-    assert L.qs_gdn_verify_step(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NUL,
+    assert L.qs_gdn_verify_step(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NUL, NUL,
                                 1, 9, 16, 48, 128, 128, 4, 0.1, 1e-6, S) == -1  # fmt: skip
-    assert L.qs_gdn_verify_step(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NUL,
+    assert L.qs_gdn_verify_step(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NUL, NUL,
                                 1, 4, 16, 48, 128, 128, 4, 0.1, 1e-6, S) == -1  # fmt: skip  (states_out aliases)
     assert "alias" in L.qs_last_error().decode()
     # attention: head dim, block size, group size, missing workspace

@@ -127,3 +127,42 @@ def test_prefill_graph_replays(dev):
         assert torch.equal(out[0], eager[0]) and torch.equal(out[1], eager[1])
         g["q"].add_(0)  # eager work between the replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("batched", [False, True])
+def test_prefill_reference_call(dev, batched):
+    """The reference prefill's call as written (prefill/pp_prefill.py:791-807): token-major q, k [T, 2048],
+    v [T, 6144], scale DK^-1/2, output_final_state, chunk_size 32, output_head_major, and the ttnn-only
+    memory_config / eye / tril / ones / masks (accepted and ignored), with and without the per-device
+    leading batch dimension of 1. 200 tokens against the fp64 recurrence: S_T rtol 1e-4, head-major o
+    rtol 2e-2."""
+    T = 200
+    d = W.prefill(T, "cpu", seed=11)
+    g = {k: v.to(dev) for k, v in d.items()}
+    q, k, v = g["q"].reshape(T, -1), g["k"].reshape(T, -1), g["v"].reshape(T, -1)
+    gg, bb, S0 = g["g"], g["beta"], g["S0"]
+    if batched:
+        q, k, v, gg, bb, S0 = q[None], k[None], v[None], gg[None], bb[None], S0[None]
+    eye, tril, ones = torch.eye(32), torch.tril(torch.ones(32, 32)), torch.ones(32, 32)
+    o, S = ops.chunk_gated_delta_rule(
+        q, k, v, gg, bb,
+        scale=128**-0.5,
+        initial_state=S0,
+        output_final_state=True,
+        chunk_size=32,
+        output_head_major=True,
+        memory_config="DRAM",
+        eye=eye,
+        tril=tril,
+        ones=ones,
+        masks=torch.zeros(32, 96),
+    )  # fmt: skip
+    if batched:
+        assert o.shape == (1, 48, T, 128) and S.shape == (1, 48, 128, 128)
+        o, S = o[0], S[0]
+    assert o.shape == (48, T, 128) and S.shape == (48, 128, 128)
+    o_ref, S_ref = ref(d, T)
+    assert_prefill_state(S, S_ref.float())
+    assert_bf16_output(o.transpose(0, 1), O.bf16(o_ref.float()))
+    with pytest.raises(ValueError, match="chunk_size"):
+        ops.chunk_gated_delta_rule(q, k, v, gg, bb, initial_state=S0, chunk_size=16)

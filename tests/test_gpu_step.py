@@ -110,3 +110,38 @@ def test_verify_step_slots_equals_copy(dev):
                 sa, ca = a.state_of(gi, b)
                 sc, cc = c.state_of(gi, b)
                 assert torch.equal(sa, sc) and torch.equal(ca, cc), (k, gi, b)
+
+
+@pytest.mark.parametrize("B", [3, 8])
+@pytest.mark.parametrize("mode", ["slots", "copy"])
+def test_verify_step_idle_user(dev, mode, B):
+    """Two verify steps (8 layers, T = 3; batch 3: a slab's rows over 4 waves, batch 8: one wave per slab) with
+    user 1 an idle slot (lens -1): its length, its current state and conv history and its pages stay as they
+    were whatever its accept length, and users 0 and 2 get bit for bit what they get in the same step with
+    every user active."""
+    mk = lambda: VerifyStep.synthetic(B, 1024, T=3, layers=8, device=dev, rollback=mode, max_blocks=20,  # noqa: E731
+                                      num_blocks=20 * B, check=True)  # fmt: skip
+    act, idle = mk(), mk()
+    idle.lens[1] = -1
+    n_gdn = sum(not d["attn"] for d in idle.layer)
+    before = [tuple(t.clone() for t in idle.state_of(gi, 1)) for gi in range(n_gdn)]
+    pages = idle.block_table[1].long()
+    pools = [(d["k_cache"][pages].clone(), d["v_cache"][pages].clone()) for d in idle.layer if d["attn"]]
+    for k in range(2):
+        act.step()
+        idle.step()
+        torch.cuda.synchronize()
+        idle.status.check()
+        assert int(idle.lens[1]) == -1, k
+        assert torch.equal(idle.lens[[0, 2]], act.lens[[0, 2]]), k
+        for la, li in zip(act.layer, idle.layer):
+            assert torch.equal(la["o"][[0, 2]], li["o"][[0, 2]]), (k, "o")
+        for gi in range(n_gdn):
+            for b in (0, 2):
+                sa, ca = act.state_of(gi, b)
+                si, ci = idle.state_of(gi, b)
+                assert torch.equal(sa, si) and torch.equal(ca, ci), (k, gi, b)
+            S1, c1 = idle.state_of(gi, 1)
+            assert torch.equal(S1, before[gi][0]) and torch.equal(c1, before[gi][1]), (k, gi, "idle state")
+        for (kc, vc), d in zip(pools, (d for d in idle.layer if d["attn"])):
+            assert torch.equal(d["k_cache"][pages], kc) and torch.equal(d["v_cache"][pages], vc), (k, "idle pages")

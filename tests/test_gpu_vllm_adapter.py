@@ -58,74 +58,135 @@ def to(xs, dev):
     return [{k: v.to(dev) for k, v in x.items()} for x in xs]
 
 
-def test_vllm_adapter_prefill_then_decode(dev):
-    gen = torch.Generator().manual_seed(2024)
-    ad = StatePathAdapter(B, MAX_LEN, layers=LAYERS, device=dev)
-    kv = ad.allocate_kv_cache((NUM_BLOCKS, NKV, 64, HD), torch.bfloat16, 1)
-    perm = torch.randperm(NUM_BLOCKS, generator=gen).to(torch.int32)
-    tables = perm[: B * 8].view(B, 8)  # vLLM-style: each slot a random set of blocks
-    taps = [t.cpu() for t in ad.taps]
-    # oracle state: the pools (whole, on the CPU), per GDN layer the slots' states and conv histories
-    kc, vc = torch.zeros(NUM_BLOCKS, NKV, 64, HD, dtype=torch.bfloat16), torch.zeros(NUM_BLOCKS, NKV, 64, HD, dtype=torch.bfloat16)
-    S = {l: torch.zeros(B, NV, DK, DV) for l in range(3)}
-    cs = {l: torch.zeros(B, C_QKV, 3) for l in range(3)}
-    pert = {l: torch.zeros(B, NV, dtype=torch.bool) for l in range(3)}
-    lens = [-1] * B
+class Ref:
+    """The oracle's copy of the adapter's state: the whole pools, per GDN layer the slots' states, conv
+    histories and perturbed heads, the slots' lengths."""
+
+    def __init__(self, ad):
+        z = lambda: torch.zeros(NUM_BLOCKS, NKV, 64, HD, dtype=torch.bfloat16)  # noqa: E731
+        self.kc, self.vc = z(), z()
+        self.S = {l: torch.zeros(B, NV, DK, DV) for l in range(3)}
+        self.cs = {l: torch.zeros(B, C_QKV, 3) for l in range(3)}
+        self.pert = {l: torch.zeros(B, NV, dtype=torch.bool) for l in range(3)}
+        self.lens = [-1] * B
+        self.taps = [t.cpu() for t in ad.taps]
+
+
+def prefill_two(dev, ad, kv, gen, tables):
+    """Prompts of 100 and 37 tokens into slots 0 and 2 (slot 1 idle), checked against the oracle."""
+    ref = Ref(ad)
     for slot, T in ((0, 100), (2, 37)):
         inp = prompt_inputs(T, gen)
         outs = ad.prefill_forward(to(inp, dev), tables[slot : slot + 1], kv, torch.tensor([T]), slot=slot)
-        O.paged_fill(kc, inp[3]["k"], tables[slot])
-        O.paged_fill(vc, inp[3]["v"], tables[slot])
+        O.paged_fill(ref.kc, inp[3]["k"], tables[slot])
+        O.paged_fill(ref.vc, inp[3]["v"], tables[slot])
         for l in range(3):
             x = inp[l]
-            y_ref, carry = O.conv1d_prefill(x["x"][:, :C_QKV].float(), None, taps[l].float())
+            y_ref, carry = O.conv1d_prefill(x["x"][:, :C_QKV].float(), None, ref.taps[l].float())
             assert torch.equal(ad.conv_state[l, slot].cpu().float(), carry), (slot, l)
-            cs[l][slot] = carry
+            ref.cs[l][slot] = carry
             # the state from the kernel's own conv outputs (their parity with the oracle is the conv tests')
             q, k, v, _ = ops.causal_conv1d_prefill(x["x"].to(dev), ad.taps[l])
             o_ref, S_ref = O.gdn_chunk_prefill(q.cpu().float(), k.cpu().float(), v.cpu().float(), x["g"], x["beta"],
                                                torch.zeros(NV, DK, DV))  # fmt: skip
             assert_prefill_state(ad.gdn_state[l, slot], S_ref)
             assert_bf16_output(outs[l], O.bf16(o_ref))
-            S[l][slot] = ad.gdn_state[l, slot].cpu()  # continue from the kernel's prompt state
-        lens[slot] = T
-    assert torch.equal(kv[0][0].cpu(), kc) and torch.equal(kv[0][1].cpu(), vc)
-    idle_state = (ad.gdn_state[:, 1].clone(), ad.conv_state[:, 1].clone())
+            ref.S[l][slot] = ad.gdn_state[l, slot].cpu()  # continue from the kernel's prompt state
+        ref.lens[slot] = T
+    assert torch.equal(kv[0][0].cpu(), ref.kc) and torch.equal(kv[0][1].cpu(), ref.vc)
+    return ref
 
+
+def check_decode(dev, ad, kv, ref, inp, outs, tables, gdn=None, conv=None):
+    """One decode step's outputs (and, given, the GDN states / conv histories after it) against the oracle
+    stepped from ``ref`` with the inputs ``inp``; advances ``ref``."""
+    gdn = ad.gdn_state.cpu() if gdn is None else gdn
+    conv = ad.conv_state.cpu() if conv is None else conv
+    active = [b for b in range(B) if ref.lens[b] >= 0]
+    for l in range(3):
+        x = inp[l]
+        o_ref, S2, cs2, y_ref = O.gdn_decode(x["x"][active].float(), ref.cs[l][active], ref.taps[l].float(),
+                                             x["g"][active], x["beta"][active], ref.S[l][active], NK, NV, DK, DV)  # fmt: skip
+        assert torch.equal(conv[l][active].float(), cs2), l
+        y_k = ops.causal_conv1d_update(x["x"][active].to(dev), ref.cs[l][active].bfloat16().to(dev), ad.taps[l]).cpu()
+        ref.pert[l][active] |= conv_mismatch_heads(y_k, y_ref, NK, NV)
+        assert perturbed_ok(ref.pert[l])
+        got = gdn[l][active]
+        ok = ~ref.pert[l][active]
+        assert_state(got[ok], S2[ok])
+        if bool((~ok).any()):
+            assert_state_perturbed(got[~ok], S2[~ok])
+        assert_bf16_output(outs[l][active], O.bf16(o_ref))
+        ref.S[l][active], ref.cs[l][active] = S2, cs2
+    a = inp[3]
+    pos_a = torch.tensor([ref.lens[b] for b in active], dtype=torch.int32)
+    O.paged_append(ref.kc, ref.vc, a["k_new"][active], a["v_new"][active], tables[active], pos_a)
+    o_ref = O.gqa_decode(a["q"][active], ref.kc, ref.vc, tables[active], pos_a + 1, HD**-0.5)
+    assert_attn_output(outs[3][active], O.bf16(o_ref))
+    assert torch.count_nonzero(outs[3][1]) == 0  # the idle slot's attention output is zero
+    ref.lens = [p + 1 if p >= 0 else p for p in ref.lens]
+
+
+def test_vllm_adapter_prefill_then_decode(dev):
+    gen = torch.Generator().manual_seed(2024)
+    ad = StatePathAdapter(B, MAX_LEN, layers=LAYERS, device=dev)
+    kv = ad.allocate_kv_cache((NUM_BLOCKS, NKV, 64, HD), torch.bfloat16, 1)
+    perm = torch.randperm(NUM_BLOCKS, generator=gen).to(torch.int32)
+    tables = perm[: B * 8].view(B, 8)  # vLLM-style: each slot a random set of blocks
+    ref = prefill_two(dev, ad, kv, gen, tables)
+    idle_state = (ad.gdn_state[:, 1].clone(), ad.conv_state[:, 1].clone())
     for step in range(3):
         inp = decode_inputs(gen)
-        pos = torch.tensor(lens, dtype=torch.int32)
-        outs = ad.decode_forward(to(inp, dev), pos, page_table=tables)
-        active = [b for b in range(B) if lens[b] >= 0]
-        for l in range(3):
-            x = inp[l]
-            o_ref, S2, cs2, y_ref = O.gdn_decode(x["x"][active].float(), cs[l][active], taps[l].float(), x["g"][active],
-                                                 x["beta"][active], S[l][active], NK, NV, DK, DV)  # fmt: skip
-            st = ad.conv_state[l].cpu()
-            assert torch.equal(st[active].float(), cs2), (step, l)
-            y_k = ops.causal_conv1d_update(x["x"][active].to(dev), cs[l][active].bfloat16().to(dev), ad.taps[l]).cpu()
-            pert[l][active] |= conv_mismatch_heads(y_k, y_ref, NK, NV)
-            assert perturbed_ok(pert[l])
-            got = ad.gdn_state[l].cpu()[active]
-            ok = ~pert[l][active]
-            assert_state(got[ok], S2[ok])
-            if bool((~ok).any()):
-                assert_state_perturbed(got[~ok], S2[~ok])
-            assert_bf16_output(outs[l][active], O.bf16(o_ref))
-            S[l][active], cs[l][active] = S2, cs2
-        a = inp[3]
-        pos_a = torch.tensor([lens[b] for b in active], dtype=torch.int32)
-        O.paged_append(kc, vc, a["k_new"][active], a["v_new"][active], tables[active], pos_a)
-        o_ref = O.gqa_decode(a["q"][active], kc, vc, tables[active], pos_a + 1, HD**-0.5)
-        assert_attn_output(outs[3][active], O.bf16(o_ref))
-        assert torch.count_nonzero(outs[3][1]) == 0  # the idle slot's attention output is zero
-        assert torch.equal(kv[0][0].cpu(), kc) and torch.equal(kv[0][1].cpu(), vc), step
+        pos = torch.tensor(ref.lens, dtype=torch.int32)
+        outs = ad.decode_forward(to(inp, dev), pos, tables, reload_page_table=True, read_from_device=True)
+        check_decode(dev, ad, kv, ref, inp, outs, tables)
+        assert torch.equal(kv[0][0].cpu(), ref.kc) and torch.equal(kv[0][1].cpu(), ref.vc), step
         assert torch.equal(ad.gdn_state[:, 1], idle_state[0]) and torch.equal(ad.conv_state[:, 1], idle_state[1])
-        lens = [p + 1 if p >= 0 else p for p in lens]
-        assert ad.lens.cpu().tolist() == lens
+        assert ad.lens.cpu().tolist() == ref.lens
 
     with pytest.raises(ValueError, match="max_seq_len"):
         ad.decode_forward(to(decode_inputs(gen), dev), torch.tensor([MAX_LEN, -1, 40], dtype=torch.int32))
+
+
+def test_vllm_adapter_async_decode(dev):
+    """Three decode_forward calls queued with no host synchronisation between them (torch's sync debug mode
+    raises on any), as the reference's asynchronous steps with late reads (generator_vllm.py:117-160): the
+    first reloads positions and the page table from the host, the second copies its inputs in, the third
+    takes inputs the caller wrote into the step's own buffers (reload_inputs=False) and the positions the
+    device advanced to.
+    Each step's outputs, states and conv histories (device copies made in stream order) match the oracle."""
+    gen = torch.Generator().manual_seed(77)
+    ad = StatePathAdapter(B, MAX_LEN, layers=LAYERS, device=dev)
+    kv = ad.allocate_kv_cache((NUM_BLOCKS, NKV, 64, HD), torch.bfloat16, 1)
+    tables = torch.randperm(NUM_BLOCKS, generator=gen).to(torch.int32)[: B * 6].view(B, 6)
+    ref = prefill_two(dev, ad, kv, gen, tables)
+    inps = [decode_inputs(gen) for _ in range(3)]
+    dev_inps = [to(x, dev) for x in inps]
+    pos = torch.tensor(ref.lens, dtype=torch.int32).pin_memory()
+    torch.cuda.synchronize()
+    snaps = []
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        for k in range(3):
+            if k == 0:
+                outs = ad.decode_forward(dev_inps[0], pos, tables.pin_memory(), reload_page_table=True)
+            elif k == 1:
+                pos1 = torch.tensor([p + 1 if p >= 0 else p for p in ref.lens], dtype=torch.int32)
+                outs = ad.decode_forward(dev_inps[1], pos1)
+            else:
+                for dst, src in zip(ad.step_inputs(), dev_inps[2]):
+                    for key, t in dst.items():
+                        t.copy_(src[key], non_blocking=True)
+                outs = ad.decode_forward(None, None, reload_inputs=False)
+            snaps.append(([o.clone() for o in outs], ad.gdn_state.clone(), ad.conv_state.clone()))
+    finally:
+        torch.cuda.set_sync_debug_mode("default")
+    ad.read_decode_output()
+    for k in range(3):
+        outs, gdn, conv = snaps[k]
+        check_decode(dev, ad, kv, ref, inps[k], [o.cpu() for o in outs], tables, gdn.cpu(), conv.cpu())
+    assert ad.lens.cpu().tolist() == ref.lens
+    assert torch.equal(kv[0][0].cpu(), ref.kc) and torch.equal(kv[0][1].cpu(), ref.vc)
 
 
 def test_vllm_adapter_rejects_bad_calls(dev):
@@ -141,3 +202,13 @@ def test_vllm_adapter_rejects_bad_calls(dev):
         ad.prefill_forward([], torch.zeros(2, 4, dtype=torch.int32), kv, torch.tensor([10]))
     with pytest.raises(ValueError, match="blocks"):
         ad.prefill_forward([], torch.zeros(1, 1, dtype=torch.int32), kv, torch.tensor([100]))
+    # a page table one block short of the new token's position: the entry past it is -1, so the row is neither
+    # written nor attended and the step reports it
+    gen = torch.Generator().manual_seed(5)
+    ad.prefill_forward(to(prompt_inputs(64, gen), dev), torch.tensor([[3]], dtype=torch.int32), kv, torch.tensor([64]))
+    before = (kv[0][0].clone(), kv[0][1].clone())
+    inp = [{k: v[:2] for k, v in x.items()} for x in decode_inputs(gen)]
+    with pytest.raises(ValueError, match="outside the KV pool"):
+        ad.decode_forward(to(inp, dev), torch.tensor([64, -1], dtype=torch.int32), torch.tensor([[3], [5]], dtype=torch.int32),
+                          reload_page_table=True, read_from_device=True)  # fmt: skip
+    assert torch.equal(kv[0][0], before[0]) and torch.equal(kv[0][1], before[1])

@@ -329,7 +329,7 @@ def test_prefill_chunked_equals_recurrence():
     beta = torch.sigmoid(torch.randn(T, NV, generator=g)).double()
     S0 = 0.02 * torch.randn(NV, DK, DK, generator=g).double()
     o, S = O.gdn_chunk_prefill(q, k, v, gg, beta, S0)
-    for chunk in (16, 64):
+    for chunk in (16, 32, 64):  # chunk-size independence, incl. the reference prefill's 32
         o2, S2 = O.gdn_chunk_prefill_wy(q, k, v, gg, beta, S0, chunk=chunk)
         torch.testing.assert_close(o2, o, rtol=1e-10, atol=1e-12)
         torch.testing.assert_close(S2, S, rtol=1e-10, atol=1e-12)

@@ -1,7 +1,8 @@
 """The allocation-free fused GDN decode (qs_gdn_decode_fused_noalloc, counters in the library's static device
-array) against the workspace entry point qs_gdn_decode_fused, both called through the C ABI: two calls in a
-row, the second with a smaller batch, each bit-identical to the workspace entry point on a copy of the same
-inputs (the same kernels run; only where the counters live differs), and an oversized batch is rejected."""
+array) against the workspace entry point qs_gdn_decode_fused, both called through the C ABI: captured into a
+HIP graph on its first call and replayed on fresh inputs; two eager calls in a row, the second with a smaller
+batch; each bit-identical to the workspace entry point on a copy of the same inputs (the same kernels run;
+only where the counters live differs); an oversized batch is rejected."""
 import ctypes
 
 import pytest
@@ -29,6 +30,41 @@ def run(entry, d, B, ws=None):
     rc = getattr(L, entry)(*args, B, NK, NV, DK, DV, 4, ctypes.c_float(DK**-0.5), ctypes.c_float(1e-6), st)
     assert rc == 0, L.qs_last_error().decode()
     return o, y
+
+
+def test_noalloc_captured_in_a_graph(dev):
+    """The allocation-free entry captured into a HIP graph on its first call in the process (the one-time
+    address lookup and the array's clear happen during the capture), then replayed twice on fresh inputs,
+    with eager work between the replays: each replay equals the workspace entry point on a copy of the same
+    inputs bit for bit, and the static counter array reads zero afterwards (the counters re-arm themselves)."""
+    L = ops.lib()
+    B = 8
+    buf = W.gdn_layer(B, dev, seed=90)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            o, y = run("qs_gdn_decode_fused_noalloc", buf, B)
+    torch.cuda.current_stream().wait_stream(s)
+    for rep in range(2):
+        fresh = W.gdn_layer(B, dev, seed=91 + rep)
+        for k in ("x", "g", "beta", "state", "conv_state", "taps"):
+            buf[k].copy_(fresh[k])
+        ref = {k: v.clone() for k, v in fresh.items()}
+        ws = torch.zeros(L.qs_gdn_workspace_bytes(B, NK), dtype=torch.uint8, device=dev)
+        o_ref, y_ref = run("qs_gdn_decode_fused", ref, B, ws)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o, o_ref) and torch.equal(y, y_ref), rep
+        assert torch.equal(buf["state"], ref["state"]) and torch.equal(buf["conv_state"], ref["conv_state"]), rep
+        _ = torch.randn(4096, device=dev).sum().item()  # eager work between the replays
+    cnt = torch.full((16384,), -1, dtype=torch.int32, device=dev)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert L.qs_gdn_noalloc_scratch_read(_p(cnt), 16384, st) == 0, L.qs_last_error().decode()
+    torch.cuda.synchronize()
+    assert int(cnt.abs().sum()) == 0
 
 
 @pytest.mark.parametrize("batches", [(8, 3)])

@@ -36,7 +36,8 @@ struct GdnArgs {
     uint16_t *o;                // [B, T, NV, DV]
     int *counters;              // decode + conv: [B, NK, 2] (q, k) self-resetting
     const int *in_slot;         // verify, nullable: [B] slot of s_in / conv_in holding user b's input
-    const int *lens;            // decode, nullable: [B]; a user with lens[b] < 0 (idle slot) is left untouched
+    const int *lens;            // nullable: [B]; a user with lens[b] < 0 is an idle slot (decode: left untouched;
+                                // verify: no token verified, slot mode carries its input slot forward)
     int n_slots;                // slots in s_in / conv_in
     int B, T, NK, NV, C;
     float scale, eps;
@@ -143,6 +144,12 @@ __device__ __forceinline__ float sum_row_groups(float x) {
     return x;
 }
 
+// First state element of lane (cg, row) of slab s of value head h in user slot `user` of s_in.
+template <int SLAB>
+__device__ __forceinline__ const float *sp_of_t(const GdnArgs &a, size_t user, int h, int s, int cg, int row) {
+    return a.s_in + (user * a.NV + h) * DK * DV + s * SLAB + cg * 4 + (size_t)row * DV;
+}
+
 // One workgroup of NW wavefronts per (user, value head, SLAB-column slab); wave w holds rows
 // w * RW .. (w + 1) * RW - 1 (RW = 128 / NW) of the slab, lane (rg = lane / CG, cg = lane % CG) rows
 // w * RW + rg + RG i (i < RPL), columns 4 cg .. 4 cg + 3. NW = 1 at large batch (each wave streams a
@@ -218,6 +225,31 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
     const int cq = kh * DK + 2 * lane, ck = qd + cq;                           // q, k channel pairs
     const int cv = 2 * qd + h * DV + s * SLAB + 2 * (lane & (SLAB / 2 - 1));  // v channel pair
     const uint16_t *conv_b = CONV ? a.conv_in + user_in * a.C * (KC - 1) : nullptr;
+    if (VERIFY && a.lens && a.lens[b] < 0) {
+        // An idle slot (uniform over the workgroup, whose units belong to one user): no token is verified and
+        // no output written. In slot mode its input is carried unchanged into the same slot of the output
+        // set, which is the set the next step reads after the acceptance left this user's slot as it was;
+        // in copy mode the caller's state is not touched at all.
+        if (a.in_slot && slot < a.T) {
+            const size_t out_b = (size_t)slot * a.B + b;
+            float *dp = a.s_out + (out_b * a.NV + h) * DK * DV + s * SLAB + cg * 4 + (size_t)(w * RW + rg) * DV;
+#pragma unroll
+            for (int i = 0; i < RPL; ++i)
+                *reinterpret_cast<f32x4 *>(dp + (size_t)(RG * i) * DV) =
+                    *reinterpret_cast<const f32x4 *>(sp_of_t<SLAB>(a, user_in, h, s, cg, w * RW + rg) + (size_t)(RG * i) * DV);
+            if (CONV) {
+                uint16_t *co = a.conv_out + out_b * a.C * (KC - 1);
+                auto carry = [&](int c) {
+                    *reinterpret_cast<u32x3 *>(co + (size_t)c * (KC - 1)) =
+                        *reinterpret_cast<const u32x3 *>(conv_b + (size_t)c * (KC - 1));
+                };
+                if (isv && lane < SLAB / 2) carry(cv);
+                if (isq && kq_owner) carry(cq);
+                if (isk && kq_owner) carry(ck);
+            }
+        }
+        return;
+    }
     ConvPair<TM> inq, ink, inv;
     if (CONV) {
         if (isq) inq = conv_load<TM>(a, conv_b, b, cq, T);
@@ -225,7 +257,7 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
         if (isv) inv = conv_load<TM>(a, conv_b, b, cv, T);
     }
     const size_t head = (size_t)(b * a.NV + h) * DK * DV;
-    const float *sp = a.s_in + (user_in * a.NV + h) * DK * DV + s * SLAB + cg * 4 + (size_t)(w * RW + rg) * DV;
+    const float *sp = sp_of_t<SLAB>(a, user_in, h, s, cg, w * RW + rg);
     f32x4 S[RPL];  // streamed once per step: nontemporal loads and stores keep it from thrashing L2 / MALL
 #pragma unroll
     for (int i = 0; i < RPL; ++i)
@@ -466,7 +498,7 @@ __global__ __launch_bounds__(256) void gates_kernel(const uint16_t *a, const uin
 // loads issued before the stores), the chunks after the state's copy the conv-state snapshot the same way
 // (2-byte units when the conv state is not a multiple of 16 bytes); chunk 0 of layer 0 also sets the new
 // sequence length. Layer z's tensors start z * (its stride) elements past the given pointers. accept_len
-// outside [1, T] leaves the user untouched.
+// outside [1, T], or an idle slot (base_lens[b] < 0), leaves the user untouched.
 constexpr int RB_UNITS = 4;  // 16-byte units per thread
 
 // Units i0, i0 + 256, i0 + 512, i0 + 768 of src to dst (those below n): every load first (clamped into
@@ -493,6 +525,7 @@ __global__ __launch_bounds__(256) void rollback_kernel(const float *states_out, 
     conv_state += z * c_stride;
     const int acc = accept[b];
     if (acc < 1 || acc > T) return;
+    if (base_lens && base_lens[b] < 0) return;  // an idle slot: nothing was verified, nothing to restore
     const size_t slot = (size_t)(acc - 1) * B + b;
     if ((int)blockIdx.x < state_chunks) {
         const float4 *src = reinterpret_cast<const float4 *>(states_out) + slot * state_f4;
@@ -645,12 +678,17 @@ __global__ void fill_zero_kernel(int *p, int n) {
 constexpr int MAX_DEVICES = 64;
 std::mutex g_scratch_mu;
 int *g_scratch_ptr[MAX_DEVICES] = {};
+bool g_scratch_cleared[MAX_DEVICES] = {};
 
-// The current device's copy of `scratch` (looked up and cleared on the first call on that device).
-int scratch_of_current_device(int **out, hipStream_t st) {
+// The current device's copy of `scratch`: its address is looked up on the first call on that device, and
+// it is cleared by a fill kernel on `st` (clear = true) until a clear has run outside a graph capture. A
+// clear enqueued while `st` is capturing becomes a node of the graph (it runs before the decode kernel on
+// every replay, which only re-zeroes counters that are zero between calls) and the next call outside a
+// capture clears again, so the array is zeroed before its first use whichever comes first.
+int scratch_of_current_device(int **out, hipStream_t st, bool clear, const char *who) {
     int dev = -1;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) {
-        qs::set_error("qs_gdn_decode_fused_noalloc: no usable current device (%d)", dev);
+        qs::set_error("%s: no usable current device (%d)", who, dev);
         return QS_EHIP;
     }
     std::lock_guard<std::mutex> lock(g_scratch_mu);
@@ -658,12 +696,20 @@ int scratch_of_current_device(int **out, hipStream_t st) {
         void *p = nullptr;
         const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess || !p) {
-            qs::set_error("qs_gdn_decode_fused_noalloc: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+            qs::set_error("%s: hipGetSymbolAddress failed: %s", who, hipGetErrorString(e));
             return QS_EHIP;
         }
-        fill_zero_kernel<<<SCRATCH_INTS / 256, 256, 0, st>>>(static_cast<int *>(p), SCRATCH_INTS);
-        if (int rc = qs::launch_status("qs_gdn_decode_fused_noalloc")) return rc;
         g_scratch_ptr[dev] = static_cast<int *>(p);
+    }
+    if (clear && !g_scratch_cleared[dev]) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cs) != hipSuccess) {
+            qs::set_error("%s: hipStreamIsCapturing failed", who);
+            return QS_EHIP;
+        }
+        fill_zero_kernel<<<SCRATCH_INTS / 256, 256, 0, st>>>(g_scratch_ptr[dev], SCRATCH_INTS);
+        if (int rc = qs::launch_status(who)) return rc;
+        if (cs == hipStreamCaptureStatusNone) g_scratch_cleared[dev] = true;
     }
     *out = g_scratch_ptr[dev];
     return QS_OK;
@@ -682,7 +728,7 @@ extern "C" int qs_gdn_decode_fused_noalloc(const uint16_t *x, uint16_t *conv_sta
                (long)B * NK, SCRATCH_INTS / 2);
     if (int e = check_conv_alignment(x, conv_state, conv_state, taps, y_out)) return e;
     int *counters = nullptr;
-    if (int e = scratch_of_current_device(&counters, QS_STREAM(stream))) return e;
+    if (int e = scratch_of_current_device(&counters, QS_STREAM(stream), true, "qs_gdn_decode_fused_noalloc")) return e;
     GdnArgs a{};
     a.x = x, a.conv_in = conv_state, a.conv_out = conv_state, a.taps = taps, a.y_out = y_out;
     a.g = g, a.beta = beta, a.s_in = state, a.s_out = state, a.o = o;
@@ -693,10 +739,24 @@ extern "C" int qs_gdn_decode_fused_noalloc(const uint16_t *x, uint16_t *conv_sta
     return qs::launch_status("qs_gdn_decode_fused_noalloc");
 }
 
+extern "C" int qs_gdn_noalloc_scratch_read(int *dst, int n, void *stream) {
+    QS_REQUIRE(dst, "qs_gdn_noalloc_scratch_read: null pointer");
+    QS_REQUIRE(n >= 1 && n <= SCRATCH_INTS, "qs_gdn_noalloc_scratch_read: n must be in [1, %d] (got %d)", SCRATCH_INTS,
+               n);
+    int *src = nullptr;
+    if (int e = scratch_of_current_device(&src, QS_STREAM(stream), false, "qs_gdn_noalloc_scratch_read")) return e;
+    const hipError_t e = hipMemcpyAsync(dst, src, (size_t)n * sizeof(int), hipMemcpyDeviceToDevice, QS_STREAM(stream));
+    if (e != hipSuccess) {
+        qs::set_error("qs_gdn_noalloc_scratch_read: hipMemcpyAsync failed: %s", hipGetErrorString(e));
+        return QS_EHIP;
+    }
+    return QS_OK;
+}
+
 extern "C" int qs_gdn_verify_step(const uint16_t *x, const uint16_t *conv_state_in, uint16_t *conv_states_out,
                                   const uint16_t *taps, const float *g, const float *beta, const float *state_in,
-                                  float *states_out, uint16_t *o, uint16_t *y_out, int B, int T, int NK, int NV,
-                                  int DKa, int DVa, int K, float scale, float eps, void *stream) {
+                                  float *states_out, uint16_t *o, uint16_t *y_out, const int *lens, int B, int T,
+                                  int NK, int NV, int DKa, int DVa, int K, float scale, float eps, void *stream) {
     QS_REQUIRE(x && conv_state_in && conv_states_out && taps && g && beta && state_in && states_out && o,
                "qs_gdn_verify_step: null pointer");
     if (int e = check_gdn_shapes(B, NK, NV, DKa, DVa)) return e;
@@ -707,6 +767,7 @@ extern "C" int qs_gdn_verify_step(const uint16_t *x, const uint16_t *conv_state_
     GdnArgs a{};
     a.x = x, a.conv_in = conv_state_in, a.conv_out = conv_states_out, a.taps = taps, a.y_out = y_out;
     a.g = g, a.beta = beta, a.s_in = state_in, a.s_out = states_out, a.o = o;
+    a.lens = lens;
     a.B = B, a.T = T, a.NK = NK, a.NV = NV, a.C = 2 * NK * DK + NV * DV, a.scale = scale, a.eps = eps;
     launch_gdn<true, true>(a, QS_STREAM(stream));
     return qs::launch_status("qs_gdn_verify_step");
@@ -715,8 +776,8 @@ extern "C" int qs_gdn_verify_step(const uint16_t *x, const uint16_t *conv_state_
 extern "C" int qs_gdn_verify_step_slots(const uint16_t *x, const uint16_t *conv_states_in, uint16_t *conv_states_out,
                                         const uint16_t *taps, const float *g, const float *beta,
                                         const float *states_in, float *states_out, const int *in_slot, int n_slots,
-                                        uint16_t *o, uint16_t *y_out, int B, int T, int NK, int NV, int DKa,
-                                        int DVa, int K, float scale, float eps, void *stream) {
+                                        uint16_t *o, uint16_t *y_out, const int *lens, int B, int T, int NK, int NV,
+                                        int DKa, int DVa, int K, float scale, float eps, void *stream) {
     QS_REQUIRE(x && conv_states_in && conv_states_out && taps && g && beta && states_in && states_out && in_slot && o,
                "qs_gdn_verify_step_slots: null pointer");
     if (int e = check_gdn_shapes(B, NK, NV, DKa, DVa)) return e;
@@ -730,6 +791,7 @@ extern "C" int qs_gdn_verify_step_slots(const uint16_t *x, const uint16_t *conv_
     a.x = x, a.conv_in = conv_states_in, a.conv_out = conv_states_out, a.taps = taps, a.y_out = y_out;
     a.g = g, a.beta = beta, a.s_in = states_in, a.s_out = states_out, a.o = o;
     a.in_slot = in_slot, a.n_slots = n_slots;
+    a.lens = lens;
     a.B = B, a.T = T, a.NK = NK, a.NV = NV, a.C = 2 * NK * DK + NV * DV, a.scale = scale, a.eps = eps;
     launch_gdn<true, true>(a, QS_STREAM(stream));
     return qs::launch_status("qs_gdn_verify_step_slots");
@@ -737,10 +799,13 @@ extern "C" int qs_gdn_verify_step_slots(const uint16_t *x, const uint16_t *conv_
 
 // Acceptance by slot selection: slot[b] <- accept[b] - 1 and seq_lens[b] <- base_lens[b] + accept[b] for
 // accept[b] in [1, T]; other users are left untouched and reported (QS_STATUS_ACCEPT) when status is given.
+// An idle slot (base_lens[b] < 0: the step's advance left its length negative) keeps its slot and length
+// whatever its accept length.
 __global__ void verify_accept_kernel(const int *accept, int *slot, int *seq_lens, const int *base_lens, int B, int T,
                                      int *status) {
     const int b = blockIdx.x * 64 + threadIdx.x;
     if (b >= B) return;
+    if (base_lens && base_lens[b] < 0) return;
     const int acc = accept[b];
     if (acc < 1 || acc > T) {
         if (status) atomicOr(status, QS_STATUS_ACCEPT);

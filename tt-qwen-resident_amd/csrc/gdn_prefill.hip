@@ -711,8 +711,15 @@ PrefillWs prefill_ws(int T, int NK, int NV) {
 
 }  // namespace
 
+// The chunk sizes a caller may name: the reference prefill's 32 (prefill/pp_prefill.py:56, :801) and this
+// kernel's 64. The chunked form equals the token-by-token recurrence for every chunk size (the intra-chunk
+// WY solve is exact algebra), so both run the 64-token decomposition; a 32-token one would differ from it
+// only in rounding.
+static bool chunk_ok(int chunk) { return chunk == CH || chunk == CH / 2; }
+
 extern "C" size_t qs_gdn_chunk_prefill_workspace_bytes(int T, int NK, int NV, int DKa, int DVa, int chunk) {
-    if (T <= 0 || NK <= 0 || NV <= 0 || NV % NK || NV / NK > MAXREP || DKa != DK || DVa != DV || chunk != CH) return 0;
+    if (T <= 0 || NK <= 0 || NV <= 0 || NV % NK || NV / NK > MAXREP || DKa != DK || DVa != DV || !chunk_ok(chunk))
+        return 0;
     return prefill_ws(T, NK, NV).total;
 }
 
@@ -727,7 +734,7 @@ extern "C" int qs_gdn_chunk_prefill(const uint16_t *q, const uint16_t *k, const 
     QS_REQUIRE(NK > 0 && NV > 0 && NV % NK == 0, "qs_gdn_chunk_prefill: NV (%d) must be a multiple of NK (%d)", NV, NK);
     QS_REQUIRE(NV / NK <= MAXREP, "qs_gdn_chunk_prefill: at most %d value heads per key head are built (got %d)", MAXREP,
                NV / NK);
-    QS_REQUIRE(chunk == CH, "qs_gdn_chunk_prefill: only chunk %d is built (got %d)", CH, chunk);
+    QS_REQUIRE(chunk_ok(chunk), "qs_gdn_chunk_prefill: chunk must be %d or %d (got %d)", CH / 2, CH, chunk);
     QS_REQUIRE((long)(T + CH) * NV * DV * 2 < (1L << 31) && (long)(T + CH) * NK * DK * 2 < (1L << 31),
                "qs_gdn_chunk_prefill: T = %d tokens exceed the 2 GB buffer range", T);
     const PrefillWs L = prefill_ws(T, NK, NV);

@@ -29,6 +29,6 @@ int launch_status(const char *what) {
 
 }  // namespace qs
 
-extern "C" int qs_abi_version(void) { return 3; }
+extern "C" int qs_abi_version(void) { return 4; }
 
 extern "C" const char *qs_last_error(void) { return g_err; }

@@ -20,14 +20,15 @@ SIGNATURES = {
     "qs_gdn_workspace_bytes": (_Z, [_I, _I]),
     "qs_gdn_decode_fused": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _F, _P]),
     "qs_gdn_decode_fused_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _F, _P]),
+    "qs_gdn_noalloc_scratch_read": (_I, [_P, _I, _P]),
     "qs_gdn_gated_norm": (_I, [_P, _P, _P, _P, _I, _I, _F, _P]),
     "qs_gdn_verify_step": (
         _I,
-        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _F, _P],
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _F, _P],
     ),
     "qs_gdn_verify_step_slots": (
         _I,
-        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _F, _P],
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _F, _P],
     ),
     "qs_verify_accept": (_I, [_P, _P, _P, _P, _I, _I, _P, _P]),
     "qs_gdn_rollback": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),

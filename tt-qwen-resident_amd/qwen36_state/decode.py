@@ -207,7 +207,9 @@ class VerifyStep:
 
     A step: lens advances by T (base <- the rows cached before the step); GDN layers keep all T intermediate
     states and conv histories; attention layers append T rows at base .. base + T - 1 and attend causally
-    among them; acceptance sets lens <- base + a and makes snapshot a - 1 the current state.
+    among them; acceptance sets lens <- base + a and makes snapshot a - 1 the current state. An idle slot
+    (lens < 0) is skipped by every launch: its length, its current state and conv history and the pools
+    stay as they are.
 
     rollback="slots" (default, the reference's scheme: slot select, no copy, README.md:413-421): two snapshot
     sets alternate; step k writes set k % 2 and reads each user's input from slot a - 1 of the other set.
@@ -292,11 +294,12 @@ class VerifyStep:
                 gi = d["gi"]
                 ops.gdn_verify_step_slots(d["x"], self.g_convs[1 - p, gi], d["taps"], d["g"], d["beta"],
                                           self.g_states[1 - p, gi], self.slot,
-                                          out=(d["o"], self.g_states[p, gi], self.g_convs[p, gi]))  # fmt: skip
+                                          out=(d["o"], self.g_states[p, gi], self.g_convs[p, gi]),
+                                          lens=self.lens)  # fmt: skip
             else:
                 gi = d["gi"]
                 ops.gdn_verify_step(d["x"], self.g_conv[gi], d["taps"], d["g"], d["beta"], self.g_state[gi],
-                                    out=(d["o"], self.g_states[0, gi], self.g_convs[0, gi]))  # fmt: skip
+                                    out=(d["o"], self.g_states[0, gi], self.g_convs[0, gi]), lens=self.lens)  # fmt: skip
 
     def rollback(self):
         """Accept: select the snapshot slots (slots mode) or restore every GDN layer from its snapshot in one

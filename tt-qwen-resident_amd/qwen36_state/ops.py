@@ -208,13 +208,16 @@ def gdn_gated_norm(o, z, norm_w, eps=EPS, out=None):
     return y
 
 
-def gdn_verify_step(x, conv_state, taps, g, beta, state, nk=NK, scale=None, eps=EPS, return_y=False, out=None):
+def gdn_verify_step(x, conv_state, taps, g, beta, state, nk=NK, scale=None, eps=EPS, return_y=False, out=None,
+                    lens=None):  # fmt: skip
     """T tokens per user through conv + delta rule, keeping every intermediate (the verify rows of the
     reference GDN head cores, kernels/gdn_head_reader.cpp:149-187, gdn_head_writer.cpp:60-66).
 
     x [B, T, C]; g, beta [B, T, NV]; conv_state [B, C, 3] and state [B, NV, DK, DV] are read only.
     Returns o [B, T, NV, DV] bf16, states [T, B, NV, DK, DV] fp32, conv_states [T, B, C, 3] bf16
-    (and the conv outputs y [B, T, C] with return_y). ``out`` = (o, states, conv_states) preallocated."""
+    (and the conv outputs y [B, T, C] with return_y). ``out`` = (o, states, conv_states) preallocated.
+    lens [B] int32 (optional, the step's lengths): a user with lens < 0 is an idle slot; nothing is computed
+    or written for it."""
     dev = state.device
     _chk(state, "state", torch.float32)
     B, nv, dk, dv = state.shape
@@ -236,16 +239,22 @@ def gdn_verify_step(x, conv_state, taps, g, beta, state, nk=NK, scale=None, eps=
         _chk(states, "out states", torch.float32, (T, B, nv, dk, dv), dev)
         _chk(convs, "out conv_states", torch.bfloat16, (T, B, C, CONV_K - 1), dev)
     y = torch.empty(B, T, C, dtype=torch.bfloat16, device=dev) if return_y else None
+    if lens is not None:
+        _chk(lens, "lens", torch.int32, (B,), dev)
     call("qs_gdn_verify_step", _p(x), _p(conv_state), _p(convs), _p(taps), _p(g), _p(beta), _p(state),
-         _p(states), _p(o), _p(y), B, T, nk, nv, dk, dv, CONV_K, float(scale), float(eps), _stream(dev))  # fmt: skip
+         _p(states), _p(o), _p(y), _p(lens), B, T, nk, nv, dk, dv, CONV_K, float(scale), float(eps),
+         _stream(dev))  # fmt: skip
     return (o, states, convs, y) if return_y else (o, states, convs)
 
 
-def gdn_verify_step_slots(x, conv_states_in, taps, g, beta, states_in, in_slot, out, nk=NK, scale=None, eps=EPS):
+def gdn_verify_step_slots(x, conv_states_in, taps, g, beta, states_in, in_slot, out, nk=NK, scale=None, eps=EPS,
+                          lens=None):  # fmt: skip
     """gdn_verify_step whose per-user input is a slot of the previous verify step's snapshots (the reference's
     slot select, kernels/gdn_head_reader.cpp:17-20): user b reads states_in[in_slot[b], b] and
     conv_states_in[in_slot[b], b]. states_in [S, B, NV, DK, DV], conv_states_in [S, B, C, 3], in_slot [B]
-    int32 on the device; out = (o, states, conv_states) must not alias the inputs."""
+    int32 on the device; out = (o, states, conv_states) must not alias the inputs. lens [B] int32 (optional,
+    the step's lengths): a user with lens < 0 is an idle slot, whose input slot is carried unchanged into
+    the same slot of ``out`` (no token verified, no o written)."""
     dev = states_in.device
     _chk(states_in, "states_in", torch.float32)
     S, B, nv, dk, dv = states_in.shape
@@ -262,8 +271,10 @@ def gdn_verify_step_slots(x, conv_states_in, taps, g, beta, states_in, in_slot, 
     _chk(states, "out states", torch.float32, (T, B, nv, dk, dv), dev)
     _chk(convs, "out conv_states", torch.bfloat16, (T, B, C, CONV_K - 1), dev)
     scale = dk**-0.5 if scale is None else scale
+    if lens is not None:
+        _chk(lens, "lens", torch.int32, (B,), dev)
     call("qs_gdn_verify_step_slots", _p(x), _p(conv_states_in), _p(convs), _p(taps), _p(g), _p(beta), _p(states_in),
-         _p(states), _p(in_slot), S, _p(o), None, B, T, nk, nv, dk, dv, CONV_K, float(scale), float(eps),
+         _p(states), _p(in_slot), S, _p(o), None, _p(lens), B, T, nk, nv, dk, dv, CONV_K, float(scale), float(eps),
          _stream(dev))  # fmt: skip
     return o, states, convs
 
@@ -271,7 +282,8 @@ def gdn_verify_step_slots(x, conv_states_in, taps, g, beta, states_in, in_slot, 
 def verify_accept(accept_len, T, slot, seq_lens=None, base_lens=None, status=None):
     """Acceptance by slot selection: slot <- accept_len - 1 (the snapshot the next verify step reads) and
     seq_lens <- base_lens + accept_len when given; no state moves (kernels/mlp_hub.cpp:48-58). An accept
-    length outside [1, T] leaves the user untouched and sets QS_STATUS_ACCEPT in ``status``."""
+    length outside [1, T] leaves the user untouched and sets QS_STATUS_ACCEPT in ``status``; an idle slot
+    (base_lens < 0) keeps its slot and length."""
     dev = slot.device
     B = slot.shape[0]
     _chk(accept_len, "accept_len", torch.int32, (B,), dev)
@@ -285,7 +297,8 @@ def verify_accept(accept_len, T, slot, seq_lens=None, base_lens=None, status=Non
 def gdn_rollback(states, conv_states, accept_len, state, conv_state, seq_lens=None, base_lens=None):
     """Restore state <- states[accept_len - 1], conv_state <- conv_states[accept_len - 1] per user (bit-exact),
     and seq_lens <- base_lens + accept_len when given (the KV truncation). accept_len [B] int32 on device,
-    each in [1, T] (the reference's slot/ring advance, kernels/mlp_hub.cpp:48-58)."""
+    each in [1, T] (the reference's slot/ring advance, kernels/mlp_hub.cpp:48-58); an idle slot (base_lens
+    < 0) is left untouched."""
     dev = state.device
     T, B, nv, dk, dv = states.shape
     C = conv_states.shape[2]
@@ -478,14 +491,42 @@ def causal_conv1d_prefill(x, taps, conv_state=None, conv_state_out=None, nk=NK, 
 
 
 def chunk_gated_delta_rule(q, k, v, g, beta, *, scale=None, initial_state=None, output_final_state=True,
-                           chunk_size=64, output_head_major=False, eps=EPS, ws=None, final_state=None):  # fmt: skip
-    """``chunk_gated_delta_rule(q, k, v, g, beta, scale, initial_state, output_final_state, chunk_size,
-    output_head_major)`` as the reference prefill calls it (prefill/pp_prefill.py:791-807): q, k [T, NK*DK]
-    or [T, NK, DK] bf16 token-major (L2-normalised inside, q times scale), v [T, NV*DV] or [T, NV, DV] bf16,
-    g, beta [T, NV] fp32, initial_state [NV, DK, DV] fp32. Returns (o, final_state): o [T, NV, DV] bf16
-    ([NV, T, DV] with output_head_major), final_state [NV, DK, DV] fp32 (None unless output_final_state).
-    final_state, when given, is written in place (it may be initial_state, or one user's slot of the decode
-    state [B, NV, DK, DV], which hands the prompt's state to the decode without a copy)."""
+                           chunk_size=64, output_head_major=False, memory_config=None, eye=None, tril=None,
+                           ones=None, masks=None, eps=EPS, ws=None, final_state=None):  # fmt: skip
+    """``chunk_gated_delta_rule(q, k, v, g, beta, *, scale, initial_state, output_final_state, chunk_size,
+    output_head_major, memory_config, eye, tril, ones, masks)`` exactly as the reference prefill calls it
+    (prefill/pp_prefill.py:791-807).
+
+    q, k [T, NK*DK] or [T, NK, DK] bf16 token-major (L2-normalised inside, q times scale), v [T, NV*DV] or
+    [T, NV, DV] bf16, g, beta [T, NV] fp32, initial_state [NV, DK, DV] fp32. The reference's per-device
+    tensors carry a leading batch dimension of 1 (q [1, T, NK*DK], g [1, T, NV], initial_state
+    [1, NV, DK, DV]); that form is accepted too and keeps the dimension on the outputs.
+    Returns (o, final_state): o [T, NV, DV] bf16 ([NV, T, DV] with output_head_major), final_state
+    [NV, DK, DV] fp32 (None unless output_final_state). final_state, when given, is written in place (it may
+    be initial_state, or one user's slot of the decode state [B, NV, DK, DV], which hands the prompt's state
+    to the decode without a copy).
+
+    chunk_size: 32 (the reference's) or 64. The chunked form equals the recurrence for any chunk size, so
+    both run the kernels' 64-token chunks. memory_config, eye, tril, ones and masks are the ttnn
+    implementation's memory placement and its precomputed constant tiles; the HIP kernels need none of
+    them, so they are accepted and ignored."""
+    del memory_config, eye, tril, ones, masks
+    if chunk_size not in (32, 64):
+        raise ValueError(f"chunk_size must be 32 or 64 (got {chunk_size})")
+    batched = isinstance(g, torch.Tensor) and g.dim() == 3
+    if batched:
+        if g.shape[0] != 1:
+            raise ValueError(f"one sequence per call: the leading batch dimension must be 1 (g {tuple(g.shape)})")
+        for name, t in (("q", q), ("k", k), ("v", v), ("beta", beta)):
+            if not isinstance(t, torch.Tensor) or t.dim() < 2 or t.shape[0] != 1:
+                raise ValueError(f"{name} must carry the leading batch dimension 1 like g")
+        q, k, v, g, beta = q[0], k[0], v[0], g[0], beta[0]
+        if initial_state is not None:
+            if initial_state.dim() != 4 or initial_state.shape[0] != 1:
+                raise ValueError("initial_state must be [1, NV, DK, DV] in the batched form")
+            initial_state = initial_state[0]
+        if final_state is not None:
+            final_state = final_state[0] if final_state.dim() == 4 else final_state
     dev = q.device
     T = q.shape[0]
     nv = g.shape[1]
@@ -504,13 +545,16 @@ def chunk_gated_delta_rule(q, k, v, g, beta, *, scale=None, initial_state=None, 
     S = torch.empty(nv, DK, DV, dtype=torch.float32, device=dev) if final_state is None else final_state
     _chk(S, "final_state", torch.float32, (nv, DK, DV), dev)
     if ws is None:
-        nbytes = lib().qs_gdn_chunk_prefill_workspace_bytes(T, nk, nv, DK, DV, chunk_size)
-        ws = workspace(("prefill", chunk_size), nbytes, dev)
+        nbytes = lib().qs_gdn_chunk_prefill_workspace_bytes(T, nk, nv, DK, DV, int(chunk_size))
+        ws = workspace("prefill", nbytes, dev)
     call("qs_gdn_chunk_prefill", _p(q), _p(k), _p(v), _p(g), _p(beta), _p(initial_state), _p(o), _p(S), _p(ws),
          T, nk, nv, DK, DV, int(chunk_size), float(scale), float(eps), _stream(dev))  # fmt: skip
     if output_head_major:
         o = o.transpose(0, 1).contiguous()
-    return o, (S if output_final_state else None)
+    S = S if output_final_state else None
+    if batched:
+        return o[None], (S[None] if S is not None else None)
+    return o, S
 
 
 # ------------------------------------------------------------------------------ the attention mixer's edges

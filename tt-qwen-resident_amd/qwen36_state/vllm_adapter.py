@@ -12,9 +12,15 @@ the block-table contract instead:
   path: the prompt conv with its carry (the carry lands in the user's decode conv slot), the chunked gated delta
   rule (its final state lands in the user's decode state slot) and the paged fill of the prompt's K / V through
   the user's page table;
-- ``decode_forward(inputs, start_pos, page_table)`` runs one decode step of every active slot over the block
-  table: positions advance on the device, K / V rows are appended at ``start_pos`` and attended through the
-  pages; a slot with ``start_pos < 0`` is idle and left untouched.
+- ``decode_forward(inputs, start_pos, page_table, reload_inputs, reload_page_table, read_from_device)`` runs
+  one decode step of every active slot over the block table: positions advance on the device, K / V rows are
+  appended at ``start_pos`` and attended through the pages; a slot with ``start_pos < 0`` is idle and left
+  untouched. Like the reference's (generator_vllm.py:117-160, ``execute_trace(blocking=False)`` at
+  model.py:1505) the call is asynchronous: it enqueues the step and returns its device output buffers
+  without waiting; the device status word of each step is read back one step late (or at once with
+  ``read_from_device=True``). With ``reload_inputs=False`` nothing is copied from the host: the caller has
+  written the step's inputs into ``step_inputs()`` (its projections can write there directly) and the
+  positions are the ones the previous step advanced to on the device.
 
 The embedding, the projections, the MLP, the lm_head and sampling are outside the state path, so the calls take
 the layers' projection outputs in place of token ids and return the layers' mixer outputs:
@@ -41,7 +47,7 @@ class StatePathAdapter:
 
     model_capabilities = {
         "supports_prefix_caching": False,
-        "supports_async_decode": False,
+        "supports_async_decode": True,
         "supports_sample_on_device": False,
     }
 
@@ -55,7 +61,9 @@ class StatePathAdapter:
         self.max_blocks = (self.max_seq_len + BLOCK - 1) // BLOCK
         self.pps = pages_per_split
         dev, B, ng = self.device, self.B, len(self.gdn)
-        self.block_table = torch.zeros(B, self.max_blocks, dtype=torch.int32, device=dev)
+        # unused entries are -1 (outside every pool): a position whose page the caller did not map is then
+        # neither written nor attended, and the kernels report it (QS_STATUS_PAGE) instead of using page 0
+        self.block_table = torch.full((B, self.max_blocks), -1, dtype=torch.int32, device=dev)
         self.lens = torch.full((B,), -1, dtype=torch.int32, device=dev)  # rows cached per slot; -1 = idle
         self.gdn_state = torch.zeros(ng, B, NV, DK, DV, dtype=torch.float32, device=dev)
         self.conv_state = torch.zeros(ng, B, C_QKV, CONV_K - 1, dtype=torch.bfloat16, device=dev)
@@ -68,6 +76,16 @@ class StatePathAdapter:
         self.status = ops.Status(dev)
         self.kv = None
         self.step = None
+        # host staging for asynchronous steps: pinned rings for the positions and the block table (a slot is
+        # rewritten only after the copy that read it has run) and for the status word read back per step
+        self._ring = 4
+        self._pos_host = [torch.empty(B, dtype=torch.int32).pin_memory() for _ in range(self._ring)]
+        self._tab_host = [torch.empty(B, self.max_blocks, dtype=torch.int32).pin_memory() for _ in range(self._ring)]
+        self._st_host = [torch.zeros(1, dtype=torch.int32).pin_memory() for _ in range(self._ring)]
+        self._in_ev = [None] * self._ring
+        self._st_ev = [None] * self._ring
+        self._n = 0  # steps enqueued
+        self._pending = []  # (step number, ring slot) of status words not checked yet
 
     # --------------------------------------------------------------------------------------------- vLLM calls
 
@@ -122,39 +140,119 @@ class StatePathAdapter:
             o, _ = ops.chunk_gated_delta_rule(q, k, v, x["g"][:T].contiguous(), x["beta"][:T].contiguous(),
                                               final_state=self.gdn_state[gi, slot])  # fmt: skip
             outs.append(o)
-        self.block_table[slot].zero_()
+        self.block_table[slot].fill_(-1)
         self.block_table[slot, :n] = row
         self.lens[slot] = T
         return outs
 
-    def decode_forward(self, inputs, start_pos, page_table=None, reload_page_table=True, read_from_device=True):
-        """One decode step of every slot: start_pos [B] (host, the position of each slot's new token = its
-        cached rows; negative = idle slot); page_table [B, n] int32 (n <= max_blocks) when the blocks moved;
+    def decode_forward(self, inputs, start_pos, page_table=None, *args, reload_inputs=True, reload_page_table=False,
+                       read_from_device=False, **kwargs):  # fmt: skip
+        """One decode step of every slot, enqueued without waiting (generator_vllm.py:117-160).
+
         inputs: one dict per layer, GDN {x [B, C], g, beta [B, NV]}, attention {q [B, 1, NQ, HD], k_new, v_new
-        [B, 1, NKV, HD]}. Returns the layers' outputs (the step's buffers: GDN o [B, NV, DV], attention
-        o [B, 1, NQ, HD]); raises ValueError when a position passes max_seq_len (generator_vllm.py:94) or
-        the device reported an invalid length or block-table entry."""
+        [B, 1, NKV, HD]}, copied into the step's buffers on the device (a tensor that already is the step's
+        buffer is not copied; inputs=None copies nothing); start_pos [B] (host or device int32: each slot's
+        new-token position = its cached rows; negative = idle slot). With reload_inputs=False neither is
+        reloaded: the caller wrote the inputs into ``step_inputs()`` and the positions are where the previous
+        step left them on the device. page_table [B, n] int32 (n <= max_blocks) is loaded when
+        reload_page_table is set (entries past n become -1). Returns the step's output buffers (GDN o
+        [B, NV, DV], attention o [B, 1, NQ, HD]), valid once the stream reaches the end of the step; they
+        are rewritten by the next step.
+
+        Errors: a host-side start_pos past max_seq_len raises ValueError at once (generator_vllm.py:94). The
+        kernels' status word (a length past the table, a block-table entry outside the pool) is copied to the
+        host after every step and checked at the next call, or at once with read_from_device=True (which
+        waits for the step); a reported condition raises ValueError naming the step."""
         if self.step is None:
             raise ValueError("allocate_kv_cache must run before decode_forward")
-        pos = torch.as_tensor(start_pos).reshape(-1).to(torch.int32)
-        if pos.shape[0] != self.B:
-            raise ValueError(f"start_pos must hold one position per slot ({self.B})")
-        if int(pos.max()) >= self.max_seq_len:
-            raise ValueError(f"position {int(pos.max())} is past max_seq_len {self.max_seq_len}")
+        # every argument is checked before anything is enqueued
+        pos = pt = None
+        if reload_inputs:
+            pos = torch.as_tensor(start_pos).reshape(-1)
+            if pos.shape[0] != self.B:
+                raise ValueError(f"start_pos must hold one position per slot ({self.B})")
+            if not pos.is_cuda:
+                pos = pos.to(torch.int32)
+                if int(pos.max()) >= self.max_seq_len:
+                    raise ValueError(f"position {int(pos.max())} is past max_seq_len {self.max_seq_len}")
+            if inputs is not None and len(inputs) != self.layers:
+                raise ValueError(f"inputs: one dict per layer ({self.layers}), got {len(inputs)}")
         if page_table is not None and reload_page_table:
             pt = torch.as_tensor(page_table)
             if pt.dim() != 2 or pt.shape[0] != self.B or pt.shape[1] > self.max_blocks:
                 raise ValueError(f"page_table must be [{self.B}, <= {self.max_blocks}]")
-            self.block_table.zero_()
-            self.block_table[:, : pt.shape[1]] = pt.to(device=self.device, dtype=torch.int32)
-        self.lens.copy_(pos)
-        for d, x in zip(self.step.layer, inputs):
-            for key in (("q", "k_new", "v_new") if d["attn"] else ("x", "g", "beta")):
-                d[key].copy_(x[key])
+        self._check_status(wait=False)
+        r = self._n % self._ring
+        if self._in_ev[r] is not None:
+            self._in_ev[r].synchronize()  # the copies that read this ring slot four steps ago have run
+        if pos is not None:
+            if pos.is_cuda:
+                self.lens.copy_(pos.to(torch.int32), non_blocking=True)
+            else:
+                self._pos_host[r].copy_(pos)
+                self.lens.copy_(self._pos_host[r], non_blocking=True)
+        if pt is not None:
+            n = pt.shape[1]
+            if pt.is_cuda:
+                self.block_table[:, n:].fill_(-1)
+                self.block_table[:, :n].copy_(pt.to(torch.int32), non_blocking=True)
+            else:
+                h = self._tab_host[r]
+                h.fill_(-1)
+                h[:, :n] = pt.to(torch.int32)
+                self.block_table.copy_(h, non_blocking=True)
+        if reload_inputs and inputs is not None:
+            for d, x in zip(self.step.layer, inputs):
+                for key in (("q", "k_new", "v_new") if d["attn"] else ("x", "g", "beta")):
+                    if x[key] is not d[key]:
+                        d[key].copy_(x[key], non_blocking=True)
+        stream = torch.cuda.current_stream(self.device)
+        ev = torch.cuda.Event()
+        ev.record(stream)
+        self._in_ev[r] = ev
         self.step.replay()
+        # the step's status word to the host (read one step late), then cleared for the next step
+        if self._st_ev[r] is not None:
+            self._st_ev[r].synchronize()
+        self._st_host[r].copy_(self.status.word, non_blocking=True)
+        self.status.word.zero_()
+        sev = torch.cuda.Event()
+        sev.record(stream)
+        self._st_ev[r] = sev
+        self._pending.append((self._n, r))
+        self._n += 1
         if read_from_device:
-            self.status.check()
+            self._check_status(wait=True)
         return [d["o"] for d in self.step.layer]
+
+    def step_inputs(self):
+        """The step's own input buffers, one dict per layer (GDN {x, g, beta}, attention {q, k_new, v_new}):
+        a caller that writes its projections here calls decode_forward(None, ..., reload_inputs=False) or
+        passes these same tensors, and no copy is made."""
+        return [{k: d[k] for k in (("q", "k_new", "v_new") if d["attn"] else ("x", "g", "beta"))}
+                for d in self.step.layer]  # fmt: skip
+
+    def read_decode_output(self, outs=None):
+        """Wait for the enqueued steps and check their status words (raises ValueError on a reported
+        condition); returns ``outs`` (the buffers decode_forward returned)."""
+        self._check_status(wait=True)
+        return outs
+
+    def _check_status(self, wait):
+        """Check the status words of finished steps, oldest first: every enqueued step with wait=True, else the
+        finished ones, and always the oldest while a full ring is pending (its host slot is needed next)."""
+        while self._pending:
+            n, r = self._pending[0]
+            if wait or len(self._pending) >= self._ring:
+                self._st_ev[r].synchronize()
+            elif not self._st_ev[r].query():
+                return
+            self._pending.pop(0)
+            v = int(self._st_host[r][0])
+            if v:
+                self._pending.clear()
+                text = "; ".join(t for bit, t in ops._STATUS_TEXT.items() if v & bit)
+                raise ValueError(f"decode step {n}: {text} (status {v:#x})")
 
     # --------------------------------------------------------------------------------------------- internals
 
