@@ -16,7 +16,7 @@ random block tables), replayed as one HIP graph that also advances every user's 
   verify-step   MTP verify at batch 1, 8192 positions, 4 tokens, 64 layers + acceptance by slot
   prefill       chunked gated delta rule over 8192 tokens + the paged K/V fill (two prompts rotate)
   conv-prefill  the prompt conv with its carry over 8192 tokens (the prefill -> decode handoff)
-  mlp-layer     the MLP half of one layer at one row, weights streamed as MXFP4 (gate | up) and MXFP8 (down)
+  mlp-layer     the MLP half of one layer at one row, weights streamed as MXFP4 (gate | up) and MXINT8 (down)
 Inputs are seeded synthetic tensors resident in HBM before the timed region.
 
 Timing: K timed replays (``--steps``) bracketed by synchronisation, each replay between its own pair of HIP
@@ -609,12 +609,12 @@ def bench_conv_prefill(args, torch, tel):
 
 
 def mlp_bytes(B, H, I):
-    """Algorithmic HBM bytes of one MLP half: the packed gate | up (MXFP4) and down (MXFP8) weights, x in,
-    gamma, x_out."""
+    """Algorithmic HBM bytes of one MLP half: the packed gate | up (MXFP4) and down (MXINT8: the same bytes as
+    MXFP8) weights, x in, gamma, x_out."""
     from qwen36_state._lib import lib
 
     L = lib()
-    return 2 * L.qs_mx_packed_bytes(H, I, 4) + L.qs_mx_packed_bytes(I, H, 8) + 2 * B * H * 4 + H * 4
+    return 2 * L.qs_mx_packed_bytes(H, I, 4) + L.qs_mx_packed_bytes(I, H, 9) + 2 * B * H * 4 + H * 4
 
 
 def bench_mlp_layer(args, torch, tel):
@@ -632,8 +632,8 @@ def bench_mlp_layer(args, torch, tel):
 
     def calls(st):
         return [("qs_mlp_decode", (_p(d["x"]), _p(d["gamma"]), _p(d["gate"].packed), _p(d["up"].packed),
-                                   _p(d["down"].packed), _p(d["out"]), _p(ws), B, H, I, ctypes.c_float(ops.EPS),
-                                   st)) for d in layers] * R  # fmt: skip
+                                   _p(d["down"].packed), d["down"].fmt, _p(d["out"]), _p(ws), B, H, I,
+                                   ctypes.c_float(ops.EPS), st)) for d in layers] * R  # fmt: skip
 
     g = capture_calls(torch, calls)
     msr, stats = timed(torch, args, g.replay, tel=tel, settle_ms=SETTLE_MS)
@@ -642,7 +642,7 @@ def bench_mlp_layer(args, torch, tel):
     stats = {k: (v / n if k.endswith("_ms") else v) for k, v in stats.items()}
     nbytes = mlp_bytes(B, H, I)
     out = entry("MLP half of one decoder layer, 1 row: rmsnorm + gate | up 5120 x 17408 MXFP4 with silu, down "
-                "17408 x 5120 MXFP8 in 4 K splits + residual (2 launches)", nbytes, ms, stats,
+                "17408 x 5120 MXINT8 in 4 K splits + residual (2 launches)", nbytes, ms, stats,
                 roofline("mlp_decode", nbytes, ms))  # fmt: skip
     out["us_per_layer"] = out["us_per_step"]
     if not args.no_cpu:

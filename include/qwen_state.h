@@ -276,13 +276,16 @@ int qs_conv1d_prefill(const uint16_t *x, int ldx, const uint16_t *conv_state_in,
 
 /* ------------------------------------------------------------------- f4: weight-streaming projections + MLP
  * Weights in OCP microscaling formats, 32 values along K per E8M0 scale: MXFP4 (fmt 4, E2M1 values; the
- * reference streams gate | up in 4-bit block floating point) and MXFP8 (fmt 8, E4M3 values; down in 8-bit
- * block floating point). A weight W [K, N] (y = h W) is quantized and laid out once, on the device, by
+ * reference streams gate | up in 4-bit block floating point), MXINT8 (fmt 9, two's-complement int8 values
+ * times 2^-6: a sign and 7 magnitude bits under the shared scale, the precision of the reference's 8-bit
+ * block floating point bfloat8_b for down and the 8-bit projections, model.py:53-58) and MXFP8 (fmt 8, E4M3
+ * values, 3 mantissa bits). A weight W [K, N] (y = h W) is quantized and laid out once, on the device, by
  * qs_mx_quantize into qs_mx_packed_bytes(K, N, fmt) bytes of MFMA fragment order (per 16-column tile and
- * K group of 128 (fmt 4) or 64 (fmt 8) values: 1024 value bytes, lane 16 g + r holding column r's values
+ * K group of 128 (fmt 4) or 64 (fmt 8, 9) values: 1024 value bytes, lane 16 g + r holding column r's values
  * KG q + 32 s + 8 g .. + 7 of every 32-value step s, then column r's step scales). Scale of a block:
- * 2^(floor(log2 amax) - emax), emax 2 (E2M1) or 8 (E4M3), exponent clamped to [-126, 127]; values round to
- * the nearest code, ties to even, saturating at 6 / 448. N % 16 == 0; K % 128 (fmt 4) or % 64 (fmt 8) == 0.
+ * 2^(floor(log2 amax) - emax), emax 2 (E2M1), 8 (E4M3) or 0 (INT8), exponent clamped to [-126, 127]; values
+ * round to the nearest code, ties to even, saturating at 6 / 448 / +-127. N % 16 == 0; K % 128 (fmt 4) or
+ * % 64 (fmt 8, 9) == 0.
  * Replaces the reference's host-side weight quantization and bank layout (common.py:115-116 `quantize`;
  * tests/bench_resident_mlp.py:51-80 `interleaved_bank_layout`). */
 size_t qs_mx_packed_bytes(int K, int N, int fmt);
@@ -299,7 +302,8 @@ int qs_mx_gemv(const uint16_t *h, const uint8_t *w, float *y, void *workspace, i
                void *stream);
 
 /* The MLP half of a decoder layer for 1 <= B <= 16 rows: h = bf16(x rsqrt(mean(x^2) + eps) gamma) per row,
- * z = bf16(silu(h G) (h U)), x_out = x + z D; gate, up packed MXFP4 [H, I], down packed MXFP8 [I, H];
+ * z = bf16(silu(h G) (h U)), x_out = x + z D; gate, up packed MXFP4 [H, I], down packed [I, H] in down_fmt
+ * (9: MXINT8, the reference's 8-bit precision; 8: MXFP8);
  * x, x_out [B, H] fp32 (may alias), gamma [H] fp32 or null when the norm weight is already folded into the
  * rows of gate and up (the reference's weights.py:107-112 does so); H % 128 == 0, I % 64 == 0. Two launches for one row
  * with H <= 5120 (the gate | up workgroups normalise the row themselves), three otherwise. The workspace
@@ -308,7 +312,7 @@ int qs_mx_gemv(const uint16_t *h, const uint8_t *w, float *y, void *workspace, i
  * mlp_hub.cpp:309-364 all-reduce on one device; torch pattern tests/bench_resident_mlp.py:98-105). */
 size_t qs_mlp_decode_workspace_bytes(int B, int H, int I);
 int qs_mlp_decode(const float *x, const float *gamma, const uint8_t *gate, const uint8_t *up, const uint8_t *down,
-                  float *x_out, void *workspace, int B, int H, int I, float eps, void *stream);
+                  int down_fmt, float *x_out, void *workspace, int B, int H, int I, float eps, void *stream);
 
 #ifdef __cplusplus
 }

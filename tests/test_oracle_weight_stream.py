@@ -3,6 +3,8 @@ E2M1 / E4M3 encodings (OCP Microscaling Formats v1.0, tables 5.2-5.3) and for bl
 ties to even, saturation, zero blocks), a hand-indexed layout case, and the MLP half's closed forms."""
 import math
 
+import numpy as np
+
 import torch
 
 from oracle import weight_stream as WS
@@ -57,14 +59,57 @@ def test_mxfp8_quantize_golden():
     assert e.tolist() == [[112]] and WS.e4m3_decode(codes[:1, 0]).item() == 320.0
 
 
+def test_int8_decode_closed_form():
+    # two's complement times 2^-6 (OCP MX v1.0 section 5.3): 0x7f = 127/64, 0x80 = -2, 0xff = -1/64
+    got = WS.int8_decode(torch.tensor([0x00, 0x01, 0x40, 0x7F, 0x80, 0x81, 0xC0, 0xFF]))
+    assert got.tolist() == [0.0, 1 / 64, 1.0, 127 / 64, -2.0, -127 / 64, -1.0, -1 / 64]
+
+
+def test_mxint8_quantize_golden():
+    # amax 1.984375 = 127/64 -> floor(log2) = 0, emax 0 -> e = 127, scale 1: code = round(64 v), ties to even,
+    # saturating at +-127 (1.999 -> 127.94 -> 127), negative values as two's complement
+    vals = [1.984375, 1.0, 0.5, -1.0, 1.999, -1.999, 2.0**-7, 3 * 2.0**-7, -3 * 2.0**-7, 0.3, 0.0]
+    codes, e = WS.mx_quantize(_block(vals), 9)
+    assert e.tolist() == [[127]]
+    assert codes[: len(vals), 0].tolist() == [127, 64, 32, 192, 127, 129, 0, 2, 254, 19, 0]
+    # amax 2 -> floor(log2) = 1 -> e = 128: codes are round(32 v); 3 -> 96
+    codes, e = WS.mx_quantize(_block([2.0, 3.0, -0.046875]), 9)
+    assert e.tolist() == [[128]] and codes[:3, 0].tolist() == [64, 96, 254]
+    # a small block: amax 0.01 -> floor(log2 0.01) = -7 -> e = 120; 0.01 2^13 = 81.92 -> 82
+    codes, e = WS.mx_quantize(_block([0.01, -0.005]), 9)
+    assert e.tolist() == [[120]] and codes[:2, 0].tolist() == [82, 215]
+    assert WS.mx_dequantize(codes, e, 9)[:2, 0].tolist() == [82 * 2.0**-13, -41 * 2.0**-13]
+    codes, e = WS.mx_quantize(torch.zeros(32, 1), 9)
+    assert e.tolist() == [[127]] and codes.sum().item() == 0
+
+
+def test_mxint8_keeps_seven_magnitude_bits():
+    """Per block, MXINT8's error is at most half a step of 2^(floor(log2 amax) - 6), one step where the value
+    saturates at 127: over random normal blocks its worst relative error on the largest values is ~2^-7,
+    against ~2^-4 for E4M3 (three mantissa bits)."""
+    g = torch.Generator().manual_seed(4)
+    w = torch.randn(4096, 8, generator=g, dtype=torch.float64) * 0.02
+    for fmt in (8, 9):
+        codes, e = WS.mx_quantize(w, fmt)
+        err = (WS.mx_dequantize(codes, e, fmt) - w).abs()
+        step = torch.pow(2.0, e.double() - 127 - (6 if fmt == 9 else 0)).repeat_interleave(32, 0)
+        if fmt == 9:
+            sat = WS.int8_decode(codes).abs() == 127 / 64
+            assert torch.all(err[~sat] <= 0.5 * step[~sat] + 1e-18) and torch.all(err <= step + 1e-18)
+        big = w.abs() > 0.5 * w.abs().reshape(-1, 32, 8).amax(1).repeat_interleave(32, 0)
+        rel = (err[big] / w.abs()[big]).max().item()
+        assert (rel < 2.0**-6) if fmt == 9 else (2.0**-6 < rel < 2.0**-3), (fmt, rel)
+
+
 def test_quantize_is_nearest_representable():
     g = torch.Generator().manual_seed(0)
     w = torch.randn(256, 8, generator=g, dtype=torch.float64) * 0.03
-    for fmt, top in ((4, 6.0), (8, 448.0)):
+    for fmt, top in ((4, 6.0), (8, 448.0), (9, 127 / 64)):
         codes, e = WS.mx_quantize(w, fmt)
         deq = WS.mx_dequantize(codes, e, fmt)
         scale = torch.pow(2.0, e.double() - 127).repeat_interleave(32, 0)
-        mags = torch.tensor(WS.E2M1, dtype=torch.float64) if fmt == 4 else WS.e4m3_decode(torch.arange(0x7F))
+        mags = {4: torch.tensor(WS.E2M1, dtype=torch.float64), 8: WS.e4m3_decode(torch.arange(0x7F)),
+                9: torch.arange(128, dtype=torch.float64) / 64}[fmt]  # fmt: skip
         y = (w / scale).abs()
         best = (y.reshape(-1, 1) - mags[None, :]).abs().min(1).values.reshape(w.shape)
         assert torch.all((deq / scale).abs() - y <= best + 1e-12)
@@ -92,6 +137,8 @@ def test_pack_layout_by_hand():
         assert p8[blk + 1024 + 2 * r + s] == scales[(64 * q + 32 * s) // 32, 16 * t + r]
     c8, s8 = WS.mx_unpack(p8, K, N, 8)
     assert torch.equal(c8, codes8) and torch.equal(s8, scales)
+    # MXINT8 shares the 8-bit layout byte for byte
+    assert np.array_equal(WS.mx_pack(codes8, scales, 9), p8)
 
 
 def _mlp_weights(H, I, seed=1):

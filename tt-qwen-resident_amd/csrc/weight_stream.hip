@@ -3,18 +3,23 @@
 //
 // Weights are OCP microscaling blocks: 32 consecutive values along K share one E8M0 scale 2^(e - 127);
 // MXFP4 stores E2M1 values (gate and up projections; the reference streams these in 4-bit block floating
-// point), MXFP8 stores E4M3 values (down projection; 8-bit block floating point in the reference). A weight
+// point); MXINT8 stores two's-complement int8 values times 2^-6, a sign and 7 magnitude bits under the shared
+// scale, the precision of the reference's 8-bit block floating point (down projection and the 8-bit
+// projections: bfloat8_b, sign + 7-bit mantissa per value, model.py:53-58); MXFP8 stores E4M3 values (3
+// mantissa bits, kept as an option). A weight
 // W [K, N] (y = h W) is laid out once, by qs_mx_quantize, in MFMA fragment order: for each 16-column tile t
-// and K group q (128 values of K for MXFP4, 64 for MXFP8) one block of 1024 value bytes and the group's
-// scales, lane l = 16 g + r (r the column in the tile) owning 16 bytes: the values of K steps
+// and K group q (128 values of K for MXFP4, 64 for the 8-bit formats) one block of 1024 value bytes and the
+// group's scales, lane l = 16 g + r (r the column in the tile) owning 16 bytes: the values of K steps
 // KG q + 32 s + 8 g .. + 7 for each 32-value step s of the group (4 steps of 4 bytes for MXFP4, low nibble
-// first; 2 steps of 8 bytes for MXFP8), then column r's scales (one per step) at 1024 + SCALES r. A wave
-// loads its part of a block as one contiguous kilobyte plus a 4- or 2-byte scale word, converts it to bf16
-// with the hardware's scaled conversions (v_cvt_scalef32_pk_bf16_fp4 / _fp8: exact, the scale folded in)
-// and multiplies on v_mfma_f32_16x16x32_bf16 with the activations (bf16, up to 16 rows) as the A operand.
+// first; 2 steps of 8 bytes for MXFP8 / MXINT8), then column r's scales (one per step) at 1024 + SCALES r. A
+// wave loads its part of a block as one contiguous kilobyte plus a 4- or 2-byte scale word and converts it to
+// bf16 exactly, the scale folded in: with the hardware's scaled conversions (v_cvt_scalef32_pk_bf16_fp4 /
+// _fp8) or, for MXINT8, on the VALU (the int8 read as an unsigned byte after flipping its sign bit, then one
+// fused multiply-add with the scale; 7-bit magnitudes times a power of two are exact in bf16). It multiplies
+// on v_mfma_f32_16x16x32_bf16 with the activations (bf16, up to 16 rows) as the A operand.
 // The kernels stream weights at the HBM rate; the conversions and MFMAs hide under the loads.
 //
-// MLP half (qs_mlp_decode): h = bf16(x rsqrt(mean(x^2) + eps) gamma); z = bf16(silu(h G) (h U)) in one
+// MLP half (qs_mlp_decode; down in MXINT8 or MXFP8): h = bf16(x rsqrt(mean(x^2) + eps) gamma); z = bf16(silu(h G) (h U)) in one
 // launch (gate and up tiles in the same workgroup; for one row the workgroups also form h themselves); the
 // down projection split over K (four ways for one row), its last split per tile adding the partials and the
 // residual: x_out = x + z D. Two launches per layer for one row.
@@ -27,7 +32,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int FMT_FP4 = 4, FMT_FP8 = 8;
+constexpr int FMT_FP4 = 4, FMT_FP8 = 8, FMT_INT8 = 9;
 constexpr int TILE_N = 16;
 constexpr int MAX_ROWS = 16;  // activation rows per call: the MFMA's M
 constexpr int DOWN_SPLIT = 4;
@@ -46,10 +51,13 @@ struct Mx<FMT_FP8> {
     static constexpr int STEPS = 2;
     static constexpr int BYTES = 1056;
 };
+template <>
+struct Mx<FMT_INT8> : Mx<FMT_FP8> {};  // the same 8-bit layout
 
+__host__ __device__ inline bool fmt_ok(int fmt) { return fmt == FMT_FP4 || fmt == FMT_FP8 || fmt == FMT_INT8; }
+__host__ __device__ inline int kg_of(int fmt) { return fmt == FMT_FP4 ? Mx<FMT_FP4>::KG : Mx<FMT_FP8>::KG; }
 __host__ __device__ inline size_t mx_bytes(int K, int N, int fmt) {
-    return fmt == FMT_FP4 ? (size_t)(N / TILE_N) * (K / Mx<FMT_FP4>::KG) * Mx<FMT_FP4>::BYTES
-                          : (size_t)(N / TILE_N) * (K / Mx<FMT_FP8>::KG) * Mx<FMT_FP8>::BYTES;
+    return (size_t)(N / TILE_N) * (K / kg_of(fmt)) * (fmt == FMT_FP4 ? Mx<FMT_FP4>::BYTES : Mx<FMT_FP8>::BYTES);
 }
 
 // E8M0 scale byte -> fp32 2^(e - 127) (e = 0 is the subnormal 2^-127)
@@ -73,6 +81,22 @@ __device__ __forceinline__ void dequant(const u32x4 v, uint32_t sc, bf16x8 (&b)[
                                                     bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v[s], f, 1)),
                                                     bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v[s], f, 2)),
                                                     bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v[s], f, 3))});
+        }
+    } else if constexpr (FMT == FMT_INT8) {
+        // q 2^(e - 133) = (q + 128) f - 128 f with f = 2^(e - 127) 2^-6: the byte with its sign bit flipped is
+        // q + 128 as an unsigned byte (v_cvt_f32_ubyte), the product and the sum are exact in fp32, and the
+        // value (7 magnitude bits times a power of two) is exact in bf16
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const float f = e8m0((sc >> (8 * s)) & 0xffu) * 0.015625f, c = -128.0f * f;
+            uint32_t wd[4];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t u = v[2 * s + h] ^ 0x80808080u;
+                wd[2 * h] = qs::cvt_pk_bf16(fmaf((float)(u & 0xffu), f, c), fmaf((float)((u >> 8) & 0xffu), f, c));
+                wd[2 * h + 1] = qs::cvt_pk_bf16(fmaf((float)((u >> 16) & 0xffu), f, c), fmaf((float)(u >> 24), f, c));
+            }
+            b[s] = __builtin_bit_cast(bf16x8, u32x4{wd[0], wd[1], wd[2], wd[3]});
         }
     } else {
 #pragma unroll
@@ -106,9 +130,15 @@ __device__ __forceinline__ uint32_t e4m3_code(float a) {
     return ((uint32_t)(E + 7) << 3) | m;
 }
 
-// one thread per (column n, 32-value K step): the block's scale 2^(floor(log2 amax) - emax), emax 2 (E2M1) or
-// 8 (E4M3), e clamped to [1, 254] (an all-zero block keeps e = 127), then every value's code, written into the
-// fragment-order layout
+// INT8 code (two's complement) of y in units of 2^-6: round to nearest even, saturating at +-127
+__device__ __forceinline__ uint32_t int8_code(float y) {
+    const float q = fminf(fmaxf(rintf(y), -127.f), 127.f);
+    return (uint32_t)(int)q & 0xffu;
+}
+
+// one thread per (column n, 32-value K step): the block's scale 2^(floor(log2 amax) - emax), emax 2 (E2M1),
+// 8 (E4M3) or 0 (INT8), e clamped to [1, 254] (an all-zero block keeps e = 127), then every value's code,
+// written into the fragment-order layout
 template <int FMT>
 __global__ __launch_bounds__(256) void mx_quantize_kernel(const float *w, uint8_t *out, int K, int N) {
     const long i = (long)blockIdx.x * 256 + threadIdx.x;
@@ -122,7 +152,7 @@ __global__ __launch_bounds__(256) void mx_quantize_kernel(const float *w, uint8_
         v[j] = w[(size_t)(32 * ks + j) * N + n];
         amax = fmaxf(amax, fabsf(v[j]));
     }
-    constexpr int emax = FMT == FMT_FP4 ? 2 : 8;
+    constexpr int emax = FMT == FMT_FP4 ? 2 : FMT == FMT_FP8 ? 8 : 0;
     int e = 127;
     if (amax > 0.f) {
         int ex;
@@ -138,9 +168,13 @@ __global__ __launch_bounds__(256) void mx_quantize_kernel(const float *w, uint8_
         uint32_t c[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float y = v[8 * g + j] * inv;
-            const uint32_t code = FMT == FMT_FP4 ? e2m1_code(fabsf(y)) : e4m3_code(fabsf(y));
-            c[j] = code | (y < 0.f && code ? (FMT == FMT_FP4 ? 8u : 0x80u) : 0u);
+            if constexpr (FMT == FMT_INT8) {
+                c[j] = int8_code(ldexpf(v[8 * g + j], 133 - e));  // units of 2^(e - 133), scaled exactly
+            } else {
+                const float y = v[8 * g + j] * inv;
+                const uint32_t code = FMT == FMT_FP4 ? e2m1_code(fabsf(y)) : e4m3_code(fabsf(y));
+                c[j] = code | (y < 0.f && code ? (FMT == FMT_FP4 ? 8u : 0x80u) : 0u);
+            }
         }
         uint8_t *lane = blk + 16 * (16 * g + r);
         if constexpr (FMT == FMT_FP4) {
@@ -477,10 +511,10 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *x, const floa
 // from 8 rows (MXFP4) / 16 rows (MXFP8) on, requested from L2 with each weight group, where the LDS bound
 // would cut K into too many short splits (measured per layer at H 5120 / I 17408: gate | up 26.9 against
 // 30.7 us at 8 rows, down 34.8 against 38.8 us at 16 rows; slower below those counts).
-bool use_hreg(int B, int fmt) { return B >= (fmt == FMT_FP4 ? 8 : 16); }
+bool use_hreg(int B, int fmt) { return B >= (fmt == FMT_FP4 ? 8 : 16); }  // 8-bit formats alike
 
 int proj_splits(int B, int K, int N, int fmt) {
-    const int kg = fmt == FMT_FP4 ? Mx<FMT_FP4>::KG : Mx<FMT_FP8>::KG;
+    const int kg = kg_of(fmt);
     const int nq = K / kg;
     int s = 1;
     while (!use_hreg(B, fmt) && s < nq && (size_t)B * h_pitch((nq + s - 1) / s, kg) * 2 > (size_t)H_LDS) ++s;
@@ -488,13 +522,12 @@ int proj_splits(int B, int K, int N, int fmt) {
     return s;
 }
 size_t h_lds_bytes(int B, int K, int fmt, int nsplit) {
-    const int kg = fmt == FMT_FP4 ? Mx<FMT_FP4>::KG : Mx<FMT_FP8>::KG;
+    const int kg = kg_of(fmt);
     return (size_t)B * h_pitch((K / kg + nsplit - 1) / nsplit, kg) * 2;
 }
 
 bool mx_shape_ok(int K, int N, int fmt) {
-    return (fmt == FMT_FP4 || fmt == FMT_FP8) && K > 0 && N > 0 && N % TILE_N == 0 &&
-           K % (fmt == FMT_FP4 ? Mx<FMT_FP4>::KG : Mx<FMT_FP8>::KG) == 0 && (size_t)N / TILE_N * 4 <= CNT_BYTES &&
+    return fmt_ok(fmt) && K > 0 && N > 0 && N % TILE_N == 0 && K % kg_of(fmt) == 0 && (size_t)N / TILE_N * 4 <= CNT_BYTES &&
            (long)K * MAX_ROWS * 2 < (1L << 31) && mx_bytes(K, N, fmt) < (1UL << 32);
 }
 
@@ -518,7 +551,7 @@ MlpWs mlp_ws(int B, int H, int I) {
     auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
     MlpWs l;
     l.sg = proj_splits(B, H, I, FMT_FP4);
-    l.sd = proj_splits(B, I, H, FMT_FP8);
+    l.sd = proj_splits(B, I, H, FMT_FP8);  // the same for MXINT8 (one layout)
     l.h = CNT_BYTES;
     l.z = l.h + up((size_t)B * H * 2);
     l.part = l.z + up((size_t)B * I * 2);
@@ -535,14 +568,17 @@ extern "C" size_t qs_mx_packed_bytes(int K, int N, int fmt) {
 
 extern "C" int qs_mx_quantize(const float *w, uint8_t *packed, int K, int N, int fmt, void *stream) {
     QS_REQUIRE(w && packed, "qs_mx_quantize: null pointer");
-    QS_REQUIRE(mx_shape_ok(K, N, fmt), "qs_mx_quantize: fmt %d (4 or 8) needs N %% 16 == 0 and K %% %d == 0 (got K %d, N %d)",
-               fmt, fmt == FMT_FP4 ? 128 : 64, K, N);
+    QS_REQUIRE(mx_shape_ok(K, N, fmt),
+               "qs_mx_quantize: fmt %d (4, 8 or 9) needs N %% 16 == 0 and K %% %d == 0 (got K %d, N %d)", fmt,
+               kg_of(fmt), K, N);
     const long n = (long)(K / 32) * N;
     const unsigned grid = (unsigned)((n + 255) / 256);
     if (fmt == FMT_FP4)
         mx_quantize_kernel<FMT_FP4><<<grid, 256, 0, QS_STREAM(stream)>>>(w, packed, K, N);
-    else
+    else if (fmt == FMT_FP8)
         mx_quantize_kernel<FMT_FP8><<<grid, 256, 0, QS_STREAM(stream)>>>(w, packed, K, N);
+    else
+        mx_quantize_kernel<FMT_INT8><<<grid, 256, 0, QS_STREAM(stream)>>>(w, packed, K, N);
     return qs::launch_status("qs_mx_quantize");
 }
 
@@ -556,8 +592,9 @@ extern "C" int qs_mx_gemv(const uint16_t *h, const uint8_t *w, float *y, void *w
                           void *stream) {
     QS_REQUIRE(h && w && y, "qs_mx_gemv: null pointer");
     QS_REQUIRE(B > 0 && B <= MAX_ROWS, "qs_mx_gemv: 1 to %d activation rows (got %d)", MAX_ROWS, B);
-    QS_REQUIRE(mx_shape_ok(K, N, fmt), "qs_mx_gemv: fmt %d (4 or 8) needs N %% 16 == 0 and K %% %d == 0 (got K %d, N %d)",
-               fmt, fmt == FMT_FP4 ? 128 : 64, K, N);
+    QS_REQUIRE(mx_shape_ok(K, N, fmt),
+               "qs_mx_gemv: fmt %d (4, 8 or 9) needs N %% 16 == 0 and K %% %d == 0 (got K %d, N %d)", fmt, kg_of(fmt),
+               K, N);
     const int s = proj_splits(B, K, N, fmt);
     QS_REQUIRE(proj_ws_bytes(B, N, 1, s) < (1UL << 32), "qs_mx_gemv: K %d, N %d need too many K splits", K, N);
     QS_REQUIRE(s == 1 || workspace, "qs_mx_gemv: this shape needs a workspace of qs_mx_gemv_workspace_bytes");
@@ -569,11 +606,15 @@ extern "C" int qs_mx_gemv(const uint16_t *h, const uint8_t *w, float *y, void *w
     a.part = s > 1 ? reinterpret_cast<float *>(static_cast<char *>(workspace) + CNT_BYTES) : nullptr;
     a.B = B, a.K = K, a.N = N, a.nsplit = s;
     hipStream_t st = QS_STREAM(stream);
-    if (use_hreg(B, fmt))
-        return fmt == FMT_FP4 ? launch_proj<FMT_FP4, 1, EPI_SUM, false, true>(a, st, "qs_mx_gemv")
-                              : launch_proj<FMT_FP8, 1, EPI_SUM, false, true>(a, st, "qs_mx_gemv");
-    return fmt == FMT_FP4 ? launch_proj<FMT_FP4, 1, EPI_SUM>(a, st, "qs_mx_gemv")
-                          : launch_proj<FMT_FP8, 1, EPI_SUM>(a, st, "qs_mx_gemv");
+    const bool hreg = use_hreg(B, fmt);
+    if (fmt == FMT_FP4)
+        return hreg ? launch_proj<FMT_FP4, 1, EPI_SUM, false, true>(a, st, "qs_mx_gemv")
+                    : launch_proj<FMT_FP4, 1, EPI_SUM>(a, st, "qs_mx_gemv");
+    if (fmt == FMT_FP8)
+        return hreg ? launch_proj<FMT_FP8, 1, EPI_SUM, false, true>(a, st, "qs_mx_gemv")
+                    : launch_proj<FMT_FP8, 1, EPI_SUM>(a, st, "qs_mx_gemv");
+    return hreg ? launch_proj<FMT_INT8, 1, EPI_SUM, false, true>(a, st, "qs_mx_gemv")
+                : launch_proj<FMT_INT8, 1, EPI_SUM>(a, st, "qs_mx_gemv");
 }
 
 extern "C" size_t qs_mlp_decode_workspace_bytes(int B, int H, int I) {
@@ -582,10 +623,12 @@ extern "C" size_t qs_mlp_decode_workspace_bytes(int B, int H, int I) {
 }
 
 extern "C" int qs_mlp_decode(const float *x, const float *gamma, const uint8_t *gate, const uint8_t *up,
-                             const uint8_t *down, float *x_out, void *workspace, int B, int H, int I, float eps,
-                             void *stream) {
+                             const uint8_t *down, int down_fmt, float *x_out, void *workspace, int B, int H, int I,
+                             float eps, void *stream) {
     QS_REQUIRE(x && gate && up && down && x_out && workspace, "qs_mlp_decode: null pointer");
     QS_REQUIRE(B > 0 && B <= MAX_ROWS, "qs_mlp_decode: 1 to %d rows (got %d)", MAX_ROWS, B);
+    QS_REQUIRE(down_fmt == FMT_INT8 || down_fmt == FMT_FP8, "qs_mlp_decode: down_fmt must be %d (MXINT8) or %d (MXFP8), got %d",
+               FMT_INT8, FMT_FP8, down_fmt);
     QS_REQUIRE(mx_shape_ok(H, I, FMT_FP4) && mx_shape_ok(I, H, FMT_FP8),
                "qs_mlp_decode: H must be a multiple of 128 and I of 64 (got H %d, I %d)", H, I);
     const MlpWs L = mlp_ws(B, H, I);
@@ -610,6 +653,10 @@ extern "C" int qs_mlp_decode(const float *x, const float *gamma, const uint8_t *
     }
     a.W0 = a.W1 = down, a.h = z, a.x = x, a.y = x_out, a.z = nullptr;
     a.K = I, a.N = H, a.nsplit = L.sd;
-    if (use_hreg(B, FMT_FP8)) return launch_proj<FMT_FP8, 1, EPI_RESID, false, true>(a, st, "qs_mlp_decode (down, residual)");
-    return launch_proj<FMT_FP8, 1, EPI_RESID>(a, st, "qs_mlp_decode (down, residual)");
+    const char *what = "qs_mlp_decode (down, residual)";
+    if (down_fmt == FMT_INT8)
+        return use_hreg(B, FMT_INT8) ? launch_proj<FMT_INT8, 1, EPI_RESID, false, true>(a, st, what)
+                                     : launch_proj<FMT_INT8, 1, EPI_RESID>(a, st, what);
+    return use_hreg(B, FMT_FP8) ? launch_proj<FMT_FP8, 1, EPI_RESID, false, true>(a, st, what)
+                                : launch_proj<FMT_FP8, 1, EPI_RESID>(a, st, what);
 }

@@ -58,7 +58,7 @@ SIGNATURES = {
     "qs_mx_gemv_workspace_bytes": (_Z, [_I, _I, _I, _I]),
     "qs_mx_gemv": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "qs_mlp_decode_workspace_bytes": (_Z, [_I, _I, _I]),
-    "qs_mlp_decode": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P]),
+    "qs_mlp_decode": (_I, [_P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _F, _P]),
 }
 
 _lib = None

@@ -604,13 +604,14 @@ def attn_mixer_decode(q, k_new, v_new, gate, wq, wk, cos, sin, k_cache, v_cache,
 # ----------------------------------------------------------- weight-streaming projections and the MLP half
 
 HIDDEN, INTER = 5120, 17408  # common.py:13-14
-MXFP4, MXFP8 = 4, 8  # fmt codes of include/qwen_state.h
+MXFP4, MXFP8, MXINT8 = 4, 8, 9  # fmt codes of include/qwen_state.h
 
 
 class MxWeight:
-    """A weight W [K, N] (y = h W) quantized on the device to OCP MXFP4 or MXFP8 and laid out in the kernels'
-    fragment order (the reference quantizes to 4- / 8-bit block floating point on the host and lays the
-    tiles out per DRAM bank: common.py:115-116, tests/bench_resident_mlp.py:51-96)."""
+    """A weight W [K, N] (y = h W) quantized on the device to OCP MXFP4, MXINT8 or MXFP8 and laid out in the
+    kernels' fragment order (the reference quantizes to 4- / 8-bit block floating point on the host and lays
+    the tiles out per DRAM bank: common.py:115-116, tests/bench_resident_mlp.py:51-96). MXINT8 keeps a sign
+    and 7 magnitude bits per value, the precision of the reference's bfloat8_b (model.py:53-58)."""
 
     def __init__(self, packed, K, N, fmt):
         self.packed, self.K, self.N, self.fmt = packed, K, N, fmt
@@ -623,7 +624,7 @@ class MxWeight:
         _chk(w, "w", torch.float32, (K, N), dev)
         nbytes = lib().qs_mx_packed_bytes(K, N, fmt)
         if nbytes == 0:
-            raise ValueError(f"fmt {fmt} (4 or 8) needs N % 16 == 0 and K % {128 if fmt == MXFP4 else 64} == 0 "
+            raise ValueError(f"fmt {fmt} (4, 8 or 9) needs N % 16 == 0 and K % {128 if fmt == MXFP4 else 64} == 0 "
                              f"(got K {K}, N {N})")  # fmt: skip
         packed = torch.empty(nbytes, dtype=torch.uint8, device=dev)
         call("qs_mx_quantize", _p(w), _p(packed), K, N, int(fmt), _stream(dev))
@@ -650,17 +651,19 @@ def mlp_decode(x, gamma, gate, up, down, eps=EPS, out=None, ws=None):
     """The MLP half of a decoder layer for 1..16 rows (tests/bench_resident_mlp.py:98-105):
     x + (silu(h G) * (h U)) D with h = bf16(x * rsqrt(mean(x^2) + eps) * gamma), z = silu(h G) * (h U) kept
     in bf16. x [B, H] fp32, gamma [H] fp32 or None when the norm weight is folded into the rows of gate and up
-    (weights.py:107-112); gate, up MxWeight MXFP4 [H, I]; down MxWeight MXFP8 [I, H].
-    Returns x_out [B, H] fp32 (``out`` may be ``x``)."""
+    (weights.py:107-112); gate, up MxWeight MXFP4 [H, I]; down MxWeight MXINT8 (the reference's 8-bit
+    precision) or MXFP8 [I, H]. Returns x_out [B, H] fp32 (``out`` may be ``x``)."""
     dev = x.device
     B, H = x.shape
     _chk(x, "x", torch.float32, (B, H), dev)
     if gamma is not None:
         _chk(gamma, "gamma", torch.float32, (H,), dev)
     I = gate.N
-    for w, name, shape, fmt in ((gate, "gate", (H, I), MXFP4), (up, "up", (H, I), MXFP4), (down, "down", (I, H), MXFP8)):
-        if (w.K, w.N) != shape or w.fmt != fmt:
-            raise ValueError(f"{name} must be a {shape} MXFP{fmt} weight (got {(w.K, w.N)} MXFP{w.fmt})")
+    for w, name, shape, fmts in ((gate, "gate", (H, I), (MXFP4,)), (up, "up", (H, I), (MXFP4,)),
+                                 (down, "down", (I, H), (MXINT8, MXFP8))):  # fmt: skip
+        if (w.K, w.N) != shape or w.fmt not in fmts:
+            raise ValueError(f"{name} must be a {shape} weight in format {' or '.join(map(str, fmts))} "
+                             f"(got {(w.K, w.N)} format {w.fmt})")  # fmt: skip
     nbytes = lib().qs_mlp_decode_workspace_bytes(B, H, I)
     if nbytes == 0:
         raise ValueError(f"1 to 16 rows, H % 128 == 0, I % 64 == 0 (got B {B}, H {H}, I {I})")
@@ -668,6 +671,6 @@ def mlp_decode(x, gamma, gate, up, down, eps=EPS, out=None, ws=None):
     _chk(y, "out", torch.float32, (B, H), dev)
     if ws is None:
         ws = workspace("mlp", nbytes, dev)
-    call("qs_mlp_decode", _p(x), _p(gamma), _p(gate.packed), _p(up.packed), _p(down.packed), _p(y), _p(ws), B, H, I,
-         float(eps), _stream(dev))  # fmt: skip
+    call("qs_mlp_decode", _p(x), _p(gamma), _p(gate.packed), _p(up.packed), _p(down.packed), int(down.fmt), _p(y),
+         _p(ws), B, H, I, float(eps), _stream(dev))  # fmt: skip
     return y

@@ -6,7 +6,7 @@ sigmoid(N(0, 1)); K/V pools ~ N(0, 1) bf16; block tables are slices of one seede
 """
 import torch
 
-from .ops import BLOCK, CONV_K, DK, DV, HD, HIDDEN, INTER, MXFP4, MXFP8, NK, NKV, NQ, NV, MxWeight
+from .ops import BLOCK, CONV_K, DK, DV, HD, HIDDEN, INTER, MXFP4, MXINT8, NK, NKV, NQ, NV, MxWeight
 
 C_QKV = 2 * NK * DK + NV * DV  # 10240 conv channels q | k | v
 
@@ -95,16 +95,17 @@ def prefill(T, device, seed=0):
     )
 
 
-def mlp_layer(B, device, seed=0, H=None, I=None, keep_fp32=False):
+def mlp_layer(B, device, seed=0, H=None, I=None, keep_fp32=False, down_fmt=MXINT8):
     """One decoder layer's MLP half: x [B, H] fp32, gamma [H], the gate | up weights [H, I] as MXFP4 and the
-    down weight [I, H] as MXFP8 (random normal scaled by 1 / sqrt(fan-in), quantized on the device, one weight
-    in fp32 at a time). keep_fp32 also returns the fp32 weights on the host as gate32, up32, down32."""
+    down weight [I, H] as MXINT8 (the reference's 8-bit precision; down_fmt MXFP8 for E4M3) (random normal
+    scaled by 1 / sqrt(fan-in), quantized on the device, one weight in fp32 at a time). keep_fp32 also
+    returns the fp32 weights on the host as gate32, up32, down32."""
     H = HIDDEN if H is None else H
     I = INTER if I is None else I
     gen = _gen(device, seed)
     d = dict(x=_randn((B, H), gen, device), gamma=1 + _randn((H,), gen, device, std=0.1))
     for name, shape, fmt, std in (("gate", (H, I), MXFP4, H**-0.5), ("up", (H, I), MXFP4, H**-0.5),
-                                  ("down", (I, H), MXFP8, 0.5 * I**-0.5)):  # fmt: skip
+                                  ("down", (I, H), down_fmt, 0.5 * I**-0.5)):  # fmt: skip
         w = _randn(shape, gen, device, std=std)
         d[name] = MxWeight.quantize(w, fmt)
         if keep_fp32:
