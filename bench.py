@@ -246,15 +246,40 @@ def kernel_time(torch, make_calls, reps):
     return e0.elapsed_time(e1) / (reps * len(fns))
 
 
-def gdn_call(d, B, ws, stream, out):
+def gdn_call(d, B, ws, stream, out, z=None, norm_w=None):
+    """The fused GDN decode (z, norm_w: with the gated RMSNorm epilogue) as a (name, args) C-ABI call."""
     from qwen36_state.ops import CONV_K, DK, DV, NK, NV
 
     return "qs_gdn_decode_fused", (
         _p(d["x"]), _p(d["conv_state"]), _p(d["taps"]), _p(d["g"]), _p(d["beta"]), _p(d["state"]), _p(out),
-        ctypes.c_void_p(0), _p(ws), ctypes.c_void_p(0), B, NK, NV, DK, DV, CONV_K, ctypes.c_float(DK**-0.5),
-        ctypes.c_float(1e-6),
+        ctypes.c_void_p(0), _p(z), NV * DV, _p(norm_w), _p(ws), ctypes.c_void_p(0), B, NK, NV, DK, DV, CONV_K,
+        ctypes.c_float(DK**-0.5), ctypes.c_float(1e-6),
         stream,
     )  # fmt: skip
+
+
+def gdn_epilogue_times(torch, layers, B, ws, reps):
+    """The GDN mixer's gated RMSNorm epilogue (model.py:274-275) two ways, per layer (ms): fused into the decode
+    launch (z, norm_w given) and as the unfused pair (the decode launch, then qs_gdn_gated_norm on its bf16 o).
+    Seeded z rows [B, NV DV] and norm_w [DV] per layer; the layers' states advance while timing (their values
+    do not change the work)."""
+    from qwen36_state.ops import DV, EPS, NV
+
+    gen = torch.Generator(device="cuda:0").manual_seed(5)
+    zs = [torch.randn(B, NV * DV, generator=gen, device="cuda:0").bfloat16() for _ in layers]
+    nw = 1 + 0.1 * torch.randn(DV, generator=gen, device="cuda:0")
+    outs = [torch.empty(B, NV, DV, dtype=torch.bfloat16, device="cuda:0") for _ in layers]
+    fused = kernel_time(torch, lambda st: [gdn_call(d, B, ws, st, o, z, nw) for d, o, z in zip(layers, outs, zs)],
+                        reps)  # fmt: skip
+
+    def pair(st):
+        calls = []
+        for d, o, z in zip(layers, outs, zs):
+            calls.append(gdn_call(d, B, ws, st, o))
+            calls.append(("qs_gdn_gated_norm", (_p(o), _p(z), _p(nw), _p(o), B * NV, DV, ctypes.c_float(EPS), st)))
+        return calls
+
+    return fused, 2 * kernel_time(torch, pair, reps)
 
 
 def attn_call(d, table, lens, B, T, pps, ws, stream, out):
@@ -391,12 +416,17 @@ def bench_step(args, torch, tel):
     for k, (t, b, n) in kern.items():
         log(f"{k}: {t * 1e3:.2f} µs per launch, {b / t / 1e6:.0f} GB/s, {n} launches per step")
     dom = max(kern, key=lambda k: kern[k][0] * kern[k][2])
+    t_fused, t_pair = gdn_epilogue_times(torch, [step.layer[l] for l in gl], step.B, step.gdn_ws, args.kernel_reps)
+    log(f"GDN with the gated RMSNorm epilogue: fused {t_fused * 1e3:.2f} µs, unfused pair {t_pair * 1e3:.2f} µs")
     work = (f"decode-step state path: {len(gl)} GDN + {len(al)} paged-attention layers, batch {args.batch}, "
             f"{args.ctx} positions per user, block 64, HIP-graph replay with the position advance")  # fmt: skip
     out = entry(work, nbytes, ms, stats, roofline(dom, kern[dom][1], kern[dom][0]),
                 dict(kernels={k: dict(us_per_launch=round(t * 1e3, 2), bytes_per_launch=b, gbs=round(b / t / 1e6, 1),
                                       launches_per_step=n) for k, (t, b, n) in kern.items()}))  # fmt: skip
     out.update(batch=args.batch, context=args.ctx, layers=args.layers, pages_per_split=args.pps)
+    out["gdn_epilogue"] = dict(fused_us_per_layer=round(t_fused * 1e3, 2), unfused_pair_us_per_layer=round(t_pair * 1e3, 2),
+                               note="GDN decode with the gated RMSNorm epilogue (not part of the state-path step): in "
+                                    "the same launch vs a second launch")  # fmt: skip
     if not args.no_cpu:
         log("timing the CPU oracle on a sample of the step")
         out["cpu_baseline"] = cpu_step(torch, step)
@@ -430,6 +460,9 @@ def bench_gdn_layer(args, torch, tel):
     out = entry("one GDN layer decode, batch 1: conv1d update (10240 channels) + L2-norm + gated delta rule on fp32 "
                 "[1, 48, 128, 128] (48 layers' buffers rotate)", nbytes, ms, stats,
                 roofline("gdn_decode_fused", nbytes, ms, "gdn_decode_fused_b1"))  # fmt: skip
+    t_fused, t_pair = gdn_epilogue_times(torch, layers, 1, ws, 2)
+    out["gdn_epilogue"] = dict(fused_us_per_layer=round(t_fused * 1e3, 2), unfused_pair_us_per_layer=round(t_pair * 1e3, 2),
+                               note="with the gated RMSNorm epilogue: in the same launch vs a second launch")  # fmt: skip
     if not args.no_cpu:
         O = _oracle()
         c = {k: v.cpu() for k, v in layers[0].items()}
@@ -825,7 +858,7 @@ def main():
         stats=dict(median_us=head["median_us"], p10_us=head["p10_us"], p90_us=head["p90_us"], replays=head["replays"]),
         telemetry=head_tel, copy_ceiling=ceiling,
     )  # fmt: skip
-    for k in ("kernels", "cpu_baseline"):
+    for k in ("kernels", "gdn_epilogue", "cpu_baseline"):
         if k in head:
             out[k] = head[k]
     if configs:

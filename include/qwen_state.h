@@ -84,12 +84,17 @@ size_t qs_gdn_workspace_bytes(int B, int NK);
 /* Conv1d update + L2-norm + delta rule of one decode step in one launch (a1+a2+a4): the GDN mixer state
  * path of torch_step model.py:255-273 behind the projection. x [B, C] is the projection's q|k|v slice
  * (C = 2 NK DK + NV DV); conv_state is shifted in place; y_out (nullable) receives the conv output.
+ * z, norm_w (both nullable; f1, the mixer's epilogue, model.py:274-275, kernels/gdn_head_compute.cpp:320-346):
+ * with them o receives bf16(o rsqrt(mean(o^2) + eps) norm_w silu(z)) per value head, normalised from the
+ * fp32 o as the reference does, instead of bf16(o); z is the projection's z slice, row b at z + b ldz
+ * (NV DV values; ldz >= NV DV, a multiple of 4, z 8-byte aligned), norm_w [DV] fp32 (16-byte aligned).
+ * eps is the L2-norm's and the RMSNorm's (both 1e-6 in the reference, model.py:264-267, common.py:15).
  * lens (nullable, [B] device int32, the step's sequence lengths): a user with lens[b] < 0 is an idle slot
  * whose state, conv history and output are left untouched. */
 int qs_gdn_decode_fused(const uint16_t *x, uint16_t *conv_state, const uint16_t *taps, const float *g,
-                        const float *beta, float *state, uint16_t *o, uint16_t *y_out, void *workspace,
-                        const int *lens, int B, int NK, int NV, int DK, int DV, int K, float scale, float eps,
-                        void *stream);
+                        const float *beta, float *state, uint16_t *o, uint16_t *y_out, const uint16_t *z, int ldz,
+                        const float *norm_w, void *workspace, const int *lens, int B, int NK, int NV, int DK, int DV,
+                        int K, float scale, float eps, void *stream);
 
 /* qs_gdn_decode_fused for callers that cannot allocate (code under HIP graph capture, serving loops that
  * forbid hipMalloc): the same kernels, with the conv counters in a static device array of the library

@@ -201,3 +201,36 @@ def test_gdn_gated_norm(dev):
         y = ops.gdn_gated_norm(o.to(dev), z.to(dev), w.to(dev))
         ulps, frac = bf16_ulp_mismatch(y, O.gdn_gated_norm(o, z, w))
         assert ulps <= 1 and frac < 1e-2, (ulps, frac)
+
+
+@pytest.mark.parametrize("B", [1, 3, 8])
+def test_gdn_decode_fused_gated_norm(dev, B):
+    """The fused decode with the mixer's gated RMSNorm epilogue in the same launch (z, norm_w; model.py:
+    274-275, kernels/gdn_head_compute.cpp:320-346): o = bf16(rmsnorm(o) norm_w silu(z)) per value head, from
+    the fp32 o as the reference normalises it, against the oracle's gdn_gated_norm(gdn_step(...)) at rtol 2e-2
+    (the oracle fed the kernel's own conv output); z is read as a strided slice of a wider projection row.
+    Batch 1 and 3 (a head's 4 slabs on 4 waves each, 16 waves per workgroup) and 8 (one wave per slab). The
+    state and conv state are bit-identical to the plain fused launch, whose o rounded to bf16 and then put
+    through the separate epilogue lands within two bf16 ulps of the fused result."""
+    d = inputs(B, seed=40 + B)
+    gen = torch.Generator().manual_seed(41 + B)
+    proj = (2 * torch.randn(B, NV * DV + 96, generator=gen)).bfloat16()  # z slice + the columns after it
+    z = proj[:, : NV * DV]
+    w = 1 + 0.1 * torch.randn(DV, generator=gen)
+    g, g2 = to(d, dev), to(d, dev)
+    y = torch.empty(B, W.C_QKV, dtype=torch.bfloat16, device=dev)
+    zd = proj.to(dev)[:, : NV * DV]
+    o = ops.gdn_decode_fused(g["x"], g["conv_state"], g["taps"], g["g"], g["beta"], g["state"], y_out=y, z=zd,
+                             norm_w=w.to(dev))  # fmt: skip
+    o_plain = ops.gdn_decode_fused(g2["x"], g2["conv_state"], g2["taps"], g2["g"], g2["beta"], g2["state"])
+    assert torch.equal(g["state"], g2["state"]) and torch.equal(g["conv_state"], g2["conv_state"])
+    q, k, v = O.split_qkv(y.cpu().float(), NK, NV, DK, DV)
+    o_ref, S = O.gdn_step(q, k, v, d["g"], d["beta"], d["state"])
+    assert_state(g["state"], S)
+    ref = O.gdn_gated_norm(o_ref, z.float().view(B, NV, DV), w)
+    assert_bf16_output(o, ref)
+    two = ops.gdn_gated_norm(o_plain, zd.contiguous().view(B, NV, DV), w.to(dev))
+    ulps, frac = bf16_ulp_mismatch(o, two)
+    assert ulps <= 2, (ulps, frac)
+    with pytest.raises(ValueError, match="both"):
+        ops.gdn_decode_fused(g["x"], g["conv_state"], g["taps"], g["g"], g["beta"], g["state"], z=zd)

@@ -24,8 +24,8 @@ def run(entry, d, B, ws=None):
     y = torch.empty_like(d["x"])
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     args = [_p(d["x"]), _p(d["conv_state"]), _p(d["taps"]), _p(d["g"]), _p(d["beta"]), _p(d["state"]), _p(o), _p(y)]
-    if ws is not None:
-        args.append(_p(ws))
+    if ws is not None:  # the workspace entry: no gated-norm epilogue (z, ldz, norm_w), then the workspace
+        args += [ctypes.c_void_p(0), 0, ctypes.c_void_p(0), _p(ws)]
     args.append(ctypes.c_void_p(0))  # lens: every user active
     rc = getattr(L, entry)(*args, B, NK, NV, DK, DV, 4, ctypes.c_float(DK**-0.5), ctypes.c_float(1e-6), st)
     assert rc == 0, L.qs_last_error().decode()

@@ -39,6 +39,9 @@ struct GdnArgs {
     const int *lens;            // nullable: [B]; a user with lens[b] < 0 is an idle slot (decode: left untouched;
                                 // verify: no token verified, slot mode carries its input slot forward)
     int n_slots;                // slots in s_in / conv_in
+    const uint16_t *z;          // decode, nullable: the projection's z rows (row b at z + b ldz), for the gated
+    int ldz;                    // RMSNorm epilogue o <- bf16(rmsnorm(o) norm_w silu(z)) per value head
+    const float *norm_w;        // [DV]
     int B, T, NK, NV, C;
     float scale, eps;
 };
@@ -167,20 +170,26 @@ __device__ __forceinline__ const float *sp_of_t(const GdnArgs &a, size_t user, i
 // stores together and a store in flight would turn each wait for a state load into a wait for everything.
 // in_slot (verify only, nullable): user b's input state and conv state are slot in_slot[b] of s_in and
 // conv_in ([n_slots, B, ...]); a slot outside [0, n_slots) reads slot 0.
-template <bool CONV, bool VERIFY, int TM, int SLAB, int NW, int WPG>
+// NORM (decode, WPG == NSLAB: a workgroup holds the 4 slabs of one value head): the gated RMSNorm epilogue of
+// the mixer (model.py:274-275, the head cores' steps 7-8, kernels/gdn_head_compute.cpp:320-346) on the fp32 o
+// of the head: the slabs' sums of squares meet in LDS (one barrier per token) and o receives
+// bf16(o rsqrt(mean(o^2) + eps) norm_w silu(z)).
+template <bool CONV, bool VERIFY, int TM, int SLAB, int NW, int WPG, bool NORM = false>
 __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
     constexpr int NSLAB = DV / SLAB;
     constexpr int CG = SLAB / 4;   // column groups of 4 (lane % CG)
     constexpr int RG = 64 / CG;    // row groups (lane / CG)
     constexpr int RW = DK / NW;    // rows per wave
     constexpr int RPL = RW / RG;   // rows per lane
-    static_assert(RPL >= 1 && RW % RG == 0 && (VERIFY || TM == 1) && (NW == 1 || WPG == 1), "slab shape");
+    static_assert(RPL >= 1 && RW % RG == 0 && (VERIFY || TM == 1), "slab shape");
+    static_assert(!NORM || (!VERIFY && WPG == NSLAB && CG <= 16), "the epilogue needs whole heads per workgroup");
     // conv roles by wave of the workgroup: q channels on wave 0, k on wave 1 (when there is one), the slab's v
     // channels on wave 2 (NW = 4) or on every wave for its own slab (NW = 1)
     constexpr int WK = (NW >= 4 || WPG >= 2) ? 1 : 0;
     constexpr int WV = NW >= 4 ? 2 : NW - 1;
-    // WPG independent single-wave slab units per workgroup (NW == 1): unit = logical workgroup x WPG + wave
-    const int gw = WPG > 1 ? (int)(threadIdx.x >> 6) : 0;
+    // WPG slab units per workgroup, NW waves each: unit = logical workgroup x WPG + gw
+    const int wid = (int)(threadIdx.x >> 6);     // wave within the workgroup
+    const int gw = WPG > 1 ? wid / NW : 0;        // slab unit within the workgroup
     const int nwg = a.B * a.NV * NSLAB / WPG;
     const int lid = qs::xcd_logical(blockIdx.x, nwg) * WPG + gw;
     const int s = lid % NSLAB;
@@ -192,8 +201,8 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
     const int rep = a.NV / a.NK;
     const int kh = h / rep;
     const int lane = threadIdx.x & 63;
-    const int w = NW > 1 ? (int)(threadIdx.x >> 6) : 0;  // wave within the slab
-    const int r = NW > 1 ? w : gw;                        // wave within the workgroup
+    const int w = NW > 1 ? wid % NW : 0;  // wave within the slab
+    const int r = wid;
     const bool isq = r == 0, isk = r == WK, isv = NW > 1 ? w == WV : true;
     const int cg = lane % CG, rg = lane / CG;
     const int T = VERIFY ? a.T : 1;
@@ -214,7 +223,8 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
     __shared__ __align__(16) float s_kn[TM][DK];
     __shared__ __align__(16) float s_v_[WPG][TM][SLAB];
     auto &s_v = s_v_[gw];
-    __shared__ __align__(16) f32x4 s_red[NW > 1 ? 2 : 1][NW][2][CG];  // per token parity: wave column sums
+    __shared__ __align__(16) f32x4 s_red_[NW > 1 ? 2 : 1][WPG][NW][2][CG];  // per token parity: wave column sums
+    __shared__ float s_nrm[2][WPG];  // NORM, per token parity: the slabs' sums of o^2
 
     // the q / k conv waves of a multi-slab workgroup issue first: their conv inputs then leave ahead of the other
     // waves' state loads and the norms every slab waits for are ready sooner (the 64-layer batch-8 step:
@@ -268,6 +278,13 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
         const int gi = ((b * T) + (t < T ? t : 0)) * a.NV + h;
         gdec[t] = a.g[gi];
         gbeta[t] = a.beta[gi];
+    }
+    // NORM: the epilogue's z and norm_w of the lane's 4 columns, requested now (used after the last token)
+    uint2 z4 = make_uint2(0, 0);
+    float4 w4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (NORM && w == 0 && lane < CG) {
+        z4 = *reinterpret_cast<const uint2 *>(a.z + (size_t)b * a.ldz + h * DV + s * SLAB + cg * 4);
+        w4 = *reinterpret_cast<const float4 *>(a.norm_w + s * SLAB + cg * 4);
     }
 
     // 2. q, k (rows 2 lane, 2 lane + 1) and the v slab for every token; L2 norms (q times scale).
@@ -371,7 +388,7 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
         if constexpr (NW > 1) {
             // the waves' column sums, added in wave order by every wave (bit-identical everywhere); two
             // buffers by token parity, so one barrier per token suffices
-            auto &red = s_red[t & 1];
+            auto &red = s_red_[t & 1][gw];
             if (rg == 0) {
                 red[w][0][cg] = f32x4{p[0], p[1], p[2], p[3]};
                 red[w][1][cg] = f32x4{r[0], r[1], r[2], r[3]};
@@ -416,7 +433,36 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, S[i]), rs, soff + RG * i * DV * 4, 0,
                                                    qs::CP_NT | qs::CP_SC1);
         }
-        if (w == 0 && lane < CG) {
+        if constexpr (NORM) {
+            // the head's o in fp32 (lanes < CG of each slab's wave 0), its sum of squares over the 4 slabs in
+            // slab order, then the gated RMSNorm, rounded once to bf16
+            float po[4] = {0.f, 0.f, 0.f, 0.f};
+            if (w == 0 && lane < CG)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) po[j] = fmaf(qk, dl[j], decay * r[j]);
+            float ss = (po[0] * po[0] + po[1] * po[1]) + (po[2] * po[2] + po[3] * po[3]);
+            // the sum over the first 16-lane row (lanes 0 .. CG - 1 hold o, the others zeros): quads by xor 1,
+            // xor 2, then row_ror 4 and 8, after which every lane of the row, lane 0 included, holds the total
+            ss += qs::dpp<0xB1>(ss);
+            ss += qs::dpp<0x4E>(ss);
+            ss += qs::dpp<0x124>(ss);
+            ss += qs::dpp<0x128>(ss);
+            if (w == 0 && lane == 0) s_nrm[t & 1][gw] = ss;
+            __syncthreads();
+            if (w == 0 && lane < CG) {
+                float tot = s_nrm[t & 1][0];
+#pragma unroll
+                for (int u = 1; u < WPG; ++u) tot += s_nrm[t & 1][u];
+                const float rn = rsqrtf(tot * (1.0f / DV) + a.eps);
+                const int d0 = s * SLAB + cg * 4;
+                const float y0 = po[0] * rn * w4.x * qs::silu(qs::bf_lo(z4.x));
+                const float y1 = po[1] * rn * w4.y * qs::silu(qs::bf_hi(z4.x));
+                const float y2 = po[2] * rn * w4.z * qs::silu(qs::bf_lo(z4.y));
+                const float y3 = po[3] * rn * w4.w * qs::silu(qs::bf_hi(z4.y));
+                *reinterpret_cast<uint2 *>(a.o + (size_t)gi * DV + d0) =
+                    make_uint2(qs::cvt_pk_bf16(y0, y1), qs::cvt_pk_bf16(y2, y3));
+            }
+        } else if (w == 0 && lane < CG) {
             float po[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) po[j] = fmaf(qk, dl[j], decay * r[j]);
@@ -558,6 +604,17 @@ template <bool CONV, bool VERIFY, int TM>
 void launch_gdn_tm(const GdnArgs &a, hipStream_t st) {
     const int units = a.B * a.NV * (DV / 32);
     const int per_key_head = (a.NV / a.NK) * (DV / 32);  // consecutive slab units sharing one key head
+    if constexpr (!VERIFY) {
+        // with the gated RMSNorm epilogue a workgroup holds one value head: its 4 slabs on one wave each at
+        // large batch, on 4 waves each (16 waves) below
+        if (a.z) {
+            if (units >= 1024)
+                gdn_kernel<CONV, VERIFY, TM, 32, 1, 4, true><<<units / 4, 256, 0, st>>>(a);
+            else
+                gdn_kernel<CONV, VERIFY, TM, 32, 4, 4, true><<<units / 4, 1024, 0, st>>>(a);
+            return;
+        }
+    }
     // a workgroup's slab units must lie in one key head (they share its q / k conv through LDS, and the
     // conv-state counter expects per_key_head / WPG arrivals): 6 per workgroup when 6 divides the key
     // head's units (3 value heads per key head: one workgroup per CU at batch 8), else 4 (always divides)
@@ -641,17 +698,22 @@ extern "C" int qs_gdn_decode_step(const uint16_t *q, const uint16_t *k, const ui
 extern "C" size_t qs_gdn_workspace_bytes(int B, int NK) { return (size_t)(B > 0 ? B : 0) * (NK > 0 ? NK : 0) * 8; }
 
 extern "C" int qs_gdn_decode_fused(const uint16_t *x, uint16_t *conv_state, const uint16_t *taps, const float *g,
-                                   const float *beta, float *state, uint16_t *o, uint16_t *y_out, void *workspace,
-                                   const int *lens, int B, int NK, int NV, int DKa, int DVa, int K, float scale,
-                                   float eps, void *stream) {
+                                   const float *beta, float *state, uint16_t *o, uint16_t *y_out, const uint16_t *z,
+                                   int ldz, const float *norm_w, void *workspace, const int *lens, int B, int NK,
+                                   int NV, int DKa, int DVa, int K, float scale, float eps, void *stream) {
     QS_REQUIRE(x && conv_state && taps && g && beta && state && o && workspace,
                "qs_gdn_decode_fused: null pointer");
     if (int e = check_gdn_shapes(B, NK, NV, DKa, DVa)) return e;
     QS_REQUIRE(K == KC, "qs_gdn_decode_fused: only K = 4 taps are supported (got %d)", K);
     if (int e = check_conv_alignment(x, conv_state, conv_state, taps, y_out)) return e;
+    QS_REQUIRE(!z == !norm_w, "qs_gdn_decode_fused: give both z and norm_w or neither");
+    QS_REQUIRE(!z || (ldz >= NV * DVa && ldz % 4 == 0 && (uintptr_t)z % 8 == 0 && (uintptr_t)norm_w % 16 == 0),
+               "qs_gdn_decode_fused: z rows need ldz >= NV DV, ldz %% 4 == 0, z 8-byte and norm_w 16-byte aligned "
+               "(got ldz %d)", ldz);
     GdnArgs a{};
     a.x = x, a.conv_in = conv_state, a.conv_out = conv_state, a.taps = taps, a.y_out = y_out;
     a.g = g, a.beta = beta, a.s_in = state, a.s_out = state, a.o = o;
+    a.z = z, a.ldz = ldz, a.norm_w = norm_w;
     a.counters = static_cast<int *>(workspace);
     a.lens = lens;
     a.B = B, a.T = 1, a.NK = NK, a.NV = NV, a.C = 2 * NK * DK + NV * DV, a.scale = scale, a.eps = eps;

@@ -18,7 +18,8 @@ SIGNATURES = {
     "qs_gdn_gates": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _P]),
     "qs_gdn_decode_step": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _P]),
     "qs_gdn_workspace_bytes": (_Z, [_I, _I]),
-    "qs_gdn_decode_fused": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _F, _P]),
+    "qs_gdn_decode_fused": (
+        _I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _F, _P]),
     "qs_gdn_decode_fused_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _F, _P]),
     "qs_gdn_noalloc_scratch_read": (_I, [_P, _I, _P]),
     "qs_gdn_gated_norm": (_I, [_P, _P, _P, _P, _I, _I, _F, _P]),

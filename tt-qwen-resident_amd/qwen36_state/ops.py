@@ -161,13 +161,15 @@ def gdn_decode_step(q, k, v, g, beta, state, scale=None, eps=EPS, out=None):
 
 
 def gdn_decode_fused(x, conv_state, taps, g, beta, state, nk=NK, scale=None, eps=EPS, out=None, y_out=None,
-                     ws=None, lens=None):  # fmt: skip
+                     ws=None, lens=None, z=None, norm_w=None):  # fmt: skip
     """Conv1d update + L2-norm + delta rule of one decode step in one launch (model.py:255-273).
 
     x [B, C] bf16 is the projection's q|k|v slice (C = 2 nk DK + NV DV); conv_state [B, C, 3] and state
     [B, NV, DK, DV] are updated in place. Returns o [B, NV, DV] bf16 (y_out, if given, receives the conv
     output [B, C]). lens [B] int32 (optional, the step's lengths): users with lens < 0 are idle slots, left
-    untouched."""
+    untouched. With z [B, NV DV] (or [B, NV, DV]; rows may be strided, e.g. a slice of the projection output)
+    and norm_w [DV] fp32 the mixer's gated RMSNorm epilogue runs in the same launch (model.py:274-275): o is
+    bf16(rmsnorm(o) norm_w silu(z)) per value head, normalised from the fp32 o."""
     dev = state.device
     _chk(state, "state", torch.float32)
     B, nv, dk, dv = state.shape
@@ -186,8 +188,20 @@ def gdn_decode_fused(x, conv_state, taps, g, beta, state, nk=NK, scale=None, eps
         ws = workspace("gdn", lib().qs_gdn_workspace_bytes(B, nk), dev)
     if lens is not None:
         _chk(lens, "lens", torch.int32, (B,), dev)
+    ldz = 0
+    if (z is None) != (norm_w is None):
+        raise ValueError("give both z and norm_w or neither")
+    if z is not None:
+        if not isinstance(z, torch.Tensor) or not z.is_cuda or z.dtype != torch.bfloat16 or z.device != dev:
+            raise ValueError(f"z must be a bf16 tensor on {dev}")
+        z = z.reshape(B, nv * dv) if z.dim() == 3 and z.is_contiguous() else z
+        if z.dim() != 2 or tuple(z.shape) != (B, nv * dv) or z.stride(1) != 1:
+            raise ValueError(f"z must be [B, NV DV] = [{B}, {nv * dv}] with unit column stride")
+        ldz = z.stride(0) if B > 1 else nv * dv
+        _chk(norm_w, "norm_w", torch.float32, (dv,), dev)
     call("qs_gdn_decode_fused", _p(x), _p(conv_state), _p(taps), _p(g), _p(beta), _p(state), _p(o), _p(y_out),
-         _p(ws), _p(lens), B, nk, nv, dk, dv, CONV_K, float(scale), float(eps), _stream(dev))  # fmt: skip
+         _p(z), ldz, _p(norm_w), _p(ws), _p(lens), B, nk, nv, dk, dv, CONV_K, float(scale), float(eps),
+         _stream(dev))  # fmt: skip
     return o
 
 
