@@ -393,11 +393,13 @@ def cpu_step(torch, step):
 # ------------------------------------------------------------------------------------------------ workloads
 
 
-def bench_step(args, torch, tel):
+def bench_step(args, torch, tel, batch=None, pps=None):
     from qwen36_state.decode import StatePathStep, layer_bytes
 
-    log(f"building the {args.layers}-layer step: batch {args.batch}, {args.ctx} positions")
-    step = StatePathStep.synthetic(args.batch, args.ctx, args.layers, device="cuda:0", pages_per_split=args.pps)
+    batch = args.batch if batch is None else batch
+    pps = args.pps if pps is None else pps
+    log(f"building the {args.layers}-layer step: batch {batch}, {args.ctx} positions")
+    step = StatePathStep.synthetic(batch, args.ctx, args.layers, device="cuda:0", pages_per_split=pps)
     gl, al = step.gdn_layers(), step.attn_layers()
     step.step()
     step.rewind()
@@ -411,19 +413,19 @@ def bench_step(args, torch, tel):
     t_att = kernel_time(torch, lambda st: [attn_call(step.layer[l], step.block_table, lens1, step.B, 1, step.pps,
                                                      step.attn_ws, st, step.layer[l]["o"]) for l in al],
                         args.kernel_reps)  # fmt: skip
-    b_gdn, b_att = layer_bytes(args.batch, args.ctx), layer_bytes(args.batch, args.ctx, attn=True)
+    b_gdn, b_att = layer_bytes(batch, args.ctx), layer_bytes(batch, args.ctx, attn=True)
     kern = {"gdn_decode_fused": (t_gdn, b_gdn, len(gl)), "paged_gqa_decode": (t_att, b_att, len(al))}
     for k, (t, b, n) in kern.items():
         log(f"{k}: {t * 1e3:.2f} µs per launch, {b / t / 1e6:.0f} GB/s, {n} launches per step")
     dom = max(kern, key=lambda k: kern[k][0] * kern[k][2])
     t_fused, t_pair = gdn_epilogue_times(torch, [step.layer[l] for l in gl], step.B, step.gdn_ws, args.kernel_reps)
     log(f"GDN with the gated RMSNorm epilogue: fused {t_fused * 1e3:.2f} µs, unfused pair {t_pair * 1e3:.2f} µs")
-    work = (f"decode-step state path: {len(gl)} GDN + {len(al)} paged-attention layers, batch {args.batch}, "
+    work = (f"decode-step state path: {len(gl)} GDN + {len(al)} paged-attention layers, batch {batch}, "
             f"{args.ctx} positions per user, block 64, HIP-graph replay with the position advance")  # fmt: skip
     out = entry(work, nbytes, ms, stats, roofline(dom, kern[dom][1], kern[dom][0]),
                 dict(kernels={k: dict(us_per_launch=round(t * 1e3, 2), bytes_per_launch=b, gbs=round(b / t / 1e6, 1),
                                       launches_per_step=n) for k, (t, b, n) in kern.items()}))  # fmt: skip
-    out.update(batch=args.batch, context=args.ctx, layers=args.layers, pages_per_split=args.pps)
+    out.update(batch=batch, context=args.ctx, layers=args.layers, pages_per_split=pps)
     out["gdn_epilogue"] = dict(fused_us_per_layer=round(t_fused * 1e3, 2), unfused_pair_us_per_layer=round(t_pair * 1e3, 2),
                                note="GDN decode with the gated RMSNorm epilogue (not part of the state-path step): in "
                                     "the same launch vs a second launch")  # fmt: skip
@@ -691,6 +693,54 @@ def bench_mlp_layer(args, torch, tel):
     return out
 
 
+def ceilings(torch, reps=4):
+    """The bare access patterns of the kernel families, timed like the kernels (back-to-back launches in a HIP
+    graph, the buffers rotating over more than twice the 256 MB Infinity Cache), in GB/s of bytes moved:
+    a nontemporal streaming read (134 MB per launch: the batch-8 attention working set; and 1 GiB), a 1:1
+    nontemporal copy (25.2 MB -> 25.2 MB, in place like the GDN state's update and to a second buffer; and
+    512 MB), and the paged attention's
+    block-table gather of the batch-8, 4096-position working set with its load schedule and no compute."""
+    from qwen36_state import workloads as W
+    from qwen36_state._lib import lib
+
+    L = lib()
+    dev = "cuda:0"
+    out = {}
+
+    def run(name, nbytes, bufs, make):
+        sink = torch.zeros(max(L.qs_probe_sink_words(nbytes), 4096), dtype=torch.int32, device=dev)
+        ms = kernel_time(torch, lambda st: [make(b, sink, st) for b in bufs], reps)
+        out[name] = dict(us=round(ms * 1e3, 2), gbs=round(nbytes / (ms * 1e-3) / 1e9, 1),
+                         frac_of_peak=round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4))  # fmt: skip
+
+    for nb, n in ((134217728, 4), (1 << 30, 1)):
+        bufs = [torch.ones(nb // 4, dtype=torch.float32, device=dev) for _ in range(n)]
+        run(f"read_{nb >> 20}MiB", nb, bufs, lambda b, sink, st: ("qs_probe_read", (_p(b), ctypes.c_size_t(b.numel() * 4),
+                                                                                   _p(sink), st)))  # fmt: skip
+        del bufs
+    for nb, n, inplace in ((25165824, 24, True), (25165824, 24, False), (536870912, 1, False)):
+        bufs = [(torch.ones(nb // 4, device=dev), None if inplace else torch.empty(nb // 4, device=dev)) for _ in range(n)]
+        run(f"copy_{nb >> 20}MiB" + ("_in_place" if inplace else ""), 2 * nb, bufs,
+            lambda b, sink, st: ("qs_probe_copy", (_p(b[0]), _p(b[0] if b[1] is None else b[1]), ctypes.c_size_t(nb),
+                                                   st)))  # fmt: skip
+        del bufs
+    torch.cuda.empty_cache()
+    B, ctx, pps = 8, 4096, 8
+    d = W.attn_layer(B, ctx, dev, seed=3, num_blocks=2048)
+    # four tables over disjoint quarters of the 2048-page pools, each a seeded permutation of its pages
+    gen = torch.Generator().manual_seed(10)
+    tabs = [(512 * i + torch.randperm(512, generator=gen)).to(torch.int32).reshape(B, ctx // 64).to(dev) for i in range(4)]
+    gbytes = B * 4 * ctx * 256 * 2 * 2
+    sink = torch.zeros(L.qs_probe_gather_sink_words(B, 4, ctx // 64, pps), dtype=torch.int32, device=dev)
+    ms = kernel_time(torch, lambda st: [("qs_probe_gather", (_p(d["k_cache"]), _p(d["v_cache"]), _p(t), B, 4, ctx // 64,
+                                                             ctx // 64, 2048, pps, _p(sink), st)) for t in tabs], reps)  # fmt: skip
+    out["gather_attn_b8_4k"] = dict(us=round(ms * 1e3, 2), gbs=round(gbytes / (ms * 1e-3) / 1e9, 1),
+                                    frac_of_peak=round(gbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4))  # fmt: skip
+    del d, tabs
+    torch.cuda.empty_cache()
+    return out
+
+
 def copy_ceiling(torch):
     """Device-to-device copy of 1 GiB (torch's copy kernel): GB/s counting the read and the write."""
     src = torch.ones(1 << 28, dtype=torch.float32, device="cuda:0")
@@ -706,6 +756,7 @@ def copy_ceiling(torch):
 
 WORKLOADS = {
     "step": bench_step,
+    "step-b1": lambda args, torch, tel: bench_step(args, torch, tel, batch=1, pps=args.pps_b1),
     "gdn-layer": bench_gdn_layer,
     "attn-layer": bench_attn_layer,
     "verify-step": bench_verify,
@@ -713,8 +764,8 @@ WORKLOADS = {
     "conv-prefill": bench_conv_prefill,
     "mlp-layer": bench_mlp_layer,
 }
-CONFIG_OF = {"gdn-layer": 0, "attn-layer": 1, "step": 2, "verify-step": 3, "prefill": 4, "conv-prefill": "f2",
-             "mlp-layer": "f4"}
+CONFIG_OF = {"gdn-layer": 0, "attn-layer": 1, "step": 2, "step-b1": "2 at batch 1", "verify-step": 3, "prefill": 4,
+             "conv-prefill": "f2", "mlp-layer": "f4"}
 
 
 # ------------------------------------------------------------------------------------------------ profiling
@@ -813,6 +864,7 @@ def main():
     ap.add_argument("--layers", type=int, default=64)
     ap.add_argument("--pps", type=int, default=8, help="pages per split-K workgroup (step workload)")
     ap.add_argument("--pps-attn1", type=int, default=8, help="pages per split (attn-layer workload)")
+    ap.add_argument("--pps-b1", type=int, default=4, help="pages per split (step-b1 workload)")
     ap.add_argument("--pps-verify", type=int, default=2, help="pages per split (verify-step workload)")
     ap.add_argument("--kernel-reps", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baselines")
@@ -840,13 +892,15 @@ def main():
     head_tel = tel.summary()
     configs = {}
     if args.workload == "all":
-        for wl in ("gdn-layer", "attn-layer", "verify-step", "prefill", "conv-prefill", "mlp-layer"):
+        for wl in ("step-b1", "gdn-layer", "attn-layer", "verify-step", "prefill", "conv-prefill", "mlp-layer"):
             log(f"workload {wl}")
             configs[wl] = WORKLOADS[wl](args, torch, tel)
             configs[wl]["config"] = CONFIG_OF[wl]
             configs[wl]["telemetry"] = tel.summary()
             log(f"{wl}: {configs[wl]['us_per_step']} µs, {configs[wl]['value']} GB/s")
     ceiling = copy_ceiling(torch)
+    probes = ceilings(torch)
+    log("ceilings: " + ", ".join(f"{k} {v['gbs']} GB/s" for k, v in probes.items()))
     ms = head["us_per_step"] / 1e3
     out = dict(
         metric=METRIC, value=head["value"], unit="GB/s", n_gpus=1, steps=args.steps, warmup=args.warmup,
@@ -856,7 +910,7 @@ def main():
                     **{k: head[k] for k in ("batch", "context", "layers", "pages_per_split") if k in head}),
         roofline=head["roofline"],
         stats=dict(median_us=head["median_us"], p10_us=head["p10_us"], p90_us=head["p90_us"], replays=head["replays"]),
-        telemetry=head_tel, copy_ceiling=ceiling,
+        telemetry=head_tel, copy_ceiling=ceiling, ceilings=probes,
     )  # fmt: skip
     for k in ("kernels", "gdn_epilogue", "cpu_baseline"):
         if k in head:

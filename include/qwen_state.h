@@ -319,6 +319,21 @@ size_t qs_mlp_decode_workspace_bytes(int B, int H, int I);
 int qs_mlp_decode(const float *x, const float *gamma, const uint8_t *gate, const uint8_t *up, const uint8_t *down,
                   int down_fmt, float *x_out, void *workspace, int B, int H, int I, float eps, void *stream);
 
+/* ------------------------------------------------------------------- measurement probes (no reference part)
+ * The bare access patterns the kernels are measured against (bench.py reports them beside each kernel):
+ * qs_probe_read streams `bytes` (a multiple of 16384) with nontemporal loads, a wave per 16 KB chunk;
+ * qs_probe_copy reads src and writes dst (which may be src) once each, the stores written through the L2 as
+ * the GDN state's are; qs_probe_gather reads the K and V tiles of
+ * pages 0 .. npages - 1 of every user's block-table row for every KV head with the paged attention's load
+ * schedule (pps pages per workgroup, no compute). The loaded data only feeds a checksum that decides a
+ * store into sink (device memory of qs_probe_sink_words(bytes) / qs_probe_gather_sink_words words). */
+size_t qs_probe_sink_words(size_t bytes);
+int qs_probe_read(const void *src, size_t bytes, uint32_t *sink, void *stream);
+int qs_probe_copy(const void *src, void *dst, size_t bytes, void *stream);
+size_t qs_probe_gather_sink_words(int B, int NKV, int max_blocks, int pps);
+int qs_probe_gather(const uint16_t *k_cache, const uint16_t *v_cache, const int *block_table, int B, int NKV,
+                    int max_blocks, int npages, int num_blocks, int pps, uint32_t *sink, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -60,6 +60,11 @@ SIGNATURES = {
     "qs_mx_gemv": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "qs_mlp_decode_workspace_bytes": (_Z, [_I, _I, _I]),
     "qs_mlp_decode": (_I, [_P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _F, _P]),
+    "qs_probe_sink_words": (_Z, [_Z]),
+    "qs_probe_read": (_I, [_P, _Z, _P, _P]),
+    "qs_probe_copy": (_I, [_P, _P, _Z, _P]),
+    "qs_probe_gather_sink_words": (_Z, [_I, _I, _I, _I]),
+    "qs_probe_gather": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P]),
 }
 
 _lib = None
