@@ -9,6 +9,8 @@ from qwen36_state import ops, workloads as W
 
 pytestmark = pytest.mark.gpu
 
+CNT_BYTES = 65536  # the fixed counter block at the head of an attention workspace
+
 
 def run_case(dev, d, pps, fused=True):
     """Attention (+ append) on the GPU and the same step through the oracle; returns (o_gpu, o_ref,
@@ -129,12 +131,37 @@ def test_in_launch_merge_counters_rearm(dev):
             o = ops.paged_gqa_decode(g["q"], g["k_cache"], g["v_cache"], g["block_table"], g["seq_lens"], d["scale"],
                                      pages_per_split=4, ws=ws)  # fmt: skip
             torch.cuda.synchronize()
-            assert int(ws[:65536].view(torch.int32).abs().sum()) == 0, "counters not re-armed"
+            assert int(ws[:CNT_BYTES].view(torch.int32).abs().sum()) == 0, "counters not re-armed"
             outs.append(o.cpu())
     assert torch.equal(outs[0], outs[2]) and torch.equal(outs[1], outs[3])
     for d, o in zip(data, outs):
         ref = O.gqa_decode(d["q"], d["k_cache"], d["v_cache"], d["block_table"], d["seq_lens"], d["scale"])
         assert_attn_output(o, O.bf16(ref))
+
+
+# More than 16 splits go through the separate merge launch (one workgroup per output row, the partials merged in
+# split order): 18, 64, 512 and 1024 splits, verify rows on the MFMA kernel at 64 and 32 splits, batch 3 with an
+# idle user. Three calls give the same bits, match the oracle, and leave the in-launch counters at zero.
+@pytest.mark.parametrize("B,ctx,T,pps", [(2, 1100, 1, 1), (1, 32768, 1, 8), (1, 32768, 1, 1), (1, 65536, 1, 1),
+                                         (1, 8192, 4, 2), (3, 2000, 4, 1)])  # fmt: skip
+def test_many_splits_repeatable(dev, B, ctx, T, pps):
+    d = W.attn_layer(B, ctx, "cpu", seed=3 * B + T + pps, T=T, num_blocks=B * (ctx // 64 + 1) + 64)
+    if B == 3:
+        d["seq_lens"][1] = 0  # idle: no workgroup of the user arrives at its counters
+    g = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in d.items()}
+    mb = d["block_table"].shape[1]
+    ws = torch.zeros(ops.lib().qs_paged_attention_workspace_bytes(B, T, 24, 4, 256, mb, pps), dtype=torch.uint8,
+                     device=dev)  # fmt: skip
+    outs = []
+    for _ in range(3):
+        o = ops.paged_gqa_decode(g["q"], g["k_cache"], g["v_cache"], g["block_table"], g["seq_lens"], d["scale"],
+                                 pages_per_split=pps, ws=ws)  # fmt: skip
+        torch.cuda.synchronize()
+        assert int(ws[:CNT_BYTES].view(torch.int32).abs().sum()) == 0, "counters not re-armed"
+        outs.append(o.cpu())
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
+    ref = O.gqa_decode(d["q"], d["k_cache"], d["v_cache"], d["block_table"], d["seq_lens"], d["scale"])
+    assert_attn_output(outs[0], O.bf16(ref))
 
 
 @pytest.mark.parametrize("ctx,pps", [(131072, 64), (131072, 2), (262144, 4)])
