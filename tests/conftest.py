@@ -25,10 +25,12 @@ for p in (REPO, os.path.join(REPO, "tt-qwen-resident_amd")):
 #                             RMS(o) whatever the element's own size; observed <= 4.4e-3 x RMS.
 STATE_RTOL, STATE_FLOOR, PREFILL_STATE_FLOOR = 1e-4, 1e-5, 1e-4
 OUT_RTOL, GDN_OUT_FLOOR, ATTN_OUT_FLOOR = 2e-2, 1e-3, 1e-2
-# Heads whose conv inputs differ from the oracle's in one bf16 ulp (the exponential inside SiLU differs in
-# the last fp32 bit between libraries) get a perturbation bound instead: one ulp of one v channel moves its
-# state column by beta |k_i| 2^-8 |v| ~ 0.5% of the state RMS (observed <= 2.9e-3 x RMS).
-PERTURBED_RTOL, PERTURBED_FLOOR = 2e-2, 1e-2
+# The conv output y (bf16) of the fused kernels agrees with the oracle's bit for bit except where SiLU's fp32
+# value sits within an ulp of a bf16 rounding boundary: the exponential's last bit decides there, and it
+# differs between libraries. The end-to-end checks therefore take the state path in two stages: y against the
+# oracle's (at most one bf16 ulp, and few heads touched), and every head's state against the oracle's delta rule
+# driven by the kernel's y, at the fp32 state tolerance. For the heads whose y agrees, that reference is the
+# oracle's own from x, bit for bit.
 
 
 def pytest_configure(config):
@@ -93,15 +95,10 @@ def assert_prefill_state(got, ref):
     _close("prefill_state", got, ref, STATE_RTOL, PREFILL_STATE_FLOOR)
 
 
-def assert_state_perturbed(got, ref):
-    """State of a head whose conv inputs differ from the oracle's by one bf16 ulp: rtol 2e-2, floor 1e-2 x RMS."""
-    _close("state_perturbed", got, ref, PERTURBED_RTOL, PERTURBED_FLOOR)
-
-
 def perturbed_ok(perturbed):
-    """The perturbed heads of one check are few: at most 6 or 2% of the heads, whichever is more. One
-    mismatched q or k channel perturbs the 3 value heads of its key head, so 6 is two mismatch events; in a
-    batch-1 layer one event is already 6% of the 48 heads."""
+    """The heads whose conv inputs differ from the oracle's are few: at most 6 or 2% of the heads, whichever is
+    more. One mismatched q or k channel touches the 3 value heads of its key head, so 6 is two mismatch events;
+    in a batch-1 layer one event is already 6% of the 48 heads."""
     n = int(perturbed.sum())
     return n <= max(6, int(0.02 * perturbed.numel()))
 
