@@ -645,17 +645,19 @@ def bench_conv_prefill(args, torch, tel):
 
 def mlp_bytes(B, H, I):
     """Algorithmic HBM bytes of one MLP half: the packed gate | up (MXFP4) and down (MXINT8: the same bytes as
-    MXFP8) weights, x in, gamma, x_out."""
+    MXFP8) weights, x in, x_out (the norm weight is folded into gate | up, as the reference loads them)."""
     from qwen36_state._lib import lib
 
     L = lib()
-    return 2 * L.qs_mx_packed_bytes(H, I, 4) + L.qs_mx_packed_bytes(I, H, 9) + 2 * B * H * 4 + H * 4
+    return 2 * L.qs_mx_packed_bytes(H, I, 4) + L.qs_mx_packed_bytes(I, H, 9) + 2 * B * H * 4
 
 
 def bench_mlp_layer(args, torch, tel):
     """The MLP half of one decoder layer at one row (the reference's 1-chip MLP bench: x [1, 5120], gate | up
     [5120, 17408] 4-bit, down [17408, 5120] 8-bit, us per layer and weight GB/s): three layers' weights
-    (560 MB, beyond the 256 MB Infinity Cache) rotate, twice per replay; per layer = replay / 6."""
+    (560 MB, beyond the 256 MB Infinity Cache) rotate, twice per replay; per layer = replay / 6. The rmsnorm
+    weight is folded into the rows of gate | up, as the reference's loader does (weights.py:107-112), so the
+    call passes no gamma (the synthetic weights stand for folded ones)."""
     from qwen36_state import ops, workloads as W
 
     B, H, I = 1, ops.HIDDEN, ops.INTER
@@ -666,7 +668,7 @@ def bench_mlp_layer(args, torch, tel):
     R = 2
 
     def calls(st):
-        return [("qs_mlp_decode", (_p(d["x"]), _p(d["gamma"]), _p(d["gate"].packed), _p(d["up"].packed),
+        return [("qs_mlp_decode", (_p(d["x"]), None, _p(d["gate"].packed), _p(d["up"].packed),
                                    _p(d["down"].packed), d["down"].fmt, _p(d["out"]), _p(ws), B, H, I,
                                    ctypes.c_float(ops.EPS), st)) for d in layers] * R  # fmt: skip
 
@@ -676,8 +678,9 @@ def bench_mlp_layer(args, torch, tel):
     ms = msr / n
     stats = {k: (v / n if k.endswith("_ms") else v) for k, v in stats.items()}
     nbytes = mlp_bytes(B, H, I)
-    out = entry("MLP half of one decoder layer, 1 row: rmsnorm + gate | up 5120 x 17408 MXFP4 with silu, down "
-                "17408 x 5120 MXINT8 in 4 K splits + residual (2 launches)", nbytes, ms, stats,
+    out = entry("MLP half of one decoder layer, 1 row: rmsnorm (weight folded into gate | up) + gate | up 5120 x "
+                "17408 MXFP4 with silu, down 17408 x 5120 MXINT8 in 4 K splits + residual (2 launches)", nbytes, ms,
+                stats,
                 roofline("mlp_decode", nbytes, ms))  # fmt: skip
     out["us_per_layer"] = out["us_per_step"]
     if not args.no_cpu:
@@ -685,9 +688,9 @@ def bench_mlp_layer(args, torch, tel):
         from oracle import weight_stream as WS
 
         d = layers[0]
-        x, gamma = d["x"].cpu(), d["gamma"].cpu()
+        x = d["x"].cpu()
         G, U, D = d["gate32"], d["up32"], d["down32"]
-        t = cpu_time(torch, lambda: WS.mlp_half(x, gamma, G, U, D))
+        t = cpu_time(torch, lambda: WS.mlp_half(x, None, G, U, D))
         out["cpu_baseline"] = cpu_entry(torch, nbytes, t, "the oracle's MLP half (fp32 weights, dequantization not "
                                         "timed) at the full shape, 1 row")  # fmt: skip
     return out
@@ -848,7 +851,7 @@ def profile_family(args, torch):
         layers = [W.mlp_layer(1, dev, seed=i) for i in range(3)]
         for _ in range(args.reps):
             for d in layers:
-                ops.mlp_decode(d["x"], d["gamma"], d["gate"], d["up"], d["down"])
+                ops.mlp_decode(d["x"], None, d["gate"], d["up"], d["down"])
         torch.cuda.synchronize()
         print(f"mlp_decode: {mlp_bytes(1, ops.HIDDEN, ops.INTER)} algorithmic bytes per layer")
 

@@ -13,16 +13,19 @@
 // KG q + 32 s + 8 g .. + 7 for each 32-value step s of the group (4 steps of 4 bytes for MXFP4, low nibble
 // first; 2 steps of 8 bytes for MXFP8 / MXINT8), then column r's scales (one per step) at 1024 + SCALES r. A
 // wave loads its part of a block as one contiguous kilobyte plus a 4- or 2-byte scale word and converts it to
-// bf16 exactly, the scale folded in: with the hardware's scaled conversions (v_cvt_scalef32_pk_bf16_fp4 /
-// _fp8) or, for MXINT8, on the VALU (the int8 read as an unsigned byte after flipping its sign bit, then one
-// fused multiply-add with the scale; 7-bit magnitudes times a power of two are exact in bf16). It multiplies
-// on v_mfma_f32_16x16x32_bf16 with the activations (bf16, up to 16 rows) as the A operand.
+// bf16 exactly: with the hardware's scaled conversions (v_cvt_scalef32_pk_bf16_fp4 / _fp8, the scale folded
+// in) or, for MXINT8, on the VALU (each int8 as an integer, one signed-byte conversion, exact in bf16; the
+// scale, a power of two, multiplies the 32-value step's product instead, which is exact). It multiplies on
+// v_mfma_f32_16x16x32_bf16 with the activations (bf16, up to 16 rows) as the A operand.
 // The kernels stream weights at the HBM rate; the conversions and MFMAs hide under the loads.
 //
 // MLP half (qs_mlp_decode; down in MXINT8 or MXFP8): h = bf16(x rsqrt(mean(x^2) + eps) gamma); z = bf16(silu(h G) (h U)) in one
 // launch (gate and up tiles in the same workgroup; for one row the workgroups also form h themselves); the
 // down projection split over K (four ways for one row), its last split per tile adding the partials and the
-// residual: x_out = x + z D. Two launches per layer for one row.
+// residual: x_out = x + z D. Two launches per layer for one row; the gate | up grid keeps every CU equally
+// loaded (tail_whole).
+#include <algorithm>
+
 #include "qs_common.h"
 
 namespace {
@@ -69,8 +72,11 @@ __device__ __forceinline__ uint32_t bits(decltype(__builtin_amdgcn_cvt_scalef32_
     return __builtin_bit_cast(uint32_t, v);
 }
 
+// MXINT8 step s of a block: its scale 2^(e - 127) 2^-6 for the lane's column
+__device__ __forceinline__ float int8_scale(uint32_t sc, int s) { return e8m0((sc >> (8 * s)) & 0xffu) * 0.015625f; }
+
 // the lane's B fragments of one block: step s holds K values KG q + 32 s + 8 g .. + 7 of the lane's column,
-// already multiplied by their scale
+// already multiplied by their scale (MXINT8: the integer codes; the scale is applied to the step's product)
 template <int FMT>
 __device__ __forceinline__ void dequant(const u32x4 v, uint32_t sc, bf16x8 (&b)[Mx<FMT>::STEPS]) {
     if constexpr (FMT == FMT_FP4) {
@@ -83,18 +89,16 @@ __device__ __forceinline__ void dequant(const u32x4 v, uint32_t sc, bf16x8 (&b)[
                                                     bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v[s], f, 3))});
         }
     } else if constexpr (FMT == FMT_INT8) {
-        // q 2^(e - 133) = (q + 128) f - 128 f with f = 2^(e - 127) 2^-6: the byte with its sign bit flipped is
-        // q + 128 as an unsigned byte (v_cvt_f32_ubyte), the product and the sum are exact in fp32, and the
-        // value (7 magnitude bits times a power of two) is exact in bf16
+        // the integers q themselves (-128 .. 127, exact in bf16; one signed-byte conversion each): the block's
+        // scale 2^(e - 133) multiplies the step's product instead (int8_scale, in the stream loop)
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-            const float f = e8m0((sc >> (8 * s)) & 0xffu) * 0.015625f, c = -128.0f * f;
             uint32_t wd[4];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const uint32_t u = v[2 * s + h] ^ 0x80808080u;
-                wd[2 * h] = qs::cvt_pk_bf16(fmaf((float)(u & 0xffu), f, c), fmaf((float)((u >> 8) & 0xffu), f, c));
-                wd[2 * h + 1] = qs::cvt_pk_bf16(fmaf((float)((u >> 16) & 0xffu), f, c), fmaf((float)(u >> 24), f, c));
+                const uint32_t u = v[2 * s + h];
+                wd[2 * h] = qs::cvt_pk_bf16((float)(int8_t)(u & 0xffu), (float)(int8_t)((u >> 8) & 0xffu));
+                wd[2 * h + 1] = qs::cvt_pk_bf16((float)(int8_t)((u >> 16) & 0xffu), (float)(int8_t)(u >> 24));
             }
             b[s] = __builtin_bit_cast(bf16x8, u32x4{wd[0], wd[1], wd[2], wd[3]});
         }
@@ -213,6 +217,7 @@ struct Proj {
     float *part;             // nsplit > 1: partial sums [nsplit, NM, B, N] fp32
     int *cnt;                // nsplit > 1: [N / 16] arrival counters, zero between launches
     int B, K, N, nsplit;
+    int nwhole;              // > 0: tiles [0, nwhole) in one split each, the others in nsplit (a balanced grid)
 };
 
 // K groups [q0, q1) of split `split` out of nq
@@ -241,11 +246,20 @@ __global__ __launch_bounds__(256, HREG ? 4 : 5) void proj_kernel(Proj a) {
     __shared__ float s_part[WAVES];
     __shared__ int s_last;
     const int ntile = a.N / TILE_N;
-    const int t = blockIdx.x % ntile, split = blockIdx.x / ntile;
+    // tile t, split `split` of nsp: every tile in a.nsplit splits (split-major), or with a.nwhole > 0 the first
+    // a.nwhole tiles whole and the rest in a.nsplit consecutive workgroups each
+    int t = (int)blockIdx.x % ntile, split = (int)blockIdx.x / ntile, nsp = a.nsplit;
+    if (a.nwhole > 0) {
+        const int i = (int)blockIdx.x - a.nwhole;
+        if (i < 0)
+            t = (int)blockIdx.x, split = 0, nsp = 1;
+        else
+            t = a.nwhole + i / a.nsplit, split = i % a.nsplit;
+    }
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, r = lane & 15, g = lane >> 4;
     const int nq = a.K / M::KG;
-    const int q0 = split_begin(nq, split, a.nsplit), ng = split_begin(nq, split + 1, a.nsplit) - q0;
-    const int P = h_pitch((nq + a.nsplit - 1) / a.nsplit, M::KG);
+    const int q0 = split_begin(nq, split, nsp), ng = split_begin(nq, split + 1, nsp) - q0;
+    const int P = h_pitch((nq + nsp - 1) / nsp, M::KG);
 
     // 1. activation rows of the split: B x ng KG values, 16 bytes per request, the first HV per thread
     // requested before the weight ring, any others after it; or, with NORM (one row, one split), the row of
@@ -330,11 +344,12 @@ __global__ __launch_bounds__(256, HREG ? 4 : 5) void proj_kernel(Proj a) {
         if (!a.gamma)
 #pragma unroll
             for (int c = 0; c < NX; ++c) gv[c] = f32x4{1.f, 1.f, 1.f, 1.f};
+        const int i0 = q0 * M::KG / 4, i1 = (q0 + ng) * M::KG / 4;  // the split's K range, in float4 pieces
 #pragma unroll
         for (int c = 0; c < NX; ++c) {
             const int i = tid + 256 * c;
-            if (i < a.K / 4)
-                *reinterpret_cast<u32x2 *>(s_h + 4 * i) =
+            if (i >= i0 && i < i1)
+                *reinterpret_cast<u32x2 *>(s_h + 4 * (i - i0)) =
                     u32x2{qs::pack_bf2(xv[c][0] * inv * gv[c][0], xv[c][1] * inv * gv[c][1]),
                           qs::pack_bf2(xv[c][2] * inv * gv[c][2], xv[c][3] * inv * gv[c][3])};
         }
@@ -358,8 +373,12 @@ __global__ __launch_bounds__(256, HREG ? 4 : 5) void proj_kernel(Proj a) {
         for (int j = 0; j < RING; ++j) {
             const int lg = w + WAVES * (it * RING + j);
             bf16x8 bw[NM][M::STEPS];
+            uint32_t scs[NM];
 #pragma unroll
-            for (int m = 0; m < NM; ++m) dequant<FMT>(ring[j].v[m], ring[j].sc[m], bw[m]);
+            for (int m = 0; m < NM; ++m) {
+                dequant<FMT>(ring[j].v[m], ring[j].sc[m], bw[m]);
+                scs[m] = ring[j].sc[m];
+            }
             u32x4 ha[HREG ? M::STEPS : 1];
             if constexpr (HREG)
 #pragma unroll
@@ -371,7 +390,18 @@ __global__ __launch_bounds__(256, HREG ? 4 : 5) void proj_kernel(Proj a) {
             for (int s = 0; s < M::STEPS; ++s) {
                 const bf16x8 av = HREG ? __builtin_bit_cast(bf16x8, ha[s]) : *reinterpret_cast<const bf16x8 *>(hq + 32 * s);
 #pragma unroll
-                for (int m = 0; m < NM; ++m) acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bw[m][s], acc[m], 0, 0, 0);
+                for (int m = 0; m < NM; ++m) {
+                    if constexpr (FMT == FMT_INT8) {
+                        // h q exactly (products of bf16 and 8-bit integers, fp32 sums), then times the scale
+                        const f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bw[m][s], f32x4{0.f, 0.f, 0.f, 0.f},
+                                                                                0, 0, 0);
+                        const float f = int8_scale(scs[m], s);
+                        acc[m] = f32x4{fmaf(f, p[0], acc[m][0]), fmaf(f, p[1], acc[m][1]), fmaf(f, p[2], acc[m][2]),
+                                       fmaf(f, p[3], acc[m][3])};
+                    } else {
+                        acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bw[m][s], acc[m], 0, 0, 0);
+                    }
+                }
             }
         }
     }
@@ -391,9 +421,9 @@ __global__ __launch_bounds__(256, HREG ? 4 : 5) void proj_kernel(Proj a) {
             for (int i = 0; i < 4; ++i) acc[m][i] += s_red[0][m][i][lane] + s_red[1][m][i][lane] + s_red[2][m][i][lane];
 
     // 6. partials and the arrival count
-    if (a.nsplit > 1) {
+    if (nsp > 1) {
         if (w == 0) {
-            const auto pr = rsrc(a.part, (uint32_t)a.nsplit * NM * a.B * a.N * 4);
+            const auto pr = rsrc(a.part, (uint32_t)nsp * NM * a.B * a.N * 4);
 #pragma unroll
             for (int m = 0; m < NM; ++m)
 #pragma unroll
@@ -409,21 +439,21 @@ __global__ __launch_bounds__(256, HREG ? 4 : 5) void proj_kernel(Proj a) {
         __syncthreads();
         if (tid == 0) {
             int *c = a.cnt + t;
-            const int last = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.nsplit - 1;
+            const int last = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsp - 1;
             if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             s_last = last;
         }
         __syncthreads();
         if (!s_last || w != 0) return;
         asm volatile("" ::: "memory");
-        const auto pr = rsrc(a.part, (uint32_t)a.nsplit * NM * a.B * a.N * 4);
+        const auto pr = rsrc(a.part, (uint32_t)nsp * NM * a.B * a.N * 4);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int b = 4 * g + i;
             if (b >= a.B) continue;
             float v[NM] = {};
             constexpr int PB = 8 / NM;  // splits' partials per round trip, summed in split order
-            for (int c0 = 0; c0 < a.nsplit; c0 += PB) {
+            for (int c0 = 0; c0 < nsp; c0 += PB) {
                 float pv[NM][PB];
 #pragma unroll
                 for (int k = 0; k < PB; ++k)
@@ -431,7 +461,7 @@ __global__ __launch_bounds__(256, HREG ? 4 : 5) void proj_kernel(Proj a) {
                     for (int m = 0; m < NM; ++m) {
                         const int sp = c0 + k;
                         const uint32_t off =
-                            sp < a.nsplit ? (uint32_t)((((sp * NM + m) * a.B + b) * a.N + col) * 4) : 0xffffff00u;
+                            sp < nsp ? (uint32_t)((((sp * NM + m) * a.B + b) * a.N + col) * 4) : 0xffffff00u;
                         pv[m][k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, off, 0, qs::CP_SC1));
                     }
 #pragma unroll
@@ -533,9 +563,24 @@ bool mx_shape_ok(int K, int N, int fmt) {
 
 template <int FMT, int NM, int EPI, bool NORM = false, bool HREG = false>
 int launch_proj(const Proj &a, hipStream_t st, const char *what) {
-    const size_t lds = HREG ? 0 : h_lds_bytes(a.B, a.K, FMT, a.nsplit);
-    proj_kernel<FMT, NM, EPI, NORM, HREG><<<(unsigned)((a.N / TILE_N) * a.nsplit), 256, lds, st>>>(a);
+    const int ntile = a.N / TILE_N;
+    const size_t lds = HREG ? 0 : h_lds_bytes(a.B, a.K, FMT, a.nwhole > 0 ? 1 : a.nsplit);
+    const unsigned grid = a.nwhole > 0 ? (unsigned)(a.nwhole + (ntile - a.nwhole) * a.nsplit) : (unsigned)(ntile * a.nsplit);
+    proj_kernel<FMT, NM, EPI, NORM, HREG><<<grid, 256, lds, st>>>(a);
     return qs::launch_status(what);
+}
+
+// A balanced grid for a one-split projection whose tile count is not a multiple of the 256 CUs: a launch's
+// time follows the most workgroups any CU holds (gate | up at I 17408: 1088 tiles, 4.25 per CU, took as long as
+// 1280 tiles), so the tiles past the last multiple of 256 are split in nst = 256 / (their count) parts, and
+// every CU holds the same work. 0 when the count does not divide 256 or the splits would be shorter than 4
+// K groups.
+int tail_whole(int ntile, int nq, int *nst) {
+    const int whole = ntile / 256 * 256, rest = ntile - whole;
+    *nst = 1;
+    if (whole == 0 || rest == 0 || 256 % rest || 256 / rest > 8 || nq / (256 / rest) < 4) return 0;
+    *nst = 256 / rest;
+    return whole;
 }
 
 // workspace: counters | partials
@@ -546,16 +591,19 @@ size_t proj_ws_bytes(int B, int N, int nm, int nsplit) {
 struct MlpWs {
     size_t h, z, part, total;
     int sg, sd;  // K splits of gate | up and of down
+    int gw, gst; // one row, one split: gate | up tiles kept whole and the split count of the rest (tail_whole)
 };
 MlpWs mlp_ws(int B, int H, int I) {
     auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
     MlpWs l;
     l.sg = proj_splits(B, H, I, FMT_FP4);
     l.sd = proj_splits(B, I, H, FMT_FP8);  // the same for MXINT8 (one layout)
+    l.gst = 1;
+    l.gw = B == 1 && l.sg == 1 && H <= 4 * 256 * NX ? tail_whole(I / TILE_N, H / kg_of(FMT_FP4), &l.gst) : 0;
     l.h = CNT_BYTES;
     l.z = l.h + up((size_t)B * H * 2);
     l.part = l.z + up((size_t)B * I * 2);
-    l.total = l.part + up(std::max((size_t)l.sg * 2 * B * I, (size_t)l.sd * B * H) * 4);
+    l.total = l.part + up(std::max({(size_t)l.sg * 2 * B * I, (size_t)l.gst * 2 * B * I, (size_t)l.sd * B * H}) * 4);
     return l;
 }
 
@@ -643,6 +691,7 @@ extern "C" int qs_mlp_decode(const float *x, const float *gamma, const uint8_t *
     a.B = B, a.K = H, a.N = I, a.nsplit = L.sg;
     if (B == 1 && L.sg == 1 && H <= 4 * 256 * NX) {  // one row: the gate | up workgroups normalise it themselves
         a.x = x, a.gamma = gamma, a.eps = eps;
+        if (L.gw > 0) a.nwhole = L.gw, a.nsplit = L.gst;  // a grid that loads every CU alike
         if (int e = launch_proj<FMT_FP4, 2, EPI_SILU, true, false>(a, st, "qs_mlp_decode (rmsnorm, gate, up)")) return e;
     } else {
         rmsnorm_kernel<<<B, 256, 0, st>>>(x, gamma, h, H, eps);
@@ -652,7 +701,7 @@ extern "C" int qs_mlp_decode(const float *x, const float *gamma, const uint8_t *
         if (e) return e;
     }
     a.W0 = a.W1 = down, a.h = z, a.x = x, a.y = x_out, a.z = nullptr;
-    a.K = I, a.N = H, a.nsplit = L.sd;
+    a.K = I, a.N = H, a.nsplit = L.sd, a.nwhole = 0;
     const char *what = "qs_mlp_decode (down, residual)";
     if (down_fmt == FMT_INT8)
         return use_hreg(B, FMT_INT8) ? launch_proj<FMT_INT8, 1, EPI_RESID, false, true>(a, st, what)
