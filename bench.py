@@ -867,7 +867,7 @@ def main():
     ap.add_argument("--layers", type=int, default=64)
     ap.add_argument("--pps", type=int, default=8, help="pages per split-K workgroup (step workload)")
     ap.add_argument("--pps-attn1", type=int, default=8, help="pages per split (attn-layer workload)")
-    ap.add_argument("--pps-b1", type=int, default=4, help="pages per split (step-b1 workload)")
+    ap.add_argument("--pps-b1", type=int, default=1, help="pages per split (step-b1 workload)")
     ap.add_argument("--pps-verify", type=int, default=2, help="pages per split (verify-step workload)")
     ap.add_argument("--kernel-reps", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baselines")
