@@ -261,9 +261,9 @@ __global__ __launch_bounds__(256, 4) void chunk_prep_kernel(PrefillArgs a) {
             }
         }
         __syncthreads();
-        // the 16 x 32 fragment blocks above the diagonal (rows 0..31, columns 32..63) are zero in P and Tm: they
-        // are not stored, and the walk reads them as an empty range
-        if (!((tid >> 2) < 32 && (tid & 3) >= 2)) {
+        // the 16 x 16 blocks above the diagonal (16-column segment past the 16-row tile) are zero in P and Tm:
+        // they are not stored, and the walk reads them as an empty range
+        if ((tid & 3) <= ((tid >> 2) >> 4)) {
             uint16_t *Pd = a.P + ((size_t)c * a.NV + h) * 2 * CH * CH;
             const int i = tid >> 2, j0 = (tid & 3) * 16;
     #pragma unroll
@@ -336,7 +336,7 @@ __global__ __launch_bounds__(256, 4) void chunk_prep_kernel(PrefillArgs a) {
             }
             uint16_t *Td = a.Tm + 2 * mat;
             const int o0 = frag_off(i, j0, CH / 32), o1 = frag_off(i, j0 + 8, CH / 32);
-            if (!(i < 32 && j0 >= 32)) {
+            if ((j0 >> 4) <= (i >> 4)) {  // no block above the diagonal (all zero; the walk reads none)
                 *reinterpret_cast<uint4 *>(Td + o0) = make_uint4(th[0], th[1], th[2], th[3]);
                 *reinterpret_cast<uint4 *>(Td + o1) = make_uint4(th[4], th[5], th[6], th[7]);
                 *reinterpret_cast<uint4 *>(Td + CH * CH + o0) = make_uint4(tl[0], tl[1], tl[2], tl[3]);
@@ -484,8 +484,8 @@ __global__ __launch_bounds__(WALK_THREADS) void chunk_walk_kernel(PrefillArgs a)
 #pragma unroll
         for (int nh = 0; nh < 2; ++nh) fV[nh] = __builtin_amdgcn_raw_buffer_load_b64(rv, vo + 32 * nh, 0, 0);
     };
-    // (the blocks above the diagonal, rows 0..31 x columns 32..63, are zero and never stored: waves 0 and 1
-    // read their second column step as an empty range)
+    // (the 16 x 16 blocks above the diagonal are zero and never stored: lane group g of wave w reads column
+    // step ks as an empty range when its 16-column segment 2 ks + g / 2 lies past row tile w)
     auto fetch_b = [&](int c) {
         const int cc = min(c, a.nch - 1);
         const auto rb = rsrc((role ? a.P : a.Tm) + ((size_t)cc * a.NV + h) * 2 * CH * CH, 2 * CH * CH * 2);
@@ -495,7 +495,7 @@ __global__ __launch_bounds__(WALK_THREADS) void chunk_walk_kernel(PrefillArgs a)
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks)
                 fB[2 * pl + ks] = __builtin_amdgcn_raw_buffer_load_b128(
-                    rb, w < 2 && ks == 1 ? 0x7fffff00 : fo + (pl * CH * CH + ks * 512) * 2, 0, 0);
+                    rb, 2 * ks + (g >> 1) > w ? 0x7fffff00 : fo + (pl * CH * CH + ks * 512) * 2, 0, 0);
     };
     // output row 16 w + fr, columns 16 nh + fq .. + 3 of chunk c (q waves: O^T accumulators), or nothing (k
     // waves: an empty range), so that every wave issues the same stores
