@@ -408,13 +408,15 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
             // to this workgroup alone (shifted in place / snapshotted here); the q/k channels are read by
             // the rep * NSLAB workgroups of key head kh, so in decode the wave holding them counts itself
             // in (its reads were consumed above; q and k count separately when different waves hold them)
-            // and the last to arrive writes the shifted state at the end and re-arms the counter. The
-            // count's return is waited for only there.
+            // and the last to arrive writes the shifted state at the end (the count wraps to zero with it).
+            // The count's return is waited for only there.
             if (isv) conv_commit<VERIFY, TM>(a, inv, yv, b, cv, T, lane < SLAB / 2, lane < SLAB / 2);
             if (isq) conv_commit<VERIFY, TM>(a, inq, yq, b, cq, T, kq_owner, VERIFY && kq_owner);
             if (isk) conv_commit<VERIFY, TM>(a, ink, yk, b, ck, T, kq_owner, VERIFY && kq_owner);
-            if (!VERIFY && (isq || isk) && lane == 0)
-                arrived = atomicAdd(a.counters + (b * a.NK + kh) * 2 + (isq ? 0 : 1), 1);
+            if (!VERIFY && (isq || isk) && lane == 0) {
+                unsigned *cnt = reinterpret_cast<unsigned *>(a.counters) + (b * a.NK + kh) * 2 + (isq ? 0 : 1);
+                arrived = (int)atomicInc(cnt, rep * NSLAB / WPG - 1);
+            }
         }
         float dl[4];
 #pragma unroll
@@ -473,10 +475,11 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
         }
     }
     if (CONV && !VERIFY && (isq || isk)) {
-        // one arrival per workgroup per counter: rep * NSLAB / WPG workgroups read key head kh's q/k history
+        // one arrival per workgroup per counter: rep * NSLAB / WPG workgroups read key head kh's q/k history.
+        // The count wraps to zero at the last arrival by itself (an increment modulo the arrivals), so nothing
+        // is left to re-arm at the end: a store here would hold the launch open for another round trip.
         const int last = __builtin_amdgcn_readfirstlane(arrived) == rep * NSLAB / WPG - 1;
         if (last) {
-            if (lane == 0) atomicExch(a.counters + (b * a.NK + kh) * 2 + (isq ? 0 : 1), 0);
             if (isq) conv_commit<false, TM>(a, inq, yq, b, cq, T, false, true);
             if (isk) conv_commit<false, TM>(a, ink, yk, b, ck, T, false, true);
         }

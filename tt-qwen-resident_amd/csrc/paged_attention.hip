@@ -473,9 +473,9 @@ constexpr int PPAD = 16 + 4;   // s_p row pitch (bf16)
 
 // Split merge inside the attention launch (nsplit <= MERGE_MAX). Every workgroup of (user b, KV head g) has
 // stored its partial with agent-coherent stores (sc1: written through the XCD's L2); each thread waits for
-// its stores to complete, then one thread counts the workgroup in. The workgroup that completes the count
-// re-arms the counter and merges: wave w of NWV takes query rows w, w + NWV, ... (two at a time), lane l owns head
-// dims 4 l .. 4 l + 3, and every split's partial and (m, l) are read with agent-coherent loads in one round
+// its stores to complete, then one thread counts the workgroup in (the count wraps to zero at the last
+// arrival). The workgroup that completes the count merges: wave w of NWV takes query rows w, w + NWV, ...
+// (two at a time), lane l owns head dims 4 l .. 4 l + 3, and every split's partial and (m, l) are read with agent-coherent loads in one round
 // trip. Global max M (log2 domain) and sum L over the splits, weights 2^(m_s - M), O = sum_s w_s O_s / L in
 // split order, so the result does not depend on which workgroup finished last. No L2-wide writeback or
 // invalidate is needed because only sc1 accesses touch the shared data. (The leader side of the
@@ -487,10 +487,10 @@ __device__ __forceinline__ void merge_in_launch(const AttnArgs &a, int b, int g,
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (tid == 0) {
-        int *c = a.cnt + (size_t)b * a.NKV + g;
-        const int last = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.nsplit - 1;
-        if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = last;
+        // an increment modulo the splits: the last arrival leaves the count at zero for the next launch
+        unsigned *c = reinterpret_cast<unsigned *>(a.cnt) + (size_t)b * a.NKV + g;
+        const unsigned ns1 = (unsigned)a.nsplit - 1;
+        s_last = __builtin_amdgcn_atomic_inc32(c, ns1, __ATOMIC_RELAXED, "agent") == ns1;
     }
     __syncthreads();
     if (!s_last) return;

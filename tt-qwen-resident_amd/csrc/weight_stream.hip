@@ -233,9 +233,9 @@ __host__ __device__ inline int h_pitch(int ngmax, int kg) { return ngmax * kg + 
 // stay exact. A operand: h rows from LDS (lane (r, g) holds h[r][32 s + 8 g .. + 7] of each 32-value step;
 // rows past B repeat row B - 1 and land in output rows that are never stored). The 4 waves' sums meet in
 // LDS. With one split the workgroup applies the epilogue; otherwise it stores its partial (written through
-// to memory), counts itself in, and the workgroup that completes the tile's count re-arms the counter, sums
-// the partials in split order and applies the epilogue: EPI_SUM y = sum, EPI_RESID y = x + sum,
-// EPI_SILU z = bf16(silu(h W0) (h W1)). NORM (one row, one split, K <= 5120): the workgroup forms the
+// to memory), counts itself in (the count wraps to zero at the last arrival), and the workgroup that
+// completes the tile's count sums the partials in split order and applies the epilogue: EPI_SUM y = sum,
+// EPI_RESID y = x + sum, EPI_SILU z = bf16(silu(h W0) (h W1)). NORM (one row, one split, K <= 5120): the workgroup forms the
 // rmsnorm'd row h from x and gamma itself instead of reading it. HREG: no staging; each ring slot also
 // holds the group's A fragments, requested from L2 with its weights (lanes of rows past B read zeros).
 template <int FMT, int NM, int EPI, bool NORM, bool HREG>
@@ -438,10 +438,9 @@ __global__ __launch_bounds__(256, HREG ? 4 : 5) void proj_kernel(Proj a) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if (tid == 0) {
-            int *c = a.cnt + t;
-            const int last = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsp - 1;
-            if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            s_last = last;
+            // an increment modulo the splits: the last arrival leaves the count at zero for the next launch
+            unsigned *c = reinterpret_cast<unsigned *>(a.cnt) + t;
+            s_last = __builtin_amdgcn_atomic_inc32(c, nsp - 1, __ATOMIC_RELAXED, "agent") == (unsigned)nsp - 1;
         }
         __syncthreads();
         if (!s_last || w != 0) return;
