@@ -39,7 +39,7 @@ def run_case(dev, d, pps, fused=True):
         (8, 4096, 1, 8),  # the batch-8 step's layer as benchmarked: 8 splits merged inside the launch
         (8, 4096, 1, 4),  # 16 splits merged inside the launch (the limit)
         (1, 8192, 4, 8),  # verify: 4 new rows, causal among them (24 query rows per KV head)
-        (1, 32768, 1, 1),  # 512 splits through the merge launch
+        (1, 32768, 1, 1),  # 512 splits (2048 workgroups) through the merge launch
         (2, 4096, 1, 64),  # one split: no merge
         (2, 3000, 6, 4),  # 36 query rows per KV head: the VALU kernel (two tokens per pass over the pages)
         (1, 700, 7, 64),  # VALU kernel, odd token count, one split
@@ -140,10 +140,11 @@ def test_in_launch_merge_counters_rearm(dev):
 
 
 # More than 16 splits go through the separate merge launch (one workgroup per output row, the partials merged in
-# split order): 18, 64, 512 and 1024 splits, verify rows on the MFMA kernel at 64 and 32 splits, batch 3 with an
-# idle user. Three calls give the same bits, match the oracle, and leave the in-launch counters at zero.
+# split order): 18, 64, 512 and 1024 splits, verify rows on the MFMA kernel at 64, 32 and 18 splits, batch 3 with
+# an idle user at 32 and 18 splits. Three calls give the same bits, match the oracle, leave the in-launch counters
+# at zero and report nothing.
 @pytest.mark.parametrize("B,ctx,T,pps", [(2, 1100, 1, 1), (1, 32768, 1, 8), (1, 32768, 1, 1), (1, 65536, 1, 1),
-                                         (1, 8192, 4, 2), (3, 2000, 4, 1)])  # fmt: skip
+                                         (1, 8192, 4, 2), (3, 2000, 4, 1), (3, 1100, 4, 1)])  # fmt: skip
 def test_many_splits_repeatable(dev, B, ctx, T, pps):
     d = W.attn_layer(B, ctx, "cpu", seed=3 * B + T + pps, T=T, num_blocks=B * (ctx // 64 + 1) + 64)
     if B == 3:
@@ -152,16 +153,29 @@ def test_many_splits_repeatable(dev, B, ctx, T, pps):
     mb = d["block_table"].shape[1]
     ws = torch.zeros(ops.lib().qs_paged_attention_workspace_bytes(B, T, 24, 4, 256, mb, pps), dtype=torch.uint8,
                      device=dev)  # fmt: skip
+    st = ops.Status(dev)
     outs = []
     for _ in range(3):
         o = ops.paged_gqa_decode(g["q"], g["k_cache"], g["v_cache"], g["block_table"], g["seq_lens"], d["scale"],
-                                 pages_per_split=pps, ws=ws)  # fmt: skip
+                                 pages_per_split=pps, ws=ws, status=st.word)  # fmt: skip
         torch.cuda.synchronize()
         assert int(ws[:CNT_BYTES].view(torch.int32).abs().sum()) == 0, "counters not re-armed"
         outs.append(o.cpu())
+    assert st.peek() == 0
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
     ref = O.gqa_decode(d["q"], d["k_cache"], d["v_cache"], d["block_table"], d["seq_lens"], d["scale"])
     assert_attn_output(outs[0], O.bf16(ref))
+
+
+@pytest.mark.parametrize("T", [1, 4])
+def test_merge_launch_ragged(dev, T):
+    """The merge launch over users of very different lengths: one user's 19 splits hold a single page of T rows
+    among 18 empty splits (whose partials carry no weight), the other's all 19 pages."""
+    d = W.attn_layer(2, 19 * 64, "cpu", seed=40 + T, T=T, num_blocks=64)
+    d["seq_lens"] = torch.tensor([T, 19 * 64 - 5], dtype=torch.int32)
+    o, o_ref, same = run_case(dev, d, pps=1)
+    assert same
+    assert_attn_output(o, o_ref)
 
 
 @pytest.mark.parametrize("ctx,pps", [(131072, 64), (131072, 2), (262144, 4)])
