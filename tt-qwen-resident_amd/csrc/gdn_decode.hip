@@ -166,8 +166,10 @@ __device__ __forceinline__ const float *sp_of_t(const GdnArgs &a, size_t user, i
 // The conv: q channels 2 lane, 2 lane + 1 of key head kh on wave WQ, the same k channels on wave WK, the
 // slab's v channels 2 (lane % (SLAB / 2)), + 1 on wave WV (all wave 0 when NW = 1).
 // Memory order: every load is issued first (conv inputs, then the state, then the gates as scalar loads);
-// no global store or atomic is issued before the state loads are consumed, because vmcnt counts loads and
-// stores together and a store in flight would turn each wait for a state load into a wait for everything.
+// no global store is issued before the state loads are consumed, because vmcnt counts loads and stores
+// together and a store in flight would turn each wait for a state load into a wait for everything. The
+// decode's arrival count (an atomic returning its value, counted like a load) is the one exception: it
+// leaves after the conv, behind the state loads, and is waited for only at the end.
 // in_slot (verify only, nullable): user b's input state and conv state are slot in_slot[b] of s_in and
 // conv_in ([n_slots, B, ...]); a slot outside [0, n_slots) reads slot 0.
 // NORM (decode, WPG == NSLAB: a workgroup holds the 4 slabs of one value head): the gated RMSNorm epilogue of
@@ -261,6 +263,21 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
         return;
     }
     ConvPair<TM> inq, ink, inv;
+    // Decode + conv: the waves holding the q/k channels count themselves in once their history is consumed.
+    // Every wave issues the same buffer atomic, out of range on every lane but lane 0 of the q and k waves, so
+    // no branch surrounds it and the compiler's waits for the state loads leave it in flight (a conditional
+    // atomic makes them wait for it). The key head's workgroup holding its first unit adds 1 - N and the others
+    // 1 (N arrivals), so the count is back at zero after every launch and the arrival that brings it there is
+    // the last. The small-batch form counts right after the conv, so the count's round trip overlaps the state
+    // loads and the first token (batch 1: 5.15 -> 4.56 us per layer); the one-wave-per-slab form after the
+    // first token's reductions (counting after the conv there measured slower at batch 8).
+    int arrived = 0;  // lane 0 of the q / k waves: the count before this arrival
+    auto count_in = [&]() {
+        const auto rc = __builtin_amdgcn_make_buffer_rsrc(qs::uniform_ptr(a.counters + (b * a.NK + kh) * 2),
+                                                          (short)0, 8, 0x00020000);
+        const int off = (lane == 0 && (isq || isk)) ? (isq ? 0 : 4) : 8;
+        return __builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(kq_owner ? 1 - rep * NSLAB / WPG : 1, rc, off, 0, 0);
+    };
     if (CONV) {
         if (isq) inq = conv_load<TM>(a, conv_b, b, cq, T);
         if (isk) ink = conv_load<TM>(a, conv_b, b, ck, T);
@@ -294,6 +311,7 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
         if (isq) conv_run<TM>(inq, T, qv, yq);
         if (isk) conv_run<TM>(ink, T, kv, yk);
         if (isv) conv_run<TM>(inv, T, vv, yv);
+        if constexpr (!VERIFY && NW > 1) arrived = count_in();
     } else {
 #pragma unroll
         for (int t = 0; t < TM; ++t) {
@@ -341,7 +359,6 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
 
     if (CONV && NW == 1 && (isq || isk)) __builtin_amdgcn_s_setprio(0);
     // 3. Delta rule, token by token, on the rows held in registers.
-    int arrived = 0;
     for (int t = 0; t < T; ++t) {
         const int gi = ((b * T) + t) * a.NV + h;
         const float decay = expf(gdec[t]);
@@ -406,17 +423,13 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
         if (CONV && t == 0) {
             // The state loads are consumed: now the conv's global outputs. v channels of this slab belong
             // to this workgroup alone (shifted in place / snapshotted here); the q/k channels are read by
-            // the rep * NSLAB workgroups of key head kh, so in decode the wave holding them counts itself
-            // in (its reads were consumed above; q and k count separately when different waves hold them)
-            // and the last to arrive writes the shifted state at the end (the count wraps to zero with it).
-            // The count's return is waited for only there.
+            // the rep * NSLAB workgroups of key head kh, which in decode count themselves in (q and k
+            // separately when different waves hold them): the last to arrive writes the shifted state at the
+            // end, where the count's return is waited for.
             if (isv) conv_commit<VERIFY, TM>(a, inv, yv, b, cv, T, lane < SLAB / 2, lane < SLAB / 2);
             if (isq) conv_commit<VERIFY, TM>(a, inq, yq, b, cq, T, kq_owner, VERIFY && kq_owner);
             if (isk) conv_commit<VERIFY, TM>(a, ink, yk, b, ck, T, kq_owner, VERIFY && kq_owner);
-            if (!VERIFY && (isq || isk) && lane == 0) {
-                unsigned *cnt = reinterpret_cast<unsigned *>(a.counters) + (b * a.NK + kh) * 2 + (isq ? 0 : 1);
-                arrived = (int)atomicInc(cnt, rep * NSLAB / WPG - 1);
-            }
+            if constexpr (!VERIFY && NW == 1) arrived = count_in();
         }
         float dl[4];
 #pragma unroll
@@ -476,9 +489,10 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
     }
     if (CONV && !VERIFY && (isq || isk)) {
         // one arrival per workgroup per counter: rep * NSLAB / WPG workgroups read key head kh's q/k history.
-        // The count wraps to zero at the last arrival by itself (an increment modulo the arrivals), so nothing
-        // is left to re-arm at the end: a store here would hold the launch open for another round trip.
-        const int last = __builtin_amdgcn_readfirstlane(arrived) == rep * NSLAB / WPG - 1;
+        // The increments sum to zero, so nothing is left to re-arm at the end (a store here would hold the
+        // launch open for another round trip).
+        const unsigned inc = kq_owner ? 1u - (unsigned)(rep * NSLAB / WPG) : 1u;
+        const int last = (unsigned)__builtin_amdgcn_readfirstlane(arrived) + inc == 0u;
         if (last) {
             if (isq) conv_commit<false, TM>(a, inq, yq, b, cq, T, false, true);
             if (isk) conv_commit<false, TM>(a, ink, yk, b, ck, T, false, true);
