@@ -155,6 +155,29 @@ __device__ __forceinline__ size_t prow(const AttnArgs &a, int G, int b, int g, i
     return (((size_t)b * a.NKV + g) * a.nsplit + sp) * (size_t)(a.T * G) + qr;
 }
 
+// The MFMA kernels' first requests, each one buffer load with no branch around it (lanes outside the range
+// read zeros without a memory access), so the compiler's waits stay exact: the first page's loads, issued
+// next, need only the block-table entries, and nothing waits for the query rows until they are staged.
+// Block-table entry p0 + lane of user b (zero past the split or the table; only entries below
+// min(max_blocks, p0 + pps) are ever read back).
+__device__ __forceinline__ int split_entries(const AttnArgs &a, int b, int p0, int lane) {
+    const int cnt = max(0, min(a.max_blocks, p0 + a.pps) - p0);
+    const auto r = __builtin_amdgcn_make_buffer_rsrc(
+        qs::uniform_ptr(const_cast<int *>(a.block_table) + (size_t)b * a.max_blocks + min(p0, a.max_blocks)), (short)0,
+        cnt * 4, 0x00020000);
+    return (int)__builtin_amdgcn_raw_buffer_load_b32(r, lane * 4, 0, 0);
+}
+// 16-byte chunk ch of query row qr = t G + hh of user b, KV head g (zeros for qr >= T G)
+__device__ __forceinline__ uint4 q_chunk(const AttnArgs &a, int G, int b, int g, int qr, int ch) {
+    const int T = a.T;
+    const auto r = __builtin_amdgcn_make_buffer_rsrc(
+        qs::uniform_ptr(const_cast<uint16_t *>(a.q) + ((size_t)b * T * a.NQ + (size_t)g * G) * HD), (short)0,
+        ((T - 1) * a.NQ + G) * HD * 2, 0x00020000);
+    const int off = qr < T * G ? ((qr / G) * a.NQ + qr % G) * HD * 2 + ch * 16 : 0x7ffffff0;
+    const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_uint4(x[0], x[1], x[2], x[3]);
+}
+
 // One workgroup per (user, KV head, split); the 4 waves work on the same page at a time, wave w owning
 // rows 16 w .. 16 w + 15, so a page's K and V (16 KB per wave) are requested in one round trip:
 //   K   lane = (row 16 w + lane / 4, piece c = lane % 4): dims 32 i + 8 c .. + 7 for i < 8, 8 x 16-byte loads
@@ -237,8 +260,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     // its 16 V rows, 4 dims per lane, rows 2 j and 2 j + 1 in entry j (.xy, .zw). Loads only issue here.
     auto load_k = [&](int pg, uint4 (&kb)[8]) {
         const auto rk = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint16_t *>(a.k_cache + (size_t)pg * pstride + (size_t)g * BLK * HD), (short)0, BLK * HD * 2,
-            0x00020000);
+            qs::uniform_ptr(const_cast<uint16_t *>(a.k_cache + (size_t)pg * pstride + (size_t)g * BLK * HD)), (short)0,
+            BLK * HD * 2, 0x00020000);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, kvo, i * 64, NT);
@@ -247,8 +270,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     };
     auto load_v = [&](int pg, uint4 (&vb)[8]) {
         const auto rv = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint16_t *>(a.v_cache + (size_t)pg * pstride + (size_t)g * BLK * HD), (short)0, BLK * HD * 2,
-            0x00020000);
+            qs::uniform_ptr(const_cast<uint16_t *>(a.v_cache + (size_t)pg * pstride + (size_t)g * BLK * HD)), (short)0,
+            BLK * HD * 2, 0x00020000);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const u32x2 x0 = __builtin_amdgcn_raw_buffer_load_b64(rv, vvo, (2 * j) * HD * 2, NT);
@@ -582,7 +605,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
     // The first page's K / V loads then wait only for the table entries, not for the length.
     const int p0 = split * a.pps;
     const int *bt = a.block_table + (size_t)b * a.max_blocks;
-    const int bt_pre = p0 + lane < min(a.max_blocks, p0 + a.pps) ? bt[p0 + lane] : -1;
+    const int bt_pre = split_entries(a, b, p0, lane);
     int n = a.seq_lens[b];
     // query rows qr = t G + hh (zero past T G): loaded into registers now, stored to LDS once the first
     // page's loads are in flight
@@ -590,12 +613,8 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
     uint4 qreg[QCH];
 #pragma unroll
     for (int k = 0; k < QCH; ++k) {
-        const int idx = tid + 256 * k, qr = idx >> 5, ch = idx & 31;
-        qreg[k] = make_uint4(0, 0, 0, 0);
-        if (qr < T * G) {
-            const int t = qr / G, hh = qr % G;
-            qreg[k] = *reinterpret_cast<const uint4 *>(a.q + (((size_t)b * T + t) * a.NQ + g * G + hh) * HD + ch * 8);
-        }
+        const int idx = tid + 256 * k;
+        qreg[k] = q_chunk(a, G, b, g, idx >> 5, idx & 31);
     }
 
     auto page_at = [&](int pi) {
@@ -606,8 +625,8 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
 
     auto load_k = [&](int pg, uint4 (&kb)[8]) {
         const auto rk = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint16_t *>(a.k_cache + (size_t)pg * pstride + (size_t)g * BLK * HD), (short)0, BLK * HD * 2,
-            0x00020000);
+            qs::uniform_ptr(const_cast<uint16_t *>(a.k_cache + (size_t)pg * pstride + (size_t)g * BLK * HD)), (short)0,
+            BLK * HD * 2, 0x00020000);
         const int off = (16 * w + l16) * HD * 2 + lg * 16;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -617,8 +636,8 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
     };
     auto load_v = [&](int pg, uint4 (&vb)[8]) {
         const auto rv = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint16_t *>(a.v_cache + (size_t)pg * pstride + (size_t)g * BLK * HD), (short)0, BLK * HD * 2,
-            0x00020000);
+            qs::uniform_ptr(const_cast<uint16_t *>(a.v_cache + (size_t)pg * pstride + (size_t)g * BLK * HD)), (short)0,
+            BLK * HD * 2, 0x00020000);
         const int off = (16 * w + (lane >> 5)) * HD * 2 + (lane & 31) * 16;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
@@ -867,7 +886,9 @@ __global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(
     const int split = lid % a.nsplit;
     const int g = (lid / a.nsplit) % a.NKV;
     const int b = lid / (a.nsplit * a.NKV);
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    // the wave index through readfirstlane: the compiler then knows every page index and page address
+    // derived from it is uniform over the wave (else each page load becomes a loop over the lanes' addresses)
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int sl = w & 3, ph = w >> 2;  // the wave's 16-row slice and page phase
     const int l16 = lane & 15, lg = lane >> 4;
     const int T = a.T;
@@ -886,18 +907,14 @@ __global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(
 
     const int p0 = split * a.pps;
     const int *bt = a.block_table + (size_t)b * a.max_blocks;
-    const int bt_pre = p0 + lane < min(a.max_blocks, p0 + a.pps) ? bt[p0 + lane] : -1;
+    const int bt_pre = split_entries(a, b, p0, lane);
     const int n = a.seq_lens[b];
     constexpr int QCH = (NQR * 32 + NTH - 1) / NTH;
     uint4 qreg[QCH];
 #pragma unroll
     for (int k = 0; k < QCH; ++k) {
-        const int idx = tid + NTH * k, qr = idx >> 5, ch = idx & 31;
-        qreg[k] = make_uint4(0, 0, 0, 0);
-        if (qr < T * G) {
-            const int t = qr / G, hh = qr % G;
-            qreg[k] = *reinterpret_cast<const uint4 *>(a.q + (((size_t)b * T + t) * a.NQ + g * G + hh) * HD + ch * 8);
-        }
+        const int idx = tid + NTH * k;
+        qreg[k] = q_chunk(a, G, b, g, idx >> 5, idx & 31);  // rows past NQR are never staged
     }
     auto page_at = [&](int pi) {
         const int pg = __builtin_amdgcn_readlane(bt_pre, pi - p0);
@@ -908,8 +925,8 @@ __global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(
     // (lane % 32) 16): a gather of 16-byte pieces of 16 rows per instruction streams ~20% slower
     auto load_rows = [&](const uint16_t *pool, int pg, uint4 (&rb)[8]) {
         const auto r = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint16_t *>(pool + (size_t)pg * pstride + (size_t)g * BLK * HD), (short)0, BLK * HD * 2,
-            0x00020000);
+            qs::uniform_ptr(const_cast<uint16_t *>(pool + (size_t)pg * pstride + (size_t)g * BLK * HD)), (short)0,
+            BLK * HD * 2, 0x00020000);
         const int off = (16 * sl + (lane >> 5)) * HD * 2 + (lane & 31) * 16;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
