@@ -244,7 +244,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             const size_t dst = (((size_t)pg * a.NKV + g) * BLK + (pos % BLK)) * HD + ch * 8;
             *reinterpret_cast<uint4 *>((kv ? a.v_cache : a.k_cache) + dst) = u;
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        qs::wait_vmem();
         __syncthreads();  // the rows are read by the wave that owns their 16-row slice (the branch is uniform)
     }
 
@@ -507,7 +507,7 @@ constexpr int MERGE_MAX = 16;
 template <int G, int NWV = 4>
 __device__ __forceinline__ void merge_in_launch(const AttnArgs &a, int b, int g, int tid) {
     __shared__ int s_last;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    qs::wait_vmem();
     __syncthreads();
     if (tid == 0) {
         // an increment modulo the splits: the last arrival leaves the count at zero for the next launch
@@ -623,10 +623,12 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
     };
     const size_t pstride = (size_t)a.NKV * BLK * HD;  // elements per page
 
+    // a page of -1 is an empty range: the loads still issue (no branch around them, so the compiler's waits
+    // stay exact) and read zeros without touching memory
     auto load_k = [&](int pg, uint4 (&kb)[8]) {
         const auto rk = __builtin_amdgcn_make_buffer_rsrc(
-            qs::uniform_ptr(const_cast<uint16_t *>(a.k_cache + (size_t)pg * pstride + (size_t)g * BLK * HD)), (short)0,
-            BLK * HD * 2, 0x00020000);
+            qs::uniform_ptr(const_cast<uint16_t *>(a.k_cache + (size_t)max(pg, 0) * pstride + (size_t)g * BLK * HD)),
+            (short)0, pg >= 0 ? BLK * HD * 2 : 0, 0x00020000);
         const int off = (16 * w + l16) * HD * 2 + lg * 16;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -636,8 +638,8 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
     };
     auto load_v = [&](int pg, uint4 (&vb)[8]) {
         const auto rv = __builtin_amdgcn_make_buffer_rsrc(
-            qs::uniform_ptr(const_cast<uint16_t *>(a.v_cache + (size_t)pg * pstride + (size_t)g * BLK * HD)), (short)0,
-            BLK * HD * 2, 0x00020000);
+            qs::uniform_ptr(const_cast<uint16_t *>(a.v_cache + (size_t)max(pg, 0) * pstride + (size_t)g * BLK * HD)),
+            (short)0, pg >= 0 ? BLK * HD * 2 : 0, 0x00020000);
         const int off = (16 * w + (lane >> 5)) * HD * 2 + (lane & 31) * 16;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
@@ -650,10 +652,8 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
     // past the user's length is simply not used
     uint4 KA[8], VA[8];
     const int pg0 = p0 < a.max_blocks ? page_at(p0) : -1;
-    if (pg0 >= 0) {
-        load_k(pg0, KA);
-        load_v(pg0, VA);
-    }
+    load_k(pg0, KA);
+    load_v(pg0, VA);
 
     if (!user_active(a, n, split == 0 && g == 0 && tid == 0)) {  // uniform over the user's workgroups
         if (split == 0) zero_rows<G>(a, b, g, tid);
@@ -662,9 +662,9 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
     const int base = n - T;  // first new position
     const int npages = (n + BLK - 1) / BLK;
     const int p1 = min(npages, p0 + a.pps);
-    if (tid == 0)
-        for (int pi = p0; pi < p1; ++pi)
-            if (page_at(pi) < 0) report_page(a);
+    // an entry of the split's pages outside the pool (lane pi - p0 checks entry pi) is reported after the
+    // page loop: an atomic here, inside a branch, would make the compiler wait for every load at the next use
+    const bool bad_pages = __any(lane < p1 - p0 && (bt_pre < 0 || bt_pre >= a.num_blocks));
 
     // Fused append, first: wave w writes the new rows of its 16-row slices in this split's pages and waits
     // for them, so its slice loads read them back from the pool. No other wave reads these slices.
@@ -686,7 +686,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
             const size_t dst = (((size_t)pg * a.NKV + g) * BLK + (pos % BLK)) * HD + ch * 8;
             *reinterpret_cast<uint4 *>((kv ? a.v_cache : a.k_cache) + dst) = u;
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        qs::wait_vmem();
         if (pg0 >= 0 && base / BLK <= p0) {  // new rows landed in the first page: read it again
             load_k(pg0, KA);
             load_v(pg0, VA);
@@ -727,7 +727,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
             const uint4 v = ok && r0w + row < n ? vb[k] : make_uint4(0, 0, 0, 0);
             *reinterpret_cast<uint4 *>(&s_v[w][row][(lane & 31) * 8]) = v;
         }
-        if (pgn >= 0) load_v(pgn, vb);
+        load_v(pgn, vb);
         f32x4_t sacc[QT];
 #pragma unroll
         for (int nt = 0; nt < QT; ++nt) sacc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -746,7 +746,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
                 }
             }
         }
-        if (pgn >= 0) load_k(pgn, kb);
+        load_k(pgn, kb);
 #pragma unroll
         for (int nt = 0; nt < QT; ++nt) {
             float sc[4];
@@ -819,6 +819,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
     }
     __syncthreads();
     for (int pi = p0; pi < p1; ++pi) page(pi, KA, VA);
+    if (bad_pages && tid == 0) report_page(a);
 
     // this wave's head dims of the split's partial (or of the output); the partials are written through
     // to the agent-coherent level (sc1), where another workgroup of this launch or the merge launch reads them
@@ -923,10 +924,12 @@ __global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(
     const size_t pstride = (size_t)a.NKV * BLK * HD;
     // K and V rows load alike, two whole 512-byte rows per instruction (lane: row 2 k + lane / 32, 16 bytes at
     // (lane % 32) 16): a gather of 16-byte pieces of 16 rows per instruction streams ~20% slower
+    // (a page of -1 is an empty range: the loads still issue, with no branch around them, so the compiler's
+    // waits stay exact, and read zeros without touching memory)
     auto load_rows = [&](const uint16_t *pool, int pg, uint4 (&rb)[8]) {
         const auto r = __builtin_amdgcn_make_buffer_rsrc(
-            qs::uniform_ptr(const_cast<uint16_t *>(pool + (size_t)pg * pstride + (size_t)g * BLK * HD)), (short)0,
-            BLK * HD * 2, 0x00020000);
+            qs::uniform_ptr(const_cast<uint16_t *>(pool + (size_t)max(pg, 0) * pstride + (size_t)g * BLK * HD)),
+            (short)0, pg >= 0 ? BLK * HD * 2 : 0, 0x00020000);
         const int off = (16 * sl + (lane >> 5)) * HD * 2 + (lane & 31) * 16;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
@@ -937,10 +940,8 @@ __global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(
     uint4 KA[8], VA[8];
     const int pf = p0 + ph;  // this wave's first page
     const int pg0 = pf < min(a.max_blocks, p0 + a.pps) ? page_at(pf) : -1;
-    if (pg0 >= 0) {
-        load_rows(a.k_cache, pg0, KA);
-        load_rows(a.v_cache, pg0, VA);
-    }
+    load_rows(a.k_cache, pg0, KA);
+    load_rows(a.v_cache, pg0, VA);
 
     if (!user_active(a, n, split == 0 && g == 0 && tid == 0)) {  // uniform over the user's workgroups
         if (split == 0) zero_rows<G, NTH>(a, b, g, tid);
@@ -949,9 +950,9 @@ __global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(
     const int base = n - T;
     const int npages = (n + BLK - 1) / BLK;
     const int p1 = min(npages, p0 + a.pps);
-    if (tid == 0)
-        for (int pi = p0; pi < p1; ++pi)
-            if (page_at(pi) < 0) report_page(a);
+    // an entry of the split's pages outside the pool (lane pi - p0 checks entry pi) is reported after the
+    // page loop: an atomic here, inside a branch, would make the compiler wait for every load at the next use
+    const bool bad_pages = __any(lane < p1 - p0 && (bt_pre < 0 || bt_pre >= a.num_blocks));
 
     // fused append: each wave writes the new rows of its own slices and waits for them (it alone reads them
     // back)
@@ -973,7 +974,7 @@ __global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(
             const size_t dst = (((size_t)pg * a.NKV + g) * BLK + (pos % BLK)) * HD + ch * 8;
             *reinterpret_cast<uint4 *>((kv ? a.v_cache : a.k_cache) + dst) = u;
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        qs::wait_vmem();
         if (pg0 >= 0 && base / BLK <= pf) {  // new rows landed in this wave's first page: read it again
             load_rows(a.k_cache, pg0, KA);
             load_rows(a.v_cache, pg0, VA);
@@ -1030,7 +1031,7 @@ __global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk)
             *reinterpret_cast<uint4 *>(&s_kv[w][2 * kk + (lane >> 5)][(lane & 31) * 8]) = KA[kk];
-        if (pgn >= 0) load_rows(a.k_cache, pgn, KA);
+        load_rows(a.k_cache, pgn, KA);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         // K fragments (row l16, dims 32 j + 8 lg .. + 7), each used by every query tile
         constexpr int KG = 8;
@@ -1061,7 +1062,7 @@ __global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(
             const uint4 v = ok && r0w + row < n ? VA[kk] : make_uint4(0, 0, 0, 0);
             *reinterpret_cast<uint4 *>(&s_kv[w][row][(lane & 31) * 8]) = v;
         }
-        if (pgn >= 0) load_rows(a.v_cache, pgn, VA);
+        load_rows(a.v_cache, pgn, VA);
         i16x4_t pb[QT];
 #pragma unroll
         for (int nt = 0; nt < QT; ++nt) {
@@ -1102,6 +1103,7 @@ __global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the reads are done before the next page's staging
     }
 
+    if (bad_pages && tid == 0) report_page(a);
     // the waves' (max, sum) per query row; the barrier also frees the q and K / V bytes for the O rows
     if (lg == 0)
 #pragma unroll

@@ -136,6 +136,16 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
+// Waits until every vector memory operation of the wave has completed. Through the builtin rather than
+// inline assembly: the compiler's own wait placement then knows nothing is in flight afterwards (after an
+// inline "s_waitcnt" it still counts earlier stores as pending, and at the next use of a loaded value waits
+// for everything). The empty asm statements keep memory accesses from moving across it.
+__device__ __forceinline__ void wait_vmem() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt and lgkmcnt at their maxima (gfx9 encoding)
+    asm volatile("" ::: "memory");
+}
+
 // A pointer made wave-uniform (its value in the first active lane), for buffer descriptors built from a
 // per-wave base.
 template <class T>
