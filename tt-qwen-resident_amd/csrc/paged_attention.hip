@@ -177,6 +177,15 @@ __device__ __forceinline__ uint4 q_chunk(const AttnArgs &a, int G, int b, int g,
     const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
     return make_uint4(x[0], x[1], x[2], x[3]);
 }
+// 16-byte chunk ch of the new K or V row of token t of user b, KV head g (rows [B, T, NKV, HD]; zeros for
+// t >= T, ch < 0 or a null pointer)
+__device__ __forceinline__ u32x4 new_chunk(const AttnArgs &a, const uint16_t *rows, int b, int g, int t, int ch) {
+    const auto r = __builtin_amdgcn_make_buffer_rsrc(
+        qs::uniform_ptr(const_cast<uint16_t *>(rows ? rows : a.q) + (size_t)b * a.T * a.NKV * HD), (short)0,
+        rows ? a.T * a.NKV * HD * 2 : 0, 0x00020000);
+    const int off = t < a.T && ch >= 0 ? ((t * a.NKV + g) * HD + ch * 8) * 2 : 0x7ffffff0;
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
 
 // One workgroup per (user, KV head, split); the 4 waves work on the same page at a time, wave w owning
 // rows 16 w .. 16 w + 15, so a page's K and V (16 KB per wave) are requested in one round trip:
@@ -917,6 +926,16 @@ __global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(
         const int idx = tid + NTH * k;
         qreg[k] = q_chunk(a, G, b, g, idx >> 5, idx & 31);  // rows past NQR are never staged
     }
+    // The step's new K / V rows (up to TN tokens, which registers allow: two, none with the mixer; more go
+    // through the pool below): token t's chunk lane % 32 of the K row (lanes < 32) or of the V row, requested
+    // before the pages like the query rows
+    constexpr int TN = MIX ? 0 : 2;
+    u32x4 nk[TN > 0 ? TN : 1], nv[TN > 0 ? TN : 1];  // vector types (not uint4): selects stay in registers
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+        nk[t] = new_chunk(a, a.k_new, b, g, t, lane < 32 ? lane : -1);
+        nv[t] = new_chunk(a, a.v_new, b, g, t, lane < 32 ? -1 : lane - 32);
+    }
     auto page_at = [&](int pi) {
         const int pg = __builtin_amdgcn_readlane(bt_pre, pi - p0);
         return (pg >= 0 && pg < a.num_blocks) ? pg : -1;
@@ -954,9 +973,17 @@ __global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(
     // page loop: an atomic here, inside a branch, would make the compiler wait for every load at the next use
     const bool bad_pages = __any(lane < p1 - p0 && (bt_pre < 0 || bt_pre >= a.num_blocks));
 
-    // fused append: each wave writes the new rows of its own slices and waits for them (it alone reads them
-    // back)
-    if (a.k_new && p0 < p1 && base / BLK < p1 && (n - 1) / BLK >= p0) {
+    // Fused append. Up to TN tokens: the new rows stay in registers (nk, nv), the page loop writes them over
+    // the staged rows of this wave's slices, and they go to the pool after the loop, so no store is in flight
+    // while pages load (the compiler would then wait for every load at each use), nothing waits for the
+    // stores, and no page is read twice. More tokens: each wave writes the new rows of its own slices to the
+    // pool and waits for them before its pages are read (it alone reads them back).
+    const bool fresh = a.k_new && T <= TN;
+    auto owned = [&](int pos) {  // a new row this wave attends: in one of its pages and in its slice
+        const int pi = pos / BLK;
+        return pi >= p0 && pi < p1 && (pos % BLK) / 16 == sl && (pi - p0) % WPP == ph;
+    };
+    if (a.k_new && !fresh && p0 < p1 && base / BLK < p1 && (n - 1) / BLK >= p0) {
         for (int idx = lane; idx < T * 64; idx += 64) {
             const int t = idx >> 6, kv = (idx >> 5) & 1, ch = idx & 31;
             const int pos = base + t, pi = pos / BLK;
@@ -968,7 +995,7 @@ __global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(
                 mixer_chunk(u, ch, a.wk, a.rcos + rc, a.rsin + rc, a.rot, a.eps, y);
                 if (!kv) u = pack8(y);
             }
-            if (pi < p0 || pi >= p1 || (pos % BLK) / 16 != sl || (pi - p0) % WPP != ph) continue;
+            if (!owned(pos)) continue;
             const int pg = bt[pi];
             if (pg < 0 || pg >= a.num_blocks) continue;  // reported with the split's pages above
             const size_t dst = (((size_t)pg * a.NKV + g) * BLK + (pos % BLK)) * HD + ch * 8;
@@ -1031,6 +1058,11 @@ __global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk)
             *reinterpret_cast<uint4 *>(&s_kv[w][2 * kk + (lane >> 5)][(lane & 31) * 8]) = KA[kk];
+        if (fresh)  // the step's new K rows over the staged ones (whatever the pool held there)
+#pragma unroll
+            for (int t = 0; t < TN; ++t)
+                if (t < T && base + t >= r0w && base + t < r0w + 16 && lane < 32)
+                    *reinterpret_cast<u32x4 *>(&s_kv[w][base + t - r0w][lane * 8]) = nk[t];
         load_rows(a.k_cache, pgn, KA);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         // K fragments (row l16, dims 32 j + 8 lg .. + 7), each used by every query tile
@@ -1062,6 +1094,11 @@ __global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(
             const uint4 v = ok && r0w + row < n ? VA[kk] : make_uint4(0, 0, 0, 0);
             *reinterpret_cast<uint4 *>(&s_kv[w][row][(lane & 31) * 8]) = v;
         }
+        if (fresh && ok)  // the new V rows
+#pragma unroll
+            for (int t = 0; t < TN; ++t)
+                if (t < T && base + t >= r0w && base + t < r0w + 16 && lane >= 32)
+                    *reinterpret_cast<u32x4 *>(&s_kv[w][base + t - r0w][(lane - 32) * 8]) = nv[t];
         load_rows(a.v_cache, pgn, VA);
         i16x4_t pb[QT];
 #pragma unroll
@@ -1104,6 +1141,16 @@ __global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(
     }
 
     if (bad_pages && tid == 0) report_page(a);
+    if (fresh)  // the new rows this wave attended into the pool (lanes < 32 the K row, the others the V row)
+#pragma unroll
+        for (int t = 0; t < TN; ++t) {
+            const int pos = base + t;
+            if (t >= T || !owned(pos)) continue;
+            const int pg = page_at(pos / BLK);
+            if (pg < 0) continue;  // reported with the split's pages
+            const size_t dst = (((size_t)pg * a.NKV + g) * BLK + (pos % BLK)) * HD + (lane & 31) * 8;
+            *reinterpret_cast<u32x4 *>((lane < 32 ? a.k_cache : a.v_cache) + dst) = lane < 32 ? nk[t] : nv[t];
+        }
     // the waves' (max, sum) per query row; the barrier also frees the q and K / V bytes for the O rows
     if (lg == 0)
 #pragma unroll
