@@ -278,6 +278,10 @@ __global__ __launch_bounds__(256, HREG ? 4 : 5) void proj_kernel(Proj a) {
             xv[c] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
             gv[c] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(gr, a.gamma ? off : 0xffffff00u, 0, 0));
         }
+        // x and gamma leave before the weight ring: the loads in flight when the stream starts are then the
+        // ring's alone, as on every later pass, and the compiler's wait for each ring slot stays exact (with
+        // gamma scheduled after the ring it waited for every load at the top of each pass)
+        __builtin_amdgcn_sched_barrier(0);
     }
     auto fetch_h = [&](int i0) {
 #pragma unroll
