@@ -293,10 +293,13 @@ def attn_call(d, table, lens, B, T, pps, ws, stream, out):
 
 
 def roofline(name, nbytes, ms, traffic_key=None, flops=None):
+    """The roofline object of one kernel family; ``traffic`` is the measured HBM bytes per launch of
+    profiles/pmc_traffic.json under ``traffic_key`` (default: the family's name; ``False``: none measured at
+    this shape, reported as null)."""
     achieved = nbytes / (ms * 1e-3) / 1e9
     traffic = None
     tf = os.path.join(REPO, "profiles", "pmc_traffic.json")
-    if os.path.exists(tf):
+    if traffic_key is not False and os.path.exists(tf):
         with open(tf) as f:
             traffic = json.load(f).get(traffic_key or name, {}).get("hbm_bytes_per_launch")
     out = dict(kernel=name, bound="hbm", achieved=round(achieved, 1), peak=PEAK_HBM_GBS, unit="GB/s",
@@ -422,7 +425,11 @@ def bench_step(args, torch, tel, batch=None, pps=None):
     log(f"GDN with the gated RMSNorm epilogue: fused {t_fused * 1e3:.2f} µs, unfused pair {t_pair * 1e3:.2f} µs")
     work = (f"decode-step state path: {len(gl)} GDN + {len(al)} paged-attention layers, batch {batch}, "
             f"{args.ctx} positions per user, block 64, HIP-graph replay with the position advance")  # fmt: skip
-    out = entry(work, nbytes, ms, stats, roofline(dom, kern[dom][1], kern[dom][0]),
+    # the PMC traffic entries were measured at these shapes (the GDN's bytes do not depend on the context)
+    tkey = {("gdn_decode_fused", 8): "gdn_decode_fused", ("gdn_decode_fused", 1): "gdn_decode_fused_b1"}.get((dom, batch))
+    if dom == "paged_gqa_decode" and (batch, args.ctx, pps) == (8, 4096, 8):
+        tkey = "paged_gqa_decode"
+    out = entry(work, nbytes, ms, stats, roofline(dom, kern[dom][1], kern[dom][0], tkey or False),
                 dict(kernels={k: dict(us_per_launch=round(t * 1e3, 2), bytes_per_launch=b, gbs=round(b / t / 1e6, 1),
                                       launches_per_step=n) for k, (t, b, n) in kern.items()}))  # fmt: skip
     out.update(batch=batch, context=args.ctx, layers=args.layers, pages_per_split=pps)
