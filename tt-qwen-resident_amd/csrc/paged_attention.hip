@@ -1183,10 +1183,16 @@ __global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(
                 float Ms, Ls;
                 row_ml(qr, Ms, Ls);
                 const float sw = M[nt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M[nt] - Ms);
+                f32x4_t *dst = reinterpret_cast<f32x4_t *>(&s_o[sl][qr][4 * lg]);  // + 4 t: head dims 16 t + ..
+                if (stage == 0) {
 #pragma unroll
-                for (int t = 0; t < 16; ++t) {
-                    f32x4_t *dst = reinterpret_cast<f32x4_t *>(&s_o[sl][qr][16 * t + 4 * lg]);
-                    *dst = stage == 0 ? oacc[nt][t] * sw : oacc[nt][t] * sw + *dst;
+                    for (int t = 0; t < 16; ++t) dst[4 * t] = oacc[nt][t] * sw;
+                } else {  // every read first, then every write: one LDS round trip, not one per piece
+                    f32x4_t prev[16];
+#pragma unroll
+                    for (int t = 0; t < 16; ++t) prev[t] = dst[4 * t];
+#pragma unroll
+                    for (int t = 0; t < 16; ++t) dst[4 * t] = oacc[nt][t] * sw + prev[t];
                 }
             }
         }
