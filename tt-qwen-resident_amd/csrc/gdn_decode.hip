@@ -189,6 +189,9 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
     // channels on wave 2 (NW = 4) or on every wave for its own slab (NW = 1)
     constexpr int WK = (NW >= 4 || WPG >= 2) ? 1 : 0;
     constexpr int WV = NW >= 4 ? 2 : NW - 1;
+    // the wave that writes o (and forms each token's q . k for it): the slab's last wave, which reaches each
+    // token's exchange first; wave 0, which also runs the q conv, was the last with o on its path as well
+    constexpr int WO = NW - 1;
     // WPG slab units per workgroup, NW waves each: unit = logical workgroup x WPG + gw
     const int wid = (int)(threadIdx.x >> 6);     // wave within the workgroup
     const int gw = WPG > 1 ? wid / NW : 0;        // slab unit within the workgroup
@@ -227,6 +230,7 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
     auto &s_v = s_v_[gw];
     __shared__ __align__(16) f32x4 s_red_[NW > 1 ? 2 : 1][WPG][NW][2][CG];  // per token parity: wave column sums
     __shared__ float s_nrm[2][WPG];  // NORM, per token parity: the slabs' sums of o^2
+    __shared__ float s_qk_[WPG][TM];  // q . k of every token of the unit
 
     // the q / k conv waves of a multi-slab workgroup issue first: their conv inputs then leave ahead of the other
     // waves' state loads and the norms every slab waits for are ready sooner (the 64-layer batch-8 step:
@@ -299,7 +303,7 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
     // NORM: the epilogue's z and norm_w of the lane's 4 columns, requested now (used after the last token)
     uint2 z4 = make_uint2(0, 0);
     float4 w4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (NORM && w == 0 && lane < CG) {
+    if (NORM && w == WO && lane < CG) {
         z4 = *reinterpret_cast<const uint2 *>(a.z + (size_t)b * a.ldz + h * DV + s * SLAB + cg * 4);
         w4 = *reinterpret_cast<const float4 *>(a.norm_w + s * SLAB + cg * 4);
     }
@@ -358,17 +362,19 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
         __builtin_amdgcn_wave_barrier();
 
     if (CONV && NW == 1 && (isq || isk)) __builtin_amdgcn_s_setprio(0);
+    // q . k of every token, before the token chain (it does not depend on the state): wave w of the unit
+    // forms tokens w, w + NW, ..., every lane writing the wave-uniform sum. Wave WO reads them after each
+    // token's exchange barrier (with one wave per slab it reads back its own writes).
+    for (int t = w; t < T; t += NW) {
+        const float2 q2 = *reinterpret_cast<const float2 *>(&s_qn[t][2 * lane]);
+        const float2 k2 = *reinterpret_cast<const float2 *>(&s_kn[t][2 * lane]);
+        s_qk_[gw][t] = qs::wave_sum_dpp(q2.x * k2.x + q2.y * k2.y);
+    }
     // 3. Delta rule, token by token, on the rows held in registers.
     for (int t = 0; t < T; ++t) {
         const int gi = ((b * T) + t) * a.NV + h;
         const float decay = expf(gdec[t]);
         const float bt = gbeta[t];
-        float qk = 0.f;  // q . k of the token (wave 0 writes o)
-        if (w == 0) {
-            const float2 q2 = *reinterpret_cast<const float2 *>(&s_qn[t][2 * lane]);
-            const float2 k2 = *reinterpret_cast<const float2 *>(&s_kn[t][2 * lane]);
-            qk = qs::wave_sum_dpp(q2.x * k2.x + q2.y * k2.y);
-        }
         float kn[RPL], qn[RPL];
 #pragma unroll
         for (int i4 = 0; i4 < (RPL + 3) / 4; ++i4) {
@@ -449,12 +455,14 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
                                                    qs::CP_NT | qs::CP_SC1);
         }
         if constexpr (NORM) {
-            // the head's o in fp32 (lanes < CG of each slab's wave 0), its sum of squares over the 4 slabs in
+            // the head's o in fp32 (lanes < CG of each slab's wave WO), its sum of squares over the 4 slabs in
             // slab order, then the gated RMSNorm, rounded once to bf16
             float po[4] = {0.f, 0.f, 0.f, 0.f};
-            if (w == 0 && lane < CG)
+            if (w == WO && lane < CG) {
+                const float qk = s_qk_[gw][t];  // q . k of the token (past the exchange barrier)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) po[j] = fmaf(qk, dl[j], decay * r[j]);
+            }
             float ss = (po[0] * po[0] + po[1] * po[1]) + (po[2] * po[2] + po[3] * po[3]);
             // the sum over the first 16-lane row (lanes 0 .. CG - 1 hold o, the others zeros): quads by xor 1,
             // xor 2, then row_ror 4 and 8, after which every lane of the row, lane 0 included, holds the total
@@ -462,9 +470,9 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
             ss += qs::dpp<0x4E>(ss);
             ss += qs::dpp<0x124>(ss);
             ss += qs::dpp<0x128>(ss);
-            if (w == 0 && lane == 0) s_nrm[t & 1][gw] = ss;
+            if (w == WO && lane == 0) s_nrm[t & 1][gw] = ss;
             __syncthreads();
-            if (w == 0 && lane < CG) {
+            if (w == WO && lane < CG) {
                 float tot = s_nrm[t & 1][0];
 #pragma unroll
                 for (int u = 1; u < WPG; ++u) tot += s_nrm[t & 1][u];
@@ -477,7 +485,8 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
                 *reinterpret_cast<uint2 *>(a.o + (size_t)gi * DV + d0) =
                     make_uint2(qs::cvt_pk_bf16(y0, y1), qs::cvt_pk_bf16(y2, y3));
             }
-        } else if (w == 0 && lane < CG) {
+        } else if (w == WO && lane < CG) {
+            const float qk = s_qk_[gw][t];  // q . k of the token (past the exchange barrier)
             float po[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) po[j] = fmaf(qk, dl[j], decay * r[j]);
