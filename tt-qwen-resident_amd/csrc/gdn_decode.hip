@@ -147,6 +147,28 @@ __device__ __forceinline__ float sum_row_groups(float x) {
     return x;
 }
 
+// The small-batch form's column sums (CG = 8) as a reduce-scatter, since the waves' exchange through LDS
+// gathers whole columns afterwards anyway: the 8 partial sums of a lane (p and r of its 4 columns) are halved
+// across lane bit 4 by v_permlane16_swap of two different values (the lower row of each pair keeps the first
+// value's pair sum, the upper row the second's), then across bit 5 by v_permlane32_swap, and the last two are
+// summed across bit 3 on DPP. Lane (cg, bits 3-5) ends with p and r of column 4 cg + 2 (bit 5) + (bit 4) over
+// all 8 row groups, in a fixed order; 14 cross-lane operations and adds instead of 40 for full sums.
+__device__ __forceinline__ float pair_sum16(float a, float b) {
+    const auto x = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(x[0]) + __uint_as_float(x[1]);
+}
+__device__ __forceinline__ float pair_sum32(float a, float b) {
+    const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(x[0]) + __uint_as_float(x[1]);
+}
+__device__ __forceinline__ void scatter_sums8(const float (&p)[4], const float (&r)[4], float &ps, float &rs) {
+    const float tp0 = pair_sum16(p[0], p[1]), tp1 = pair_sum16(p[2], p[3]);
+    const float tr0 = pair_sum16(r[0], r[1]), tr1 = pair_sum16(r[2], r[3]);
+    const float up = pair_sum32(tp0, tp1), ur = pair_sum32(tr0, tr1);
+    ps = up + qs::dpp<0x128>(up);  // xor 8 (row_ror:8)
+    rs = ur + qs::dpp<0x128>(ur);
+}
+
 // First state element of lane (cg, row) of slab s of value head h in user slot `user` of s_in.
 template <int SLAB>
 __device__ __forceinline__ const float *sp_of_t(const GdnArgs &a, size_t user, int h, int s, int cg, int row) {
@@ -403,18 +425,24 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
             r[2] = fmaf(qn[i], S[i].z, r[2]);
             r[3] = fmaf(qn[i], S[i].w, r[3]);
         }
+        if constexpr (NW == 1) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            p[j] = sum_row_groups<CG>(p[j]);
-            r[j] = sum_row_groups<CG>(r[j]);
-        }
-        if constexpr (NW > 1) {
-            // the waves' column sums, added in wave order by every wave (bit-identical everywhere); two
-            // buffers by token parity, so one barrier per token suffices
+            for (int j = 0; j < 4; ++j) {
+                p[j] = sum_row_groups<CG>(p[j]);
+                r[j] = sum_row_groups<CG>(r[j]);
+            }
+        } else {
+            // the wave's column sums, one column component per lane (scatter_sums8), then the waves' sums
+            // added in wave order by every wave (bit-identical everywhere); two buffers by token parity, so one
+            // barrier per token suffices
+            static_assert(NW == 1 || CG == 8, "the reduce-scatter takes 8 column groups");
+            float ps, rs;
+            scatter_sums8(p, r, ps, rs);
             auto &red = s_red_[t & 1][gw];
-            if (rg == 0) {
-                red[w][0][cg] = f32x4{p[0], p[1], p[2], p[3]};
-                red[w][1][cg] = f32x4{r[0], r[1], r[2], r[3]};
+            if (((lane >> 3) & 1) == 0) {
+                const int c = ((lane >> 5) & 1) * 2 + ((lane >> 4) & 1);
+                reinterpret_cast<float *>(&red[w][0][cg])[c] = ps;
+                reinterpret_cast<float *>(&red[w][1][cg])[c] = rs;
             }
             __syncthreads();
             f32x4 P = red[0][0][cg], R = red[0][1][cg];
