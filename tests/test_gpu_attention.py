@@ -73,6 +73,37 @@ def test_attention_unfused_equals_fused(dev):
     assert_attn_output(o1, ref)
 
 
+@pytest.mark.parametrize(
+    "G,T,lens,pps",
+    [
+        (6, 4, [8194], 2),  # the verify shape; new rows at 62..65 of a page pair that two splits share
+        (6, 4, [8194], 1),  # each of those pages its own split
+        (6, 5, [700, 337, 4099], 4),  # ragged users: new rows inside one slice, across slices, across pages
+        (6, 3, [337], 64),  # one split (no merge); rows 14..16 span two waves' slices
+        (4, 8, [1000, 9 * 64 + 4], 2),  # 8 new rows, the most held in registers; the second user's span pages
+        (8, 4, [130, 64], 1),  # 32 query rows; the second user's new rows end its only page
+        (2, 9, [777], 2),  # 9 new rows: more than the registers hold, through the pool instead
+        (2, 16, [2000], 4),  # the most new rows a call takes (16)
+    ],
+)
+def test_verify_append_from_registers(dev, G, T, lens, pps):
+    """The MFMA kernel (17 to 32 query rows per KV head) with up to 8 new rows appends from registers (the new
+    K rows in the score operand, the new V rows as the page is staged, the pool written after the page loop);
+    more rows go through the pool first. Either way: output bit-equal to the unfused append followed by
+    attention, pools equal to the oracle's append, output within the oracle's tolerance."""
+    d = W.attn_layer(len(lens), max(lens), "cpu", seed=G * 100 + T + pps, T=T, num_blocks=512)
+    d["seq_lens"] = torch.tensor(lens, dtype=torch.int32)
+    nkv = d["k_cache"].shape[1]
+    q = d["q"] if G * nkv <= d["q"].shape[2] else torch.cat([d["q"], d["q"]], dim=2)
+    d["q"] = q[:, :, : G * nkv].contiguous()
+    assert 16 < T * G <= 32  # the MFMA kernel's range
+    o1, ref, same1 = run_case(dev, d, pps, fused=True)
+    o2, _, same2 = run_case(dev, d, pps, fused=False)
+    assert same1 and same2
+    assert torch.equal(o1.cpu(), o2.cpu())
+    assert_attn_output(o1, ref)
+
+
 def test_attention_repeatable(dev):
     d = W.attn_layer(1, 32768, "cpu", seed=9)
     g = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in d.items()}

@@ -609,6 +609,12 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
     __shared__ __align__(16) uint16_t s_v[4][16][VPAD];     // the page's V rows, slice by slice
     __shared__ __align__(16) uint16_t s_p[4][QT][16][PPAD];  // P^T of each slice: [query row][slice row]
     __shared__ float s_m[4][NQR], s_l[4][NQR];              // slice max (log2 domain) and row sum
+    // Fused append from registers and LDS (up to TN tokens, no mixer): the new rows are requested with the
+    // query rows, staged in LDS with them, written over the page's rows as those are used (K in the registers
+    // of the score operand, V as it is staged) and stored to the pool after the page loop, so nothing waits for
+    // a store and no page is read twice.
+    constexpr int TN = MIX ? 0 : (32 / G < 8 ? 32 / G : 8);
+    __shared__ __align__(16) uint16_t s_new[TN > 0 ? TN : 1][2][HD];  // token t's new K and V rows
 
     // Issued first, in this order: the split's block-table entries, the user's length and the query rows.
     // The first page's K / V loads then wait only for the table entries, not for the length.
@@ -624,6 +630,13 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
     for (int k = 0; k < QCH; ++k) {
         const int idx = tid + 256 * k;
         qreg[k] = q_chunk(a, G, b, g, idx >> 5, idx & 31);
+    }
+    // the new rows, chunk tid % 32 of token tid / 32 (zeros past T, or with more than TN tokens)
+    const bool fresh = a.k_new && T <= TN;
+    u32x4 nkc = {0u, 0u, 0u, 0u}, nvc = {0u, 0u, 0u, 0u};
+    if constexpr (TN > 0) {
+        nkc = new_chunk(a, fresh ? a.k_new : nullptr, b, g, tid >> 5, tid & 31);
+        nvc = new_chunk(a, fresh ? a.v_new : nullptr, b, g, tid >> 5, tid & 31);
     }
 
     auto page_at = [&](int pi) {
@@ -675,9 +688,10 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
     // page loop: an atomic here, inside a branch, would make the compiler wait for every load at the next use
     const bool bad_pages = __any(lane < p1 - p0 && (bt_pre < 0 || bt_pre >= a.num_blocks));
 
-    // Fused append, first: wave w writes the new rows of its 16-row slices in this split's pages and waits
-    // for them, so its slice loads read them back from the pool. No other wave reads these slices.
-    if (a.k_new && p0 < p1 && base / BLK < p1 && (n - 1) / BLK >= p0) {
+    // Fused append otherwise (more tokens, or the mixer's normalised and rotated k rows), first: wave w writes
+    // the new rows of its 16-row slices in this split's pages and waits for them, so its slice loads read them
+    // back from the pool. No other wave reads these slices.
+    if (a.k_new && !fresh && p0 < p1 && base / BLK < p1 && (n - 1) / BLK >= p0) {
         for (int idx = lane; idx < T * 64; idx += 64) {
             const int t = idx >> 6, kv = (idx >> 5) & 1, ch = idx & 31;
             const int pos = base + t, pi = pos / BLK;
@@ -730,13 +744,35 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
         const int r0w = pi * BLK + 16 * w;  // first position of this wave's slice
         // V rows (zero where the page is invalid or past the user's length: a stale row times a zero
         // probability could be NaN)
+        // new rows in this wave's slice of the page (uniform): token pos - base at slice row pos - r0w
+        const bool has_new = TN > 0 && fresh && ok && r0w + 16 > base && r0w < n;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            const int row = 2 * k + (lane >> 5);
-            const uint4 v = ok && r0w + row < n ? vb[k] : make_uint4(0, 0, 0, 0);
-            *reinterpret_cast<uint4 *>(&s_v[w][row][(lane & 31) * 8]) = v;
+            const int row = 2 * k + (lane >> 5), pos = r0w + row;
+            const bool live = ok && pos < n;
+            u32x4 v = {live ? vb[k].x : 0u, live ? vb[k].y : 0u, live ? vb[k].z : 0u, live ? vb[k].w : 0u};
+            if constexpr (TN > 0)
+                if (has_new) {
+                    const int t = pos - base;
+                    const u32x4 x = *reinterpret_cast<const u32x4 *>(&s_new[min(max(t, 0), TN - 1)][1][(lane & 31) * 8]);
+                    v = live && t >= 0 ? x : v;
+                }
+            *reinterpret_cast<u32x4 *>(&s_v[w][row][(lane & 31) * 8]) = v;
         }
         load_v(pgn, vb);
+        if constexpr (TN > 0)
+            if (has_new) {  // the new K row at this lane's row l16 of the slice, over the pool's (dims 32 j + 8 lg)
+                const int t = r0w + l16 - base;
+                const bool kp = t >= 0 && r0w + l16 < n;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const u32x4 x = *reinterpret_cast<const u32x4 *>(&s_new[min(max(t, 0), TN - 1)][0][32 * j + 8 * lg]);
+                    kb[j].x = kp ? x[0] : kb[j].x;
+                    kb[j].y = kp ? x[1] : kb[j].y;
+                    kb[j].z = kp ? x[2] : kb[j].z;
+                    kb[j].w = kp ? x[3] : kb[j].w;
+                }
+            }
         f32x4_t sacc[QT];
 #pragma unroll
         for (int nt = 0; nt < QT; ++nt) sacc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -826,9 +862,26 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
         }
         *reinterpret_cast<uint4 *>(&s_q[qr][ch * 8]) = u;
     }
+    if constexpr (TN > 0)
+        if (tid < TN * 32) {
+            *reinterpret_cast<u32x4 *>(&s_new[tid >> 5][0][(tid & 31) * 8]) = nkc;
+            *reinterpret_cast<u32x4 *>(&s_new[tid >> 5][1][(tid & 31) * 8]) = nvc;
+        }
     __syncthreads();
     for (int pi = p0; pi < p1; ++pi) page(pi, KA, VA);
     if (bad_pages && tid == 0) report_page(a);
+    if constexpr (TN > 0)
+        if (fresh)  // the new rows of this wave's slices into the pool (lanes < 32 the K row, the others the V row)
+#pragma unroll
+            for (int t = 0; t < TN; ++t) {
+                const int pos = base + t, pi = pos / BLK;
+                if (t >= T || pi < p0 || pi >= p1 || (pos % BLK) / 16 != w) continue;
+                const int pg = page_at(pi);
+                if (pg < 0) continue;  // reported with the split's pages
+                const size_t row = (((size_t)pg * a.NKV + g) * BLK + pos % BLK) * HD + (lane & 31) * 8;
+                *reinterpret_cast<u32x4 *>((lane < 32 ? a.k_cache : a.v_cache) + row) =
+                    *reinterpret_cast<const u32x4 *>(&s_new[t][lane >> 5][(lane & 31) * 8]);
+            }
 
     // this wave's head dims of the split's partial (or of the output); the partials are written through
     // to the agent-coherent level (sc1), where another workgroup of this launch or the merge launch reads them
