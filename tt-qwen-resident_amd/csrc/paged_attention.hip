@@ -736,7 +736,10 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
         for (int dd = 0; dd < 4; ++dd) oacc[nt][dd] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
 
-    // one page: scores of this wave's slice into LDS, barrier, every slice's P V into this wave's dims, barrier
+    // Q^T fragments (query row l16 + 16 nt, dims 32 j + 8 lg .. + 7), held in registers for the split once
+    // the query rows are staged (with the mixer, whose residues double them, they are read from LDS per page)
+    bf16x8_t qbr[MIX ? 1 : QT][MIX ? 1 : 8];
+
     // one page: scores of this wave's slice into LDS, barrier, every slice's P V into this wave's dims,
     // barrier. kb / vb hold the page's K and V rows; each is refilled with the next page's rows as soon as
     // it has been consumed (V after staging, K after the score MFMAs), so one buffer of each suffices.
@@ -783,8 +786,11 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
             const bf16x8_t ak = __builtin_bit_cast(bf16x8_t, kb[j]);
 #pragma unroll
             for (int nt = 0; nt < QT; ++nt) {
-                const bf16x8_t bq = __builtin_bit_cast(
-                    bf16x8_t, *reinterpret_cast<const uint4 *>(&s_q[l16 + 16 * nt][32 * j + 8 * lg]));
+                bf16x8_t bq;
+                if constexpr (MIX)
+                    bq = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(&s_q[l16 + 16 * nt][32 * j + 8 * lg]));
+                else
+                    bq = qbr[nt][j];
                 sacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, bq, sacc[nt], 0, 0, 0);
                 if constexpr (MIX) {
                     const bf16x8_t bl = __builtin_bit_cast(
@@ -870,6 +876,12 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
             *reinterpret_cast<u32x4 *>(&s_new[tid >> 5][1][(tid & 31) * 8]) = nvc;
         }
     __syncthreads();
+    if constexpr (!MIX)
+#pragma unroll
+        for (int nt = 0; nt < QT; ++nt)
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                qbr[nt][j] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(&s_q[l16 + 16 * nt][32 * j + 8 * lg]));
     for (int pi = p0; pi < p1; ++pi) page(pi, KA, VA);
     if (bad_pages && tid == 0) report_page(a);
     if constexpr (TN > 0)
