@@ -1326,35 +1326,42 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, int G) {
     const int rowh = blockIdx.x;  // ((b * T + t) * NKV + g) * G + h
     const int h = rowh % G, row = rowh / G;
     const int g = row % a.NKV, bt = row / a.NKV;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ns = a.nsplit, R = a.T * G;
     const int n = a.seq_lens[bt / a.T];
-    if (n < a.T || n > a.max_blocks * BLK) {  // inactive user (reported by the attention launch): zero row
-        if (w == 0)
-            *reinterpret_cast<uint2 *>(a.o + ((size_t)bt * a.NQ + g * G + h) * HD + 4 * lane) = make_uint2(0, 0);
-        return;
-    }
+    // The row's partials are requested before the length is checked: their addresses do not depend on it and
+    // lie in the workspace either way, so the launch waits for one round trip, not two. Buffer loads, with a
+    // wave's split offset in a scalar register and the lane's 16 bytes as the vector offset, need no per-load
+    // address arithmetic; the (m, l) of splits past ns lie past the descriptor's range and read zeros.
     const size_t pr = prow(a, G, bt / a.T, g, 0, (bt % a.T) * G + h);
-    const size_t sstride = (size_t)R * HD;  // floats between consecutive splits of one row
-    const float *ml = a.part_ml + pr * 2;
-    const float *po = a.part_o + pr * HD + 4 * lane;
-    auto mlv = [&](int sp) { return *reinterpret_cast<const float2 *>(ml + (size_t)sp * R * 2); };
+    const int sbytes = R * HD * 4;  // bytes between consecutive splits of one row's O
+    const auto rpo = __builtin_amdgcn_make_buffer_rsrc(qs::uniform_ptr(a.part_o + pr * HD), (short)0, ns * sbytes,
+                                                       0x00020000);
+    const auto rml = __builtin_amdgcn_make_buffer_rsrc(qs::uniform_ptr(a.part_ml + pr * 2), (short)0, ns * R * 8,
+                                                       0x00020000);
+    auto load_split = [&](int sp, float4 &v, float &m) {  // sp wave-uniform, < ns
+        const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(rpo, lane * 16, sp * sbytes, 0);
+        v = make_float4(__uint_as_float(u[0]), __uint_as_float(u[1]), __uint_as_float(u[2]), __uint_as_float(u[3]));
+        m = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rml, 0, sp * R * 8, 0));
+    };
     float4 x[MCH];
-    float2 mw[MCH];
+    float mw[MCH];
 #pragma unroll
-    for (int k = 0; k < MCH; ++k) {
-        const int sp = min(w + 4 * k, ns - 1);
-        x[k] = *reinterpret_cast<const float4 *>(po + sp * sstride);
-        mw[k] = mlv(sp);
-    }
+    for (int k = 0; k < MCH; ++k) load_split(min(w + 4 * k, ns - 1), x[k], mw[k]);
     // global max and sum over all splits: lane l covers splits l, l + 64, ...
     float M = -INFINITY;
     float2 mg[MAX_SPLITS / 64];
 #pragma unroll
     for (int j = 0; j < MAX_SPLITS / 64; ++j) {
-        mg[j] = make_float2(-INFINITY, 0.f);
-        if (lane + 64 * j < ns) mg[j] = mlv(lane + 64 * j);
+        const u32x2 u = __builtin_amdgcn_raw_buffer_load_b64(rml, (lane + 64 * j) * R * 8, 0, 0);
+        mg[j] = lane + 64 * j < ns ? make_float2(__uint_as_float(u[0]), __uint_as_float(u[1]))
+                                   : make_float2(-INFINITY, 0.f);
         M = fmaxf(M, mg[j].x);
+    }
+    if (n < a.T || n > a.max_blocks * BLK) {  // inactive user (reported by the attention launch): zero row
+        if (w == 0)
+            *reinterpret_cast<uint2 *>(a.o + ((size_t)bt * a.NQ + g * G + h) * HD + 4 * lane) = make_uint2(0, 0);
+        return;
     }
     M = qs::wave_max_bcast(M);
     float L = 0.f;
@@ -1370,16 +1377,12 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, int G) {
         }
     };
 #pragma unroll
-    for (int k = 0; k < MCH; ++k) acc(w + 4 * k, x[k], mw[k].x);
+    for (int k = 0; k < MCH; ++k) acc(w + 4 * k, x[k], mw[k]);
     for (int s0 = 4 * MCH; s0 < ns; s0 += 4 * MCH) {  // further splits, a batch of loads at a time
 #pragma unroll
-        for (int k = 0; k < MCH; ++k) {
-            const int sp = min(s0 + w + 4 * k, ns - 1);
-            x[k] = *reinterpret_cast<const float4 *>(po + sp * sstride);
-            mw[k] = mlv(sp);
-        }
+        for (int k = 0; k < MCH; ++k) load_split(min(s0 + w + 4 * k, ns - 1), x[k], mw[k]);
 #pragma unroll
-        for (int k = 0; k < MCH; ++k) acc(s0 + w + 4 * k, x[k], mw[k].x);
+        for (int k = 0; k < MCH; ++k) acc(s0 + w + 4 * k, x[k], mw[k]);
     }
     s_part[w][lane] = O;
     __syncthreads();
