@@ -222,9 +222,13 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
     const int s = lid % NSLAB;
     const int h = (lid / NSLAB) % a.NV;
     const int b = lid / (NSLAB * a.NV);
-    // an idle slot keeps its state, conv history and output as they are (the workgroup's units belong to one
-    // user: a user's B NV NSLAB units are a multiple of WPG, so the exit is uniform over the workgroup)
-    if (!VERIFY && a.lens && a.lens[b] < 0) return;
+    // decode: the user's length (idle slots are negative), requested before any other load and checked once
+    // the rest are requested; an empty range (no lengths given) reads 0
+    const int lb = VERIFY ? 0
+                          : (int)__builtin_amdgcn_raw_buffer_load_b32(
+                                __builtin_amdgcn_make_buffer_rsrc(const_cast<int *>(a.lens), (short)0, a.lens ? a.B * 4 : 0,
+                                                                  0x00020000),
+                                b * 4, 0, 0);
     const int rep = a.NV / a.NK;
     const int kh = h / rep;
     const int lane = threadIdx.x & 63;
@@ -329,6 +333,14 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
         z4 = *reinterpret_cast<const uint2 *>(a.z + (size_t)b * a.ldz + h * DV + s * SLAB + cg * 4);
         w4 = *reinterpret_cast<const float4 *>(a.norm_w + s * SLAB + cg * 4);
     }
+    // An idle slot keeps its state, conv history and output as they are. The check comes once the loads are
+    // requested (they only read, within the buffers), so the length's round trip overlaps them, and waits for
+    // the length alone (requested first); nothing has been stored or counted yet. The workgroup's units belong
+    // to one user (a user's B NV NSLAB units are a multiple of WPG), so the exit is uniform over the workgroup.
+    // The fence keeps the compiler from sinking the loads below the exit (they are dead on that path), which
+    // would make them wait for the length.
+    asm volatile("" ::: "memory");
+    if (!VERIFY && lb < 0) return;
 
     // 2. q, k (rows 2 lane, 2 lane + 1) and the v slab for every token; L2 norms (q times scale).
     float qv[2][TM], kv[2][TM], vv[2][TM];
