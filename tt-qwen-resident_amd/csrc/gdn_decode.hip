@@ -222,13 +222,15 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
     const int s = lid % NSLAB;
     const int h = (lid / NSLAB) % a.NV;
     const int b = lid / (NSLAB * a.NV);
-    // decode: the user's length (idle slots are negative), requested before any other load and checked once
-    // the rest are requested; an empty range (no lengths given) reads 0
-    const int lb = VERIFY ? 0
-                          : (int)__builtin_amdgcn_raw_buffer_load_b32(
-                                __builtin_amdgcn_make_buffer_rsrc(const_cast<int *>(a.lens), (short)0, a.lens ? a.B * 4 : 0,
-                                                                  0x00020000),
-                                b * 4, 0, 0);
+    // The user's length (idle slots are negative) and, in a verify step, its input slot, requested together
+    // before any other load (an empty range reads 0 when the array is not given): decode checks the length once
+    // its other loads are requested; a verify step needs the slot for its addresses, one round trip for both.
+    auto user_int = [&](const int *p) {
+        return (int)__builtin_amdgcn_raw_buffer_load_b32(
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<int *>(p), (short)0, p ? a.B * 4 : 0, 0x00020000), b * 4, 0, 0);
+    };
+    const int lb = user_int(a.lens);
+    const int slot_in = VERIFY ? user_int(a.in_slot) : 0;
     const int rep = a.NV / a.NK;
     const int kh = h / rep;
     const int lane = threadIdx.x & 63;
@@ -241,11 +243,7 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
     // workgroup holding its first unit writes the shared q/k channel outputs
     const int u0 = lid - gw;
     const bool kq_owner = ((u0 / NSLAB) % a.NV) % rep == 0 && u0 % NSLAB == 0;
-    int slot = 0;
-    if (VERIFY && a.in_slot) {
-        slot = a.in_slot[b];
-        slot = (slot >= 0 && slot < a.n_slots) ? slot : 0;
-    }
+    const int slot = VERIFY && slot_in >= 0 && slot_in < a.n_slots ? slot_in : 0;
     const size_t user_in = (size_t)slot * a.B + b;  // this user's input in s_in / conv_in
 
     // q / k normalised per token, row r = w' RW + g + RG i stored at w' RW + g RPL + i: lane rg of wave w
@@ -267,7 +265,7 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
     const int cq = kh * DK + 2 * lane, ck = qd + cq;                           // q, k channel pairs
     const int cv = 2 * qd + h * DV + s * SLAB + 2 * (lane & (SLAB / 2 - 1));  // v channel pair
     const uint16_t *conv_b = CONV ? a.conv_in + user_in * a.C * (KC - 1) : nullptr;
-    if (VERIFY && a.lens && a.lens[b] < 0) {
+    if (VERIFY && lb < 0) {
         // An idle slot (uniform over the workgroup, whose units belong to one user): no token is verified and
         // no output written. In slot mode its input is carried unchanged into the same slot of the output
         // set, which is the set the next step reads after the acceptance left this user's slot as it was;
