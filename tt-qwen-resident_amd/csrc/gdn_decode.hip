@@ -214,6 +214,13 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
     // the wave that writes o (and forms each token's q . k for it): the slab's last wave, which reaches each
     // token's exchange first; wave 0, which also runs the q conv, was the last with o on its path as well
     constexpr int WO = NW - 1;
+    // The one-wave-per-slab form: the load addresses' kernel arguments, requested with the first batch of
+    // argument loads (the compiler would otherwise request them after the index arithmetic below, a second
+    // round trip before the first load; the other forms already request them in one batch, and the fence
+    // measured slower there)
+    if constexpr (NW == 1)
+        asm volatile("" ::"s"(a.x), "s"(a.conv_in), "s"(a.taps), "s"(a.g), "s"(a.beta), "s"(a.s_in), "s"(a.lens),
+                     "s"(a.in_slot), "s"(a.q), "s"(a.k), "s"(a.v));
     // WPG slab units per workgroup, NW waves each: unit = logical workgroup x WPG + gw
     const int wid = (int)(threadIdx.x >> 6);     // wave within the workgroup
     const int gw = WPG > 1 ? wid / NW : 0;        // slab unit within the workgroup
