@@ -602,7 +602,8 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
     const int split = lid % a.nsplit;
     const int g = (lid / a.nsplit) % a.NKV;
     const int b = lid / (a.nsplit * a.NKV);
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    // the wave index through readfirstlane: the compiler then knows the wave's page and slice tests are uniform
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15, lg = lane >> 4;
     const int T = a.T;
 
@@ -749,33 +750,46 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
         const int r0w = pi * BLK + 16 * w;  // first position of this wave's slice
         // V rows (zero where the page is invalid or past the user's length: a stale row times a zero
         // probability could be NaN)
-        // new rows in this wave's slice of the page (uniform): token pos - base at slice row pos - r0w
+        // new rows in this wave's slice of the page (uniform): token pos - base at slice row pos - r0w; their
+        // LDS reads are issued together, ahead of the staging
         const bool has_new = TN > 0 && fresh && ok && r0w + 16 > base && r0w < n;
+        auto stage_v = [&](const u32x4 (&x)[8], bool patch) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int row = 2 * k + (lane >> 5), pos = r0w + row;
-            const bool live = ok && pos < n;
-            u32x4 v = {live ? vb[k].x : 0u, live ? vb[k].y : 0u, live ? vb[k].z : 0u, live ? vb[k].w : 0u};
-            if constexpr (TN > 0)
-                if (has_new) {
-                    const int t = pos - base;
-                    const u32x4 x = *reinterpret_cast<const u32x4 *>(&s_new[min(max(t, 0), TN - 1)][1][(lane & 31) * 8]);
-                    v = live && t >= 0 ? x : v;
-                }
-            *reinterpret_cast<u32x4 *>(&s_v[w][row][(lane & 31) * 8]) = v;
+            for (int k = 0; k < 8; ++k) {
+                const int row = 2 * k + (lane >> 5), pos = r0w + row;
+                const bool live = ok && pos < n;
+                u32x4 v = {live ? vb[k].x : 0u, live ? vb[k].y : 0u, live ? vb[k].z : 0u, live ? vb[k].w : 0u};
+                if (patch) v = live && pos >= base ? x[k] : v;
+                *reinterpret_cast<u32x4 *>(&s_v[w][row][(lane & 31) * 8]) = v;
+            }
+        };
+        if (TN > 0 && has_new) {
+            u32x4 x[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int t = r0w + 2 * k + (lane >> 5) - base;
+                x[k] = *reinterpret_cast<const u32x4 *>(&s_new[min(max(t, 0), TN > 0 ? TN - 1 : 0)][1][(lane & 31) * 8]);
+            }
+            stage_v(x, true);
+        } else {
+            const u32x4 x[8] = {};
+            stage_v(x, false);
         }
         load_v(pgn, vb);
         if constexpr (TN > 0)
             if (has_new) {  // the new K row at this lane's row l16 of the slice, over the pool's (dims 32 j + 8 lg)
                 const int t = r0w + l16 - base;
                 const bool kp = t >= 0 && r0w + l16 < n;
+                u32x4 x[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    x[j] = *reinterpret_cast<const u32x4 *>(&s_new[min(max(t, 0), TN - 1)][0][32 * j + 8 * lg]);
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const u32x4 x = *reinterpret_cast<const u32x4 *>(&s_new[min(max(t, 0), TN - 1)][0][32 * j + 8 * lg]);
-                    kb[j].x = kp ? x[0] : kb[j].x;
-                    kb[j].y = kp ? x[1] : kb[j].y;
-                    kb[j].z = kp ? x[2] : kb[j].z;
-                    kb[j].w = kp ? x[3] : kb[j].w;
+                    kb[j].x = kp ? x[j][0] : kb[j].x;
+                    kb[j].y = kp ? x[j][1] : kb[j].y;
+                    kb[j].z = kp ? x[j][2] : kb[j].z;
+                    kb[j].w = kp ? x[j][3] : kb[j].w;
                 }
             }
         f32x4_t sacc[QT];
