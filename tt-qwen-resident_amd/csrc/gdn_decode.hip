@@ -233,7 +233,7 @@ __global__ __launch_bounds__(64 * NW * WPG) void gdn_kernel(GdnArgs a) {
         asm volatile("" ::"s"(a.x), "s"(a.conv_in), "s"(a.taps), "s"(a.g), "s"(a.beta), "s"(a.s_in), "s"(a.lens),
                      "s"(a.in_slot), "s"(a.q), "s"(a.k), "s"(a.v));
     // WPG slab units per workgroup, NW waves each: unit = logical workgroup x WPG + gw
-    const int wid = (int)(threadIdx.x >> 6);     // wave within the workgroup
+    const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // wave within the workgroup (uniform)
     const int gw = WPG > 1 ? wid / NW : 0;        // slab unit within the workgroup
     const int nwg = a.B * a.NV * NSLAB / WPG;
     const int lid = qs::xcd_logical(blockIdx.x, nwg) * WPG + gw;
