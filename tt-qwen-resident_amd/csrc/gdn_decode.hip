@@ -198,8 +198,9 @@ __device__ __forceinline__ const float *sp_of_t(const GdnArgs &a, size_t user, i
 // so the update and the stores of S' follow the reduction with no second reduction in between.
 // The conv: q channels 2 lane, 2 lane + 1 of key head kh on wave WQ, the same k channels on wave WK, the
 // slab's v channels 2 (lane % (SLAB / 2)), + 1 on wave WV (all wave 0 when NW = 1).
-// Memory order: every load is issued first (conv inputs, then the state, then the gates as scalar loads);
-// no global store is issued before the state loads are consumed, because vmcnt counts loads and stores
+// Memory order: every load is issued first (the user's length and, in a verify step, its input slot; then the
+// conv inputs, the state and the gates as scalar loads); the idle-slot exit comes after those requests; no
+// global store is issued before the state loads are consumed, because vmcnt counts loads and stores
 // together and a store in flight would turn each wait for a state load into a wait for everything. The
 // decode's arrival count (an atomic returning its value, counted like a load) is the one exception: it
 // leaves after the conv, behind the state loads, and is waited for only at the end.
