@@ -995,6 +995,7 @@ __global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(
     auto s_kv = reinterpret_cast<uint16_t (*)[16][VPAD]>(s_raw + QB + QLB);
     auto s_o = reinterpret_cast<float (*)[NQR][OPAD]>(s_raw);
     __shared__ float s_ml[NWV][NQR][2];
+    __shared__ __align__(16) uint16_t s_nk[WPP == 1 && !MIX ? 2 : 1][HD];  // WPP = 1: the new K rows, for the score operand
 
     const int p0 = split * a.pps;
     const int *bt = a.block_table + (size_t)b * a.max_blocks;
@@ -1037,10 +1038,26 @@ __global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(
             rb[k] = make_uint4(x[0], x[1], x[2], x[3]);
         }
     };
+    // one page per workgroup (WPP = 1): K straight into the score operand's layout (lane: row 16 sl + l16,
+    // dims 32 j + 8 lg .. + 7), no staging through LDS
+    auto load_kfrag = [&](int pg, uint4 (&rb)[8]) {
+        const auto r = __builtin_amdgcn_make_buffer_rsrc(
+            qs::uniform_ptr(const_cast<uint16_t *>(a.k_cache + (size_t)max(pg, 0) * pstride + (size_t)g * BLK * HD)),
+            (short)0, pg >= 0 ? BLK * HD * 2 : 0, 0x00020000);
+        const int off = (16 * sl + l16) * HD * 2 + lg * 16;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, off, j * 64, NT);
+            rb[j] = make_uint4(x[0], x[1], x[2], x[3]);
+        }
+    };
     uint4 KA[8], VA[8];
     const int pf = p0 + ph;  // this wave's first page
     const int pg0 = pf < min(a.max_blocks, p0 + a.pps) ? page_at(pf) : -1;
-    load_rows(a.k_cache, pg0, KA);
+    if constexpr (WPP == 1)
+        load_kfrag(pg0, KA);
+    else
+        load_rows(a.k_cache, pg0, KA);
     load_rows(a.v_cache, pg0, VA);
 
     if (!user_active(a, n, split == 0 && g == 0 && tid == 0)) {  // uniform over the user's workgroups
@@ -1104,6 +1121,10 @@ __global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(
         }
         *reinterpret_cast<uint4 *>(&s_q[qr][ch * 8]) = u;
     }
+    if constexpr (WPP == 1 && TN > 0)
+        if (w == 0 && lane < 32)
+#pragma unroll
+            for (int t = 0; t < TN; ++t) *reinterpret_cast<u32x4 *>(&s_nk[t][lane * 8]) = nk[t];
     __syncthreads();
     // Q^T fragments, held in registers for the split
     bf16x8_t qb[QT][8], qlo[QT][MIX ? 8 : 1];
@@ -1134,6 +1155,36 @@ __global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(
         const int pgn = pi + WPP < p1 ? page_at(pi + WPP) : -1;
         const bool ok = page_at(pi) >= 0;
         const int r0w = pi * BLK + 16 * sl;
+        f32x4_t sacc[QT];
+        if constexpr (WPP == 1) {  // K already in the operand's layout; the new rows patched from LDS
+            if (TN > 0 && fresh && base + T > r0w && base < r0w + 16) {  // new rows in this slice (uniform)
+                const int t = r0w + l16 - base;
+                const bool kp = t >= 0 && t < T;
+                u32x4 x[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    x[j] = *reinterpret_cast<const u32x4 *>(&s_nk[min(max(t, 0), TN > 0 ? TN - 1 : 0)][32 * j + 8 * lg]);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    KA[j].x = kp ? x[j][0] : KA[j].x;
+                    KA[j].y = kp ? x[j][1] : KA[j].y;
+                    KA[j].z = kp ? x[j][2] : KA[j].z;
+                    KA[j].w = kp ? x[j][3] : KA[j].w;
+                }
+            }
+#pragma unroll
+            for (int nt = 0; nt < QT; ++nt) {
+                sacc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const bf16x8_t kb = __builtin_bit_cast(bf16x8_t, KA[j]);
+                    sacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qb[nt][j], sacc[nt], 0, 0, 0);
+                    if constexpr (MIX)
+                        sacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qlo[nt][j], sacc[nt], 0, 0, 0);
+                }
+            }
+            load_kfrag(pgn, KA);
+        } else {
         // K rows through the wave's LDS slice into the A operand (row l16, dims 32 j + 8 lg .. + 7); the next
         // page's K is requested as soon as the rows are in LDS. Scores of masked rows are replaced below.
 #pragma unroll
@@ -1148,7 +1199,6 @@ __global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         // K fragments (row l16, dims 32 j + 8 lg .. + 7), each used by every query tile
         constexpr int KG = 8;
-        f32x4_t sacc[QT];
 #pragma unroll
         for (int nt = 0; nt < QT; ++nt) sacc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1167,6 +1217,7 @@ __global__ __launch_bounds__(256 * WPP, WPP == 1 ? 2 : 1) void attn_wave_kernel(
                 }
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the K reads are done before V overwrites the slice
+        }
         // this page's V rows into the slice (zero where invalid or past the length: a stale row times a zero
         // probability could be NaN), then the next page's V into the registers
 #pragma unroll
