@@ -955,7 +955,8 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
 // 16 (w % 4) .. + 15 of pages p0 + w / 4, p0 + w / 4 + WPP, ... of the split (WPP pages in flight per
 // workgroup) and walks them on its own, with no workgroup barrier inside the page loop:
 //   scores  S^T [16 rows x 16 q] = K Q^T on 8 v_mfma_f32_16x16x32_bf16 (K rows loaded as whole 512-byte rows
-//           and turned into the A operand through the wave's LDS slice, Q^T held in registers);
+//           and turned into the A operand through the wave's LDS slice; with one page per workgroup, whose
+//           chain nothing overlaps, loaded straight in the operand's layout; Q^T held in registers);
 //   softmax per query row against the wave's running max M (log2 domain): P = 2^(s - M) rounded to bf16
 //           lands, lane for lane, in the B-operand layout of the P V product, so P never leaves the
 //           registers; M moves only when a slice max exceeds it by 2^8 (the accumulators are then rescaled),
