@@ -56,6 +56,32 @@ def test_bad_table_entry_reported(dev):
     assert st.peek() == ops.STATUS_PAGE
 
 
+@pytest.mark.parametrize("T", [1, 4])  # the one-token kernel and the verify kernel, both appending in the launch
+def test_bad_entry_on_the_new_rows_page(dev, T):
+    """A table entry outside the pool on the page that holds a user's new rows: reported, neither attended
+    nor written (the user's new rows that land in valid pages still reach the pool, and no other page
+    changes); the other user is untouched by it and matches the oracle."""
+    d = W.attn_layer(2, 10 * 64 + 2, "cpu", seed=11 + T, T=T, num_blocks=64)  # 11 pages per user
+    last = (int(d["seq_lens"][1]) - 1) // 64  # the page of user 1's last new row
+    d["block_table"][1, last] = 64  # one past the pool
+    g = to(d, dev)
+    st = ops.Status(dev)
+    o = ops.paged_gqa_decode(g["q"], g["k_cache"], g["v_cache"], g["block_table"], g["seq_lens"], d["scale"],
+                             k_new=g["k_new"], v_new=g["v_new"], pages_per_split=2, status=st.word)  # fmt: skip
+    assert st.peek() == ops.STATUS_PAGE
+    kc, vc = d["k_cache"].clone(), d["v_cache"].clone()
+    O.paged_append(kc, vc, d["k_new"][:1], d["v_new"][:1], d["block_table"][:1], d["seq_lens"][:1] - T)
+    for t in range(T):  # user 1: only the rows whose page is in the pool
+        pos = int(d["seq_lens"][1]) - T + t
+        page = int(d["block_table"][1, pos // 64])
+        if page < 64:
+            kc[page, :, pos % 64] = d["k_new"][1, t]
+            vc[page, :, pos % 64] = d["v_new"][1, t]
+    assert torch.equal(g["k_cache"].cpu(), kc) and torch.equal(g["v_cache"].cpu(), vc)
+    ref = O.gqa_decode(d["q"][:1], kc, vc, d["block_table"][:1], d["seq_lens"][:1], d["scale"])
+    assert_attn_output(o[:1], O.bf16(ref))
+
+
 def test_advance_lengths(dev):
     lens = torch.tensor([0, 4095, -1, 8191, 8190], dtype=torch.int32, device=dev)
     base = torch.empty_like(lens)
