@@ -3,12 +3,14 @@
 //
 // Decomposition of the delta rule. For value column v the step is column-separable:
 //     delta_v = beta (v_v - e^g sum_k k_k S_kv),  S'_kv = e^g S_kv + k_k delta_v,  o_v = sum_k q_k S'_kv
-// so one wavefront owns a 128 x 32 slab S[:, 32 s .. 32 s + 31] of one (user, value head): 4 slabs per head,
-// B * NV * 4 single-wave workgroups. Lane (rg = lane / 8, cg = lane % 8) holds rows rg + 8 i (i < 16), columns 4 cg .. 4 cg + 3 of the
-// slab in 64 VGPRs; each dwordx4 load or store instruction covers 8 full 128-byte rows. The k-reductions
-// (S^T k and S'^T q) sum a lane's rows in registers, then the row groups (lane bits 3..5) with one DPP step
-// and two lane swaps in a fixed order (bit-reproducible run to run), so no step needs a workgroup barrier.
-// The state is read once and written once per token.
+// so the unit is a 128 x 32 slab S[:, 32 s .. 32 s + 31] of one (user, value head), 4 slabs per head.
+// At large batch one wavefront owns a slab (the slab waves of a workgroup share the key head's q/k conv):
+// lane (rg = lane / 8, cg = lane % 8) holds rows rg + 8 i (i < 16), columns 4 cg .. 4 cg + 3 in 64 VGPRs,
+// each dwordx4 load or store instruction covers 8 full 128-byte rows, and the k-reductions (S^T k and
+// S^T q) sum a lane's rows in registers, then the row groups (lane bits 3..5) with one DPP step and two lane
+// swaps in a fixed order (bit-reproducible run to run), with no workgroup barrier. At small batch a slab's
+// rows are split over 4 waves; per token each wave reduce-scatters its column sums and the waves add them
+// through LDS behind one barrier. The state is read once and written once per token.
 #include <mutex>
 
 #include "qs_common.h"
