@@ -10,9 +10,11 @@
 //   attn_mfma_kernel  17 to 32 query rows (verify steps up to T = 5 at G = 6): MFMA, the 4 waves on the same
 //                     page, each wave owning a quarter of the head dims in P V;
 //   attn_kernel       more query rows: VALU dot products, the 4 waves on the same page.
-// The step's new rows are attended from registers (one-token kernel, up to two tokens) or LDS (the MFMA
-// kernel, up to 8) and stored to the pool after the page loop; with the mixer or more tokens they are
-// appended first, by the wave that reads them back from the pool.
+// The step's new rows are loaded with the query rows and attended without a round trip through the pool:
+// the one-token kernel (up to two tokens) holds them in registers and patches them over the page rows they
+// replace (K through a one-row LDS copy when the page goes straight into the score operand), the MFMA kernel
+// (up to 8) stages them in LDS; both store them to the pool after the page loop. With the mixer or more
+// tokens they are appended first, by the wave that reads them back from the pool.
 // The splits' partials (m, l, unnormalised O per query row) go to the workspace and are merged in split order
 // (the leader side of the reference: global max, rescale, sum, normalise, kernels/attn_leader_writer.cpp:
 // 86-106 and kernels/attn_leader_compute.cpp:42-79) by the last workgroup of the (user, KV head) to finish
