@@ -159,15 +159,19 @@ def test_verify_one_token_equals_decode(dev):
     assert torch.equal(o1, o2[:, 0]) and torch.equal(g1["state"], st[0]) and torch.equal(g1["conv_state"], cv[0])
 
 
-def test_verify_slots_equals_copy_rollback(dev):
+@pytest.mark.parametrize("B,T,accepted", [
+    (3, 3, [2, 3, 1]),                  # 4 waves per slab, slots among the first four
+    (2, 8, [8, 5]),                     # slots 7 and 4: past the four whose histories are read ahead
+    (8, 6, [1, 2, 3, 4, 5, 6, 6, 1]),   # one wave per slab (batch 8), every slot
+])  # fmt: skip
+def test_verify_slots_equals_copy_rollback(dev, B, T, accepted):
     """Slot selection (the next verify reads snapshot a - 1 of the previous step in place) reproduces the
     copy rollback bit for bit: same outputs, snapshots and conv histories for the next verify step."""
-    B, T = 3, 3
     d = inputs(B, seed=51, T=T)
     g = to(d, dev)
     o1, states, convs = ops.gdn_verify_step(g["x"], g["conv_state"], g["taps"], g["g"], g["beta"], g["state"])
-    acc = torch.tensor([2, 3, 1], dtype=torch.int32, device=dev)
-    base = torch.tensor([10, 20, 30], dtype=torch.int32, device=dev)
+    acc = torch.tensor(accepted, dtype=torch.int32, device=dev)
+    base = torch.arange(10, 10 * B + 1, 10, dtype=torch.int32, device=dev)
     # copy path: restore, then verify from the restored state
     st, cv = g["state"].clone(), g["conv_state"].clone()
     seq_c = torch.zeros(B, dtype=torch.int32, device=dev)
@@ -184,6 +188,8 @@ def test_verify_slots_equals_copy_rollback(dev):
     ops.gdn_verify_step_slots(g2["x"], convs, g2["taps"], g2["g"], g2["beta"], states, slot, out=out)
     for a, b in zip(out, ref):
         assert torch.equal(a, b)
+    if B != 3:
+        return
     # an out-of-range accept length leaves the slot and the length untouched
     bad = torch.tensor([0, 5, 2], dtype=torch.int32, device=dev)
     ops.verify_accept(bad, T, slot, seq_s, base)
